@@ -1,0 +1,133 @@
+/*
+ * mosaic_amd -- C ABI of the MI355X (gfx950) quantized-weight matrix path.
+ *
+ * Conventions (every entry point):
+ *   - returns int status: 0 OK, < 0 invalid argument (message in
+ *     mosaic_last_error()), > 0 the hipError_t of a failed launch;
+ *   - every pointer is a device pointer owned by the caller (the library never
+ *     allocates); shapes are int64_t; `stream` is a hipStream_t (NULL = the
+ *     default stream) and work is only enqueued, never synchronized;
+ *   - bf16 tensors are passed as raw 16-bit words, e8m0 scales and e4m3 codes
+ *     as raw bytes, MXFP4 weights as packed bytes [N, K/2] with the low nibble
+ *     holding the even K element and one e8m0 byte per 32 K ([N, K/32]).
+ *
+ * Each declaration names the reference operator it replaces (paths relative
+ * to the reference repository root).
+ */
+#ifndef MOSAIC_AMD_H
+#define MOSAIC_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOSAIC_AMD_ABI_VERSION 1
+
+/* dtype codes */
+#define MOSAIC_DTYPE_F32 0
+#define MOSAIC_DTYPE_BF16 1
+
+/* router score functions (model/layers.py:110-115, .mosaicvm/source/inference_model.py:572-577) */
+#define MOSAIC_SCORE_SIGMOID 0
+#define MOSAIC_SCORE_SOFTMAX 1
+#define MOSAIC_SCORE_SQRTSOFTPLUS 2
+
+/* ------------------------------------------------------------ runtime ---- */
+int mosaic_version(void);
+/* Thread-local text of the last non-zero status. */
+const char* mosaic_last_error(void);
+
+/* ------------------------------------------------------------- codecs ---- */
+/* MXFP4 quantizer, NK layout: w [n, k] (f32 or bf16) -> packed [n, k/2] + e8m0 [n, k/32].
+ * recipe 0 = "ceil" (scale 2^ceil(log2(amax/6)); upstream fp4_quant_kernel,
+ *   .mosaicvm/source/inference_kernel.py:128-183), recipe 1 = "floor"
+ *   (kernels/fp4_source.py:35-64 pack_mxfp4_nk fallback). */
+int mosaic_mx_quantize(const void* w, int w_dtype, uint8_t* packed, uint8_t* scale, int64_t n, int64_t k,
+                       int recipe, void* stream);
+
+/* MXFP4 dequant, NK layout -> out [n, k] f32 or bf16.
+ * Replaces dequant_mxfp4 (kernels/mxfp4.py:130-160) and the decode kernels
+ * decode_e2m1_* (kernels/mxfp4_decode.py:132-223). */
+int mosaic_mx_dequant(const uint8_t* packed, const uint8_t* scale, void* out, int out_dtype, int64_t n, int64_t k,
+                      void* stream);
+
+/* 1 x block E4M3 activation quantizer: x [m, k] (f32/bf16) -> codes [m, k] + f32 scales [m, k/block].
+ * mode 0: power-of-two scale, act_quant_ref (kernels/fp4_source.py:110-129);
+ * mode 1: s = max(amax,1e-4)/448, upstream act_quant (.mosaicvm/source/inference_kernel.py:40-125);
+ * mode 2: s = amax/448, fp8_act_quant (.mosaicvm/source/hubkernel_act_quant.py:27-35). */
+int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s, int64_t m, int64_t k, int block, int mode,
+                     void* stream);
+
+/* E4M3 byte <-> f32 (decode_e4m3 kernels/fp4_source.py:87-91, decode_e4m3_all
+ * kernels/mxfp4_decode.py:243; encoder = torch's float8_e4m3fn cast, RNE). */
+int mosaic_e4m3_decode(const uint8_t* in, float* out, int64_t n, void* stream);
+int mosaic_e4m3_encode(const float* in, uint8_t* out, int64_t n, void* stream);
+
+/* ------------------------------------------------------ A16 MXFP4 linear -- */
+/* y [m, n] bf16 = x [m, k] bf16 . dequant(W)^T, fp32 accumulation, NK layout.
+ * Replaces the A16 "dequant-then-matmul" linear: skinny_mxfp4_gemm semantics
+ * (kernels/skinny_fp4.py:113-144) on the checkpoint NK layout. k % 128 == 0. */
+int mosaic_mx_linear_a16(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
+                         int64_t n, int64_t k, void* stream);
+
+/* -------------------------------------------------------------- routing -- */
+/* logits [m, e] f32 -> ids [m, top_k] int32 + weights [m, top_k] f32.
+ * Replaces Router.forward (model/layers.py:118-150) / Gate.forward
+ * (.mosaicvm/source/inference_model.py:569-589).  Picks are listed by
+ * descending key (the logit, or score + bias when bias != NULL); equal keys go
+ * to the lower expert index.  e <= 512, top_k <= 16. */
+int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, int64_t top_k, int score_func, int renorm,
+                          float route_scale, const float* bias, int32_t* ids, float* weights, void* stream);
+
+/* Stable expert sort + uncapped tile list for ids [m, top_k] (+ one shared
+ * expert row per token when has_shared, virtual expert id e).
+ * Replaces layout_assignments (kernels/moe_layout.py:8-27) and emit_tiles
+ * (kernels/w4a16_grouped.py:151-169).  Assignment count m*top_k(+m) <= 8192.
+ * Outputs: counts [e(+1)], offsets [e(+1)+1], perm / perm_token / perm_weight /
+ * sorted_ids [A], inv_pos [A], tile_* [tile_cap], n_tiles [1]. */
+int mosaic_moe_layout(const int32_t* ids, const float* weights, int64_t m, int64_t top_k, int64_t e, int has_shared,
+                      int block_m, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* perm_token,
+                      float* perm_weight, int32_t* sorted_ids, int32_t* inv_pos, int32_t* tile_expert,
+                      int32_t* tile_start, int32_t* tile_rows, int32_t* n_tiles, int64_t tile_cap, void* stream);
+
+/* Tile list from per-expert counts [e] int32: one (expert, m_start, rows)
+ * entry per block_m rows, ascending expert order, no per-expert cap.
+ * Replaces emit_tiles (kernels/w4a16_grouped.py:151-169; the reference caps
+ * each expert at MAX_TILES=32, :55-60).  e <= 4096. */
+int mosaic_emit_tiles(const int32_t* counts, int64_t e, int block_m, int32_t* tile_expert, int32_t* tile_start,
+                      int32_t* tile_rows, int32_t* n_tiles, int64_t tile_cap, void* stream);
+
+/* --------------------------------------------------- A16 routed MoE layer -- */
+/* Workspace bytes needed by mosaic_moe_a16_forward. */
+size_t mosaic_moe_a16_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                                      int has_shared);
+
+/* Full routed-expert MoE layer, A16 contract of grouped_expert_forward
+ * (model/layers.py:329-373) + shared expert (model/layers.py:284-297):
+ *   x [m, hidden] bf16; if logits != NULL the router runs first and writes
+ *   ids/weights [m, top_k], else ids/weights are inputs;
+ *   gu_* : routed gate|up bank [e, 2*inter, hidden/2] + [e, 2*inter, hidden/32]
+ *          (gate rows 0..inter-1, up rows inter..2*inter-1);
+ *   d_*  : routed down bank [e, hidden, inter/2] + [e, hidden, inter/32];
+ *   sh_* : the shared expert (same shapes without e) or all NULL;
+ *   y [m, hidden] bf16.
+ * fp32 gate/up, SwiGLU (clamped when swiglu_limit > 0), x route weight before
+ * the down projection, bf16 cast, fp32 down, per-token sum of expert partials
+ * in ascending expert id, shared expert last, one bf16 rounding.
+ * hidden % 128 == 0, inter % 128 == 0. */
+int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
+                           const uint8_t* gu_packed, const uint8_t* gu_scale, const uint8_t* d_packed,
+                           const uint8_t* d_scale, const uint8_t* sh_gu_packed, const uint8_t* sh_gu_scale,
+                           const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
+                           int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
+                           int renorm, float route_scale, const float* route_bias, float swiglu_limit,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOSAIC_AMD_H */

@@ -1,0 +1,108 @@
+// Shared device/host helpers for the gfx950 quantized-weight matrix path.
+//
+// Element formats (OCP MX): E2M1 nibbles packed two per byte, low nibble =
+// even K; E8M0 scale byte b decodes to 2^(b-127) by writing b into the fp32
+// exponent field; E4M3 is OCP e4m3fn (max 448, 0x7F/0xFF NaN).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mosaic {
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+
+// ----------------------------------------------------------- status ABI ----
+// 0 = OK, <0 = invalid argument, >0 = hipError_t of the failing launch.
+enum : int { kOk = 0, kInvalid = -1, kUnsupported = -2, kTooLarge = -3 };
+
+void set_last_error(const char* fmt, ...);
+
+#define MOSAIC_CHECK_ARG(cond, ...)                     \
+  do {                                                  \
+    if (!(cond)) {                                      \
+      ::mosaic::set_last_error(__VA_ARGS__);            \
+      return ::mosaic::kInvalid;                        \
+    }                                                   \
+  } while (0)
+
+#define MOSAIC_RETURN_LAUNCH(name)                                           \
+  do {                                                                       \
+    hipError_t _e = hipGetLastError();                                       \
+    if (_e != hipSuccess) {                                                  \
+      ::mosaic::set_last_error("%s: launch failed: %s", name,                \
+                               hipGetErrorString(_e));                       \
+      return (int)_e;                                                        \
+    }                                                                        \
+    return ::mosaic::kOk;                                                    \
+  } while (0)
+
+#define MOSAIC_LAUNCH_CHECK(name)                                            \
+  do {                                                                       \
+    hipError_t _e = hipGetLastError();                                       \
+    if (_e != hipSuccess) {                                                  \
+      ::mosaic::set_last_error("%s: launch failed: %s", name,                \
+                               hipGetErrorString(_e));                       \
+      return (int)_e;                                                        \
+    }                                                                        \
+  } while (0)
+
+// ----------------------------------------------------------- bit helpers ---
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f32_bits(float f) { return __float_as_uint(f); }
+
+// e8m0 byte -> fp32 2^(b-127) (0x00 -> 0.0, 0xFF -> +inf)
+__device__ __forceinline__ float e8m0_f32(uint32_t b) { return __uint_as_float(b << 23); }
+
+__device__ __forceinline__ float bf16_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// fp32 -> bf16 bits, round-to-nearest-even (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// 128-bit streaming load that bypasses cache allocation (read-once data)
+__device__ __forceinline__ u32x4_t load_nt_u32x4(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+
+// Two E2M1 nibbles of byte `sel` of `word` -> two bf16 scaled by `scale`
+// (gfx950 v_cvt_scalef32_pk_bf16_fp4; low nibble -> element 0).
+#define MOSAIC_CVT_FP4_BF16(word, scale, sel) \
+  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((word), (scale), (sel))
+
+// 16 packed bytes (32 E2M1 values, one MX block) -> 4 x bf16x8 scaled
+__device__ __forceinline__ void mx_block_to_bf16(const u32x4_t w, float scale, bf16x8_t out[4]) {
+  const uint32_t words[4] = {w[0], w[1], w[2], w[3]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16x2_t p0 = MOSAIC_CVT_FP4_BF16(words[i], scale, 0);
+    bf16x2_t p1 = MOSAIC_CVT_FP4_BF16(words[i], scale, 1);
+    bf16x2_t p2 = MOSAIC_CVT_FP4_BF16(words[i], scale, 2);
+    bf16x2_t p3 = MOSAIC_CVT_FP4_BF16(words[i], scale, 3);
+    out[i][0] = p0[0]; out[i][1] = p0[1];
+    out[i][2] = p1[0]; out[i][3] = p1[1];
+    out[i][4] = p2[0]; out[i][5] = p2[1];
+    out[i][6] = p3[0]; out[i][7] = p3[1];
+  }
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+__device__ __forceinline__ float swiglu_f32(float gate, float up, float limit) {
+  if (limit > 0.f) {
+    gate = fminf(gate, limit);
+    up = fmaxf(fminf(up, limit), -limit);
+  }
+  return (gate / (1.0f + expf(-gate))) * up;
+}
+
+}  // namespace mosaic

@@ -1,0 +1,23 @@
+// C-ABI status plumbing: thread-local last-error text and the library version.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+#include "../../include/mosaic_amd.h"
+
+namespace mosaic {
+
+static thread_local char g_last_error[512] = "";
+
+void set_last_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+}  // namespace mosaic
+
+extern "C" const char* mosaic_last_error(void) { return mosaic::g_last_error; }
+
+extern "C" int mosaic_version(void) { return MOSAIC_AMD_ABI_VERSION; }

@@ -1,0 +1,291 @@
+"""Typed torch wrappers over the C ABI (device tensors in, device tensors out).
+
+Every function validates shapes/dtypes on the host, allocates its outputs with
+``torch.empty`` on the input's device, and enqueues the HIP kernels on torch's
+current stream.  Nothing here synchronizes or reads device data back.  There
+is no CPU path: a CPU tensor raises ``ValueError``.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+DT_F32, DT_BF16 = 0, 1
+SCORE_FUNCS = {"sigmoid": 0, "softmax": 1, "sqrtsoftplus": 2}
+ACT_MODES = {"pow2": 0, "amax": 1, "hf": 2}
+RECIPES = {"ceil": 0, "floor": 1}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _cuda(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (mosaic_amd has no CPU path), got {t.device}")
+    return t.contiguous()
+
+
+def _u8(t: torch.Tensor, name: str) -> torch.Tensor:
+    t = _cuda(t, name)
+    if t.dtype in (torch.uint8, torch.int8, torch.float8_e8m0fnu, torch.float8_e4m3fn):
+        return t.view(torch.uint8)
+    if hasattr(torch, "float4_e2m1fn_x2") and t.dtype == torch.float4_e2m1fn_x2:
+        return t.view(torch.uint8)
+    raise ValueError(f"{name}: expected a byte tensor (uint8/int8/e8m0/e4m3/fp4x2), got {t.dtype}")
+
+
+def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
+    t = _cuda(t, name)
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: expected bfloat16, got {t.dtype}")
+    return t
+
+
+# --------------------------------------------------------------- codecs -----
+def mx_quantize(w: torch.Tensor, recipe: str = "ceil") -> tuple[torch.Tensor, torch.Tensor]:
+    """w [R, C] (bf16/f32) -> (packed u8 [R, C/2], e8m0 u8 [R, C/32]), blocks of
+    32 along the last dim."""
+    w = _cuda(w, "w")
+    if w.dim() != 2:
+        raise ValueError(f"mx_quantize expects a 2-D tensor, got {tuple(w.shape)}")
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        w = w.to(torch.float32)
+    r, c = w.shape
+    if c % 32:
+        raise ValueError(f"last dim {c} must be a multiple of 32")
+    packed = torch.empty(r, c // 2, dtype=torch.uint8, device=w.device)
+    scale = torch.empty(r, c // 32, dtype=torch.uint8, device=w.device)
+    _lib.call("mosaic_mx_quantize", _ptr(w), DT_BF16 if w.dtype == torch.bfloat16 else DT_F32, _ptr(packed),
+              _ptr(scale), r, c, RECIPES[recipe], _stream())
+    return packed, scale
+
+
+def mx_dequant(packed: torch.Tensor, scale: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """packed [R, C/2] + e8m0 [R, C/32] -> [R, C] (bf16 or f32)."""
+    packed = _u8(packed, "packed")
+    scale = _u8(scale, "scale")
+    if packed.dim() != 2:
+        raise ValueError(f"packed must be 2-D, got {tuple(packed.shape)}")
+    r, ch = packed.shape
+    c = 2 * ch
+    if c % 32 or tuple(scale.shape) != (r, c // 32):
+        raise ValueError(f"scale shape {tuple(scale.shape)} != ({r}, {c // 32})")
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"dtype {dtype}")
+    out = torch.empty(r, c, dtype=dtype, device=packed.device)
+    _lib.call("mosaic_mx_dequant", _ptr(packed), _ptr(scale), _ptr(out),
+              DT_BF16 if dtype == torch.bfloat16 else DT_F32, r, c, _stream())
+    return out
+
+
+def act_quant(x: torch.Tensor, block: int = 128, mode: str = "pow2") -> tuple[torch.Tensor, torch.Tensor]:
+    """x [M, K] -> (e4m3fn codes [M, K], f32 scales [M, K/block])."""
+    x = _cuda(x, "x")
+    if x.dim() != 2:
+        raise ValueError(f"act_quant expects [M, K], got {tuple(x.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.to(torch.float32)
+    m, k = x.shape
+    if k % block:
+        raise ValueError(f"K={k} must be a multiple of act block {block}")
+    q = torch.empty(m, k, dtype=torch.uint8, device=x.device)
+    s = torch.empty(m, k // block, dtype=torch.float32, device=x.device)
+    _lib.call("mosaic_act_quant", _ptr(x), DT_BF16 if x.dtype == torch.bfloat16 else DT_F32, _ptr(q), _ptr(s), m, k,
+              block, ACT_MODES[mode], _stream())
+    return q.view(torch.float8_e4m3fn), s
+
+
+def e4m3_decode(codes: torch.Tensor) -> torch.Tensor:
+    codes = _u8(codes, "codes")
+    out = torch.empty(codes.shape, dtype=torch.float32, device=codes.device)
+    _lib.call("mosaic_e4m3_decode", _ptr(codes), _ptr(out), codes.numel(), _stream())
+    return out
+
+
+def e4m3_encode(x: torch.Tensor) -> torch.Tensor:
+    x = _cuda(x, "x").to(torch.float32)
+    out = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    _lib.call("mosaic_e4m3_encode", _ptr(x), _ptr(out), x.numel(), _stream())
+    return out
+
+
+# ------------------------------------------------------------- A16 linear ---
+def mx_linear_a16(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """y [M, N] bf16 = x [M, K] bf16 . dequant(packed [N, K/2], scale [N, K/32])^T."""
+    x = _bf16(x, "x")
+    packed = _u8(packed, "packed")
+    scale = _u8(scale, "scale")
+    if x.dim() != 2 or packed.dim() != 2:
+        raise ValueError("x and packed must be 2-D")
+    m, k = x.shape
+    n, kh = packed.shape
+    if kh * 2 != k:
+        raise ValueError(f"packed K {kh * 2} != x K {k}")
+    if k % 128:
+        raise ValueError(f"K={k} must be a multiple of 128")
+    if tuple(scale.shape) != (n, k // 32):
+        raise ValueError(f"scale shape {tuple(scale.shape)} != ({n}, {k // 32})")
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    _lib.call("mosaic_mx_linear_a16", _ptr(x), _ptr(packed), _ptr(scale), _ptr(y), m, n, k, _stream())
+    return y
+
+
+# ---------------------------------------------------------------- routing ---
+def moe_route_topk(logits: torch.Tensor, top_k: int, score_func: str = "sigmoid", renorm: bool = True,
+                   route_scale: float = 1.0, bias: torch.Tensor | None = None):
+    """logits [M, E] -> (ids int32 [M, k], weights f32 [M, k])."""
+    logits = _cuda(logits, "logits").to(torch.float32)
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [M, E], got {tuple(logits.shape)}")
+    m, e = logits.shape
+    if bias is not None:
+        bias = _cuda(bias, "bias").to(torch.float32)
+        if tuple(bias.shape) != (e,):
+            raise ValueError(f"bias shape {tuple(bias.shape)} != ({e},)")
+    ids = torch.empty(m, top_k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(m, top_k, dtype=torch.float32, device=logits.device)
+    _lib.call("mosaic_moe_route_topk", _ptr(logits), m, e, top_k, SCORE_FUNCS[score_func], int(renorm),
+              float(route_scale), _ptr(bias), _ptr(ids), _ptr(w), _stream())
+    return ids, w
+
+
+def _tile_cap(a: int, e_ext: int, block_m: int) -> int:
+    u = min(a, e_ext)
+    return (a + u * (block_m - 1)) // block_m
+
+
+def moe_layout(ids: torch.Tensor, weights: torch.Tensor | None, n_experts: int, has_shared: bool = False,
+               block_m: int = 16) -> dict:
+    """Stable expert sort + tile list of ids [M, k] (+ a shared-expert row per token)."""
+    ids = _cuda(ids, "ids")
+    if ids.dim() == 1:
+        ids = ids.view(-1, 1)
+    m, k = ids.shape
+    ids32 = ids.to(torch.int32).contiguous()
+    if weights is None:
+        weights = torch.ones(m, k, dtype=torch.float32, device=ids.device)
+    weights = _cuda(weights, "weights").to(torch.float32).reshape(m, k).contiguous()
+    a = m * k + (m if has_shared else 0)
+    e_ext = n_experts + (1 if has_shared else 0)
+    cap = _tile_cap(a, e_ext, block_m)
+    dev = ids.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = dict(
+        counts=torch.empty(e_ext, **i32), offsets=torch.empty(e_ext + 1, **i32), perm=torch.empty(a, **i32),
+        perm_token=torch.empty(a, **i32), perm_weight=torch.empty(a, dtype=torch.float32, device=dev),
+        sorted_ids=torch.empty(a, **i32), inv_pos=torch.empty(a, **i32), tile_expert=torch.empty(max(cap, 1), **i32),
+        tile_start=torch.empty(max(cap, 1), **i32), tile_rows=torch.empty(max(cap, 1), **i32),
+        n_tiles=torch.empty(1, **i32))
+    _lib.call("mosaic_moe_layout", _ptr(ids32), _ptr(weights), m, k, n_experts, int(has_shared), block_m,
+              _ptr(out["counts"]), _ptr(out["offsets"]), _ptr(out["perm"]), _ptr(out["perm_token"]),
+              _ptr(out["perm_weight"]), _ptr(out["sorted_ids"]), _ptr(out["inv_pos"]), _ptr(out["tile_expert"]),
+              _ptr(out["tile_start"]), _ptr(out["tile_rows"]), _ptr(out["n_tiles"]), cap, _stream())
+    out["tile_cap"] = cap
+    return out
+
+
+def emit_tiles(counts: torch.Tensor, block_m: int, tile_cap: int):
+    """counts [E] -> (expert_index [cap], m_start [cap], n_tiles [1], tile_rows [cap])."""
+    counts = _cuda(counts, "counts").to(torch.int32).contiguous()
+    e = counts.numel()
+    dev = counts.device
+    cap = max(int(tile_cap), 1)
+    ei = torch.empty(cap, dtype=torch.int32, device=dev)
+    ms = torch.empty(cap, dtype=torch.int32, device=dev)
+    rows = torch.empty(cap, dtype=torch.int32, device=dev)
+    nt = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("mosaic_emit_tiles", _ptr(counts), e, block_m, _ptr(ei), _ptr(ms), _ptr(rows), _ptr(nt), int(tile_cap),
+              _stream())
+    return ei, ms, nt, rows
+
+
+# ---------------------------------------------------------- A16 MoE layer ---
+class MoEWorkspace:
+    """Reusable device workspace for ``moe_a16_forward`` (grown on demand)."""
+
+    def __init__(self):
+        self.buf: torch.Tensor | None = None
+
+    def get(self, nbytes: int, device) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != torch.device(device):
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        return self.buf
+
+
+_DEFAULT_WS = MoEWorkspace()
+
+
+def moe_a16_forward(x: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor, d_packed: torch.Tensor,
+                    d_scale: torch.Tensor, *, logits: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                    weights: torch.Tensor | None = None, top_k: int | None = None, shared=None,
+                    score_func: str = "sigmoid", renorm: bool = True, route_scale: float = 1.0,
+                    route_bias: torch.Tensor | None = None, swiglu_limit: float = 0.0,
+                    workspace: MoEWorkspace | None = None):
+    """A16 routed MoE layer (+ optional shared expert) -> (y bf16 [M, H], ids, weights).
+
+    Banks: gu_packed [E, 2I, H/2], gu_scale [E, 2I, H/32], d_packed [E, H, I/2],
+    d_scale [E, H, I/32]; shared = (gu_packed, gu_scale, d_packed, d_scale) of
+    one expert or None.  Either ``logits`` [M, E] (router runs on the device)
+    or ``ids``/``weights`` [M, k] are given."""
+    x = _bf16(x, "x")
+    if x.dim() != 2:
+        raise ValueError(f"x must be [M, H], got {tuple(x.shape)}")
+    m, h = x.shape
+    gu_packed, gu_scale = _u8(gu_packed, "gu_packed"), _u8(gu_scale, "gu_scale")
+    d_packed, d_scale = _u8(d_packed, "d_packed"), _u8(d_scale, "d_scale")
+    if gu_packed.dim() != 3 or d_packed.dim() != 3:
+        raise ValueError("expert banks must be 3-D [E, N, K/2]")
+    e, n2, hh = gu_packed.shape
+    inter = n2 // 2
+    if hh * 2 != h or n2 % 2:
+        raise ValueError(f"gate/up bank {tuple(gu_packed.shape)} does not match hidden {h}")
+    if tuple(gu_scale.shape) != (e, n2, h // 32):
+        raise ValueError(f"gate/up scale shape {tuple(gu_scale.shape)} != ({e}, {n2}, {h // 32})")
+    if tuple(d_packed.shape) != (e, h, inter // 2) or tuple(d_scale.shape) != (e, h, inter // 32):
+        raise ValueError(f"down bank {tuple(d_packed.shape)}/{tuple(d_scale.shape)} does not match "
+                         f"[{e}, {h}, {inter}/2]")
+    sh = [None] * 4
+    if shared is not None:
+        sh = [_u8(t, f"shared[{i}]") for i, t in enumerate(shared)]
+        want = [(n2, h // 2), (n2, h // 32), (h, inter // 2), (h, inter // 32)]
+        for t, wshape, nm in zip(sh, want, ("gu_packed", "gu_scale", "d_packed", "d_scale")):
+            if tuple(t.shape) != wshape:
+                raise ValueError(f"shared {nm} shape {tuple(t.shape)} != {wshape}")
+    if logits is not None:
+        logits = _cuda(logits, "logits").to(torch.float32)
+        if tuple(logits.shape) != (m, e):
+            raise ValueError(f"logits shape {tuple(logits.shape)} != ({m}, {e})")
+        if top_k is None:
+            raise ValueError("top_k is required with logits")
+        ids = torch.empty(m, top_k, dtype=torch.int32, device=x.device)
+        weights = torch.empty(m, top_k, dtype=torch.float32, device=x.device)
+    else:
+        if ids is None or weights is None:
+            raise ValueError("give logits or ids and weights")
+        ids = _cuda(ids, "ids")
+        if ids.dim() == 1:
+            ids = ids.view(m, -1)
+        top_k = ids.shape[1]
+        ids = ids.to(torch.int32).contiguous()
+        weights = _cuda(weights, "weights").to(torch.float32).reshape(m, top_k).contiguous()
+    if route_bias is not None:
+        route_bias = _cuda(route_bias, "route_bias").to(torch.float32)
+    has_shared = int(shared is not None)
+    nbytes = _lib.lib().mosaic_moe_a16_workspace_bytes(m, h, inter, e, top_k, has_shared)
+    ws = (workspace or _DEFAULT_WS).get(nbytes, x.device)
+    y = torch.empty(m, h, dtype=torch.bfloat16, device=x.device)
+    _lib.call("mosaic_moe_a16_forward", _ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gu_packed),
+              _ptr(gu_scale), _ptr(d_packed), _ptr(d_scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]),
+              _ptr(y), m, h, inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale),
+              _ptr(route_bias), float(swiglu_limit), _ptr(ws), ws.numel(), _stream())
+    return y, ids, weights

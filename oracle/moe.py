@@ -1,0 +1,216 @@
+"""Routed-expert MoE oracles (numpy) -- TEST INFRASTRUCTURE ONLY, see ``oracle/__init__``.
+
+* ``route_topk`` (A10): ``Gate.forward`` (``.mosaicvm/source/inference_model.py:569-589``)
+  and ``Router.forward`` (``model/layers.py:118-150``): scores = f(logits)
+  (sigmoid | softmax | sqrtsoftplus), optional selection bias, top-k, weights =
+  unbiased scores gathered at the picks, renormalized (non-softmax) and scaled.
+  Order and ties (the reference leaves them to ``torch.topk``): picks are listed
+  by descending selection key, equal keys go to the lower expert index.  Without
+  a bias the selection key is the logit itself (each f is monotone, so this is
+  the same ranking wherever f(logit) has no fp32 ties).
+* ``layout_assignments`` (A11): ``kernels/moe_layout.py:8-27`` with a STABLE
+  order (inside one expert, ascending flat assignment index).
+* ``emit_tiles`` (A12): ``kernels/w4a16_grouped.py:151-169`` without the
+  ``MAX_TILES=32`` per-expert cap (``:55-60``).
+* ``moe_layer_a16`` (A13-A17, A16 contract): ``grouped_expert_forward``
+  (``model/layers.py:329-373``) over MXFP4 experts plus the shared expert
+  (``model/layers.py:284-297``; upstream ``MoE.forward`` adds the shared expert
+  to the fp32 routed sum, ``inference_model.py:638-649``): fp32 gate/up,
+  clamps (gate max-only, up both sides) when limit > 0, SiLU*up, route weight
+  BEFORE the down projection, bf16 cast, fp32 down, per-token sum in
+  ascending expert id, shared expert added last, one bf16 rounding.
+* ``moe_layer_a8`` (A8 contract of ``fused_moe_mxint``, ``kernels/mxint.py:1435-1739``):
+  A8 gate/up to a bf16 [A, 2*inter] tensor, fp32 SwiGLU, x route weight, bf16,
+  act_quant_ref, A8 down to bf16 partials, fp32 ascending-expert-id sum, bf16.
+
+Pinned by ``tests/test_oracle_moe.py``: the reference tests' KATs (counts
+[1,1,0,2] of ``tests/test_moe_layout.py:13-24``; the tile-list closed form of
+``tests/test_emit_tiles.py:14-34``), brute-force top-k by full sort, an
+independent per-token loop (``tests/test_exact_expert_semantics.py:38-55``
+style), and the weight-before-down guard (``:78-107``).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import codecs as C
+from . import linear as L
+
+
+# --------------------------------------------------------------- routing ----
+def _sigmoid32(x):
+    x = np.asarray(x, dtype=np.float32)
+    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-x).astype(np.float32))).astype(np.float32)
+
+
+def score_fn(logits: np.ndarray, func: str) -> np.ndarray:
+    lg = np.asarray(logits, dtype=np.float32)
+    if func == "sigmoid":
+        return _sigmoid32(lg)
+    if func == "softmax":
+        e = np.exp((lg - lg.max(axis=-1, keepdims=True)).astype(np.float64))
+        return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    if func == "sqrtsoftplus":
+        return np.sqrt(np.logaddexp(0.0, lg.astype(np.float64))).astype(np.float32)
+    raise ValueError(func)
+
+
+def topk_lower_index(keys: np.ndarray, k: int) -> np.ndarray:
+    """Row-wise top-k of fp32 keys: descending key, equal keys -> lower index.
+    NaN keys are never picked before a number."""
+    keys = np.asarray(keys, dtype=np.float32)
+    m, n = keys.shape
+    out = np.empty((m, k), dtype=np.int64)
+    idx = np.arange(n)
+    for r in range(m):
+        kr = np.where(np.isnan(keys[r]), -np.inf, keys[r]).astype(np.float64)
+        order = np.lexsort((idx, -kr))
+        out[r] = order[:k]
+    return out
+
+
+def route_topk(logits: np.ndarray, top_k: int = 8, score_func: str = "sigmoid",
+               bias: np.ndarray | None = None, renorm: bool = True,
+               route_scale: float = 1.0):
+    """logits [M, E] fp32 -> (ids int64 [M, k], weights fp32 [M, k])."""
+    logits = np.asarray(logits, dtype=np.float32)
+    scores = score_fn(logits, score_func)
+    if bias is None:
+        key = logits
+    else:
+        key = (scores + np.asarray(bias, dtype=np.float32)).astype(np.float32)
+    ids = topk_lower_index(key, top_k)
+    w = np.take_along_axis(scores, ids, axis=1).astype(np.float32)
+    if renorm and score_func != "softmax":
+        ssum = np.zeros(w.shape[0], dtype=np.float32)
+        for j in range(top_k):  # fp32 sum in slot order
+            ssum = (ssum + w[:, j]).astype(np.float32)
+        w = (w / ssum[:, None]).astype(np.float32)
+    w = (w * np.float32(route_scale)).astype(np.float32)
+    return ids, w
+
+
+# ---------------------------------------------------------------- layout ----
+def layout_assignments(expert_ids: np.ndarray, n_experts: int):
+    """flat ids [A] -> (sorted_ids [A], perm [A], offsets [E+1], counts [E]).
+    perm[p] = flat assignment index placed at sorted position p; stable."""
+    ids = np.asarray(expert_ids).reshape(-1).astype(np.int64)
+    perm = np.argsort(ids, kind="stable")
+    counts = np.bincount(ids, minlength=n_experts).astype(np.int32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return ids[perm], perm.astype(np.int64), offsets, counts
+
+
+def emit_tiles(counts: np.ndarray, block_m: int):
+    """counts [E] -> (expert_index, m_start, tile_rows) lists, one entry per
+    block_m rows of each expert in ascending expert order (uncapped)."""
+    ei, ms, rows = [], [], []
+    for e, c in enumerate(np.asarray(counts).tolist()):
+        nt = (c + block_m - 1) // block_m
+        for t in range(nt):
+            ei.append(e)
+            ms.append(t * block_m)
+            rows.append(min(block_m, c - t * block_m))
+    return (np.array(ei, dtype=np.int32), np.array(ms, dtype=np.int32),
+            np.array(rows, dtype=np.int32))
+
+
+# ------------------------------------------------------------ MoE (A16) -----
+def _silu32(g):
+    g = np.asarray(g, dtype=np.float32)
+    return (g / (np.float32(1.0) + np.exp(-g).astype(np.float32))).astype(np.float32)
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray, limit: float) -> np.ndarray:
+    """fp32 SwiGLU with the optional clamps of ``model/layers.py:358-362``."""
+    gate = np.asarray(gate, dtype=np.float32)
+    up = np.asarray(up, dtype=np.float32)
+    if limit > 0:
+        gate = np.minimum(gate, np.float32(limit))
+        up = np.clip(up, -np.float32(limit), np.float32(limit))
+    return (_silu32(gate) * up).astype(np.float32)
+
+
+def expert_a16(xrow: np.ndarray, wgu: np.ndarray, wd: np.ndarray, weight: float,
+               limit: float) -> np.ndarray:
+    """One token through one expert given DEQUANTIZED fp32 weights
+    wgu [2*inter, H] (gate rows then up rows) and wd [H, inter] -> fp32 [H]."""
+    inter = wgu.shape[0] // 2
+    gu = (wgu.astype(np.float64) @ np.asarray(xrow, dtype=np.float64)).astype(np.float32)
+    z = swiglu(gu[:inter], gu[inter:], limit)
+    z = (z * np.float32(weight)).astype(np.float32)
+    zd = C.round_bf16(z)
+    return (wd.astype(np.float64) @ zd.astype(np.float64)).astype(np.float32)
+
+
+def moe_layer_a16(x, ids, weights, bank_gu, bank_gu_s, bank_d, bank_d_s,
+                  shared=None, swiglu_limit: float = 0.0, out_bf16: bool = True):
+    """A16 MoE layer over MXFP4 NK banks.
+
+    x [M, H] (bf16-valued fp32); ids [M, k]; weights [M, k] fp32;
+    bank_gu [E, 2*inter, H/2] u8, bank_gu_s [E, 2*inter, H/32] u8,
+    bank_d [E, H, inter/2] u8, bank_d_s [E, H, inter/32] u8 (numpy arrays or
+    callables e -> array, so a test can stream experts from the device);
+    shared = (gu, gu_s, d, d_s) or None.  Returns [M, H].
+    """
+    get = (lambda b, e: b(e)) if callable(bank_gu) else (lambda b, e: b[e])
+    x = np.asarray(x, dtype=np.float32)
+    ids = np.asarray(ids)
+    weights = np.asarray(weights, dtype=np.float32)
+    m, h = x.shape
+    out = np.zeros((m, h), dtype=np.float32)
+    cache = {}
+
+    def deq(e):
+        if e not in cache:
+            cache[e] = (C.dequant_mxfp4(get(bank_gu, e), get(bank_gu_s, e)),
+                        C.dequant_mxfp4(get(bank_d, e), get(bank_d_s, e)))
+        return cache[e]
+
+    for t in range(m):
+        order = np.argsort(ids[t], kind="stable")  # ascending expert id
+        acc = np.zeros(h, dtype=np.float32)
+        for s in order:
+            wgu, wd = deq(int(ids[t, s]))
+            acc = (acc + expert_a16(x[t], wgu, wd, float(weights[t, s]), swiglu_limit)).astype(np.float32)
+        if shared is not None:
+            sgu = C.dequant_mxfp4(shared[0], shared[1]) if "sgu" not in cache else cache["sgu"]
+            sd = C.dequant_mxfp4(shared[2], shared[3]) if "sd" not in cache else cache["sd"]
+            cache["sgu"], cache["sd"] = sgu, sd
+            acc = (acc + expert_a16(x[t], sgu, sd, 1.0, swiglu_limit)).astype(np.float32)
+        out[t] = acc
+    return C.round_bf16(out) if out_bf16 else out
+
+
+# ------------------------------------------------------------- MoE (A8) -----
+def moe_layer_a8(x, ids, weights, bank_gu, bank_gu_s, bank_d, bank_d_s,
+                 swiglu_limit: float = 10.0, shared=None):
+    """``fused_moe_mxint`` contract (``kernels/mxint.py:1587-1722``): gate/up A8
+    into bf16, SwiGLU fp32, x route weight, bf16, act_quant_ref, A8 down into
+    bf16 partials, fp32 sum in ascending expert id, bf16.  ``shared`` (optional)
+    is run through the same A8 expert with weight 1 and added last."""
+    get = (lambda b, e: b(e)) if callable(bank_gu) else (lambda b, e: b[e])
+    x = np.asarray(x, dtype=np.float32)
+    ids = np.asarray(ids)
+    weights = np.asarray(weights, dtype=np.float32)
+    m, h = x.shape
+    out = np.zeros((m, h), dtype=np.float32)
+
+    def one(xrow, gu, gus, d, ds, w):
+        inter = gu.shape[0] // 2
+        g = L.mx_linear_a8(xrow[None, :], gu, gus, out_bf16=True)[0]
+        z = swiglu(g[:inter], g[inter:], swiglu_limit)
+        z = C.round_bf16((z * np.float32(w)).astype(np.float32))
+        return L.mx_linear_a8(z[None, :], d, ds, out_bf16=True)[0]
+
+    for t in range(m):
+        order = np.argsort(ids[t], kind="stable")
+        acc = np.zeros(h, dtype=np.float32)
+        for s in order:
+            e = int(ids[t, s])
+            acc = (acc + one(x[t], get(bank_gu, e), get(bank_gu_s, e), get(bank_d, e),
+                             get(bank_d_s, e), float(weights[t, s]))).astype(np.float32)
+        if shared is not None:
+            acc = (acc + one(x[t], shared[0], shared[1], shared[2], shared[3], 1.0)).astype(np.float32)
+        out[t] = acc
+    return C.round_bf16(out)

@@ -1,0 +1,186 @@
+"""GPU parity of the A16 MXFP4 linear, routing, expert sort and A16 MoE layer.
+
+Float bar: |got - ref| <= 2e-2 * max(1, |ref|) elementwise against the CPU
+oracle's dequant-then-matmul of identical packed bytes (BASELINE tolerance).
+Index bar: routing ids, permutation, tile list bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codecs as C
+from oracle import linear as L
+from oracle import moe as MO
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _ops():
+    from mosaic_amd import ops
+    return ops
+
+
+def assert_close(got, ref, tol=TOL, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
+    worst = float(err.max()) if err.size else 0.0
+    assert worst <= tol, f"{what}: max scaled error {worst:.3e} > {tol} (at {np.unravel_index(err.argmax(), err.shape)})"
+
+
+def _bf16(a):
+    return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(torch.bfloat16)
+
+
+def _quant_weights(rng, n, k, std=0.02):
+    w = (rng.standard_normal((n, k)) * std).astype(np.float32)
+    w = _bf16(w).float().numpy()
+    return C.quantize_mxfp4_ceil(w)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 2048, 7168), (3, 40, 256), (16, 64, 1024), (17, 130, 384),
+                                   (33, 48, 7168), (5, 7168, 2048)])
+def test_linear_a16_vs_oracle(dev, m, n, k):
+    ops = _ops()
+    rng = np.random.default_rng(m * 1000 + n + k)
+    packed, scale = _quant_weights(rng, n, k)
+    x = _bf16(rng.standard_normal((m, k)))
+    ref = L.mx_linear_a16(x.float().numpy(), packed, scale)
+    y = ops.mx_linear_a16(x.to(dev), torch.from_numpy(packed).to(dev), torch.from_numpy(scale).to(dev))
+    assert_close(y.float().cpu().numpy(), ref, what=f"linear m={m} n={n} k={k}")
+
+
+def test_linear_a16_onehot_picks_column(dev):
+    """x = e_j selects dequantized column j exactly (closed form)."""
+    ops = _ops()
+    rng = np.random.default_rng(1)
+    n, k = 64, 256
+    packed, scale = _quant_weights(rng, n, k, std=1.0)
+    x = np.zeros((16, k), dtype=np.float32)
+    cols = rng.choice(k, 16, replace=False)
+    x[np.arange(16), cols] = 1.0
+    y = ops.mx_linear_a16(_bf16(x).to(dev), torch.from_numpy(packed).to(dev),
+                          torch.from_numpy(scale).to(dev)).float().cpu().numpy()
+    w = C.dequant_mxfp4(packed, scale)
+    np.testing.assert_array_equal(y, C.round_bf16(w[:, cols].T))
+
+
+@pytest.mark.parametrize("m,e,k,func", [(1, 256, 8, "sigmoid"), (64, 256, 8, "sigmoid"), (16, 64, 6, "softmax"),
+                                        (9, 256, 8, "sqrtsoftplus"), (4, 16, 16, "sigmoid")])
+def test_route_topk_vs_oracle(dev, m, e, k, func):
+    ops = _ops()
+    rng = np.random.default_rng(m + e + k)
+    logits = rng.standard_normal((m, e)).astype(np.float32)
+    logits[0, 5] = logits[0, 9] = logits[0].max() + 1.0  # exact tie -> lower index first
+    ids, w = ops.moe_route_topk(torch.from_numpy(logits).to(dev), k, func)
+    ids_ref, w_ref = MO.route_topk(logits, k, func)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=1e-5, atol=1e-7)
+    assert ids.cpu().numpy()[0, 0] == 5 and ids.cpu().numpy()[0, 1] == 9
+
+
+@pytest.mark.parametrize("m,k,e,shared", [(1, 8, 256, True), (4, 8, 256, False), (64, 8, 256, True),
+                                          (300, 8, 16, True), (2, 1, 4, False)])
+def test_layout_vs_oracle(dev, m, k, e, shared):
+    ops = _ops()
+    rng = np.random.default_rng(m * 7 + e)
+    ids = np.stack([rng.choice(e, k, replace=False) for _ in range(m)]).astype(np.int64)
+    w = rng.random((m, k)).astype(np.float32)
+    out = ops.moe_layout(torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev), e, has_shared=shared,
+                         block_m=16)
+    flat = ids.reshape(-1)
+    if shared:
+        flat = np.concatenate([flat, np.full(m, e)])
+    sorted_ids, perm, offsets, counts = MO.layout_assignments(flat, e + int(shared))
+    np.testing.assert_array_equal(out["perm"].cpu().numpy(), perm)
+    np.testing.assert_array_equal(out["sorted_ids"].cpu().numpy(), sorted_ids)
+    np.testing.assert_array_equal(out["counts"].cpu().numpy(), counts)
+    np.testing.assert_array_equal(out["offsets"].cpu().numpy(), offsets)
+    inv = np.empty_like(perm)
+    inv[perm] = np.arange(perm.size)
+    np.testing.assert_array_equal(out["inv_pos"].cpu().numpy(), inv)
+    tok = np.where(perm < m * k, perm // k, perm - m * k)
+    np.testing.assert_array_equal(out["perm_token"].cpu().numpy(), tok)
+    ei, ms, rows = MO.emit_tiles(counts, 16)
+    nt = int(out["n_tiles"].cpu().item())
+    assert nt == ei.size
+    np.testing.assert_array_equal(out["tile_expert"].cpu().numpy()[:nt], ei)
+    np.testing.assert_array_equal(out["tile_start"].cpu().numpy()[:nt], ms)
+    np.testing.assert_array_equal(out["tile_rows"].cpu().numpy()[:nt], rows)
+
+
+def test_layout_reference_kat(dev):
+    """tests/test_moe_layout.py:13-24: ids [3,0,3,1] -> counts [1,1,0,2]."""
+    ops = _ops()
+    out = ops.moe_layout(torch.tensor([[3], [0], [3], [1]], device=dev), None, 4)
+    assert out["counts"].cpu().tolist() == [1, 1, 0, 2]
+    assert out["offsets"].cpu().tolist() == [0, 1, 2, 2, 4]
+    assert out["sorted_ids"].cpu().tolist() == [0, 1, 3, 3]
+    assert out["perm"].cpu().tolist() == [1, 3, 0, 2]
+
+
+@pytest.mark.parametrize("block_m", [1, 8, 16])
+def test_emit_tiles_reference_kat(dev, block_m):
+    """tests/test_emit_tiles.py:14-34 closed form, without the 32-tile cap."""
+    ops = _ops()
+    counts = [0, 1, block_m - 1, block_m, block_m + 1, 3 * block_m + 2, 40 * block_m + 3]
+    exp = []
+    for e, c in enumerate(counts):
+        for t in range((c + block_m - 1) // block_m):
+            exp.append((e, t * block_m, min(block_m, c - t * block_m)))
+    ei, ms, nt, rows = ops.emit_tiles(torch.tensor(counts, device=dev), block_m, 128)
+    n = int(nt.item())
+    assert n == len(exp)
+    assert list(zip(ei[:n].tolist(), ms[:n].tolist(), rows[:n].tolist())) == exp
+    ei, ms, nt, rows = ops.emit_tiles(torch.zeros(5, dtype=torch.int32, device=dev), block_m, 8)
+    assert int(nt.item()) == 0
+
+
+def _make_bank(rng, e, h, inter):
+    gu = [_quant_weights(rng, 2 * inter, h) for _ in range(e)]
+    d = [_quant_weights(rng, h, inter) for _ in range(e)]
+    return (np.stack([g[0] for g in gu]), np.stack([g[1] for g in gu]), np.stack([x[0] for x in d]),
+            np.stack([x[1] for x in d]))
+
+
+@pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
+    (1, 16, 256, 128, 4, True, 0.0), (3, 16, 256, 128, 4, False, 10.0), (20, 8, 384, 256, 2, True, 0.0),
+    (37, 32, 512, 128, 8, True, 10.0)])
+def test_moe_a16_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
+    ops = _ops()
+    rng = np.random.default_rng(m + e + h)
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    sh = _make_bank(rng, 1, h, inter) if shared else None
+    x = _bf16(rng.standard_normal((m, h)))
+    logits = rng.standard_normal((m, e)).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    y, ids, w = ops.moe_a16_forward(x.to(dev), T(gp), T(gs), T(dp), T(ds), logits=T(logits), top_k=k,
+                                    shared=None if sh is None else tuple(T(t[0]) for t in sh),
+                                    swiglu_limit=limit)
+    ids_ref, w_ref = MO.route_topk(logits, k, "sigmoid")
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    ref = MO.moe_layer_a16(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds,
+                           shared=None if sh is None else tuple(t[0] for t in sh), swiglu_limit=limit)
+    assert_close(y.float().cpu().numpy(), ref, what="moe a16")
+
+
+def test_moe_a16_given_ids_weight_before_down(dev):
+    """ids/weights supplied (fused_moe_* call form); scaling z before down
+    differs from scaling the output after (tests/test_exact_expert_semantics.py:78-107)."""
+    ops = _ops()
+    rng = np.random.default_rng(8)
+    e, h, inter, m, k = 4, 256, 128, 2, 2
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    x = _bf16(rng.standard_normal((m, h)) * 6.0)
+    ids = np.array([[1, 3], [0, 2]])
+    w = np.array([[0.25, 1.5], [0.5, 0.01]], dtype=np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    y, _, _ = ops.moe_a16_forward(x.to(dev), T(gp), T(gs), T(dp), T(ds), ids=T(ids), weights=T(w), swiglu_limit=10.0)
+    ref = MO.moe_layer_a16(x.float().numpy(), ids, w, gp, gs, dp, ds, swiglu_limit=10.0)
+    assert_close(y.float().cpu().numpy(), ref, what="moe given ids")
+    unit = MO.moe_layer_a16(x.float().numpy(), ids, np.ones_like(w), gp, gs, dp, ds, swiglu_limit=10.0)
+    assert not np.allclose(y.float().cpu().numpy(), unit, atol=1e-3)
