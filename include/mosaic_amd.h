@@ -73,6 +73,24 @@ int mosaic_e4m3_encode(const float* in, uint8_t* out, int64_t n, void* stream);
 int mosaic_mx_linear_a16(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
                          int64_t n, int64_t k, void* stream);
 
+/* MXT16 prepack: bit-exact permutation of an NK MXFP4 matrix (n % 16 == 0,
+ * k % 128 == 0) into the 16-row MFMA tile order read by the A16 kernels:
+ *   packed_t[g][S][l][16 B] = packed[16g + l%16][16*(4S + l/16) .. +16]
+ *   scale_t [g][S4][l][s]   = scale[16g + l%16][4*(4*S4 + s) + l/16]  (0 past k)
+ * (g = 16-row group, S = 128-K super-step, S4 = 4 super-steps, l = lane 0..63).
+ * packed_t has n*k/2 bytes, scale_t n/16 * ceil(k/512) * 256 bytes.
+ * Replaces the reference's bit-exact invertible bank prepacks (prepack_qpa /
+ * prepack_expert_bank_mxint*, kernels/qpa_mma.py:90-150, kernels/mxint.py:165-285);
+ * mosaic_mxt16_unpack is the inverse. */
+int mosaic_mxt16_prepack(const uint8_t* packed, const uint8_t* scale, uint8_t* packed_t, uint8_t* scale_t, int64_t n,
+                         int64_t k, void* stream);
+int mosaic_mxt16_unpack(const uint8_t* packed_t, const uint8_t* scale_t, uint8_t* packed, uint8_t* scale, int64_t n,
+                        int64_t k, void* stream);
+
+/* A16 linear on an MXT16-prepacked weight (same contract as mosaic_mx_linear_a16). */
+int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_t, const uint8_t* scale_t, uint16_t* y,
+                            int64_t m, int64_t n, int64_t k, void* stream);
+
 /* -------------------------------------------------------------- routing -- */
 /* logits [m, e] f32 -> ids [m, top_k] int32 + weights [m, top_k] f32.
  * Replaces Router.forward (model/layers.py:118-150) / Gate.forward
@@ -85,13 +103,17 @@ int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, int64_t top
 /* Stable expert sort + uncapped tile list for ids [m, top_k] (+ one shared
  * expert row per token when has_shared, virtual expert id e).
  * Replaces layout_assignments (kernels/moe_layout.py:8-27) and emit_tiles
- * (kernels/w4a16_grouped.py:151-169).  Assignment count m*top_k(+m) <= 8192.
+ * (kernels/w4a16_grouped.py:151-169).  Assignment count m*top_k(+m) <= 4096.
  * Outputs: counts [e(+1)], offsets [e(+1)+1], perm / perm_token / perm_weight /
- * sorted_ids [A], inv_pos [A], tile_* [tile_cap], n_tiles [1]. */
+ * sorted_ids [A] (by sorted position), inv_pos [A] (by flat assignment),
+ * combine_pos [m, top_k(+1)] (each token's sorted positions in ascending
+ * expert id, shared last), tile_expert / tile_start / tile_rows / tile_p0
+ * [tile_cap], n_tiles [1]. */
 int mosaic_moe_layout(const int32_t* ids, const float* weights, int64_t m, int64_t top_k, int64_t e, int has_shared,
                       int block_m, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* perm_token,
-                      float* perm_weight, int32_t* sorted_ids, int32_t* inv_pos, int32_t* tile_expert,
-                      int32_t* tile_start, int32_t* tile_rows, int32_t* n_tiles, int64_t tile_cap, void* stream);
+                      float* perm_weight, int32_t* sorted_ids, int32_t* inv_pos, int32_t* combine_pos,
+                      int32_t* tile_expert, int32_t* tile_start, int32_t* tile_rows, int32_t* tile_p0,
+                      int32_t* n_tiles, int64_t tile_cap, void* stream);
 
 /* Tile list from per-expert counts [e] int32: one (expert, m_start, rows)
  * entry per block_m rows, ascending expert order, no per-expert cap.
@@ -109,10 +131,10 @@ size_t mosaic_moe_a16_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, 
  * (model/layers.py:329-373) + shared expert (model/layers.py:284-297):
  *   x [m, hidden] bf16; if logits != NULL the router runs first and writes
  *   ids/weights [m, top_k], else ids/weights are inputs;
- *   gu_* : routed gate|up bank [e, 2*inter, hidden/2] + [e, 2*inter, hidden/32]
- *          (gate rows 0..inter-1, up rows inter..2*inter-1);
- *   d_*  : routed down bank [e, hidden, inter/2] + [e, hidden, inter/32];
- *   sh_* : the shared expert (same shapes without e) or all NULL;
+ *   gu_* : routed gate|up bank [e, 2*inter, hidden/2] (gate rows 0..inter-1,
+ *          up rows inter..2*inter-1), every expert MXT16-prepacked;
+ *   d_*  : routed down bank [e, hidden, inter/2], MXT16-prepacked;
+ *   sh_* : the shared expert (one MXT16-prepacked matrix pair) or all NULL;
  *   y [m, hidden] bf16.
  * fp32 gate/up, SwiGLU (clamped when swiglu_limit > 0), x route weight before
  * the down projection, bf16 cast, fp32 down, per-token sum of expert partials

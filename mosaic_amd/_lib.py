@@ -27,8 +27,11 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_e4m3_decode": (c_int, [P, P, I64, P]),
     "mosaic_e4m3_encode": (c_int, [P, P, I64, P]),
     "mosaic_mx_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P]),
+    "mosaic_mxt16_prepack": (c_int, [P, P, P, P, I64, I64, P]),
+    "mosaic_mxt16_unpack": (c_int, [P, P, P, P, I64, I64, P]),
+    "mosaic_mxt16_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P]),
     "mosaic_moe_route_topk": (c_int, [P, I64, I64, I64, I, I, F, P, P, P, P]),
-    "mosaic_moe_layout": (c_int, [P, P, I64, I64, I64, I, I, P, P, P, P, P, P, P, P, P, P, P, I64, P]),
+    "mosaic_moe_layout": (c_int, [P, P, I64, I64, I64, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, P]),
     "mosaic_emit_tiles": (c_int, [P, I64, I, P, P, P, P, I64, P]),
     "mosaic_moe_a16_workspace_bytes": (c_size_t, [I64, I64, I64, I64, I64, I]),
     "mosaic_moe_a16_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,

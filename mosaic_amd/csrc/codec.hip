@@ -195,6 +195,43 @@ __global__ void __launch_bounds__(256) e4m3_encode_kernel(const float* __restric
   out[i] = (uint8_t)e4m3_rne(in[i]);
 }
 
+
+// ------------------------------------------------------- MXT16 prepack -----
+// Tile layout for the 16-row MFMA tiles (bit-exact permutation of 16-byte MX
+// blocks and of scale bytes; see mx_a16.hip):
+//   packed_t[g][S][l][16 B] = packed[16g + l%16][16*(4S + l/16) .. +16]
+//   scale_t [g][S4][l][s]   = scale[16g + l%16][4*(4*S4 + s) + l/16]  (0 past K)
+// g = row group of 16, S = 128-K super-step, S4 = group of 4 super-steps.
+__global__ void __launch_bounds__(256) mxt16_pack_kernel(const uint8_t* __restrict__ packed,
+                                                         const uint8_t* __restrict__ scale, uint8_t* __restrict__ pt,
+                                                         uint8_t* __restrict__ st, int64_t n_groups, int ns, int ns4,
+                                                         int64_t kb, int inverse) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one lane-slot
+  const int64_t per_g = (int64_t)ns4 * 4 * 64;
+  if (i >= n_groups * per_g) return;
+  const int64_t g = i / per_g;
+  const int64_t rem = i % per_g;
+  const int S = (int)(rem / 64);
+  const int l = (int)(rem % 64);
+  const int c = l & 15, q = l >> 4;
+  const int64_t row = 16 * g + c;
+  const int blk = 4 * S + q;  // MX block index along K
+  if (S < ns) {
+    const int64_t src = row * (kb * 16) + (int64_t)blk * 16;
+    const int64_t dst = (((int64_t)g * ns + S) * 64 + l) * 16;
+    if (!inverse)
+      *reinterpret_cast<u32x4_t*>(pt + dst) = *reinterpret_cast<const u32x4_t*>(packed + src);
+    else
+      *reinterpret_cast<u32x4_t*>(const_cast<uint8_t*>(packed) + src) = *reinterpret_cast<const u32x4_t*>(pt + dst);
+  }
+  const int S4 = S >> 2, s = S & 3;
+  const int64_t sdst = (((int64_t)g * ns4 + S4) * 64 + l) * 4 + s;
+  if (!inverse)
+    st[sdst] = (S < ns) ? scale[row * kb + blk] : (uint8_t)0;
+  else if (S < ns)
+    const_cast<uint8_t*>(scale)[row * kb + blk] = st[sdst];
+}
+
 static inline unsigned grid1d(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 }  // namespace mosaic
@@ -268,4 +305,28 @@ extern "C" int mosaic_e4m3_encode(const float* in, uint8_t* out, int64_t n, void
   if (n == 0) return kOk;
   hipLaunchKernelGGL(e4m3_encode_kernel, dim3(grid1d(n, 256)), dim3(256), 0, (hipStream_t)stream, in, out, n);
   MOSAIC_RETURN_LAUNCH("e4m3_encode");
+}
+
+extern "C" int mosaic_mxt16_prepack(const uint8_t* packed, const uint8_t* scale, uint8_t* packed_t, uint8_t* scale_t,
+                                    int64_t n, int64_t k, void* stream) {
+  MOSAIC_CHECK_ARG(packed && scale && packed_t && scale_t, "mxt16_prepack: null pointer");
+  MOSAIC_CHECK_ARG(n > 0 && n % 16 == 0, "mxt16_prepack: N=%lld must be a positive multiple of 16", (long long)n);
+  MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_prepack: K=%lld must be a positive multiple of 128", (long long)k);
+  const int ns = (int)(k / 128), ns4 = (ns + 3) / 4;
+  const int64_t total = (n / 16) * (int64_t)ns4 * 4 * 64;
+  hipLaunchKernelGGL(mxt16_pack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, packed, scale,
+                     packed_t, scale_t, n / 16, ns, ns4, k / 32, 0);
+  MOSAIC_RETURN_LAUNCH("mxt16_prepack");
+}
+
+extern "C" int mosaic_mxt16_unpack(const uint8_t* packed_t, const uint8_t* scale_t, uint8_t* packed, uint8_t* scale,
+                                   int64_t n, int64_t k, void* stream) {
+  MOSAIC_CHECK_ARG(packed && scale && packed_t && scale_t, "mxt16_unpack: null pointer");
+  MOSAIC_CHECK_ARG(n > 0 && n % 16 == 0, "mxt16_unpack: N=%lld must be a positive multiple of 16", (long long)n);
+  MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_unpack: K=%lld must be a positive multiple of 128", (long long)k);
+  const int ns = (int)(k / 128), ns4 = (ns + 3) / 4;
+  const int64_t total = (n / 16) * (int64_t)ns4 * 4 * 64;
+  hipLaunchKernelGGL(mxt16_pack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, packed, scale,
+                     const_cast<uint8_t*>(packed_t), const_cast<uint8_t*>(scale_t), n / 16, ns, ns4, k / 32, 1);
+  MOSAIC_RETURN_LAUNCH("mxt16_unpack");
 }

@@ -95,6 +95,47 @@ __device__ __forceinline__ void mx_block_to_bf16(const u32x4_t w, float scale, b
   }
 }
 
+// ---------------------------------------------------- DPP wave primitives ----
+// gfx9 DPP controls: quad_perm [1,0,3,2] / [2,3,0,1], row_half_mirror,
+// row_mirror, row_shr:n, row_bcast:15, row_bcast:31.
+#define MOSAIC_DPP(old, v, ctrl, rmask) \
+  ((uint32_t)__builtin_amdgcn_update_dpp((int)(old), (int)(v), (ctrl), (rmask), 0xF, false))
+
+// max over the 64 lanes (all lanes active), broadcast to every lane
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, MOSAIC_DPP(0u, v, 0xB1, 0xF));
+  v = max(v, MOSAIC_DPP(0u, v, 0x4E, 0xF));
+  v = max(v, MOSAIC_DPP(0u, v, 0x141, 0xF));
+  v = max(v, MOSAIC_DPP(0u, v, 0x140, 0xF));
+  v = max(v, MOSAIC_DPP(0u, v, 0x142, 0xA));
+  v = max(v, MOSAIC_DPP(0u, v, 0x143, 0xC));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  // order-preserving map of floats to unsigned (NaN-free input)
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  u = wave_max_u32(u);
+  u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+  return __uint_as_float(u);
+}
+
+// inclusive prefix sum over the 64 lanes (all lanes active)
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += MOSAIC_DPP(0u, v, 0x111, 0xF);
+  v += MOSAIC_DPP(0u, v, 0x112, 0xF);
+  v += MOSAIC_DPP(0u, v, 0x114, 0xF);
+  v += MOSAIC_DPP(0u, v, 0x118, 0xF);
+  v += MOSAIC_DPP(0u, v, 0x142, 0xA);
+  v += MOSAIC_DPP(0u, v, 0x143, 0xC);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_bcast_u32(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float swiglu_f32(float gate, float up, float limit) {

@@ -13,7 +13,7 @@ namespace mosaic {
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
-constexpr int kRouteMaxAssign = 8192;   // A_ext limit of the single-workgroup path
+constexpr int kRouteMaxAssign = 4096;   // A_ext limit of the single-workgroup path
 constexpr int kRouteMaxExperts = 512;   // routed experts (+1 virtual shared expert)
 constexpr int kRouteMaxTopK = 16;
 
@@ -33,16 +33,13 @@ __device__ __forceinline__ float score_of(float logit, int func) {
   return logit;  // softmax handled by the caller
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
-  uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// One wave routes one token.  Selection key: the logit when there is no bias
-// (every score function is monotone), else score + bias.  Ties -> lower index.
+// One wave routes one token; logits stay in registers.  Selection key: the
+// logit when there is no bias (every score function is monotone), else
+// score + bias.  Ties -> lower index.  Lane 0 writes the k picks to
+// s_ids/s_w (workgroup-local scratch) and to the global outputs.
 __device__ void route_one_token(const float* __restrict__ lg, int E, int K, int func, int renorm, float scale,
-                                const float* __restrict__ bias, int32_t* ids_out, float* w_out) {
+                                const float* __restrict__ bias, int16_t* s_ids, float* s_w, int32_t* ids_out,
+                                float* w_out) {
   const int lane = threadIdx.x & 63;
   constexpr int kPer = kRouteMaxExperts / 64;
   float lv[kPer];
@@ -56,8 +53,7 @@ __device__ void route_one_token(const float* __restrict__ lg, int E, int K, int 
   }
   float denom = 1.f;
   if (func == MOSAIC_SCORE_SOFTMAX) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max_f32(mx);
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -65,7 +61,7 @@ __device__ void route_one_token(const float* __restrict__ lg, int E, int K, int 
       if (e < E) s += expf(lv[j] - mx);
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);  // softmax only
     denom = s;
   }
 #pragma unroll
@@ -82,72 +78,74 @@ __device__ void route_one_token(const float* __restrict__ lg, int E, int K, int 
       key[j] = 0;  // never selected while a real expert remains
     }
   }
-  float wsel[kRouteMaxTopK];
-  int isel[kRouteMaxTopK];
   for (int r = 0; r < K; ++r) {
     uint64_t best = 0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) best = key[j] > best ? key[j] : best;
+    const uint32_t hi = wave_max_u32((uint32_t)(best >> 32));
+    const uint32_t lo = wave_max_u32(((uint32_t)(best >> 32) == hi) ? (uint32_t)best : 0u);
+    const int e = (int)(0xFFFFFFFFu - lo);
+    float mine = 0.f;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      uint64_t o = shfl_xor_u64(best, off);
-      best = o > best ? o : best;
-    }
-    int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
-#pragma unroll
-    for (int j = 0; j < kPer; ++j)
+    for (int j = 0; j < kPer; ++j) {
+      if (j == (e >> 6)) mine = lv[j];
       if (lane + 64 * j == e) key[j] = 0;
-    float l = lg[e];
-    float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(l - mx) / denom : score_of(l, func);
-    isel[r] = e;
-    wsel[r] = sc;
+    }
+    const float l = __uint_as_float(wave_bcast_u32(__float_as_uint(mine), e & 63));
+    if (lane == 0) {
+      s_ids[r] = (int16_t)e;
+      s_w[r] = (func == MOSAIC_SCORE_SOFTMAX) ? expf(l - mx) / denom : score_of(l, func);
+    }
   }
   if (lane == 0) {
     float sum = 0.f;
-    for (int r = 0; r < K; ++r) sum += wsel[r];
+    for (int r = 0; r < K; ++r) sum += s_w[r];
     for (int r = 0; r < K; ++r) {
-      float w = wsel[r];
+      float w = s_w[r];
       if (renorm && func != MOSAIC_SCORE_SOFTMAX) w = w / sum;
-      w_out[r] = w * scale;
-      ids_out[r] = isel[r];
+      w = w * scale;
+      s_w[r] = w;
+      w_out[r] = w;
+      ids_out[r] = s_ids[r];
     }
   }
 }
 
-
 // Flat assignment a < M*K is (token a/K, slot a%K); a >= M*K is the shared
 // expert's row for token a - M*K (virtual expert id E, weight 1).
 __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int32_t* ids, float* weights, int M, int E,
-    int K, int func, int renorm, float route_scale, int has_shared, int block_m, int tile_cap, LayoutOut out) {
+    const float* __restrict__ logits, const float* __restrict__ bias, const int32_t* ids_in,
+    const float* weights_in, int32_t* ids_out, float* weights_out, int M, int E, int K, int func, int renorm,
+    float route_scale, int has_shared, int block_m, int tile_cap, LayoutOut out) {
   __shared__ int16_t s_ids[kRouteMaxAssign];
+  __shared__ float s_w[kRouteMaxAssign];
   __shared__ int32_t s_cnt[kRouteMaxExperts + 2];
   __shared__ int32_t s_off[kRouteMaxExperts + 2];
   __shared__ int32_t s_run[kRouteMaxExperts + 2];
-  __shared__ int32_t s_tab[kRouteWaves][kRouteMaxExperts + 2];
+  __shared__ int16_t s_tab[kRouteWaves][kRouteMaxExperts + 2];
   __shared__ int32_t s_toff[kRouteMaxExperts + 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int A = M * K;
   const int A_ext = A + (has_shared ? M : 0);
   const int E_ext = E + (has_shared ? 1 : 0);
+  const int W = K + (has_shared ? 1 : 0);
 
-  // 1. routing (one wave per token) or read the given ids
+  for (int i = tid; i < out.n_counters; i += kRouteThreads) out.counters[i] = 0;
+  // 1. routing (one wave per token) into s_ids/s_w, or read the given ids
   if (logits) {
     for (int t = wave; t < M; t += kRouteWaves)
-      route_one_token(logits + (int64_t)t * E, E, K, func, renorm, route_scale, bias, ids + (int64_t)t * K,
-                      weights + (int64_t)t * K);
-    __threadfence();
-  }
-  __syncthreads();
-  for (int a = tid; a < A_ext; a += kRouteThreads) {
-    int e;
-    if (a < A) {
-      e = ids[a];  // written above by another wave of this workgroup
-      e = (e < 0 || e >= E) ? -1 : e;
-    } else {
-      e = E;
+      route_one_token(logits + (int64_t)t * E, E, K, func, renorm, route_scale, bias, s_ids + t * K, s_w + t * K,
+                      ids_out + (int64_t)t * K, weights_out + (int64_t)t * K);
+  } else {
+    for (int a = tid; a < A; a += kRouteThreads) {
+      int e = ids_in[a];
+      s_ids[a] = (int16_t)((e < 0 || e >= E) ? -1 : e);
+      s_w[a] = weights_in[a];
     }
-    s_ids[a] = (int16_t)e;
+  }
+  for (int a = A + tid; a < A_ext; a += kRouteThreads) {
+    s_ids[a] = (int16_t)E;
+    s_w[a] = 1.0f;
   }
   for (int e = tid; e < E_ext; e += kRouteThreads) { s_cnt[e] = 0; s_run[e] = 0; }
   __syncthreads();
@@ -157,24 +155,19 @@ __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
     if (e >= 0) atomicAdd(&s_cnt[e], 1);
   }
   __syncthreads();
-  // 3. exclusive scans of counts and of tile counts (wave 0, 64 lanes in chunks)
+  // 3. exclusive scans of counts and of tile counts (wave 0, DPP scans over 64-lane chunks)
   if (wave == 0) {
-    int carry = 0, tcarry = 0;
+    uint32_t carry = 0, tcarry = 0;
     for (int base = 0; base < E_ext; base += 64) {
-      int e = base + lane;
-      int c = (e < E_ext) ? s_cnt[e] : 0;
-      int tc = (c + block_m - 1) / block_m;
-      int inc = c, tinc = tc;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        int o = __shfl_up(inc, off, 64), to = __shfl_up(tinc, off, 64);
-        if (lane >= off) { inc += o; tinc += to; }
-      }
-      if (e < E_ext) { s_off[e] = carry + inc - c; s_toff[e] = tcarry + tinc - tc; }
-      carry += __shfl(inc, 63, 64);
-      tcarry += __shfl(tinc, 63, 64);
+      const int e = base + lane;
+      const uint32_t c = (e < E_ext) ? (uint32_t)s_cnt[e] : 0u;
+      const uint32_t tc = (c + block_m - 1) / block_m;
+      const uint32_t inc = wave_incl_scan_u32(c), tinc = wave_incl_scan_u32(tc);
+      if (e < E_ext) { s_off[e] = (int)(carry + inc - c); s_toff[e] = (int)(tcarry + tinc - tc); }
+      carry += wave_bcast_u32(inc, 63);
+      tcarry += wave_bcast_u32(tinc, 63);
     }
-    if (lane == 0) { s_off[E_ext] = carry; s_toff[E_ext] = tcarry; }
+    if (lane == 0) { s_off[E_ext] = (int)carry; s_toff[E_ext] = (int)tcarry; }
   }
   __syncthreads();
   // 4. stable positions: chunks of 1024 assignments in order; inside a wave the
@@ -182,11 +175,12 @@ __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
   int nbits = 1;
   while ((1 << nbits) <= E_ext) ++nbits;
   for (int base = 0; base < A_ext; base += kRouteThreads) {
-    for (int i = tid; i < kRouteWaves * E_ext; i += kRouteThreads) s_tab[i / E_ext][i % E_ext] = 0;
+    for (int e2 = tid; e2 < E_ext; e2 += kRouteThreads)
+#pragma unroll
+      for (int w = 0; w < kRouteWaves; ++w) s_tab[w][e2] = 0;
     __syncthreads();
     const int a = base + tid;
     const bool live = a < A_ext && s_ids[a] >= 0;
-    if (a < A_ext && !live) out.inv_pos[a] = -1;
     const int e = live ? s_ids[a] : 0;
     uint64_t mask = __ballot(live);
     for (int b = 0; b < nbits; ++b) {
@@ -195,22 +189,38 @@ __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
     }
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int rank_w = __popcll(mask & lt);
-    if (live && rank_w == 0) s_tab[wave][e] = __popcll(mask);
+    if (live && rank_w == 0) s_tab[wave][e] = (int16_t)__popcll(mask);
     __syncthreads();
-    if (live) {
-      int before = s_run[e];
-      for (int w = 0; w < wave; ++w) before += s_tab[w][e];
-      const int p = s_off[e] + before + rank_w;
-      out.perm[p] = a;
-      out.sorted_ids[p] = e;
-      out.inv_pos[a] = p;
-      if (a < A) {
-        out.perm_token[p] = a / K;
-        out.perm_weight[p] = weights[a];
+    if (a < A_ext) {
+      // slot of this assignment in its token's ascending-expert list
+      const int t = a < A ? a / K : a - A;
+      int rank;
+      if (a >= A) {
+        rank = K;
       } else {
-        out.perm_token[p] = a - A;
-        out.perm_weight[p] = 1.0f;
+        const int s = a - t * K;
+        const int my = s_ids[a];
+        int nvalid = 0, below = 0, inv_before = 0;
+        for (int s2 = 0; s2 < K; ++s2) {
+          const int o = s_ids[t * K + s2];
+          nvalid += (o >= 0);
+          below += (o >= 0 && my >= 0 && o < my);
+          inv_before += (o < 0 && s2 < s);
+        }
+        rank = my >= 0 ? below : nvalid + inv_before;
       }
+      int p = -1;
+      if (live) {
+        int before = s_run[e];
+        for (int w = 0; w < wave; ++w) before += s_tab[w][e];
+        p = s_off[e] + before + rank_w;
+        out.perm[p] = a;
+        out.sorted_ids[p] = e;
+        out.perm_token[p] = t;
+        out.perm_weight[p] = s_w[a];
+      }
+      out.inv_pos[a] = p;
+      out.combine_pos[(int64_t)t * W + rank] = p;
     }
     __syncthreads();
     for (int x = tid; x < E_ext; x += kRouteThreads) {
@@ -231,6 +241,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
         out.tile_expert[slot] = e;
         out.tile_start[slot] = t * block_m;
         out.tile_rows[slot] = min(block_m, s_cnt[e] - t * block_m);
+        out.tile_p0[slot] = s_off[e] + t * block_m;
       }
     }
   }
@@ -240,17 +251,19 @@ __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
   }
 }
 
-// Routing only: one wave per token.
+// Routing only: one wave per token (4 tokens per 256-thread block).
 __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict__ logits,
                                                          const float* __restrict__ bias, int32_t* ids, float* w,
                                                          int M, int E, int K, int func, int renorm,
                                                          float route_scale) {
+  __shared__ int16_t s_i[4][kRouteMaxTopK];
+  __shared__ float s_w[4][kRouteMaxTopK];
+  const int wave = threadIdx.x >> 6;
   const int t = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   if (t >= M) return;
-  route_one_token(logits + (int64_t)t * E, E, K, func, renorm, route_scale, bias, ids + (int64_t)t * K,
-                  w + (int64_t)t * K);
+  route_one_token(logits + (int64_t)t * E, E, K, func, renorm, route_scale, bias, s_i[wave], s_w[wave],
+                  ids + (int64_t)t * K, w + (int64_t)t * K);
 }
-
 
 // Tile list from expert counts (emit_tiles contract, no per-expert cap).
 __global__ void __launch_bounds__(1024) emit_tiles_kernel(const int32_t* __restrict__ counts, int E, int block_m,
@@ -259,21 +272,16 @@ __global__ void __launch_bounds__(1024) emit_tiles_kernel(const int32_t* __restr
   __shared__ int32_t s_toff[4097];
   const int tid = threadIdx.x, lane = tid & 63;
   if (tid < 64) {
-    int carry = 0;
+    uint32_t carry = 0;
     for (int base = 0; base < E; base += 64) {
-      int e = base + lane;
-      int c = (e < E) ? counts[e] : 0;
-      int tc = c > 0 ? (c + block_m - 1) / block_m : 0;
-      int inc = tc;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        int o = __shfl_up(inc, off, 64);
-        if (lane >= off) inc += o;
-      }
-      if (e < E) s_toff[e] = carry + inc - tc;
-      carry += __shfl(inc, 63, 64);
+      const int e = base + lane;
+      const int c = (e < E) ? counts[e] : 0;
+      const uint32_t tc = c > 0 ? (uint32_t)((c + block_m - 1) / block_m) : 0u;
+      const uint32_t inc = wave_incl_scan_u32(tc);
+      if (e < E) s_toff[e] = (int)(carry + inc - tc);
+      carry += wave_bcast_u32(inc, 63);
     }
-    if (lane == 0) s_toff[E] = carry;
+    if (lane == 0) s_toff[E] = (int)carry;
   }
   __syncthreads();
   for (int e = tid; e < E; e += blockDim.x) {
@@ -291,9 +299,10 @@ __global__ void __launch_bounds__(1024) emit_tiles_kernel(const int32_t* __restr
   if (tid == 0) n_tiles[0] = min(s_toff[E], tile_cap);
 }
 
-int launch_route_layout(const float* logits, const float* bias, int32_t* ids, float* weights, int64_t M, int64_t E,
-                        int64_t K, int func, int renorm, float route_scale, int has_shared, int block_m,
-                        int64_t tile_cap, const LayoutOut& out, hipStream_t st) {
+int launch_route_layout(const float* logits, const float* bias, const int32_t* ids_in, const float* weights_in,
+                        int32_t* ids_out, float* weights_out, int64_t M, int64_t E, int64_t K, int func, int renorm,
+                        float route_scale, int has_shared, int block_m, int64_t tile_cap, const LayoutOut& out,
+                        hipStream_t st) {
   const int64_t A_ext = M * K + (has_shared ? M : 0);
   MOSAIC_CHECK_ARG(M >= 1 && E >= 1 && K >= 1, "moe layout: M=%lld E=%lld K=%lld", (long long)M, (long long)E,
                    (long long)K);
@@ -304,8 +313,10 @@ int launch_route_layout(const float* logits, const float* bias, int32_t* ids, fl
                    kRouteMaxAssign);
   MOSAIC_CHECK_ARG(block_m >= 1, "moe layout: block_m=%d", block_m);
   MOSAIC_CHECK_ARG(func >= 0 && func <= 2, "moe layout: score func %d", func);
-  hipLaunchKernelGGL(route_layout_kernel, dim3(1), dim3(kRouteThreads), 0, st, logits, bias, ids, weights, (int)M,
-                     (int)E, (int)K, func, renorm, route_scale, has_shared, block_m, (int)tile_cap, out);
+  MOSAIC_CHECK_ARG(logits ? (ids_out && weights_out) : (ids_in && weights_in), "moe layout: missing ids/weights");
+  hipLaunchKernelGGL(route_layout_kernel, dim3(1), dim3(kRouteThreads), 0, st, logits, bias, ids_in, weights_in,
+                     ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
+                     (int)tile_cap, out);
   MOSAIC_RETURN_LAUNCH("moe_route_layout");
 }
 
@@ -332,15 +343,15 @@ extern "C" int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, 
 extern "C" int mosaic_moe_layout(const int32_t* ids, const float* weights, int64_t m, int64_t top_k, int64_t e,
                                  int has_shared, int block_m, int32_t* counts, int32_t* offsets, int32_t* perm,
                                  int32_t* perm_token, float* perm_weight, int32_t* sorted_ids, int32_t* inv_pos,
-                                 int32_t* tile_expert, int32_t* tile_start, int32_t* tile_rows, int32_t* n_tiles,
-                                 int64_t tile_cap, void* stream) {
+                                 int32_t* combine_pos, int32_t* tile_expert, int32_t* tile_start, int32_t* tile_rows,
+                                 int32_t* tile_p0, int32_t* n_tiles, int64_t tile_cap, void* stream) {
   MOSAIC_CHECK_ARG(ids && weights && counts && offsets && perm && perm_token && perm_weight && sorted_ids &&
-                       inv_pos && tile_expert && tile_start && tile_rows && n_tiles,
+                       inv_pos && combine_pos && tile_expert && tile_start && tile_rows && tile_p0 && n_tiles,
                    "moe_layout: null pointer");
-  LayoutOut out{counts, offsets, perm, perm_token, perm_weight, sorted_ids, inv_pos,
-                tile_expert, tile_start, tile_rows, n_tiles};
-  return launch_route_layout(nullptr, nullptr, const_cast<int32_t*>(ids), const_cast<float*>(weights), m, e, top_k,
-                             0, 0, 1.0f, has_shared, block_m, tile_cap, out, (hipStream_t)stream);
+  LayoutOut out{counts, offsets, perm, perm_token, perm_weight, sorted_ids, inv_pos, combine_pos,
+                tile_expert, tile_start, tile_rows, tile_p0, n_tiles, nullptr, 0};
+  return launch_route_layout(nullptr, nullptr, ids, weights, nullptr, nullptr, m, e, top_k, 0, 0, 1.0f, has_shared,
+                             block_m, tile_cap, out, (hipStream_t)stream);
 }
 
 extern "C" int mosaic_emit_tiles(const int32_t* counts, int64_t e, int block_m, int32_t* tile_expert,

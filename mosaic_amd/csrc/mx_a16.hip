@@ -2,14 +2,19 @@
 // registers (v_cvt_scalef32_pk_bf16_fp4, block scale applied in the convert)
 // and multiplied on v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
 //
-// Tile shape: one wave owns a 16 (tokens) x 16 (weight rows) output tile and
-// walks K in super-steps of 128.  In a super-step, lane l (c = l%16,
-// q = l/16) loads the 16-byte MX block b = 4S+q of weight row c (one 128-bit
-// load, 32 nibbles, one e8m0 byte) and the 32 bf16 of its token row c at the
-// same K, then issues four MFMAs over the 4 x 8-element sub-slices.  A and B
-// use the same lane->K map, so the K order inside the MFMA does not matter.
-// Weight bytes are read exactly once per token tile; scales come from one
-// aligned dword per super-step (bytes 4S..4S+3 of the scale row).
+// MFMA tile: one wave owns a 16 (tokens) x 16 (weight rows) output tile and
+// walks K in super-steps of 128.  In a super-step lane l (c = l%16, q = l/16)
+// holds the 16-byte MX block b = 4S+q of weight row c (32 nibbles + one e8m0
+// byte) and the 32 bf16 of token row c at the same K, and issues four MFMAs
+// over the 8-element sub-slices.  A and B use the same lane->K map, so the K
+// order inside the MFMA is irrelevant to the result.
+//
+// Weight layouts:
+//  * raw NK ([N, K/2] + [N, K/32], the checkpoint layout): each wave load
+//    touches 16 rows x 64 B;
+//  * MXT16 (prepacked, codec.hip): the 64 lanes' blocks of one super-step are
+//    one contiguous 1 KB, scales one contiguous 256 B per 4 super-steps, so
+//    every weight load is a fully coalesced streaming read.
 #include "common.h"
 #include "moe_internal.h"
 #include "../../include/mosaic_amd.h"
@@ -18,194 +23,304 @@ namespace mosaic {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-template <int U>
-__device__ __forceinline__ void a16_steps(const uint8_t* __restrict__ wrow, const uint8_t* __restrict__ srow,
-                                          const uint16_t* __restrict__ xrow, bool xvalid, int q, int S,
-                                          f32x4_t& acc) {
-  u32x4_t wv[U];
-  uint32_t sv[U];
-  u32x4_t xv[U][4];
+// x operand of one super-step: 32 bf16 of the lane's token row (zeros if invalid)
+__device__ __forceinline__ void load_x_step(const uint16_t* __restrict__ xrow, bool xvalid, int q, int S,
+                                            u32x4_t (&xv)[4]) {
+  if (xvalid) {
+    const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xrow + 32 * (4 * S + q));
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    wv[u] = load_nt_u32x4(wrow + 16 * (4 * (S + u) + q));
-    sv[u] = *reinterpret_cast<const uint32_t*>(srow + 4 * (S + u));
-  }
+    for (int j = 0; j < 4; ++j) xv[j] = xp[j];
+  } else {
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    if (xvalid) {
-      const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(xrow + 32 * (4 * (S + u) + q));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xv[u][j] = xp[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xv[u][j] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const float sf = e8m0_f32((sv[u] >> (8 * q)) & 0xFFu);
-    bf16x8_t wb[4];
-    mx_block_to_bf16(wv[u], sf, wb);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[u][s]), wb[s], acc, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) xv[j] = u32x4_t{0u, 0u, 0u, 0u};
   }
 }
 
-// D[token 4q+r][col c] += sum over super-steps [s_begin, s_end) of the tile.
-__device__ __forceinline__ f32x4_t tile_dot_a16(const uint8_t* __restrict__ wrow, const uint8_t* __restrict__ srow,
-                                                const uint16_t* __restrict__ xrow, bool xvalid, int q, int s_begin,
-                                                int s_end) {
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  int S = s_begin;
-  for (; S + 4 <= s_end; S += 4) a16_steps<4>(wrow, srow, xrow, xvalid, q, S, acc);
-  for (; S < s_end; ++S) a16_steps<1>(wrow, srow, xrow, xvalid, q, S, acc);
-  return acc;
+__device__ __forceinline__ void mfma_block(const u32x4_t w, float sf, const u32x4_t (&xv)[4], f32x4_t& acc) {
+  bf16x8_t wb[4];
+  mx_block_to_bf16(w, sf, wb);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[s]), wb[s], acc, 0, 0, 0);
+}
+
+// ------------------------------------------------------- raw NK layout -----
+template <int T, int U>
+__device__ __forceinline__ void raw_batch(const uint8_t* const (&wp)[T], const uint8_t* const (&sp)[T],
+                                          const uint16_t* __restrict__ xrow, bool xvalid, int q, int S,
+                                          f32x4_t (&acc)[T]) {
+  u32x4_t wv[U][T];
+  uint32_t sv[U][T];
+  u32x4_t xv[U][4];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      wv[u][t] = load_nt_u32x4(wp[t] + 16 * (4 * (S + u) + q));
+      sv[u][t] = *reinterpret_cast<const uint32_t*>(sp[t] + 4 * (S + u));
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u) load_x_step(xrow, xvalid, q, S + u, xv[u]);
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int t = 0; t < T; ++t) mfma_block(wv[u][t], e8m0_f32((sv[u][t] >> (8 * q)) & 0xFFu), xv[u], acc[t]);
+}
+
+template <int T>
+__device__ __forceinline__ void tile_dot_raw(const uint8_t* const (&wp)[T], const uint8_t* const (&sp)[T],
+                                             const uint16_t* __restrict__ xrow, bool xvalid, int q, int s0, int s1,
+                                             f32x4_t (&acc)[T]) {
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int S = s0;
+  for (; S + 2 <= s1; S += 2) raw_batch<T, 2>(wp, sp, xrow, xvalid, q, S, acc);
+  if (S < s1) raw_batch<T, 1>(wp, sp, xrow, xvalid, q, S, acc);
+}
+
+// ---------------------------------------------------------- MXT16 layout ---
+// wt[t] = packed_t of row group g_t + 16*lane; st[t] = scale_t of g_t + 4*lane.
+// A group is the 4 super-steps of one scale dword (S % 4 == 0).
+template <int T>
+__device__ __forceinline__ void t16_group(const uint8_t* const (&wt)[T], const uint8_t* const (&st)[T],
+                                          const uint16_t* __restrict__ xrow, bool xvalid, int q, int S,
+                                          f32x4_t (&acc)[T]) {
+  u32x4_t wv[4][T];
+  uint32_t sv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) wv[u][t] = load_nt_u32x4(wt[t] + (int64_t)(S + u) * 1024);
+    sv[t] = *reinterpret_cast<const uint32_t*>(st[t] + (int64_t)(S >> 2) * 256);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    u32x4_t xv[4];
+    load_x_step(xrow, xvalid, q, S + u, xv);
+#pragma unroll
+    for (int t = 0; t < T; ++t) mfma_block(wv[u][t], e8m0_f32((sv[t] >> (8 * u)) & 0xFFu), xv, acc[t]);
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void t16_step(const uint8_t* const (&wt)[T], const uint8_t* const (&st)[T],
+                                         const uint16_t* __restrict__ xrow, bool xvalid, int q, int S,
+                                         f32x4_t (&acc)[T]) {
+  u32x4_t wv[T];
+  uint32_t sv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    wv[t] = load_nt_u32x4(wt[t] + (int64_t)S * 1024);
+    sv[t] = *reinterpret_cast<const uint32_t*>(st[t] + (int64_t)(S >> 2) * 256);
+  }
+  u32x4_t xv[4];
+  load_x_step(xrow, xvalid, q, S, xv);
+#pragma unroll
+  for (int t = 0; t < T; ++t) mfma_block(wv[t], e8m0_f32((sv[t] >> (8 * (S & 3))) & 0xFFu), xv, acc[t]);
+}
+
+// super-steps [s0, s1); s0 is a multiple of 4
+template <int T>
+__device__ __forceinline__ void tile_dot_t16(const uint8_t* const (&wt)[T], const uint8_t* const (&st)[T],
+                                             const uint16_t* __restrict__ xrow, bool xvalid, int q, int s0, int s1,
+                                             f32x4_t (&acc)[T]) {
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int S = s0;
+  for (; S + 4 <= s1; S += 4) t16_group<T>(wt, st, xrow, xvalid, q, S, acc);
+  for (; S < s1; ++S) t16_step<T>(wt, st, xrow, xvalid, q, S, acc);
+}
+
+// K slice of wave ks out of KS: whole 4-step groups, the last wave takes the tail
+__device__ __forceinline__ void k_slice(int ns, int ks, int KS, int& s0, int& s1) {
+  const int ng = ns / 4;
+  s0 = 4 * (ng * ks / KS);
+  s1 = (ks == KS - 1) ? ns : 4 * (ng * (ks + 1) / KS);
+}
+
+// MXT16 pointers of row group g for this lane
+__device__ __forceinline__ void t16_ptrs(const uint8_t* pt, const uint8_t* st, int64_t g, int ns, int lane,
+                                         const uint8_t*& w, const uint8_t*& s) {
+  const int ns4 = (ns + 3) / 4;
+  w = pt + (g * ns * 64 + lane) * 16;
+  s = st + (g * ns4 * 64 + lane) * 4;
 }
 
 // ---------------------------------------------------- MoE gate/up + SwiGLU --
-// grid (inter/32, tile_cap), 256 threads.  Wave w of block x owns inter
-// indices j0 = (4x+w)*8 .. j0+7: MFMA columns 0..7 are gate rows j0+c,
-// columns 8..15 the matching up rows inter+j0+c-8.  The epilogue pairs
-// column c with c+8 (lane l^8), applies SwiGLU and the route weight, and
-// stores z[p][j] as bf16 for every sorted assignment position p of the tile.
-__global__ void __launch_bounds__(256) moe_a16_gateup_kernel(
+// grid (inter/(8T), tile_cap), KS waves.  Column tiles 0..T/2-1 are gate row
+// groups (j0/16 + t), tiles T/2.. the matching up row groups, so after the K
+// reduction gate and up of one z element sit in the same lane.
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) moe_a16_gateup_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ gu_p, const uint8_t* __restrict__ gu_s,
     const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s, const int32_t* __restrict__ tile_expert,
-    const int32_t* __restrict__ tile_start, const int32_t* __restrict__ tile_rows,
-    const int32_t* __restrict__ n_tiles, const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_token,
-    const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H, int I, int E, float limit) {
+    const int32_t* __restrict__ tile_rows, const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles,
+    const int32_t* __restrict__ perm_token, const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H,
+    int I, int E, float limit) {
+  __shared__ f32x4_t red[KS][T][64];
   const int tile = blockIdx.y;
   if (tile >= n_tiles[0]) return;
-  const int e = tile_expert[tile], rows = tile_rows[tile];
-  const int p0 = offsets[e] + tile_start[tile];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int j0 = (blockIdx.x * 4 + wave) * 8;
-  if (j0 >= I) return;
-  const int64_t rb = H / 2, sb = H / 32;
-  const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * 2 * I * rb;
-  const uint8_t* bs = (e == E) ? sh_s : gu_s + (int64_t)e * 2 * I * sb;
-  const int wr = (c < 8) ? (j0 + c) : (I + j0 + c - 8);
+  const int j0 = blockIdx.x * 8 * T;
+  const int ns = H / 128, ns4 = (ns + 3) / 4;
+  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * ebytes;
+  const uint8_t* bs = (e == E) ? sh_s : gu_s + (int64_t)e * sbytes;
+  const uint8_t* wt[T];
+  const uint8_t* st[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int g = (t < T / 2) ? (j0 / 16 + t) : ((I + j0) / 16 + t - T / 2);
+    t16_ptrs(bp, bs, g, ns, lane, wt[t], st[t]);
+  }
   const bool xvalid = c < rows;
   const uint16_t* xrow = x + (int64_t)(xvalid ? perm_token[p0 + c] : 0) * H;
-  f32x4_t acc = tile_dot_a16(bp + (int64_t)wr * rb, bs + (int64_t)wr * sb, xrow, xvalid, q, 0, H / 128);
+  int s0, s1;
+  k_slice(ns, ks, KS, s0, s1);
+  f32x4_t acc[T];
+  tile_dot_t16<T>(wt, st, xrow, xvalid, q, s0, s1, acc);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float other = __shfl_xor(acc[r], 8, 64);
-    const int ti = 4 * q + r;
-    if (c < 8 && ti < rows) {
-      const float zv = swiglu_f32(acc[r], other, limit) * perm_weight[p0 + ti];
-      z[(int64_t)(p0 + ti) * I + j0 + c] = f32_bf16(zv);
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T / 2) {
+    const int t = ks;
+    f32x4_t g = red[0][t][lane], u = red[0][t + T / 2][lane];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) {
+      g += red[k2][t][lane];
+      u += red[k2][t + T / 2][lane];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ti = 4 * q + r;
+      if (ti < rows) {
+        const float zv = swiglu_f32(g[r], u[r], limit) * perm_weight[p0 + ti];
+        z[(int64_t)(p0 + ti) * I + j0 + 16 * t + c] = f32_bf16(zv);
+      }
     }
   }
 }
 
 // ------------------------------------------------------------- MoE down ----
-// grid (ceil(H/64), tile_cap), 256 threads; wave tile = 16 hidden rows.
-__global__ void __launch_bounds__(256) moe_a16_down_kernel(
+// grid (H/(16T), tile_cap), KS waves: fp32 partial rows yp[p][h] per sorted
+// assignment position p.
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) moe_a16_down_kernel(
     const uint16_t* __restrict__ z, const uint8_t* __restrict__ d_p, const uint8_t* __restrict__ d_s,
     const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s, const int32_t* __restrict__ tile_expert,
-    const int32_t* __restrict__ tile_start, const int32_t* __restrict__ tile_rows,
-    const int32_t* __restrict__ n_tiles, const int32_t* __restrict__ offsets, float* __restrict__ yp, int H, int I,
-    int E) {
+    const int32_t* __restrict__ tile_rows, const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles,
+    float* __restrict__ yp, int H, int I, int E) {
+  __shared__ f32x4_t red[KS][T][64];
   const int tile = blockIdx.y;
   if (tile >= n_tiles[0]) return;
-  const int e = tile_expert[tile], rows = tile_rows[tile];
-  const int p0 = offsets[e] + tile_start[tile];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int h0 = (blockIdx.x * 4 + wave) * 16;
-  if (h0 >= H) return;
-  const int64_t rb = I / 2, sb = I / 32;
-  const uint8_t* bp = (e == E) ? sh_p : d_p + (int64_t)e * H * rb;
-  const uint8_t* bs = (e == E) ? sh_s : d_s + (int64_t)e * H * sb;
+  const int h0 = blockIdx.x * 16 * T;
+  const int ns = I / 128, ns4 = (ns + 3) / 4;
+  const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : d_p + (int64_t)e * ebytes;
+  const uint8_t* bs = (e == E) ? sh_s : d_s + (int64_t)e * sbytes;
+  const uint8_t* wt[T];
+  const uint8_t* st[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) t16_ptrs(bp, bs, h0 / 16 + t, ns, lane, wt[t], st[t]);
   const bool xvalid = c < rows;
   const uint16_t* zrow = z + (int64_t)(p0 + (xvalid ? c : 0)) * I;
-  f32x4_t acc = tile_dot_a16(bp + (int64_t)(h0 + c) * rb, bs + (int64_t)(h0 + c) * sb, zrow, xvalid, q, 0, I / 128);
+  int s0, s1;
+  k_slice(ns, ks, KS, s0, s1);
+  f32x4_t acc[T];
+  tile_dot_t16<T>(wt, st, zrow, xvalid, q, s0, s1, acc);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int ti = 4 * q + r;
-    if (ti < rows) yp[(int64_t)(p0 + ti) * H + h0 + c] = acc[r];
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ti = 4 * q + r;
+      if (ti < rows) yp[(int64_t)(p0 + ti) * H + h0 + 16 * t + c] = v[r];
+    }
   }
 }
 
 // ------------------------------------------------------------ combine ------
-// y[t][h] = bf16( sum of t's expert partials in ascending expert id, then the
-// shared expert's partial ).  Assignments dropped by the layout (inv_pos < 0)
-// contribute nothing.
+// y[t][h] = bf16( sum over j of yp[combine_pos[t][j]][h] ): the token's expert
+// partials in ascending expert id, the shared expert last.
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ yp,
-                                                          const int32_t* __restrict__ ids,
-                                                          const int32_t* __restrict__ inv_pos,
-                                                          uint16_t* __restrict__ y, int M, int K, int H,
-                                                          int has_shared) {
+                                                          const int32_t* __restrict__ combine_pos,
+                                                          uint16_t* __restrict__ y, int M, int W, int H) {
   const int t = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= M || h >= H) return;
-  int ord[16];
-  int key[16];
-  for (int s = 0; s < K; ++s) {
-    int k = ids[(int64_t)t * K + s];
-    int j = s;
-    while (j > 0 && key[j - 1] > k) {  // stable insertion sort by expert id
-      key[j] = key[j - 1];
-      ord[j] = ord[j - 1];
-      --j;
-    }
-    key[j] = k;
-    ord[j] = s;
+  float sum = 0.f;
+  for (int j = 0; j < W; ++j) {
+    const int p = combine_pos[(int64_t)t * W + j];
+    if (p >= 0) sum += yp[(int64_t)p * H + h];
   }
-  float acc = 0.f;
-  for (int s = 0; s < K; ++s) {
-    const int p = inv_pos[(int64_t)t * K + ord[s]];
-    if (p >= 0) acc += yp[(int64_t)p * H + h];
-  }
-  if (has_shared) {
-    const int p = inv_pos[(int64_t)M * K + t];
-    if (p >= 0) acc += yp[(int64_t)p * H + h];
-  }
-  y[(int64_t)t * H + h] = f32_bf16(acc);
+  y[(int64_t)t * H + h] = f32_bf16(sum);
 }
 
 // ------------------------------------------------------- single linear -----
-// y [M, N] = x [M, K] . W^T.  grid (ceil(N/16), ceil(M/16)), 8 waves per block:
-// wave w takes super-steps [w*S/8, (w+1)*S/8) of the same 16x16 tile, partial
-// tiles are summed in wave order through LDS by wave 0.
-constexpr int kLinWaves = 8;
-__global__ void __launch_bounds__(kLinWaves * 64) mx_linear_a16_kernel(const uint16_t* __restrict__ x,
-                                                                        const uint8_t* __restrict__ packed,
-                                                                        const uint8_t* __restrict__ scale,
-                                                                        uint16_t* __restrict__ y, int M, int N,
-                                                                        int K) {
-  __shared__ f32x4_t part[kLinWaves][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// y [M, N] = x [M, K] . W^T.  grid (ceil(N/(16T)), ceil(M/16)), KS waves take
+// K slices of the same T column tiles; slices meet in LDS in slice order.
+template <int T, int KS, bool TILED>
+__global__ void __launch_bounds__(KS * 64) mx_linear_a16_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint8_t* __restrict__ packed,
+                                                                 const uint8_t* __restrict__ scale,
+                                                                 uint16_t* __restrict__ y, int M, int N, int K) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
-  const int row = min(n0 + c, N - 1);
+  const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16;
   const bool xvalid = (m0 + c) < M;
   const uint16_t* xrow = x + (int64_t)(xvalid ? m0 + c : 0) * K;
   const int ns = K / 128;
-  const int s0 = (int)((int64_t)ns * wave / kLinWaves), s1 = (int)((int64_t)ns * (wave + 1) / kLinWaves);
-  f32x4_t acc = tile_dot_a16(packed + (int64_t)row * (K / 2), scale + (int64_t)row * (K / 32), xrow, xvalid, q, s0,
-                             s1);
-  part[wave][lane] = acc;
+  f32x4_t acc[T];
+  if constexpr (TILED) {
+    const uint8_t* wt[T];
+    const uint8_t* st[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) t16_ptrs(packed, scale, min(n0 / 16 + t, N / 16 - 1), ns, lane, wt[t], st[t]);
+    int s0, s1;
+    k_slice(ns, ks, KS, s0, s1);
+    tile_dot_t16<T>(wt, st, xrow, xvalid, q, s0, s1, acc);
+  } else {
+    const uint8_t* wp[T];
+    const uint8_t* sp[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int row = min(n0 + 16 * t + c, N - 1);
+      wp[t] = packed + (int64_t)row * (K / 2);
+      sp[t] = scale + (int64_t)row * (K / 32);
+    }
+    tile_dot_raw<T>(wp, sp, xrow, xvalid, q, ns * ks / KS, ns * (ks + 1) / KS, acc);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
   __syncthreads();
-  if (wave == 0) {
-    f32x4_t sum = part[0][lane];
-    for (int w = 1; w < kLinWaves; ++w) sum += part[w][lane];
+  if (ks < T) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+    const int n = n0 + 16 * t + c;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int mi = m0 + 4 * q + r;
-      if (mi < M && n0 + c < N) y[(int64_t)mi * N + n0 + c] = f32_bf16(sum[r]);
+      if (mi < M && n < N) y[(int64_t)mi * N + n] = f32_bf16(v[r]);
     }
   }
 }
 
 // ----------------------------------------------------------- workspace -----
 struct MoeWorkspace {
-  int32_t *counts, *offsets, *perm, *perm_token, *sorted_ids, *inv_pos;
+  int32_t *counts, *offsets, *perm, *perm_token, *sorted_ids, *inv_pos, *combine_pos;
   float* perm_weight;
-  int32_t *tile_expert, *tile_start, *tile_rows, *n_tiles;
+  int32_t *tile_expert, *tile_start, *tile_rows, *tile_p0, *n_tiles;
   uint16_t* z;
   float* yp;
   int64_t tile_cap;
@@ -234,9 +349,11 @@ static MoeWorkspace carve_moe_workspace(char* base, int64_t M, int64_t H, int64_
   w.perm_weight = (float*)take(4 * A);
   w.sorted_ids = (int32_t*)take(4 * A);
   w.inv_pos = (int32_t*)take(4 * A);
+  w.combine_pos = (int32_t*)take(4 * A);
   w.tile_expert = (int32_t*)take(4 * w.tile_cap);
   w.tile_start = (int32_t*)take(4 * w.tile_cap);
   w.tile_rows = (int32_t*)take(4 * w.tile_cap);
+  w.tile_p0 = (int32_t*)take(4 * w.tile_cap);
   w.n_tiles = (int32_t*)take(4);
   w.z = (uint16_t*)take(2 * A * I);
   w.yp = (float*)take(4 * A * H);
@@ -245,6 +362,29 @@ static MoeWorkspace carve_moe_workspace(char* base, int64_t M, int64_t H, int64_
 }
 
 constexpr int kMoeBlockM = 16;
+constexpr int kGuT = 2, kGuKS = 4;   // gate/up: 16 z outputs per workgroup
+constexpr int kDnT = 2, kDnKS = 4;   // down: 32 hidden rows per workgroup
+
+template <int T, int KS, bool TILED>
+static void launch_linear(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
+                          int64_t n, int64_t k, hipStream_t st) {
+  dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)), (unsigned)((m + 15) / 16));
+  hipLaunchKernelGGL((mx_linear_a16_kernel<T, KS, TILED>), grid, dim3(KS * 64), 0, st, x, packed, scale, y, (int)m,
+                     (int)n, (int)k);
+}
+
+template <bool TILED>
+static void dispatch_linear(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
+                            int64_t n, int64_t k, hipStream_t st) {
+  // enough waves to cover the chip: wide N takes more column tiles per wave
+  const int64_t mt = (m + 15) / 16;
+  if (((n + 63) / 64) * mt * 8 >= 4096)
+    launch_linear<4, 8, TILED>(x, packed, scale, y, m, n, k, st);
+  else if (((n + 31) / 32) * mt * 8 >= 4096)
+    launch_linear<2, 8, TILED>(x, packed, scale, y, m, n, k, st);
+  else
+    launch_linear<1, 8, TILED>(x, packed, scale, y, m, n, k, st);
+}
 
 }  // namespace mosaic
 
@@ -257,10 +397,21 @@ extern "C" int mosaic_mx_linear_a16(const uint16_t* x, const uint8_t* packed, co
   MOSAIC_CHECK_ARG(m >= 0 && n >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
                    "mx_linear_a16: shape out of range");
   if (m == 0 || n == 0) return kOk;
-  dim3 grid((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16));
-  hipLaunchKernelGGL(mx_linear_a16_kernel, grid, dim3(kLinWaves * 64), 0, (hipStream_t)stream, x, packed, scale, y,
-                     (int)m, (int)n, (int)k);
+  dispatch_linear<false>(x, packed, scale, y, m, n, k, (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("mx_linear_a16");
+}
+
+extern "C" int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_t, const uint8_t* scale_t,
+                                       uint16_t* y, int64_t m, int64_t n, int64_t k, void* stream) {
+  MOSAIC_CHECK_ARG(x && packed_t && scale_t && y, "mxt16_linear_a16: null pointer");
+  MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_linear_a16: K=%lld must be a positive multiple of 128",
+                   (long long)k);
+  MOSAIC_CHECK_ARG(n > 0 && n % 16 == 0, "mxt16_linear_a16: N=%lld must be a positive multiple of 16", (long long)n);
+  MOSAIC_CHECK_ARG(m >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
+                   "mxt16_linear_a16: shape out of range");
+  if (m == 0) return kOk;
+  dispatch_linear<true>(x, packed_t, scale_t, y, m, n, k, (hipStream_t)stream);
+  MOSAIC_RETURN_LAUNCH("mxt16_linear_a16");
 }
 
 extern "C" size_t mosaic_moe_a16_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts,
@@ -291,21 +442,21 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
                    w.bytes);
   hipStream_t st = (hipStream_t)stream;
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,
-               w.tile_expert, w.tile_start, w.tile_rows, w.n_tiles};
-  int rc = launch_route_layout(logits, route_bias, ids, weights, m, n_experts, top_k, score_func, renorm,
-                               route_scale, has_shared, kMoeBlockM, w.tile_cap, lo, st);
+               w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0};
+  int rc = launch_route_layout(logits, route_bias, ids, weights, ids, weights, m, n_experts, top_k, score_func,
+                               renorm, route_scale, has_shared, kMoeBlockM, w.tile_cap, lo, st);
   if (rc != 0) return rc;
   const unsigned tcap = (unsigned)w.tile_cap;
-  hipLaunchKernelGGL(moe_a16_gateup_kernel, dim3((unsigned)((inter + 31) / 32), tcap), dim3(256), 0, st, x,
-                     gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_start, w.tile_rows,
-                     w.n_tiles, w.offsets, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
+  hipLaunchKernelGGL((moe_a16_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)(inter / (8 * kGuT)), tcap),
+                     dim3(kGuKS * 64), 0, st, x, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert,
+                     w.tile_rows, w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
                      (int)n_experts, swiglu_limit);
   MOSAIC_LAUNCH_CHECK("moe_a16_gateup");
-  hipLaunchKernelGGL(moe_a16_down_kernel, dim3((unsigned)((hidden + 63) / 64), tcap), dim3(256), 0, st, w.z,
-                     d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_start, w.tile_rows,
-                     w.n_tiles, w.offsets, w.yp, (int)hidden, (int)inter, (int)n_experts);
+  hipLaunchKernelGGL((moe_a16_down_kernel<kDnT, kDnKS>), dim3((unsigned)(hidden / (16 * kDnT)), tcap),
+                     dim3(kDnKS * 64), 0, st, w.z, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert,
+                     w.tile_rows, w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
   MOSAIC_LAUNCH_CHECK("moe_a16_down");
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
-                     w.yp, ids, w.inv_pos, y, (int)m, (int)top_k, (int)hidden, has_shared);
+                     w.yp, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
   MOSAIC_RETURN_LAUNCH("moe_combine");
 }

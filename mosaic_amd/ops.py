@@ -8,6 +8,7 @@ is no CPU path: a CPU tensor raises ``ValueError``.
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 
 import torch
 
@@ -140,6 +141,69 @@ def mx_linear_a16(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor) ->
     return y
 
 
+# ------------------------------------------------------- MXT16 prepack ------
+@dataclass
+class MXT16:
+    """An MXFP4 NK weight (or a stack of them) prepacked into MFMA tile order.
+
+    ``packed`` keeps the raw tensor's shape [..., N, K/2]; ``scale`` is
+    [..., N/16 * ceil(K/512) * 256] bytes.  ``n``/``k`` are the per-matrix dims."""
+    packed: torch.Tensor
+    scale: torch.Tensor
+    n: int
+    k: int
+
+    @property
+    def lead(self) -> tuple:
+        return tuple(self.packed.shape[:-2])
+
+
+def _t16_scale_bytes(n: int, k: int) -> int:
+    return (n // 16) * ((k // 128 + 3) // 4) * 256
+
+
+def mxt16_prepack(packed: torch.Tensor, scale: torch.Tensor) -> MXT16:
+    """Raw NK MXFP4 ([..., N, K/2] + [..., N, K/32]) -> MXT16 (bit-exact permutation)."""
+    packed = _u8(packed, "packed")
+    scale = _u8(scale, "scale")
+    if packed.dim() < 2:
+        raise ValueError(f"packed must be [..., N, K/2], got {tuple(packed.shape)}")
+    n, kh = packed.shape[-2], packed.shape[-1]
+    k = 2 * kh
+    if n % 16 or k % 128:
+        raise ValueError(f"MXT16 needs N % 16 == 0 and K % 128 == 0, got N={n} K={k}")
+    if tuple(scale.shape) != tuple(packed.shape[:-1]) + (k // 32,):
+        raise ValueError(f"scale shape {tuple(scale.shape)} != {tuple(packed.shape[:-1]) + (k // 32,)}")
+    lead = tuple(packed.shape[:-2])
+    rows = packed.numel() // kh
+    pt = torch.empty_like(packed)
+    st = torch.empty(lead + (_t16_scale_bytes(n, k),), dtype=torch.uint8, device=packed.device)
+    _lib.call("mosaic_mxt16_prepack", _ptr(packed), _ptr(scale), _ptr(pt), _ptr(st), rows, k, _stream())
+    return MXT16(pt, st, n, k)
+
+
+def mxt16_unpack(w: MXT16) -> tuple[torch.Tensor, torch.Tensor]:
+    """Inverse of ``mxt16_prepack``."""
+    rows = w.packed.numel() // (w.k // 2)
+    packed = torch.empty_like(w.packed)
+    scale = torch.empty(w.lead + (w.n, w.k // 32), dtype=torch.uint8, device=w.packed.device)
+    _lib.call("mosaic_mxt16_unpack", _ptr(w.packed), _ptr(w.scale), _ptr(packed), _ptr(scale), rows, w.k, _stream())
+    return packed, scale
+
+
+def mxt16_linear_a16(x: torch.Tensor, w: MXT16) -> torch.Tensor:
+    """y [M, N] bf16 = x [M, K] bf16 . dequant(W)^T for a prepacked 2-D weight."""
+    x = _bf16(x, "x")
+    if w.lead:
+        raise ValueError("mxt16_linear_a16 takes a single matrix")
+    if x.dim() != 2 or x.shape[1] != w.k:
+        raise ValueError(f"x shape {tuple(x.shape)} does not match K={w.k}")
+    m = x.shape[0]
+    y = torch.empty(m, w.n, dtype=torch.bfloat16, device=x.device)
+    _lib.call("mosaic_mxt16_linear_a16", _ptr(x), _ptr(w.packed), _ptr(w.scale), _ptr(y), m, w.n, w.k, _stream())
+    return y
+
+
 # ---------------------------------------------------------------- routing ---
 def moe_route_topk(logits: torch.Tensor, top_k: int, score_func: str = "sigmoid", renorm: bool = True,
                    route_scale: float = 1.0, bias: torch.Tensor | None = None):
@@ -183,13 +247,15 @@ def moe_layout(ids: torch.Tensor, weights: torch.Tensor | None, n_experts: int, 
     out = dict(
         counts=torch.empty(e_ext, **i32), offsets=torch.empty(e_ext + 1, **i32), perm=torch.empty(a, **i32),
         perm_token=torch.empty(a, **i32), perm_weight=torch.empty(a, dtype=torch.float32, device=dev),
-        sorted_ids=torch.empty(a, **i32), inv_pos=torch.empty(a, **i32), tile_expert=torch.empty(max(cap, 1), **i32),
+        sorted_ids=torch.empty(a, **i32), inv_pos=torch.empty(a, **i32),
+        combine_pos=torch.empty(m, k + int(has_shared), **i32), tile_expert=torch.empty(max(cap, 1), **i32),
         tile_start=torch.empty(max(cap, 1), **i32), tile_rows=torch.empty(max(cap, 1), **i32),
-        n_tiles=torch.empty(1, **i32))
+        tile_p0=torch.empty(max(cap, 1), **i32), n_tiles=torch.empty(1, **i32))
     _lib.call("mosaic_moe_layout", _ptr(ids32), _ptr(weights), m, k, n_experts, int(has_shared), block_m,
               _ptr(out["counts"]), _ptr(out["offsets"]), _ptr(out["perm"]), _ptr(out["perm_token"]),
-              _ptr(out["perm_weight"]), _ptr(out["sorted_ids"]), _ptr(out["inv_pos"]), _ptr(out["tile_expert"]),
-              _ptr(out["tile_start"]), _ptr(out["tile_rows"]), _ptr(out["n_tiles"]), cap, _stream())
+              _ptr(out["perm_weight"]), _ptr(out["sorted_ids"]), _ptr(out["inv_pos"]), _ptr(out["combine_pos"]),
+              _ptr(out["tile_expert"]), _ptr(out["tile_start"]), _ptr(out["tile_rows"]), _ptr(out["tile_p0"]),
+              _ptr(out["n_tiles"]), cap, _stream())
     out["tile_cap"] = cap
     return out
 
@@ -225,42 +291,37 @@ class MoEWorkspace:
 _DEFAULT_WS = MoEWorkspace()
 
 
-def moe_a16_forward(x: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor, d_packed: torch.Tensor,
-                    d_scale: torch.Tensor, *, logits: torch.Tensor | None = None, ids: torch.Tensor | None = None,
-                    weights: torch.Tensor | None = None, top_k: int | None = None, shared=None,
-                    score_func: str = "sigmoid", renorm: bool = True, route_scale: float = 1.0,
-                    route_bias: torch.Tensor | None = None, swiglu_limit: float = 0.0,
+def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logits: torch.Tensor | None = None,
+                    ids: torch.Tensor | None = None, weights: torch.Tensor | None = None, top_k: int | None = None,
+                    shared: tuple[MXT16, MXT16] | None = None, score_func: str = "sigmoid", renorm: bool = True,
+                    route_scale: float = 1.0, route_bias: torch.Tensor | None = None, swiglu_limit: float = 0.0,
                     workspace: MoEWorkspace | None = None):
     """A16 routed MoE layer (+ optional shared expert) -> (y bf16 [M, H], ids, weights).
 
-    Banks: gu_packed [E, 2I, H/2], gu_scale [E, 2I, H/32], d_packed [E, H, I/2],
-    d_scale [E, H, I/32]; shared = (gu_packed, gu_scale, d_packed, d_scale) of
-    one expert or None.  Either ``logits`` [M, E] (router runs on the device)
-    or ``ids``/``weights`` [M, k] are given."""
+    ``gate_up``: MXT16 bank of [E, 2I, H/2] (gate rows then up rows per expert);
+    ``down``: MXT16 bank of [E, H, I/2]; ``shared``: (gate_up, down) MXT16 of one
+    expert or None.  Either ``logits`` [M, E] (the router runs on the device) or
+    ``ids``/``weights`` [M, k] are given."""
     x = _bf16(x, "x")
     if x.dim() != 2:
         raise ValueError(f"x must be [M, H], got {tuple(x.shape)}")
     m, h = x.shape
-    gu_packed, gu_scale = _u8(gu_packed, "gu_packed"), _u8(gu_scale, "gu_scale")
-    d_packed, d_scale = _u8(d_packed, "d_packed"), _u8(d_scale, "d_scale")
-    if gu_packed.dim() != 3 or d_packed.dim() != 3:
-        raise ValueError("expert banks must be 3-D [E, N, K/2]")
-    e, n2, hh = gu_packed.shape
-    inter = n2 // 2
-    if hh * 2 != h or n2 % 2:
-        raise ValueError(f"gate/up bank {tuple(gu_packed.shape)} does not match hidden {h}")
-    if tuple(gu_scale.shape) != (e, n2, h // 32):
-        raise ValueError(f"gate/up scale shape {tuple(gu_scale.shape)} != ({e}, {n2}, {h // 32})")
-    if tuple(d_packed.shape) != (e, h, inter // 2) or tuple(d_scale.shape) != (e, h, inter // 32):
-        raise ValueError(f"down bank {tuple(d_packed.shape)}/{tuple(d_scale.shape)} does not match "
-                         f"[{e}, {h}, {inter}/2]")
+    if not isinstance(gate_up, MXT16) or not isinstance(down, MXT16):
+        raise TypeError("gate_up/down must be MXT16 banks (ops.mxt16_prepack)")
+    if len(gate_up.lead) != 1 or len(down.lead) != 1:
+        raise ValueError("gate_up/down must be stacked [E, N, K/2] banks")
+    e = gate_up.lead[0]
+    inter = gate_up.n // 2
+    if gate_up.k != h or gate_up.n % 2:
+        raise ValueError(f"gate/up bank N={gate_up.n} K={gate_up.k} does not match hidden {h}")
+    if down.lead != (e,) or down.n != h or down.k != inter:
+        raise ValueError(f"down bank {down.lead}+[{down.n}, {down.k}] does not match [{e}, {h}, {inter}]")
     sh = [None] * 4
     if shared is not None:
-        sh = [_u8(t, f"shared[{i}]") for i, t in enumerate(shared)]
-        want = [(n2, h // 2), (n2, h // 32), (h, inter // 2), (h, inter // 32)]
-        for t, wshape, nm in zip(sh, want, ("gu_packed", "gu_scale", "d_packed", "d_scale")):
-            if tuple(t.shape) != wshape:
-                raise ValueError(f"shared {nm} shape {tuple(t.shape)} != {wshape}")
+        sgu, sd = shared
+        if sgu.lead or sd.lead or (sgu.n, sgu.k) != (2 * inter, h) or (sd.n, sd.k) != (h, inter):
+            raise ValueError("shared expert shapes do not match the routed bank")
+        sh = [sgu.packed, sgu.scale, sd.packed, sd.scale]
     if logits is not None:
         logits = _cuda(logits, "logits").to(torch.float32)
         if tuple(logits.shape) != (m, e):
@@ -284,8 +345,8 @@ def moe_a16_forward(x: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Te
     nbytes = _lib.lib().mosaic_moe_a16_workspace_bytes(m, h, inter, e, top_k, has_shared)
     ws = (workspace or _DEFAULT_WS).get(nbytes, x.device)
     y = torch.empty(m, h, dtype=torch.bfloat16, device=x.device)
-    _lib.call("mosaic_moe_a16_forward", _ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gu_packed),
-              _ptr(gu_scale), _ptr(d_packed), _ptr(d_scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]),
-              _ptr(y), m, h, inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale),
+    _lib.call("mosaic_moe_a16_forward", _ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gate_up.packed),
+              _ptr(gate_up.scale), _ptr(down.packed), _ptr(down.scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]),
+              _ptr(sh[3]), _ptr(y), m, h, inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale),
               _ptr(route_bias), float(swiglu_limit), _ptr(ws), ws.numel(), _stream())
     return y, ids, weights

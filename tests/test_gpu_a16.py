@@ -69,6 +69,41 @@ def test_linear_a16_onehot_picks_column(dev):
     np.testing.assert_array_equal(y, C.round_bf16(w[:, cols].T))
 
 
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (2048, 7168), (32, 640)])
+def test_mxt16_prepack_bitexact_roundtrip(dev, n, k):
+    """The prepack is the documented permutation of 16-byte blocks and scale
+    bytes, and unpack inverts it (reference test class: prepacks are bit-exact
+    invertible, tests/test_qpa_mma.py:18-52)."""
+    ops = _ops()
+    rng = np.random.default_rng(n + k)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scale = rng.integers(0, 256, (n, k // 32), dtype=np.uint8)
+    w = ops.mxt16_prepack(torch.from_numpy(packed).to(dev), torch.from_numpy(scale).to(dev))
+    ns, ns4 = k // 128, (k // 128 + 3) // 4
+    blocks = packed.reshape(n // 16, 16, ns, 4, 16)              # g, c, S, q, byte
+    want_p = blocks.transpose(0, 2, 3, 1, 4).reshape(-1)         # g, S, q, c, byte
+    np.testing.assert_array_equal(w.packed.cpu().numpy().reshape(-1), want_p)
+    sc = np.zeros((n // 16, 16, ns4 * 4, 4), dtype=np.uint8)     # g, c, S, q
+    sc[:, :, :ns, :] = scale.reshape(n // 16, 16, ns, 4)
+    want_s = sc.reshape(n // 16, 16, ns4, 4, 4).transpose(0, 2, 4, 1, 3).reshape(-1)  # g, S4, q, c, s
+    np.testing.assert_array_equal(w.scale.cpu().numpy().reshape(-1), want_s)
+    p2, s2 = ops.mxt16_unpack(w)
+    np.testing.assert_array_equal(p2.cpu().numpy(), packed)
+    np.testing.assert_array_equal(s2.cpu().numpy(), scale)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 2048, 7168), (3, 48, 640), (16, 64, 1024), (20, 7168, 2048)])
+def test_mxt16_linear_a16_vs_oracle(dev, m, n, k):
+    ops = _ops()
+    rng = np.random.default_rng(m * 31 + n + k)
+    packed, scale = _quant_weights(rng, n, k)
+    x = _bf16(rng.standard_normal((m, k)))
+    ref = L.mx_linear_a16(x.float().numpy(), packed, scale)
+    w = ops.mxt16_prepack(torch.from_numpy(packed).to(dev), torch.from_numpy(scale).to(dev))
+    y = ops.mxt16_linear_a16(x.to(dev), w)
+    assert_close(y.float().cpu().numpy(), ref, what=f"mxt16 linear m={m} n={n} k={k}")
+
+
 @pytest.mark.parametrize("m,e,k,func", [(1, 256, 8, "sigmoid"), (64, 256, 8, "sigmoid"), (16, 64, 6, "softmax"),
                                         (9, 256, 8, "sqrtsoftplus"), (4, 16, 16, "sigmoid")])
 def test_route_topk_vs_oracle(dev, m, e, k, func):
@@ -105,8 +140,16 @@ def test_layout_vs_oracle(dev, m, k, e, shared):
     np.testing.assert_array_equal(out["inv_pos"].cpu().numpy(), inv)
     tok = np.where(perm < m * k, perm // k, perm - m * k)
     np.testing.assert_array_equal(out["perm_token"].cpu().numpy(), tok)
+    cpos = np.empty((m, k + int(shared)), dtype=np.int64)
+    for t in range(m):
+        order = np.argsort(ids[t], kind="stable")
+        cpos[t, :k] = inv[t * k + order]
+        if shared:
+            cpos[t, k] = inv[m * k + t]
+    np.testing.assert_array_equal(out["combine_pos"].cpu().numpy(), cpos)
     ei, ms, rows = MO.emit_tiles(counts, 16)
     nt = int(out["n_tiles"].cpu().item())
+    np.testing.assert_array_equal(out["tile_p0"].cpu().numpy()[:nt], offsets[ei] + ms)
     assert nt == ei.size
     np.testing.assert_array_equal(out["tile_expert"].cpu().numpy()[:nt], ei)
     np.testing.assert_array_equal(out["tile_start"].cpu().numpy()[:nt], ms)
@@ -158,8 +201,10 @@ def test_moe_a16_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     x = _bf16(rng.standard_normal((m, h)))
     logits = rng.standard_normal((m, e)).astype(np.float32)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    y, ids, w = ops.moe_a16_forward(x.to(dev), T(gp), T(gs), T(dp), T(ds), logits=T(logits), top_k=k,
-                                    shared=None if sh is None else tuple(T(t[0]) for t in sh),
+    gu_b, d_b = ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds))
+    shb = None if sh is None else (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])),
+                                   ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    y, ids, w = ops.moe_a16_forward(x.to(dev), gu_b, d_b, logits=T(logits), top_k=k, shared=shb,
                                     swiglu_limit=limit)
     ids_ref, w_ref = MO.route_topk(logits, k, "sigmoid")
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
@@ -179,7 +224,8 @@ def test_moe_a16_given_ids_weight_before_down(dev):
     ids = np.array([[1, 3], [0, 2]])
     w = np.array([[0.25, 1.5], [0.5, 0.01]], dtype=np.float32)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    y, _, _ = ops.moe_a16_forward(x.to(dev), T(gp), T(gs), T(dp), T(ds), ids=T(ids), weights=T(w), swiglu_limit=10.0)
+    y, _, _ = ops.moe_a16_forward(x.to(dev), ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds)),
+                                  ids=T(ids), weights=T(w), swiglu_limit=10.0)
     ref = MO.moe_layer_a16(x.float().numpy(), ids, w, gp, gs, dp, ds, swiglu_limit=10.0)
     assert_close(y.float().cpu().numpy(), ref, what="moe given ids")
     unit = MO.moe_layer_a16(x.float().numpy(), ids, np.ones_like(w), gp, gs, dp, ds, swiglu_limit=10.0)
