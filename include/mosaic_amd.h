@@ -139,14 +139,17 @@ size_t mosaic_moe_a16_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, 
  * fp32 gate/up, SwiGLU (clamped when swiglu_limit > 0), x route weight before
  * the down projection, bf16 cast, fp32 down, per-token sum of expert partials
  * in ascending expert id, shared expert last, one bf16 rounding.
- * hidden % 128 == 0, inter % 128 == 0. */
+ * hidden % 128 == 0, inter % 128 == 0.
+ * stage_events: NULL, or 5 hipEvent_t recorded on `stream` at start, after
+ * routing+layout, after gate/up+SwiGLU, after down, after combine (the stage
+ * boundaries of fused_moe_mxint's stage_times, kernels/mxint.py:1494-1500). */
 int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
                            const uint8_t* gu_packed, const uint8_t* gu_scale, const uint8_t* d_packed,
                            const uint8_t* d_scale, const uint8_t* sh_gu_packed, const uint8_t* sh_gu_scale,
                            const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
                            int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
                            int renorm, float route_scale, const float* route_bias, float swiglu_limit,
-                           void* workspace, size_t workspace_bytes, void* stream);
+                           void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream);
 
 #ifdef __cplusplus
 }

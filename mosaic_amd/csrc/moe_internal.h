@@ -21,6 +21,8 @@ struct LayoutOut {
   int32_t* n_tiles;      // [1]
   int32_t* counters;     // [n_counters] zeroed by the layout kernel (arrival counters of later kernels)
   int n_counters;
+  int small_ok;          // the caller does not read counts/offsets: A_ext <= 64 may take the
+                         // single-wave path, which leaves them unwritten
 };
 
 // Enqueue routing (when logits != nullptr) + stable layout + tile list.

@@ -33,70 +33,83 @@ __device__ __forceinline__ float score_of(float logit, int func) {
   return logit;  // softmax handled by the caller
 }
 
-// One wave routes one token; logits stay in registers.  Selection key: the
-// logit when there is no bias (every score function is monotone), else
-// score + bias.  Ties -> lower index.  Lane 0 writes the k picks to
-// s_ids/s_w (workgroup-local scratch) and to the global outputs.
-__device__ void route_one_token(const float* __restrict__ lg, int E, int K, int func, int renorm, float scale,
-                                const float* __restrict__ bias, int16_t* s_ids, float* s_w, int32_t* ids_out,
-                                float* w_out) {
+// One wave routes one token; logits stay in registers (PER per lane, E <=
+// 64*PER).  Selection key: the logit when there is no bias (every score
+// function is monotone), else score + bias.  Ties -> lower index.  Each round
+// is two 32-bit DPP max-reductions over (key, ~index); lane r then computes
+// the score of pick r, and lane 0 renormalizes.  Picks go to s_ids/s_w
+// (workgroup scratch) and to the global outputs.
+template <int PER>
+__device__ __forceinline__ void route_one_token_t(const float* __restrict__ lg, int E, int K, int func, int renorm,
+                                                  float scale, const float* __restrict__ bias, int16_t* s_ids,
+                                                  float* s_w, int32_t* ids_out, float* w_out) {
   const int lane = threadIdx.x & 63;
-  constexpr int kPer = kRouteMaxExperts / 64;
-  float lv[kPer];
-  uint64_t key[kPer];
+  float lv[PER];
+  uint32_t khi[PER], klo[PER];
   float mx = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    int e = lane + 64 * j;
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + 64 * j;
     lv[j] = (e < E) ? lg[e] : -INFINITY;
-    if (e < E) mx = fmaxf(mx, lv[j]);
+    mx = fmaxf(mx, lv[j]);
   }
   float denom = 1.f;
   if (func == MOSAIC_SCORE_SOFTMAX) {
     mx = wave_max_f32(mx);
-    float s = 0.f;
+    float sum = 0.f;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      int e = lane + 64 * j;
-      if (e < E) s += expf(lv[j] - mx);
-    }
+    for (int j = 0; j < PER; ++j)
+      if (lane + 64 * j < E) sum += expf(lv[j] - mx);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);  // softmax only
-    denom = s;
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    denom = sum;
   }
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    int e = lane + 64 * j;
-    if (e < E) {
-      float k = lv[j];
-      if (bias) {
-        float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(lv[j] - mx) / denom : score_of(lv[j], func);
-        k = sc + bias[e];
-      }
-      key[j] = ((uint64_t)order_key(k) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-    } else {
-      key[j] = 0;  // never selected while a real expert remains
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + 64 * j;
+    float k = lv[j];
+    if (bias && e < E) {
+      const float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(lv[j] - mx) / denom : score_of(lv[j], func);
+      k = sc + bias[e];
     }
+    khi[j] = (e < E) ? order_key(k) : 0u;  // absent experts sort below every real one
+    klo[j] = (e < E) ? 0xFFFFFFFFu - (uint32_t)e : 0u;
   }
+  int my_pick = -1;
+  float my_logit = 0.f;
   for (int r = 0; r < K; ++r) {
-    uint64_t best = 0;
+    uint32_t bh = 0u, bl = 0u;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) best = key[j] > best ? key[j] : best;
-    const uint32_t hi = wave_max_u32((uint32_t)(best >> 32));
-    const uint32_t lo = wave_max_u32(((uint32_t)(best >> 32) == hi) ? (uint32_t)best : 0u);
+    for (int j = 0; j < PER; ++j) {
+      const bool better = khi[j] > bh || (khi[j] == bh && klo[j] > bl);
+      bh = better ? khi[j] : bh;
+      bl = better ? klo[j] : bl;
+    }
+    const uint32_t hi = wave_max_u32(bh);
+    const uint32_t lo = wave_max_u32(bh == hi ? bl : 0u);
     const int e = (int)(0xFFFFFFFFu - lo);
     float mine = 0.f;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      if (j == (e >> 6)) mine = lv[j];
-      if (lane + 64 * j == e) key[j] = 0;
+    for (int j = 0; j < PER; ++j) {
+      const bool own = (lane + 64 * j) == e;
+      mine = own ? lv[j] : mine;
+      khi[j] = own ? 0u : khi[j];
+      klo[j] = own ? 0u : klo[j];
     }
     const float l = __uint_as_float(wave_bcast_u32(__float_as_uint(mine), e & 63));
-    if (lane == 0) {
-      s_ids[r] = (int16_t)e;
-      s_w[r] = (func == MOSAIC_SCORE_SOFTMAX) ? expf(l - mx) / denom : score_of(l, func);
+    if (lane == r) {
+      my_pick = e;
+      my_logit = l;
     }
   }
+  if (lane < K) {
+    const float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(my_logit - mx) / denom : score_of(my_logit, func);
+    s_ids[lane] = (int16_t)my_pick;
+    s_w[lane] = sc;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (lane == 0) {
     float sum = 0.f;
     for (int r = 0; r < K; ++r) sum += s_w[r];
@@ -109,6 +122,19 @@ __device__ void route_one_token(const float* __restrict__ lg, int E, int K, int 
       ids_out[r] = s_ids[r];
     }
   }
+}
+
+__device__ __forceinline__ void route_one_token(const float* __restrict__ lg, int E, int K, int func, int renorm,
+                                                float scale, const float* __restrict__ bias, int16_t* s_ids,
+                                                float* s_w, int32_t* ids_out, float* w_out) {
+  if (E <= 64)
+    route_one_token_t<1>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+  else if (E <= 128)
+    route_one_token_t<2>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+  else if (E <= 256)
+    route_one_token_t<4>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+  else
+    route_one_token_t<8>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
 }
 
 // Flat assignment a < M*K is (token a/K, slot a%K); a >= M*K is the shared
@@ -299,6 +325,88 @@ __global__ void __launch_bounds__(1024) emit_tiles_kernel(const int32_t* __restr
   if (tid == 0) n_tiles[0] = min(s_toff[E], tile_cap);
 }
 
+// Small-layout fast path (A_ext <= 64, M <= 16) for the MoE forward: one wave
+// routes each token, then wave 0 lays out every assignment (lane a = flat
+// assignment a) with two passes over the <= 64 ids.  Writes what the MoE
+// kernels read (perm / perm_token / perm_weight / sorted_ids / inv_pos /
+// combine_pos / tile list); counts and offsets are left untouched.
+constexpr int kSmallAssign = 64;
+__global__ void __launch_bounds__(1024) route_layout_small_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, const int32_t* ids_in,
+    const float* weights_in, int32_t* ids_out, float* weights_out, int M, int E, int K, int func, int renorm,
+    float route_scale, int has_shared, int block_m, LayoutOut out) {
+  __shared__ int16_t s_ids[kSmallAssign];
+  __shared__ float s_w[kSmallAssign];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int A = M * K;
+  const int A_ext = A + (has_shared ? M : 0);
+  const int W = K + (has_shared ? 1 : 0);
+  if (logits) {
+    if (wave < M)
+      route_one_token(logits + (int64_t)wave * E, E, K, func, renorm, route_scale, bias, s_ids + wave * K,
+                      s_w + wave * K, ids_out + (int64_t)wave * K, weights_out + (int64_t)wave * K);
+  } else if (wave == 0) {
+    for (int a = lane; a < A; a += 64) {
+      const int e = ids_in[a];
+      s_ids[a] = (int16_t)((e < 0 || e >= E) ? -1 : e);
+      s_w[a] = weights_in[a];
+    }
+  }
+  if (wave == 0)
+    for (int a = A + lane; a < A_ext; a += 64) { s_ids[a] = (int16_t)E; s_w[a] = 1.0f; }
+  __syncthreads();
+  if (wave != 0) return;
+  // every lane holds its assignment's (expert, token); the passes over all
+  // assignments broadcast them with readlane (no memory round trips)
+  const int a = lane;
+  const bool in = a < A_ext;
+  const int e = in ? s_ids[a] : 0x7FFF;
+  const bool live = in && e >= 0;
+  const int t = a < A ? a / K : a - A;
+  int less = 0, eq_before = 0, cnt = 0, tok_less = 0, tok_inv_before = 0, tok_valid = 0;
+  for (int b = 0; b < A_ext; ++b) {
+    const int eb = __builtin_amdgcn_readlane(e, b);
+    const int tb = __builtin_amdgcn_readlane(t, b);
+    const bool vb = eb >= 0;
+    less += (vb && eb < e);
+    eq_before += (vb && eb == e && b < a);
+    cnt += (vb && eb == e);
+    const bool same_tok = tb == t;
+    tok_valid += (same_tok && vb);
+    tok_less += (same_tok && vb && eb < e);
+    tok_inv_before += (same_tok && !vb && b < a);
+  }
+  // tile count of a's expert if a heads its expert segment, else 0
+  const int my_tiles = (live && eq_before == 0) ? (cnt + block_m - 1) / block_m : 0;
+  int tiles_before = 0;
+  for (int b = 0; b < A_ext; ++b) {
+    const int eb = __builtin_amdgcn_readlane(e, b);
+    const int nb = __builtin_amdgcn_readlane(my_tiles, b);
+    tiles_before += (eb >= 0 && eb < e) ? nb : 0;
+  }
+  const uint32_t total_tiles = wave_bcast_u32(wave_incl_scan_u32((uint32_t)my_tiles), 63);
+  if (in) {
+    const int p = live ? less + eq_before : -1;
+    if (live) {
+      out.perm[p] = a;
+      out.sorted_ids[p] = e;
+      out.perm_token[p] = t;
+      out.perm_weight[p] = s_w[a];
+    }
+    out.inv_pos[a] = p;
+    const int rank = a >= A ? K : (live ? tok_less : tok_valid + tok_inv_before);
+    out.combine_pos[(int64_t)t * W + rank] = p;
+    for (int j = 0; j < my_tiles; ++j) {  // head lane emits its expert's tiles
+      const int slot = tiles_before + j;
+      out.tile_expert[slot] = e;
+      out.tile_start[slot] = j * block_m;
+      out.tile_rows[slot] = min(block_m, cnt - j * block_m);
+      out.tile_p0[slot] = less + j * block_m;
+    }
+  }
+  if (lane == 0) out.n_tiles[0] = (int)total_tiles;
+}
+
 int launch_route_layout(const float* logits, const float* bias, const int32_t* ids_in, const float* weights_in,
                         int32_t* ids_out, float* weights_out, int64_t M, int64_t E, int64_t K, int func, int renorm,
                         float route_scale, int has_shared, int block_m, int64_t tile_cap, const LayoutOut& out,
@@ -314,6 +422,14 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
   MOSAIC_CHECK_ARG(block_m >= 1, "moe layout: block_m=%d", block_m);
   MOSAIC_CHECK_ARG(func >= 0 && func <= 2, "moe layout: score func %d", func);
   MOSAIC_CHECK_ARG(logits ? (ids_out && weights_out) : (ids_in && weights_in), "moe layout: missing ids/weights");
+  if (out.small_ok && A_ext <= kSmallAssign && M <= 16) {
+    const unsigned threads = (unsigned)(64 * (logits ? (M > 1 ? M : 1) : 1));
+    hipLaunchKernelGGL(route_layout_small_kernel, dim3(1), dim3(threads), 0, st, logits, bias, ids_in, weights_in,
+                       ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
+                       out);
+    MOSAIC_RETURN_LAUNCH("moe_route_layout_small");
+  }
+  MOSAIC_CHECK_ARG(out.counts && out.offsets, "moe layout: counts/offsets required");
   hipLaunchKernelGGL(route_layout_kernel, dim3(1), dim3(kRouteThreads), 0, st, logits, bias, ids_in, weights_in,
                      ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
                      (int)tile_cap, out);
@@ -349,7 +465,7 @@ extern "C" int mosaic_moe_layout(const int32_t* ids, const float* weights, int64
                        inv_pos && combine_pos && tile_expert && tile_start && tile_rows && tile_p0 && n_tiles,
                    "moe_layout: null pointer");
   LayoutOut out{counts, offsets, perm, perm_token, perm_weight, sorted_ids, inv_pos, combine_pos,
-                tile_expert, tile_start, tile_rows, tile_p0, n_tiles, nullptr, 0};
+                tile_expert, tile_start, tile_rows, tile_p0, n_tiles, nullptr, 0, 0};
   return launch_route_layout(nullptr, nullptr, ids, weights, nullptr, nullptr, m, e, top_k, 0, 0, 1.0f, has_shared,
                              block_m, tile_cap, out, (hipStream_t)stream);
 }

@@ -426,7 +426,8 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
                                       const uint8_t* sh_d_scale, uint16_t* y, int64_t m, int64_t hidden,
                                       int64_t inter, int64_t n_experts, int64_t top_k, int score_func, int renorm,
                                       float route_scale, const float* route_bias, float swiglu_limit,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
+                                      void* workspace, size_t workspace_bytes, void* const* stage_events,
+                                      void* stream) {
   MOSAIC_CHECK_ARG(x && ids && weights && gu_packed && gu_scale && d_packed && d_scale && y && workspace,
                    "moe_a16_forward: null pointer");
   const int has_shared = sh_gu_packed != nullptr;
@@ -441,22 +442,33 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
   MOSAIC_CHECK_ARG(workspace_bytes >= w.bytes, "moe_a16_forward: workspace %zu < %zu bytes", workspace_bytes,
                    w.bytes);
   hipStream_t st = (hipStream_t)stream;
+  auto mark = [&](int i) {
+    if (stage_events && stage_events[i]) (void)hipEventRecord((hipEvent_t)stage_events[i], st);
+  };
+  mark(0);
+  // counts/offsets are not read by the MoE kernels, so small decode batches may
+  // take the single-wave layout path
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,
-               w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0};
+               w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0, 1};
   int rc = launch_route_layout(logits, route_bias, ids, weights, ids, weights, m, n_experts, top_k, score_func,
                                renorm, route_scale, has_shared, kMoeBlockM, w.tile_cap, lo, st);
   if (rc != 0) return rc;
+  mark(1);
   const unsigned tcap = (unsigned)w.tile_cap;
   hipLaunchKernelGGL((moe_a16_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)(inter / (8 * kGuT)), tcap),
                      dim3(kGuKS * 64), 0, st, x, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert,
                      w.tile_rows, w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
                      (int)n_experts, swiglu_limit);
   MOSAIC_LAUNCH_CHECK("moe_a16_gateup");
+  mark(2);
   hipLaunchKernelGGL((moe_a16_down_kernel<kDnT, kDnKS>), dim3((unsigned)(hidden / (16 * kDnT)), tcap),
                      dim3(kDnKS * 64), 0, st, w.z, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert,
                      w.tile_rows, w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
   MOSAIC_LAUNCH_CHECK("moe_a16_down");
+  mark(3);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
                      w.yp, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
-  MOSAIC_RETURN_LAUNCH("moe_combine");
+  MOSAIC_LAUNCH_CHECK("moe_combine");
+  mark(4);
+  return kOk;
 }

@@ -295,7 +295,7 @@ def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logits: tor
                     ids: torch.Tensor | None = None, weights: torch.Tensor | None = None, top_k: int | None = None,
                     shared: tuple[MXT16, MXT16] | None = None, score_func: str = "sigmoid", renorm: bool = True,
                     route_scale: float = 1.0, route_bias: torch.Tensor | None = None, swiglu_limit: float = 0.0,
-                    workspace: MoEWorkspace | None = None):
+                    workspace: MoEWorkspace | None = None, stage_events: "StageEvents | None" = None):
     """A16 routed MoE layer (+ optional shared expert) -> (y bf16 [M, H], ids, weights).
 
     ``gate_up``: MXT16 bank of [E, 2I, H/2] (gate rows then up rows per expert);
@@ -348,5 +348,30 @@ def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logits: tor
     _lib.call("mosaic_moe_a16_forward", _ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gate_up.packed),
               _ptr(gate_up.scale), _ptr(down.packed), _ptr(down.scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]),
               _ptr(sh[3]), _ptr(y), m, h, inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale),
-              _ptr(route_bias), float(swiglu_limit), _ptr(ws), ws.numel(), _stream())
+              _ptr(route_bias), float(swiglu_limit), _ptr(ws), ws.numel(),
+              None if stage_events is None else stage_events.array, _stream())
     return y, ids, weights
+
+
+MOE_STAGES = ("layout_sec", "gu_sec", "down_sec", "reduction_sec")
+
+
+class StageEvents:
+    """Five HIP events recorded by the MoE forward at its stage boundaries
+    (start, after routing+layout, after gate/up+SwiGLU, after down, after
+    combine); ``times()`` returns seconds per stage like the reference's
+    ``stage_times`` dict (``kernels/mxint.py:1702-1714``)."""
+
+    def __init__(self):
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        for e in self.events:  # torch creates the underlying hipEvent on first record
+            e.record()
+        torch.cuda.current_stream().synchronize()
+        self.array = (ctypes.c_void_p * 5)(*[ctypes.c_void_p(e.cuda_event) for e in self.events])
+
+    def times(self) -> dict:
+        ev = self.events
+        ev[-1].synchronize()
+        out = {k: ev[i].elapsed_time(ev[i + 1]) / 1e3 for i, k in enumerate(MOE_STAGES)}
+        out["total_sec"] = sum(out[k] for k in MOE_STAGES)
+        return out

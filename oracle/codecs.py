@@ -98,7 +98,7 @@ def dequant_mxfp4(packed: np.ndarray, scale_bytes: np.ndarray) -> np.ndarray:
     product of an E2M1 value and a power of two is exact in fp32 and bf16."""
     vals = decode_e2m1(packed)
     s = np.repeat(e8m0_to_f32(scale_bytes), MX_BLOCK, axis=-1)
-    with np.errstate(invalid="ignore"):
+    with np.errstate(invalid="ignore", over="ignore"):
         return vals * s
 
 
