@@ -91,6 +91,28 @@ int mosaic_mxt16_unpack(const uint8_t* packed_t, const uint8_t* scale_t, uint8_t
 int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_t, const uint8_t* scale_t, uint16_t* y,
                             int64_t m, int64_t n, int64_t k, void* stream);
 
+/* A8 MXFP4 linear ("source semantics"): y [m, n] bf16 = sum over K32 groups of
+ * (A_g . W_g^T) * sa[:, g/4] * sw[:, g] with xq e4m3 [m, k] and power-of-two
+ * f32 scales sa [m, k/128] (mosaic_act_quant mode 0), W an MXT16-prepacked
+ * MXFP4 weight [n, k]; fp32 accumulation on the scaled MFMA.
+ * Replaces reference_fp4_linear_source_semantics (kernels/fp4_source.py:132-156)
+ * and the A8 GEMVs xsimt_gemm / qpa_mma_gemm / mxint_*_gemm (kernels/xsimt.py:292-325,
+ * kernels/qpa_mma.py:498-541, kernels/mxint.py:362-401,1014-1054); upstream fp4_gemm
+ * (.mosaicvm/source/inference_kernel.py:441-536). */
+int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* packed_t, const uint8_t* scale_t,
+                           uint16_t* y, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* ---------------------------------------------------- FP8 block GEMM ----- */
+/* C [m, n] = sum over 128-K blocks of (A_kb . B_kb^T) * a_s[m, kb] * b_s[n/128, kb]
+ * with A e4m3 [m, k] + f32 a_s [m, k/128], B e4m3 [n, k] (row-major, the
+ * checkpoint layout) + f32 b_s [ceil(n/128), k/128]; fp32 accumulation; C is
+ * bf16 or f32 (out_dtype).  k % 128 == 0.
+ * Replaces fp8_gemm (.mosaicvm/source/inference_kernel.py:203-273),
+ * w8a8_block_fp8_matmul (.mosaicvm/source/hubkernel_matmul.py:333-360) and
+ * fp8_linear's fused decode GEMM (bench/fp8_core.py:160-231). */
+int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
+                          int out_dtype, int64_t m, int64_t n, int64_t k, void* stream);
+
 /* -------------------------------------------------------------- routing -- */
 /* logits [m, e] f32 -> ids [m, top_k] int32 + weights [m, top_k] f32.
  * Replaces Router.forward (model/layers.py:118-150) / Gate.forward

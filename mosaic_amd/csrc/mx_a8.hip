@@ -1,0 +1,176 @@
+// A8 MXFP4 path ("source semantics") on gfx950: e4m3 activations with a
+// power-of-two scale per 1x128 block against MXFP4 weights (E2M1 + e8m0 per
+// 32 K) on v_mfma_scale_f32_16x16x128_f8f6f4.  Both scales are powers of two,
+// so they go straight into the MFMA's e8m0 operands: the activation scale of
+// a lane's 32 K values is the exponent byte of its 1x128 scale, the weight
+// scale is the MXT16 scale byte selected by opsel.  Nothing is dequantized
+// and no VALU rescale is needed; the MFMA accumulates in fp32.
+//
+// MFMA operands of super-step S (128 K): lane l (c = l%16, q = l/16) holds
+//   A: e4m3 of token row c at K [128S + 16q, +16) and [128S + 64 + 16q, +16)
+//      (the MFMA's 8-bit operand order: two 16-byte loads),
+//   B: the MXT16 16-byte block (row c, MX block 4S+q) = K [128S + 32q, +32)
+//      (the 4-bit operand order: one 16-byte load, low nibble first).
+// The activation scale is constant over a super-step, so which lane supplies
+// it for which 32-K block does not matter.
+#include "common.h"
+#include "moe_internal.h"
+#include "../../include/mosaic_amd.h"
+
+namespace mosaic {
+
+// e8m0 byte of a power-of-two fp32 scale (its biased exponent)
+__device__ __forceinline__ int pow2_e8m0(float s) { return (int)((__float_as_uint(s) >> 23) & 0xFFu); }
+
+template <int SEL>
+__device__ __forceinline__ f32x4_t mfma_a8(const i32x8_t a, int sa, const u32x4_t w, uint32_t sw, f32x4_t acc) {
+  const i32x8_t b = {(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 0, 4, 0, sa, SEL, (int)sw);
+}
+
+__device__ __forceinline__ i32x8_t load_a8_operand(const uint8_t* __restrict__ xrow, int S, int q) {
+  const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(xrow + 128 * S + 16 * q);
+  const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(xrow + 128 * S + 64 + 16 * q);
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+// 4 super-steps [S, S+4) of T column tiles (S % 4 == 0)
+template <int T>
+__device__ __forceinline__ void a8_group(const uint8_t* const (&wt)[T], const uint8_t* const (&st)[T],
+                                         const uint8_t* __restrict__ xrow, const float* __restrict__ sarow,
+                                         bool xvalid, int q, int S, f32x4_t (&acc)[T]) {
+  u32x4_t wv[4][T];
+  uint32_t sv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) wv[u][t] = load_nt_u32x4(wt[t] + (int64_t)(S + u) * 1024);
+    sv[t] = *reinterpret_cast<const uint32_t*>(st[t] + (int64_t)(S >> 2) * 256);
+  }
+  i32x8_t av[4];
+  int sa[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    av[u] = xvalid ? load_a8_operand(xrow, S + u, q) : i32x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    sa[u] = xvalid ? pow2_e8m0(sarow[S + u]) : 127;
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    acc[t] = mfma_a8<0>(av[0], sa[0], wv[0][t], sv[t], acc[t]);
+    acc[t] = mfma_a8<1>(av[1], sa[1], wv[1][t], sv[t], acc[t]);
+    acc[t] = mfma_a8<2>(av[2], sa[2], wv[2][t], sv[t], acc[t]);
+    acc[t] = mfma_a8<3>(av[3], sa[3], wv[3][t], sv[t], acc[t]);
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void a8_step(const uint8_t* const (&wt)[T], const uint8_t* const (&st)[T],
+                                        const uint8_t* __restrict__ xrow, const float* __restrict__ sarow,
+                                        bool xvalid, int q, int S, f32x4_t (&acc)[T]) {
+  const i32x8_t av = xvalid ? load_a8_operand(xrow, S, q) : i32x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  const int sa = xvalid ? pow2_e8m0(sarow[S]) : 127;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const u32x4_t w = load_nt_u32x4(wt[t] + (int64_t)S * 1024);
+    const uint32_t s4 = *reinterpret_cast<const uint32_t*>(st[t] + (int64_t)(S >> 2) * 256);
+    const uint32_t sw = (s4 >> (8 * (S & 3))) & 0xFFu;  // the byte moved to position 0
+    acc[t] = mfma_a8<0>(av, sa, w, sw, acc[t]);
+  }
+}
+
+template <int T>
+__device__ __forceinline__ void tile_dot_a8(const uint8_t* const (&wt)[T], const uint8_t* const (&st)[T],
+                                            const uint8_t* __restrict__ xrow, const float* __restrict__ sarow,
+                                            bool xvalid, int q, int s0, int s1, f32x4_t (&acc)[T]) {
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int S = s0;
+  for (; S + 4 <= s1; S += 4) a8_group<T>(wt, st, xrow, sarow, xvalid, q, S, acc);
+  for (; S < s1; ++S) a8_step<T>(wt, st, xrow, sarow, xvalid, q, S, acc);
+}
+
+__device__ __forceinline__ void a8_k_slice(int ns, int ks, int KS, int& s0, int& s1) {
+  const int ng = ns / 4;
+  s0 = 4 * (ng * ks / KS);
+  s1 = (ks == KS - 1) ? ns : 4 * (ng * (ks + 1) / KS);
+}
+
+__device__ __forceinline__ void a8_ptrs(const uint8_t* pt, const uint8_t* st, int64_t g, int ns, int lane,
+                                        const uint8_t*& w, const uint8_t*& s) {
+  const int ns4 = (ns + 3) / 4;
+  w = pt + (g * ns * 64 + lane) * 16;
+  s = st + (g * ns4 * 64 + lane) * 4;
+}
+
+// ------------------------------------------------------- single linear -----
+// y [M, N] bf16 = A8 linear of (xq e4m3 [M, K], sa f32 pow2 [M, K/128]) with an
+// MXT16 weight.  grid (N/(16T), ceil(M/16)), KS waves = K slices.
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) mx_linear_a8_kernel(const uint8_t* __restrict__ xq,
+                                                                const float* __restrict__ sa,
+                                                                const uint8_t* __restrict__ packed_t,
+                                                                const uint8_t* __restrict__ scale_t,
+                                                                uint16_t* __restrict__ y, int M, int N, int K) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16;
+  const int ns = K / 128;
+  const bool xvalid = (m0 + c) < M;
+  const int xr = xvalid ? m0 + c : 0;
+  const uint8_t* wt[T];
+  const uint8_t* st[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) a8_ptrs(packed_t, scale_t, min(n0 / 16 + t, N / 16 - 1), ns, lane, wt[t], st[t]);
+  int s0, s1;
+  a8_k_slice(ns, ks, KS, s0, s1);
+  f32x4_t acc[T];
+  tile_dot_a8<T>(wt, st, xq + (int64_t)xr * K, sa + (int64_t)xr * ns, xvalid, q, s0, s1, acc);
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+    const int n = n0 + 16 * t + c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int mi = m0 + 4 * q + r;
+      if (mi < M && n < N) y[(int64_t)mi * N + n] = f32_bf16(v[r]);
+    }
+  }
+}
+
+template <int T, int KS>
+static void launch_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* pt, const uint8_t* st, uint16_t* y,
+                             int64_t m, int64_t n, int64_t k, hipStream_t s) {
+  dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)), (unsigned)((m + 15) / 16));
+  hipLaunchKernelGGL((mx_linear_a8_kernel<T, KS>), grid, dim3(KS * 64), 0, s, xq, sa, pt, st, y, (int)m, (int)n,
+                     (int)k);
+}
+
+}  // namespace mosaic
+
+using namespace mosaic;
+
+extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* packed_t,
+                                      const uint8_t* scale_t, uint16_t* y, int64_t m, int64_t n, int64_t k,
+                                      void* stream) {
+  MOSAIC_CHECK_ARG(xq && sa && packed_t && scale_t && y, "mxt16_linear_a8: null pointer");
+  MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_linear_a8: K=%lld must be a positive multiple of 128",
+                   (long long)k);
+  MOSAIC_CHECK_ARG(n > 0 && n % 16 == 0, "mxt16_linear_a8: N=%lld must be a positive multiple of 16", (long long)n);
+  MOSAIC_CHECK_ARG(m >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
+                   "mxt16_linear_a8: shape out of range");
+  if (m == 0) return kOk;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t mt = (m + 15) / 16;
+  if (((n + 63) / 64) * mt * 8 >= 4096)
+    launch_linear_a8<4, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
+  else if (((n + 31) / 32) * mt * 8 >= 4096)
+    launch_linear_a8<2, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
+  else
+    launch_linear_a8<1, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
+  MOSAIC_RETURN_LAUNCH("mxt16_linear_a8");
+}

@@ -204,6 +204,54 @@ def mxt16_linear_a16(x: torch.Tensor, w: MXT16) -> torch.Tensor:
     return y
 
 
+def mxt16_linear_a8(x: torch.Tensor | None, w: MXT16, prequant: tuple | None = None) -> torch.Tensor:
+    """A8 linear: y [M, N] bf16 from bf16 x (quantized here, 1x128 power-of-two
+    e4m3) or ``prequant`` = (codes e4m3 [M, K], scales f32 [M, K/128])."""
+    if w.lead:
+        raise ValueError("mxt16_linear_a8 takes a single matrix")
+    if prequant is None:
+        xq, sa = act_quant(x, 128, "pow2")
+    else:
+        xq, sa = prequant
+    xq = _u8(xq, "xq")
+    sa = _cuda(sa, "sa").to(torch.float32).contiguous()
+    if xq.dim() != 2 or xq.shape[1] != w.k or tuple(sa.shape) != (xq.shape[0], w.k // 128):
+        raise ValueError(f"activation shapes {tuple(xq.shape)}/{tuple(sa.shape)} do not match K={w.k}")
+    m = xq.shape[0]
+    y = torch.empty(m, w.n, dtype=torch.bfloat16, device=xq.device)
+    _lib.call("mosaic_mxt16_linear_a8", _ptr(xq), _ptr(sa), _ptr(w.packed), _ptr(w.scale), _ptr(y), m, w.n, w.k,
+              _stream())
+    return y
+
+
+# ------------------------------------------------------- FP8 block GEMM -----
+def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
+                   out_dtype=torch.bfloat16) -> torch.Tensor:
+    """C [M, N] = block-scaled e4m3 GEMM (A [M, K] + a_s [M, K/128], B [N, K] + b_s [ceil(N/128), K/128])."""
+    a = _u8(a, "a")
+    b = _u8(b, "b")
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("a and b must be 2-D")
+    m, k = a.shape
+    n, kb = b.shape
+    if kb != k:
+        raise ValueError(f"K mismatch: a {k}, b {kb}")
+    if k % 128:
+        raise ValueError(f"K={k} must be a multiple of 128")
+    a_s = _cuda(a_s, "a_s").to(torch.float32).contiguous()
+    b_s = _cuda(b_s, "b_s").to(torch.float32).contiguous()
+    if tuple(a_s.shape) != (m, k // 128):
+        raise ValueError(f"a_s shape {tuple(a_s.shape)} != ({m}, {k // 128})")
+    if tuple(b_s.shape) != ((n + 127) // 128, k // 128):
+        raise ValueError(f"b_s shape {tuple(b_s.shape)} != ({(n + 127) // 128}, {k // 128})")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"out_dtype {out_dtype}")
+    c = torch.empty(m, n, dtype=out_dtype, device=a.device)
+    _lib.call("mosaic_fp8_block_gemm", _ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(c),
+              DT_F32 if out_dtype == torch.float32 else DT_BF16, m, n, k, _stream())
+    return c
+
+
 # ---------------------------------------------------------------- routing ---
 def moe_route_topk(logits: torch.Tensor, top_k: int, score_func: str = "sigmoid", renorm: bool = True,
                    route_scale: float = 1.0, bias: torch.Tensor | None = None):

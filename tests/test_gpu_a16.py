@@ -104,6 +104,43 @@ def test_mxt16_linear_a16_vs_oracle(dev, m, n, k):
     assert_close(y.float().cpu().numpy(), ref, what=f"mxt16 linear m={m} n={n} k={k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 2048, 7168), (3, 48, 640), (16, 64, 1024), (20, 7168, 2048),
+                                   (70, 96, 512)])
+def test_mxt16_linear_a8_vs_oracle(dev, m, n, k):
+    """A8 "source semantics" linear (kernels/fp4_source.py:132-156) on the scaled MFMA."""
+    ops = _ops()
+    rng = np.random.default_rng(m * 13 + n + k)
+    packed, scale = _quant_weights(rng, n, k)
+    x = _bf16(rng.standard_normal((m, k)))
+    ref = L.mx_linear_a8(x.float().numpy(), packed, scale)
+    w = ops.mxt16_prepack(torch.from_numpy(packed).to(dev), torch.from_numpy(scale).to(dev))
+    y = ops.mxt16_linear_a8(x.to(dev), w)
+    assert_close(y.float().cpu().numpy(), ref, what=f"mxt16 a8 m={m} n={n} k={k}")
+    # and it is the A8 contract, not the A16 one: rounding of x to e4m3 shows
+    a16 = L.mx_linear_a16(x.float().numpy(), packed, scale, out_bf16=False)
+    assert np.abs(y.float().cpu().numpy() - a16).max() > 1e-3
+
+
+def test_mxt16_linear_a8_onehot_and_scales_kat(dev):
+    """Closed form: one-hot e4m3 x (value 1.0, activation scale 2^a) selects
+    2^a * dequantized weight column k exactly, with per-32 weight scales
+    2^(b-127) -- pins the MFMA operand order and both e8m0 scale paths."""
+    ops = _ops()
+    rng = np.random.default_rng(3)
+    n, k = 32, 256
+    codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    packed = C.pack_codes(codes)
+    scale = (120 + (np.arange(n)[:, None] + np.arange(k // 32)[None, :]) % 9).astype(np.uint8)
+    w = ops.mxt16_prepack(torch.from_numpy(packed).to(dev), torch.from_numpy(scale).to(dev))
+    W = C.dequant_mxfp4(packed, scale)
+    xq = np.zeros((k, k), dtype=np.uint8)
+    xq[np.arange(k), np.arange(k)] = 0x38  # e4m3 1.0
+    a = (np.arange(k) % 5 - 2).astype(np.float32)
+    sa = np.repeat((2.0 ** a)[:, None], k // 128, axis=1).astype(np.float32)
+    y = ops.mxt16_linear_a8(None, w, prequant=(torch.from_numpy(xq).to(dev), torch.from_numpy(sa).to(dev)))
+    np.testing.assert_array_equal(y.float().cpu().numpy(), C.round_bf16(W.T * (2.0 ** a)[:, None]))
+
+
 @pytest.mark.parametrize("m,e,k,func", [(1, 256, 8, "sigmoid"), (64, 256, 8, "sigmoid"), (16, 64, 6, "softmax"),
                                         (9, 256, 8, "sqrtsoftplus"), (4, 16, 16, "sigmoid")])
 def test_route_topk_vs_oracle(dev, m, e, k, func):
