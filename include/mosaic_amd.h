@@ -173,6 +173,25 @@ int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, int32_t* ids,
                            int renorm, float route_scale, const float* route_bias, float swiglu_limit,
                            void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream);
 
+/* ---------------------------------------------------- A8 routed MoE layer -- */
+size_t mosaic_moe_a8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                                     int has_shared);
+
+/* Routed-expert MoE layer, A8 contract of fused_moe_mxint (kernels/mxint.py:1435-1739;
+ * exact_moe / fused_moe_qpa, kernels/exact_moe.py:12-19, kernels/qpa_mma.py:681-784):
+ * tokens act-quantized 1x128 pow2 e4m3, A8 gate/up into bf16, fp32 SwiGLU with
+ * the clamps when swiglu_limit > 0, x route weight, bf16, 1x128 pow2 e4m3
+ * requant, A8 down into bf16 partials, fp32 sum in ascending expert id (an
+ * optional shared expert is added last), bf16.  Arguments as
+ * mosaic_moe_a16_forward (MXT16 banks). */
+int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
+                          const uint8_t* gu_packed, const uint8_t* gu_scale, const uint8_t* d_packed,
+                          const uint8_t* d_scale, const uint8_t* sh_gu_packed, const uint8_t* sh_gu_scale,
+                          const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
+                          int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
+                          int renorm, float route_scale, const float* route_bias, float swiglu_limit,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

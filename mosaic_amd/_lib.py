@@ -36,6 +36,9 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_moe_layout": (c_int, [P, P, I64, I64, I64, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, P]),
     "mosaic_emit_tiles": (c_int, [P, I64, I, P, P, P, P, I64, P]),
     "mosaic_moe_a16_workspace_bytes": (c_size_t, [I64, I64, I64, I64, I64, I]),
+    "mosaic_moe_a8_workspace_bytes": (c_size_t, [I64, I64, I64, I64, I64, I]),
+    "mosaic_moe_a8_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,
+                                      P, c_size_t, P]),
     "mosaic_moe_a16_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,
                                        P, c_size_t, P, P]),
 }

@@ -31,4 +31,66 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
                         float route_scale, int has_shared, int block_m, int64_t tile_cap, const LayoutOut& out,
                         hipStream_t st);
 
+constexpr int kMoeBlockM = 16;  // token rows per MoE tile (one 16-row MFMA tile)
+
+// y[t][h] = bf16(sum over j of yp[combine_pos[t][j]][h]) (defined in mx_a16.hip)
+__global__ void moe_combine_kernel(const float* __restrict__ yp, const int32_t* __restrict__ combine_pos,
+                                   uint16_t* __restrict__ y, int M, int W, int H);
+
+// Device workspace of one MoE forward (caller-allocated, carved here).
+struct MoeWorkspace {
+  int32_t *counts, *offsets, *perm, *perm_token, *sorted_ids, *inv_pos, *combine_pos;
+  float* perm_weight;
+  int32_t *tile_expert, *tile_start, *tile_rows, *tile_p0, *n_tiles;
+  uint16_t* z;     // [A, I] bf16 SwiGLU output (route weight applied)
+  float* yp;       // [A, H] fp32 expert partials
+  uint8_t* xq;     // A8 only: [M, H] e4m3 tokens
+  float* xs;       // A8 only: [M, H/128] scales
+  uint8_t* zq;     // A8 only: [A, I] e4m3 z
+  float* zs;       // A8 only: [A, I/128] scales
+  int64_t tile_cap;
+  size_t bytes;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// base == nullptr only sizes the workspace
+inline MoeWorkspace carve_moe_workspace(char* base, int64_t M, int64_t H, int64_t I, int64_t E, int64_t K,
+                                        int has_shared, int block_m, bool a8) {
+  MoeWorkspace w{};
+  const int64_t A = M * K + (has_shared ? M : 0);
+  const int64_t Ee = E + (has_shared ? 1 : 0);
+  const int64_t u = A < Ee ? A : Ee;
+  w.tile_cap = (A + u * (block_m - 1)) / block_m;
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  w.counts = (int32_t*)take(4 * (Ee + 1));
+  w.offsets = (int32_t*)take(4 * (Ee + 2));
+  w.perm = (int32_t*)take(4 * A);
+  w.perm_token = (int32_t*)take(4 * A);
+  w.perm_weight = (float*)take(4 * A);
+  w.sorted_ids = (int32_t*)take(4 * A);
+  w.inv_pos = (int32_t*)take(4 * A);
+  w.combine_pos = (int32_t*)take(4 * A);
+  w.tile_expert = (int32_t*)take(4 * w.tile_cap);
+  w.tile_start = (int32_t*)take(4 * w.tile_cap);
+  w.tile_rows = (int32_t*)take(4 * w.tile_cap);
+  w.tile_p0 = (int32_t*)take(4 * w.tile_cap);
+  w.n_tiles = (int32_t*)take(4);
+  w.z = (uint16_t*)take(2 * A * I);
+  w.yp = (float*)take(4 * A * H);
+  if (a8) {
+    w.xq = (uint8_t*)take(M * H);
+    w.xs = (float*)take(4 * M * (H / 128));
+    w.zq = (uint8_t*)take(A * I);
+    w.zs = (float*)take(4 * A * (I / 128));
+  }
+  w.bytes = off;
+  return w;
+}
+
 }  // namespace mosaic

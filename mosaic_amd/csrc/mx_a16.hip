@@ -316,52 +316,6 @@ __global__ void __launch_bounds__(KS * 64) mx_linear_a16_kernel(const uint16_t* 
   }
 }
 
-// ----------------------------------------------------------- workspace -----
-struct MoeWorkspace {
-  int32_t *counts, *offsets, *perm, *perm_token, *sorted_ids, *inv_pos, *combine_pos;
-  float* perm_weight;
-  int32_t *tile_expert, *tile_start, *tile_rows, *tile_p0, *n_tiles;
-  uint16_t* z;
-  float* yp;
-  int64_t tile_cap;
-  size_t bytes;
-};
-
-static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-static MoeWorkspace carve_moe_workspace(char* base, int64_t M, int64_t H, int64_t I, int64_t E, int64_t K,
-                                        int has_shared, int block_m) {
-  MoeWorkspace w{};
-  const int64_t A = M * K + (has_shared ? M : 0);
-  const int64_t Ee = E + (has_shared ? 1 : 0);
-  const int64_t u = A < Ee ? A : Ee;
-  w.tile_cap = (A + u * (block_m - 1)) / block_m;
-  size_t off = 0;
-  auto take = [&](size_t bytes) -> char* {
-    char* p = base ? base + off : nullptr;
-    off += align256(bytes);
-    return p;
-  };
-  w.counts = (int32_t*)take(4 * (Ee + 1));
-  w.offsets = (int32_t*)take(4 * (Ee + 2));
-  w.perm = (int32_t*)take(4 * A);
-  w.perm_token = (int32_t*)take(4 * A);
-  w.perm_weight = (float*)take(4 * A);
-  w.sorted_ids = (int32_t*)take(4 * A);
-  w.inv_pos = (int32_t*)take(4 * A);
-  w.combine_pos = (int32_t*)take(4 * A);
-  w.tile_expert = (int32_t*)take(4 * w.tile_cap);
-  w.tile_start = (int32_t*)take(4 * w.tile_cap);
-  w.tile_rows = (int32_t*)take(4 * w.tile_cap);
-  w.tile_p0 = (int32_t*)take(4 * w.tile_cap);
-  w.n_tiles = (int32_t*)take(4);
-  w.z = (uint16_t*)take(2 * A * I);
-  w.yp = (float*)take(4 * A * H);
-  w.bytes = off;
-  return w;
-}
-
-constexpr int kMoeBlockM = 16;
 constexpr int kGuT = 2, kGuKS = 4;   // gate/up: 16 z outputs per workgroup
 constexpr int kDnT = 2, kDnKS = 4;   // down: 32 hidden rows per workgroup
 
@@ -416,7 +370,7 @@ extern "C" int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_
 
 extern "C" size_t mosaic_moe_a16_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts,
                                                  int64_t top_k, int has_shared) {
-  return carve_moe_workspace(nullptr, m, hidden, inter, n_experts, top_k, has_shared, kMoeBlockM).bytes;
+  return carve_moe_workspace(nullptr, m, hidden, inter, n_experts, top_k, has_shared, kMoeBlockM, false).bytes;
 }
 
 extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
@@ -438,7 +392,8 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
   MOSAIC_CHECK_ARG(inter > 0 && inter % 128 == 0, "moe_a16_forward: inter=%lld must be a multiple of 128",
                    (long long)inter);
   MOSAIC_CHECK_ARG(m >= 1, "moe_a16_forward: m=%lld", (long long)m);
-  MoeWorkspace w = carve_moe_workspace((char*)workspace, m, hidden, inter, n_experts, top_k, has_shared, kMoeBlockM);
+  MoeWorkspace w =
+      carve_moe_workspace((char*)workspace, m, hidden, inter, n_experts, top_k, has_shared, kMoeBlockM, false);
   MOSAIC_CHECK_ARG(workspace_bytes >= w.bytes, "moe_a16_forward: workspace %zu < %zu bytes", workspace_bytes,
                    w.bytes);
   hipStream_t st = (hipStream_t)stream;

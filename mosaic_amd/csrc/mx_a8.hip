@@ -150,6 +150,110 @@ static void launch_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* 
                      (int)k);
 }
 
+// ---------------------------------------------------- MoE (A8 contract) ----
+// fused_moe_mxint semantics (kernels/mxint.py:1587-1722): the gate/up GEMM
+// output is a bf16 tensor, SwiGLU runs in fp32 on those bf16 values, the route
+// weight scales z before the bf16 cast, z is re-quantized 1x128 pow2 e4m3 for
+// the down GEMM, whose output rows are bf16 partials summed in fp32 in
+// ascending expert id.
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) moe_a8_gateup_kernel(
+    const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ gu_p,
+    const uint8_t* __restrict__ gu_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
+    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
+    const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, const int32_t* __restrict__ perm_token,
+    const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H, int I, int E, float limit) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int tile = blockIdx.y;
+  if (tile >= n_tiles[0]) return;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int j0 = blockIdx.x * 8 * T;
+  const int ns = H / 128, ns4 = (ns + 3) / 4;
+  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * ebytes;
+  const uint8_t* bs = (e == E) ? sh_s : gu_s + (int64_t)e * sbytes;
+  const uint8_t* wt[T];
+  const uint8_t* st[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int g = (t < T / 2) ? (j0 / 16 + t) : ((I + j0) / 16 + t - T / 2);
+    a8_ptrs(bp, bs, g, ns, lane, wt[t], st[t]);
+  }
+  const bool xvalid = c < rows;
+  const int tok = xvalid ? perm_token[p0 + c] : 0;
+  int s0, s1;
+  a8_k_slice(ns, ks, KS, s0, s1);
+  f32x4_t acc[T];
+  tile_dot_a8<T>(wt, st, xq + (int64_t)tok * H, xs + (int64_t)tok * ns, xvalid, q, s0, s1, acc);
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T / 2) {
+    const int t = ks;
+    f32x4_t g = red[0][t][lane], u = red[0][t + T / 2][lane];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) {
+      g += red[k2][t][lane];
+      u += red[k2][t + T / 2][lane];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ti = 4 * q + r;
+      if (ti < rows) {
+        const float gb = bf16_f32(f32_bf16(g[r])), ub = bf16_f32(f32_bf16(u[r]));
+        const float zv = swiglu_f32(gb, ub, limit) * perm_weight[p0 + ti];
+        z[(int64_t)(p0 + ti) * I + j0 + 16 * t + c] = f32_bf16(zv);
+      }
+    }
+  }
+}
+
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) moe_a8_down_kernel(
+    const uint8_t* __restrict__ zq, const float* __restrict__ zs, const uint8_t* __restrict__ d_p,
+    const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
+    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
+    const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, float* __restrict__ yp, int H, int I,
+    int E) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int tile = blockIdx.y;
+  if (tile >= n_tiles[0]) return;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int h0 = blockIdx.x * 16 * T;
+  const int ns = I / 128, ns4 = (ns + 3) / 4;
+  const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : d_p + (int64_t)e * ebytes;
+  const uint8_t* bs = (e == E) ? sh_s : d_s + (int64_t)e * sbytes;
+  const uint8_t* wt[T];
+  const uint8_t* st[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) a8_ptrs(bp, bs, h0 / 16 + t, ns, lane, wt[t], st[t]);
+  const bool xvalid = c < rows;
+  const int row = p0 + (xvalid ? c : 0);
+  int s0, s1;
+  a8_k_slice(ns, ks, KS, s0, s1);
+  f32x4_t acc[T];
+  tile_dot_a8<T>(wt, st, zq + (int64_t)row * I, zs + (int64_t)row * ns, xvalid, q, s0, s1, acc);
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ti = 4 * q + r;
+      if (ti < rows) yp[(int64_t)(p0 + ti) * H + h0 + 16 * t + c] = bf16_f32(f32_bf16(v[r]));
+    }
+  }
+}
+
 }  // namespace mosaic
 
 using namespace mosaic;
@@ -173,4 +277,58 @@ extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const 
   else
     launch_linear_a8<1, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
   MOSAIC_RETURN_LAUNCH("mxt16_linear_a8");
+}
+
+extern "C" size_t mosaic_moe_a8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts,
+                                                int64_t top_k, int has_shared) {
+  return carve_moe_workspace(nullptr, m, hidden, inter, n_experts, top_k, has_shared, kMoeBlockM, true).bytes;
+}
+
+extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
+                                     const uint8_t* gu_packed, const uint8_t* gu_scale, const uint8_t* d_packed,
+                                     const uint8_t* d_scale, const uint8_t* sh_gu_packed, const uint8_t* sh_gu_scale,
+                                     const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
+                                     int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
+                                     int renorm, float route_scale, const float* route_bias, float swiglu_limit,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  MOSAIC_CHECK_ARG(x && ids && weights && gu_packed && gu_scale && d_packed && d_scale && y && workspace,
+                   "moe_a8_forward: null pointer");
+  const int has_shared = sh_gu_packed != nullptr;
+  MOSAIC_CHECK_ARG(!has_shared || (sh_gu_scale && sh_d_packed && sh_d_scale),
+                   "moe_a8_forward: shared expert needs all four tensors");
+  MOSAIC_CHECK_ARG(hidden > 0 && hidden % 128 == 0, "moe_a8_forward: hidden=%lld must be a multiple of 128",
+                   (long long)hidden);
+  MOSAIC_CHECK_ARG(inter > 0 && inter % 128 == 0, "moe_a8_forward: inter=%lld must be a multiple of 128",
+                   (long long)inter);
+  MOSAIC_CHECK_ARG(m >= 1, "moe_a8_forward: m=%lld", (long long)m);
+  MoeWorkspace w =
+      carve_moe_workspace((char*)workspace, m, hidden, inter, n_experts, top_k, has_shared, kMoeBlockM, true);
+  MOSAIC_CHECK_ARG(workspace_bytes >= w.bytes, "moe_a8_forward: workspace %zu < %zu bytes", workspace_bytes,
+                   w.bytes);
+  hipStream_t st = (hipStream_t)stream;
+  LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,
+               w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0, 1};
+  int rc = launch_route_layout(logits, route_bias, ids, weights, ids, weights, m, n_experts, top_k, score_func,
+                               renorm, route_scale, has_shared, kMoeBlockM, w.tile_cap, lo, st);
+  if (rc != 0) return rc;
+  rc = mosaic_act_quant(x, MOSAIC_DTYPE_BF16, w.xq, w.xs, m, hidden, 128, 0, stream);
+  if (rc != 0) return rc;
+  const unsigned tcap = (unsigned)w.tile_cap;
+  constexpr int GT = 2, GKS = 4, DT = 2, DKS = 4;
+  hipLaunchKernelGGL((moe_a8_gateup_kernel<GT, GKS>), dim3((unsigned)(inter / (8 * GT)), tcap), dim3(GKS * 64), 0,
+                     st, w.xq, w.xs, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_rows,
+                     w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
+                     (int)n_experts, swiglu_limit);
+  MOSAIC_LAUNCH_CHECK("moe_a8_gateup");
+  const int64_t A = m * top_k + (has_shared ? m : 0);
+  // rows of z past the real assignments are never read by the down kernel
+  rc = mosaic_act_quant(w.z, MOSAIC_DTYPE_BF16, w.zq, w.zs, A, inter, 128, 0, stream);
+  if (rc != 0) return rc;
+  hipLaunchKernelGGL((moe_a8_down_kernel<DT, DKS>), dim3((unsigned)(hidden / (16 * DT)), tcap), dim3(DKS * 64), 0,
+                     st, w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows,
+                     w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
+  MOSAIC_LAUNCH_CHECK("moe_a8_down");
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
+                     w.yp, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
+  MOSAIC_RETURN_LAUNCH("moe_a8_combine");
 }

@@ -339,17 +339,27 @@ class MoEWorkspace:
 _DEFAULT_WS = MoEWorkspace()
 
 
-def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logits: torch.Tensor | None = None,
-                    ids: torch.Tensor | None = None, weights: torch.Tensor | None = None, top_k: int | None = None,
-                    shared: tuple[MXT16, MXT16] | None = None, score_func: str = "sigmoid", renorm: bool = True,
-                    route_scale: float = 1.0, route_bias: torch.Tensor | None = None, swiglu_limit: float = 0.0,
-                    workspace: MoEWorkspace | None = None, stage_events: "StageEvents | None" = None):
+def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, **kw):
     """A16 routed MoE layer (+ optional shared expert) -> (y bf16 [M, H], ids, weights).
 
     ``gate_up``: MXT16 bank of [E, 2I, H/2] (gate rows then up rows per expert);
     ``down``: MXT16 bank of [E, H, I/2]; ``shared``: (gate_up, down) MXT16 of one
     expert or None.  Either ``logits`` [M, E] (the router runs on the device) or
     ``ids``/``weights`` [M, k] are given."""
+    return _moe_forward(False, x, gate_up, down, **kw)
+
+
+def moe_a8_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, **kw):
+    """A8 routed MoE layer (fused_moe_mxint contract), same arguments as ``moe_a16_forward``."""
+    kw.pop("stage_events", None)
+    return _moe_forward(True, x, gate_up, down, **kw)
+
+
+def _moe_forward(a8: bool, x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logits: torch.Tensor | None = None,
+                 ids: torch.Tensor | None = None, weights: torch.Tensor | None = None, top_k: int | None = None,
+                 shared: tuple[MXT16, MXT16] | None = None, score_func: str = "sigmoid", renorm: bool = True,
+                 route_scale: float = 1.0, route_bias: torch.Tensor | None = None, swiglu_limit: float = 0.0,
+                 workspace: MoEWorkspace | None = None, stage_events: "StageEvents | None" = None):
     x = _bf16(x, "x")
     if x.dim() != 2:
         raise ValueError(f"x must be [M, H], got {tuple(x.shape)}")
@@ -390,14 +400,17 @@ def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logits: tor
     if route_bias is not None:
         route_bias = _cuda(route_bias, "route_bias").to(torch.float32)
     has_shared = int(shared is not None)
-    nbytes = _lib.lib().mosaic_moe_a16_workspace_bytes(m, h, inter, e, top_k, has_shared)
+    kind = "a8" if a8 else "a16"
+    nbytes = getattr(_lib.lib(), f"mosaic_moe_{kind}_workspace_bytes")(m, h, inter, e, top_k, has_shared)
     ws = (workspace or _DEFAULT_WS).get(nbytes, x.device)
     y = torch.empty(m, h, dtype=torch.bfloat16, device=x.device)
-    _lib.call("mosaic_moe_a16_forward", _ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gate_up.packed),
-              _ptr(gate_up.scale), _ptr(down.packed), _ptr(down.scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]),
-              _ptr(sh[3]), _ptr(y), m, h, inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale),
-              _ptr(route_bias), float(swiglu_limit), _ptr(ws), ws.numel(),
-              None if stage_events is None else stage_events.array, _stream())
+    args = [_ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gate_up.packed), _ptr(gate_up.scale),
+            _ptr(down.packed), _ptr(down.scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(y), m, h,
+            inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale), _ptr(route_bias),
+            float(swiglu_limit), _ptr(ws), ws.numel()]
+    if not a8:
+        args.append(None if stage_events is None else stage_events.array)
+    _lib.call(f"mosaic_moe_{kind}_forward", *args, _stream())
     return y, ids, weights
 
 

@@ -267,3 +267,26 @@ def test_moe_a16_given_ids_weight_before_down(dev):
     assert_close(y.float().cpu().numpy(), ref, what="moe given ids")
     unit = MO.moe_layer_a16(x.float().numpy(), ids, np.ones_like(w), gp, gs, dp, ds, swiglu_limit=10.0)
     assert not np.allclose(y.float().cpu().numpy(), unit, atol=1e-3)
+
+
+@pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
+    (1, 16, 256, 128, 4, False, 10.0), (3, 16, 256, 128, 4, True, 10.0), (20, 8, 384, 256, 2, False, 0.0),
+    (37, 32, 512, 128, 8, True, 10.0)])
+def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
+    """A8 layer (fused_moe_mxint contract) vs the A8 oracle of identical bytes."""
+    ops = _ops()
+    rng = np.random.default_rng(m + e + h + 1)
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    sh = _make_bank(rng, 1, h, inter) if shared else None
+    x = _bf16(rng.standard_normal((m, h)))
+    logits = rng.standard_normal((m, e)).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    gu_b, d_b = ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds))
+    shb = None if sh is None else (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])),
+                                   ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    y, ids, w = ops.moe_a8_forward(x.to(dev), gu_b, d_b, logits=T(logits), top_k=k, shared=shb, swiglu_limit=limit)
+    ids_ref, w_ref = MO.route_topk(logits, k, "sigmoid")
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    ref = MO.moe_layer_a8(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds, swiglu_limit=limit,
+                          shared=None if sh is None else tuple(t[0] for t in sh))
+    assert_close(y.float().cpu().numpy(), ref, what="moe a8")
