@@ -113,6 +113,12 @@ int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* pa
 int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
                           int out_dtype, int64_t m, int64_t n, int64_t k, void* stream);
 
+/* e4m3 [n, k] with one f32 scale per block_n x block_k block -> bf16 [n, k].
+ * Replaces dequant_fp8 (runtime/fp8.py:52-64), dsa.dequant_weight
+ * (model/dsa.py:72-78) and fp8_core's dequant_kernel (bench/fp8_core.py:60-91). */
+int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16_t* out, int64_t n, int64_t k, int block_n,
+                             int block_k, void* stream);
+
 /* -------------------------------------------------------------- routing -- */
 /* logits [m, e] f32 -> ids [m, top_k] int32 + weights [m, top_k] f32.
  * Replaces Router.forward (model/layers.py:118-150) / Gate.forward

@@ -32,6 +32,7 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_mxt16_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P]),
     "mosaic_fp8_block_gemm": (c_int, [P, P, P, P, P, I, I64, I64, I64, P]),
     "mosaic_mxt16_linear_a8": (c_int, [P, P, P, P, P, I64, I64, I64, P]),
+    "mosaic_fp8_block_dequant": (c_int, [P, P, P, I64, I64, I, I, P]),
     "mosaic_moe_route_topk": (c_int, [P, I64, I64, I64, I, I, F, P, P, P, P]),
     "mosaic_moe_layout": (c_int, [P, P, I64, I64, I64, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, P]),
     "mosaic_emit_tiles": (c_int, [P, I64, I, P, P, P, P, I64, P]),

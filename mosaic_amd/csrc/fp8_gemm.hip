@@ -118,9 +118,40 @@ static void launch_fp8_skinny(const uint8_t* a, const float* as, const uint8_t* 
                      (int)k, out_f32);
 }
 
+// w [N, K] e4m3 with one fp32 scale per (bn x bk) block -> bf16 [N, K]
+__global__ void __launch_bounds__(256) fp8_block_dequant_kernel(const uint8_t* __restrict__ w,
+                                                                const float* __restrict__ s,
+                                                                uint16_t* __restrict__ out, int64_t n, int64_t k,
+                                                                int bn, int bk, int64_t sk) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n * k) return;
+  const int64_t row = i / k, col = i % k;
+  const float sc = s[(row / bn) * sk + col / bk];
+  const uint32_t v = *reinterpret_cast<const uint32_t*>(w + i);
+  const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)v, false);
+  const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)v, true);
+  uint16_t* o = out + i;
+  o[0] = f32_bf16(lo[0] * sc);
+  o[1] = f32_bf16(lo[1] * sc);
+  o[2] = f32_bf16(hi[0] * sc);
+  o[3] = f32_bf16(hi[1] * sc);
+}
+
 }  // namespace mosaic
 
 using namespace mosaic;
+
+extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16_t* out, int64_t n, int64_t k,
+                                        int block_n, int block_k, void* stream) {
+  MOSAIC_CHECK_ARG(w && s && out, "fp8_block_dequant: null pointer");
+  MOSAIC_CHECK_ARG(n >= 0 && k > 0 && k % 4 == 0 && block_n > 0 && block_k > 0 && block_k % 4 == 0,
+                   "fp8_block_dequant: K=%lld, block %dx%d", (long long)k, block_n, block_k);
+  if (n == 0) return kOk;
+  const int64_t total = n * k / 4;
+  hipLaunchKernelGGL(fp8_block_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, w, s, out, n, k, block_n, block_k, (k + block_k - 1) / block_k);
+  MOSAIC_RETURN_LAUNCH("fp8_block_dequant");
+}
 
 extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
                                      int out_dtype, int64_t m, int64_t n, int64_t k, void* stream) {

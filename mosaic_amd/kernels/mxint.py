@@ -1,0 +1,81 @@
+"""A8 MXFP4 GEMV and the fused MoE with the reference ``kernels/mxint.py`` signatures.
+
+The reference's integer-exact limb arithmetic (qA split into three s8 limbs on
+dp4a / mma.s8) has no counterpart here: gfx950's scaled MFMA consumes the e4m3
+activations and E2M1 weights directly with both power-of-two scales, so the
+banks are simply MXT16-prepacked MXFP4 (``weight_repr`` is accepted and
+ignored)."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .. import ops
+from . import _a8
+
+
+@dataclass
+class MXT16Bank:
+    """Prepacked expert bank: gate|up [E, 2I, H/2] and down [E, H, I/2] in MXT16."""
+    gate_up: ops.MXT16
+    down: ops.MXT16
+
+    @property
+    def n_out_gu(self) -> int:
+        return self.gate_up.n
+
+    @property
+    def n_out_d(self) -> int:
+        return self.down.n
+
+
+def prepack_expert_bank_mxint(packed_g, scale_g, packed_u=None, scale_u=None, packed_d=None, scale_d=None,
+                              chunk: int = 32) -> MXT16Bank:
+    """NK packed expert tensors (gate|up concatenated, or gate and up separately)
+    -> MXT16Bank (``kernels/mxint.py:165-206``)."""
+    if packed_d is None or scale_d is None:
+        raise TypeError("packed_d/scale_d are required")
+    if packed_u is not None:
+        packed_g = torch.cat([ops._u8(packed_g, "packed_g"), ops._u8(packed_u, "packed_u")], dim=1)
+        scale_g = torch.cat([ops._u8(scale_g, "scale_g"), ops._u8(scale_u, "scale_u")], dim=1)
+    return MXT16Bank(ops.mxt16_prepack(packed_g, scale_g), ops.mxt16_prepack(packed_d, scale_d))
+
+
+prepack_expert_bank_mxint_packed4 = prepack_expert_bank_mxint
+
+
+def mxint_dp4a_gemm(x, packed, scale_w, n_out, prequant=None, xint=None, prepacked=None,
+                    weight_repr: str = "hot8") -> torch.Tensor:
+    """x [M, K] bf16 -> [M, N] bf16, A8 (``kernels/mxint.py:362-401``)."""
+    return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
+
+
+def mxint_imma_gemm(x, packed, scale_w, n_out, prequant=None, xint=None, qpa_k=8, ordered=True, prepacked=None,
+                    weight_repr: str = "hot8") -> torch.Tensor:
+    """x [M, K] bf16 -> [M, N] bf16, A8 (``kernels/mxint.py:1014-1054``)."""
+    return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
+
+
+def fused_moe_mxint(x, expert_ids, expert_weights, packed_gate_up=None, scale_gate_up=None, packed_down=None,
+                    scale_down=None, bank: MXT16Bank | None = None, crossover: int = 0, imma_k: int = 8,
+                    swiglu_limit: float = 10.0, stage_times: dict | None = None, weight_repr: str = "hot8",
+                    epilogue: str = "torch", gu_bank=None, down_bank=None, masked_bank=None) -> torch.Tensor:
+    """A8 routed MoE -> [k_tok, H] bf16 (``kernels/mxint.py:1435-1739``).
+
+    x [k_tok, H] bf16; expert_ids [k_tok, top_k] (or [k_tok]); expert_weights
+    fp32 of the same shape (None = ones).  Weights come from ``bank`` (MXT16Bank)
+    or raw NK tensors (prepacked on every call, as the reference does without a
+    bank).  Sync-free: nothing is read back to the host."""
+    if weight_repr not in ("hot8", "packed4", "hybrid"):
+        raise ValueError(f"weight_repr must be hot8|packed4|hybrid, got {weight_repr}")
+    if bank is None:
+        if packed_gate_up is None or packed_down is None:
+            raise TypeError("fused_moe_mxint requires bank= or packed_gate_up/packed_down")
+        bank = prepack_expert_bank_mxint(packed_gate_up, scale_gate_up, packed_d=packed_down, scale_d=scale_down)
+    ids = expert_ids if expert_ids.dim() == 2 else expert_ids.reshape(-1, 1)
+    k_tok, top_k = ids.shape
+    w = (torch.ones(k_tok, top_k, dtype=torch.float32, device=x.device) if expert_weights is None
+         else expert_weights.reshape(k_tok, top_k).to(torch.float32))
+    y, _, _ = ops.moe_a8_forward(x, bank.gate_up, bank.down, ids=ids, weights=w, swiglu_limit=swiglu_limit)
+    return y

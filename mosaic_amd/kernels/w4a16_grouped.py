@@ -1,0 +1,17 @@
+"""Tile list for grouped expert GEMMs (reference ``kernels/w4a16_grouped.py:151-169``)."""
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+
+BLOCK_M = 16
+
+
+def emit_tiles(counts: torch.Tensor, block_m: int = BLOCK_M, max_tiles: int | None = None):
+    """counts [E] int32 -> (expert_index [Tcap], m_start [Tcap], n_tiles [1], tile_rows [Tcap]).
+    No per-expert cap: the reference stops at MAX_TILES=32 per expert (``:55-60``)."""
+    e = counts.numel()
+    t_cap = int(max_tiles) if max_tiles is not None else max(e, 1)
+    ei, ms, nt, rows = ops.emit_tiles(counts, block_m, t_cap)
+    return ei, ms, nt, rows

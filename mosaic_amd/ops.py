@@ -252,6 +252,21 @@ def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: tor
     return c
 
 
+def fp8_block_dequant(w: torch.Tensor, s: torch.Tensor, block: tuple[int, int] = (128, 128)) -> torch.Tensor:
+    """e4m3 [N, K] + f32 scales [ceil(N/bn), ceil(K/bk)] -> bf16 [N, K]."""
+    w = _u8(w, "w")
+    if w.dim() != 2:
+        raise ValueError("w must be 2-D")
+    n, k = w.shape
+    bn, bk = block
+    s = _cuda(s, "s").to(torch.float32).contiguous()
+    if tuple(s.shape) != ((n + bn - 1) // bn, (k + bk - 1) // bk):
+        raise ValueError(f"scale shape {tuple(s.shape)} does not tile [{n}, {k}] by {block}")
+    out = torch.empty(n, k, dtype=torch.bfloat16, device=w.device)
+    _lib.call("mosaic_fp8_block_dequant", _ptr(w), _ptr(s), _ptr(out), n, k, bn, bk, _stream())
+    return out
+
+
 # ---------------------------------------------------------------- routing ---
 def moe_route_topk(logits: torch.Tensor, top_k: int, score_func: str = "sigmoid", renorm: bool = True,
                    route_scale: float = 1.0, bias: torch.Tensor | None = None):
