@@ -198,6 +198,70 @@ int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int32_t* ids, 
                           int renorm, float route_scale, const float* route_bias, float swiglu_limit,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* ----------------------------------------------------------- DSA decode -- */
+/* Workspace bytes of mosaic_dsa_indexer_topk for b rows of l cached tokens. */
+size_t mosaic_dsa_indexer_workspace_bytes(int64_t b, int64_t l);
+
+/* FP8 lightning indexer + top-k, replacing Indexer.forward's scoring and topk
+ * (.mosaicvm/source/inference_model.py:408-439; mosaicvm/model/dsa_layers.py:281-321)
+ * and the select kernel (mosaicvm/kernels/dsa_attention.py:19-68):
+ *   q [b, h, d] e4m3 + q_s [b, h] f32, k [b, l, d] e4m3 + k_s [b, l] f32,
+ *   w [b, h] f32 (weights_proj(x) * softmax_scale * h^-0.5);
+ *   score[t] = sum_h w_h ReLU(q_h . k_t q_s[h] k_s[t]) in the canonical order
+ *   (exact dot rounded once to fp32, * q_s, * k_s, ReLU, * w_h, fp32 sum over h
+ *   ascending); idx_out [b, topk] int32 = tokens by descending score, ties to
+ *   the lower index, + offset; tokens t >= lengths[b] (lengths NULL = all l)
+ *   are masked and missing slots are -1.  d == 128, h in {16, 32, 48, 64},
+ *   topk <= 4096.  Non-finite q/k codes or scales give unspecified indices. */
+int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
+                            const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h, int64_t d, int64_t l,
+                            int64_t topk, int32_t offset, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The canonical indexer scores themselves, scores [b, l] f32 (the index_score
+ * tensor of Indexer.forward, .mosaicvm/source/inference_model.py:424-425). */
+int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
+                              float* scores, int64_t b, int64_t h, int64_t d, int64_t l, void* stream);
+
+/* First stage of mosaic_dsa_indexer_topk on its own: per token an interval
+ * [lo, hi] (each [b, l] f32) that contains the canonical score, from the fp8
+ * MFMA pass.  Diagnostic; same arguments as the scoring above. */
+int mosaic_dsa_indexer_bounds(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
+                              float* lo, float* hi, int64_t b, int64_t h, int64_t d, int64_t l, void* stream);
+
+/* Workspace bytes of mosaic_mla_sparse_decode. */
+size_t mosaic_mla_decode_workspace_bytes(int64_t b, int64_t h, int64_t topk);
+
+/* MLA decode over the selected KV entries, replacing sparse_attn
+ * (.mosaicvm/source/inference_kernel.py:276-368), sparse_attn_fused
+ * (mosaicvm/kernels/dsa_sparse.py:92-110) and sparse_attn_ref (mosaicvm/model/dsa.py:214-242):
+ *   q [b, h, d_latent + d_rope] bf16; the cache of each row holds n tokens of
+ *   kv_latent [b, n, d_latent] e4m3 with kv_scale [b, n, d_latent/scale_block] f32
+ *   (dequantized to bf16, as act_quant_sim, mosaicvm/model/dsa.py:81-90) and
+ *   kv_rope [b, n, d_rope] bf16; idx [b, topk] int32 (-1, or >= n, = masked);
+ *   sink [h] f32 or NULL.  s_t = q . kv_t * softmax_scale (fp32);
+ *   out [b, h, d_latent] bf16 = sum_t bf16(exp(s_t - m)) v_t / (sum_t exp(s_t - m)
+ *   + exp(sink - m)), v_t = the latent part.  A row with no valid entry gives 0.
+ *   d_latent = 512, d_rope = 64, h in {16, 32, 48, 64} or a multiple of 64 up
+ *   to 256, scale_block a power of two in 16..512. */
+int mosaic_mla_sparse_decode(const uint16_t* q, const uint8_t* kv_latent, const float* kv_scale,
+                             const uint16_t* kv_rope, const float* sink, const int32_t* idx, uint16_t* out, int64_t b,
+                             int64_t h, int64_t n, int64_t topk, int64_t d_latent, int64_t d_rope,
+                             int64_t scale_block, float softmax_scale, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* MLA / sparse attention over a bf16 KV, the upstream sparse_attn contract
+ * (.mosaicvm/source/inference_kernel.py:355-368) and sparse_attn_fused
+ * (mosaicvm/kernels/dsa_sparse.py:92-110): q [rows, h, d] bf16, kv [rows /
+ * rows_per_kv, n, d] bf16 (query row r reads KV batch r / rows_per_kv), idx
+ * [rows, topk] int32, sink [h] f32 or NULL; out [rows, h, 512] bf16 with
+ * V = kv[..., :512].  d = 512 (V = K, the V4 geometry) or 576 (512 latent + 64
+ * rope).  Same math and head limits as mosaic_mla_sparse_decode; the workspace
+ * is mosaic_mla_decode_workspace_bytes(rows, h, topk). */
+int mosaic_mla_sparse_decode_bf16(const uint16_t* q, const uint16_t* kv, const float* sink, const int32_t* idx,
+                                  uint16_t* out, int64_t rows, int64_t h, int64_t n, int64_t topk, int64_t d,
+                                  int64_t rows_per_kv, float softmax_scale, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

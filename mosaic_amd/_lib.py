@@ -42,6 +42,15 @@ SIGNATURES: dict[str, tuple] = {
                                       P, c_size_t, P]),
     "mosaic_moe_a16_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,
                                        P, c_size_t, P, P]),
+    "mosaic_dsa_indexer_workspace_bytes": (c_size_t, [I64, I64]),
+    "mosaic_dsa_indexer_topk": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int32, P, c_size_t,
+                                        P]),
+    "mosaic_dsa_indexer_scores": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, P]),
+    "mosaic_dsa_indexer_bounds": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
+    "mosaic_mla_decode_workspace_bytes": (c_size_t, [I64, I64, I64]),
+    "mosaic_mla_sparse_decode": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, F, P, c_size_t,
+                                         P]),
+    "mosaic_mla_sparse_decode_bf16": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, F, P, c_size_t, P]),
 }
 
 _LIB = None

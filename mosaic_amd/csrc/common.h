@@ -74,6 +74,21 @@ __device__ __forceinline__ u32x4_t load_nt_u32x4(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
 }
 
+// 8-bit MFMA operand of one 128-byte K block for v_mfma_scale_f32_16x16x128_f8f6f4:
+// lane (c = l%16, q = l/16) holds bytes [16q, 16q+16) and [64+16q, 64+16q+16)
+// of row c (the same lane->K map on the A and B sides).
+__device__ __forceinline__ i32x8_t load_fp8_operand(const uint8_t* __restrict__ row, int kb, int q) {
+  const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(row + (int64_t)kb * 128 + 16 * q);
+  const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(row + (int64_t)kb * 128 + 64 + 16 * q);
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+__device__ __forceinline__ i32x8_t load_fp8_operand_nt(const uint8_t* __restrict__ row, int kb, int q) {
+  const u32x4_t lo = load_nt_u32x4(row + (int64_t)kb * 128 + 16 * q);
+  const u32x4_t hi = load_nt_u32x4(row + (int64_t)kb * 128 + 64 + 16 * q);
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
 // Two E2M1 nibbles of byte `sel` of `word` -> two bf16 scaled by `scale`
 // (gfx950 v_cvt_scalef32_pk_bf16_fp4; low nibble -> element 0).
 #define MOSAIC_CVT_FP4_BF16(word, scale, sel) \

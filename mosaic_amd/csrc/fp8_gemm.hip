@@ -16,18 +16,6 @@
 
 namespace mosaic {
 
-__device__ __forceinline__ i32x8_t load_fp8_operand(const uint8_t* __restrict__ row, int kb, int q) {
-  const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(row + (int64_t)kb * 128 + 16 * q);
-  const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(row + (int64_t)kb * 128 + 64 + 16 * q);
-  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-}
-
-__device__ __forceinline__ i32x8_t load_fp8_operand_nt(const uint8_t* __restrict__ row, int kb, int q) {
-  const u32x4_t lo = load_nt_u32x4(row + (int64_t)kb * 128 + 16 * q);
-  const u32x4_t hi = load_nt_u32x4(row + (int64_t)kb * 128 + 64 + 16 * q);
-  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-}
-
 // unit-scale fp8 x fp8 block product of one 128-K block
 __device__ __forceinline__ f32x4_t mfma_fp8_block(const i32x8_t a, const i32x8_t b) {
   const f32x4_t z = {0.f, 0.f, 0.f, 0.f};

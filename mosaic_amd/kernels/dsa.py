@@ -1,0 +1,75 @@
+"""DSA drop-ins: the lightning indexer with top-k and sparse (MLA) attention.
+
+* ``sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale)`` -- upstream
+  signature (``.mosaicvm/source/inference_kernel.py:355-368``): q [b, m, h, d]
+  bf16, kv [b, n, d] bf16, topk_idxs [b, m, topk] int32 -> o [b, m, h, d].
+  V = K (d = 512, the V4 geometry); heads are padded to the kernel's head
+  groups and stripped, as upstream pads to 16.
+* ``sparse_attn_fused(q, kv, sink, topk_idxs, scale)`` and ``sparse_attn_ref``
+  -- ``mosaicvm/kernels/dsa_sparse.py:92-110`` / ``mosaicvm/model/dsa.py:214-242``:
+  q [s, h, d], kv [n, d], topk_idxs [s, t] -> o [s, h, d] (bf16 only; d = 512).
+* ``indexer_topk`` / ``indexer_scores`` -- the FP8 indexer of ``Indexer.forward``
+  (``.mosaicvm/source/inference_model.py:408-439``) from quantized q/k.
+* ``mla_decode_fp8`` -- MLA decode over an FP8 latent cache (BASELINE format).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+
+_HEAD_STEPS = (16, 32, 48, 64)
+
+
+def _padded_heads(h: int) -> int:
+    for v in _HEAD_STEPS:
+        if h <= v:
+            return v
+    return -(-h // 64) * 64
+
+
+def _attend(q3: torch.Tensor, kv3: torch.Tensor, sink, idx2: torch.Tensor, scale: float) -> torch.Tensor:
+    rows, h, d = q3.shape
+    if d != 512:
+        raise ValueError(f"sparse attention drop-in supports head dim 512 (V = K), got {d}; "
+                         "use ops.mla_sparse_decode_bf16 for the 576 = 512 + 64 MLA layout")
+    hp = _padded_heads(h)
+    if hp != h:
+        q3 = torch.cat([q3, q3.new_zeros(rows, hp - h, d)], dim=1)
+        if sink is not None:
+            sink = torch.cat([sink.float(), sink.new_zeros(hp - h, dtype=torch.float32)])
+    o = ops.mla_sparse_decode_bf16(q3, kv3, idx2, scale, None if sink is None else sink.float().contiguous())
+    return o[:, :h] if hp != h else o
+
+
+def sparse_attn(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk_idxs: torch.Tensor,
+                softmax_scale: float) -> torch.Tensor:
+    b, s, h, d = q.size()
+    o = _attend(q.reshape(b * s, h, d).contiguous(), kv.contiguous(), attn_sink,
+                topk_idxs.reshape(b * s, -1), softmax_scale)
+    return o.reshape(b, s, h, d)
+
+
+def sparse_attn_fused(q: torch.Tensor, kv: torch.Tensor, sink: torch.Tensor, topk_idxs: torch.Tensor,
+                      scale: float) -> torch.Tensor:
+    if q.dtype != torch.bfloat16 or kv.dtype != torch.bfloat16:
+        raise ValueError("sparse_attn_fused: bf16 q and kv required")
+    s, h, d = q.shape
+    return _attend(q.contiguous(), kv.contiguous().unsqueeze(0), sink, topk_idxs, scale)
+
+
+sparse_attn_ref = sparse_attn_fused
+
+
+def indexer_topk(q_fp8, q_scale, k_fp8, k_scale, weights, topk: int, lengths=None, offset: int = 0):
+    """q [B, H, 128] e4m3 + [B, H] f32, k [B, L, 128] e4m3 + [B, L] f32,
+    weights [B, H] f32 -> topk_idxs [B, topk] int32."""
+    return ops.dsa_indexer_topk(q_fp8, q_scale, k_fp8, k_scale, weights, topk, lengths, offset)
+
+
+def indexer_scores(q_fp8, q_scale, k_fp8, k_scale, weights):
+    return ops.dsa_indexer_scores(q_fp8, q_scale, k_fp8, k_scale, weights)
+
+
+def mla_decode_fp8(q, kv_latent, kv_scale, kv_rope, topk_idxs, softmax_scale, attn_sink=None):
+    return ops.mla_sparse_decode(q, kv_latent, kv_scale, kv_rope, topk_idxs, softmax_scale, attn_sink)

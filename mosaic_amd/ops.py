@@ -451,3 +451,123 @@ class StageEvents:
         out = {k: ev[i].elapsed_time(ev[i + 1]) / 1e3 for i, k in enumerate(MOE_STAGES)}
         out["total_sec"] = sum(out[k] for k in MOE_STAGES)
         return out
+
+
+# ----------------------------------------------------------- DSA decode -----
+def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
+    t = _cuda(t, name)
+    if t.dtype != torch.float32:
+        raise ValueError(f"{name}: expected float32, got {t.dtype}")
+    return t
+
+
+def _indexer_args(q, q_s, k, k_s, w):
+    q, k = _u8(q, "q"), _u8(k, "k")
+    q_s, k_s, w = _f32(q_s, "q_s"), _f32(k_s, "k_s"), _f32(w, "weights")
+    if q.dim() != 3 or k.dim() != 3:
+        raise ValueError(f"q must be [B, H, D] and k [B, L, D], got {tuple(q.shape)} and {tuple(k.shape)}")
+    b, h, d = q.shape
+    if k.shape[0] != b or k.shape[2] != d:
+        raise ValueError(f"k shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    l_ = k.shape[1]
+    if tuple(q_s.shape) != (b, h) or tuple(w.shape) != (b, h) or tuple(k_s.shape) != (b, l_):
+        raise ValueError("q_s and weights must be [B, H], k_s [B, L]")
+    return q, q_s, k, k_s, w, b, h, d, l_
+
+
+def dsa_indexer_topk(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: torch.Tensor, w: torch.Tensor,
+                     topk: int, lengths: torch.Tensor | None = None, offset: int = 0,
+                     workspace: MoEWorkspace | None = None) -> torch.Tensor:
+    """FP8 lightning indexer + exact top-k -> idx int32 [B, topk] (descending
+    canonical score, ties to the lower index, + offset, -1 where fewer than
+    topk tokens are valid)."""
+    q, q_s, k, k_s, w, b, h, d, l_ = _indexer_args(q, q_s, k, k_s, w)
+    if lengths is not None:
+        lengths = _cuda(lengths, "lengths").to(torch.int32).contiguous()
+        if tuple(lengths.shape) != (b,):
+            raise ValueError(f"lengths must be [B], got {tuple(lengths.shape)}")
+    idx = torch.empty(b, topk, dtype=torch.int32, device=q.device)
+    nbytes = _lib.lib().mosaic_dsa_indexer_workspace_bytes(b, l_)
+    ws = (workspace or _DEFAULT_WS).get(nbytes, q.device)
+    _lib.call("mosaic_dsa_indexer_topk", _ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(w), _ptr(lengths), _ptr(idx),
+              b, h, d, l_, int(topk), int(offset), _ptr(ws), ws.numel(), _stream())
+    return idx
+
+
+def dsa_indexer_scores(q, q_s, k, k_s, w) -> torch.Tensor:
+    """The canonical indexer scores [B, L] f32."""
+    q, q_s, k, k_s, w, b, h, d, l_ = _indexer_args(q, q_s, k, k_s, w)
+    out = torch.empty(b, l_, dtype=torch.float32, device=q.device)
+    _lib.call("mosaic_dsa_indexer_scores", _ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(w), _ptr(out), b, h, d, l_,
+              _stream())
+    return out
+
+
+def dsa_indexer_bounds(q, q_s, k, k_s, w) -> tuple[torch.Tensor, torch.Tensor]:
+    """The fp8-MFMA stage: (lo, hi) [B, L] f32 enclosing every canonical score."""
+    q, q_s, k, k_s, w, b, h, d, l_ = _indexer_args(q, q_s, k, k_s, w)
+    lo = torch.empty(b, l_, dtype=torch.float32, device=q.device)
+    hi = torch.empty_like(lo)
+    _lib.call("mosaic_dsa_indexer_bounds", _ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(w), _ptr(lo), _ptr(hi), b, h,
+              d, l_, _stream())
+    return lo, hi
+
+
+def mla_sparse_decode(q: torch.Tensor, kv_latent: torch.Tensor, kv_scale: torch.Tensor, kv_rope: torch.Tensor,
+                      idx: torch.Tensor, softmax_scale: float, sink: torch.Tensor | None = None,
+                      workspace: MoEWorkspace | None = None) -> torch.Tensor:
+    """MLA decode over selected entries: q [B, H, 576] bf16, kv_latent [B, N, 512]
+    e4m3, kv_scale [B, N, 512/block] f32, kv_rope [B, N, 64] bf16, idx [B, T]
+    int32 -> o [B, H, 512] bf16."""
+    q, kv_rope = _bf16(q, "q"), _bf16(kv_rope, "kv_rope")
+    kv_latent, kv_scale = _u8(kv_latent, "kv_latent"), _f32(kv_scale, "kv_scale")
+    idx = _cuda(idx, "idx").to(torch.int32).contiguous()
+    if q.dim() != 3 or kv_latent.dim() != 3 or kv_rope.dim() != 3 or kv_scale.dim() != 3 or idx.dim() != 2:
+        raise ValueError("q/kv_latent/kv_scale/kv_rope must be 3-D and idx 2-D")
+    b, h, dqk = q.shape
+    n, dl = kv_latent.shape[1], kv_latent.shape[2]
+    dr = kv_rope.shape[2]
+    if dqk != dl + dr or kv_latent.shape[0] != b or tuple(kv_rope.shape[:2]) != (b, n) or \
+            tuple(kv_scale.shape[:2]) != (b, n) or idx.shape[0] != b:
+        raise ValueError("q / kv / idx shapes do not agree")
+    if dl % kv_scale.shape[2]:
+        raise ValueError(f"kv_scale last dim {kv_scale.shape[2]} does not divide {dl}")
+    scale_block = dl // kv_scale.shape[2]
+    if sink is not None:
+        sink = _f32(sink, "sink")
+        if tuple(sink.shape) != (h,):
+            raise ValueError(f"sink must be [H], got {tuple(sink.shape)}")
+    topk = idx.shape[1]
+    out = torch.empty(b, h, dl, dtype=torch.bfloat16, device=q.device)
+    nbytes = _lib.lib().mosaic_mla_decode_workspace_bytes(b, h, topk)
+    ws = (workspace or _DEFAULT_WS).get(nbytes, q.device)
+    _lib.call("mosaic_mla_sparse_decode", _ptr(q), _ptr(kv_latent), _ptr(kv_scale), _ptr(kv_rope), _ptr(sink),
+              _ptr(idx), _ptr(out), b, h, n, topk, dl, dr, scale_block, float(softmax_scale), _ptr(ws), ws.numel(),
+              _stream())
+    return out
+
+
+def mla_sparse_decode_bf16(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, softmax_scale: float,
+                           sink: torch.Tensor | None = None, workspace: MoEWorkspace | None = None) -> torch.Tensor:
+    """Sparse attention over a bf16 KV: q [R, H, D] bf16, kv [B, N, D] bf16 with
+    R a multiple of B (query row r reads kv[r // (R // B)]), idx [R, T] int32
+    -> o [R, H, 512] bf16 with V = kv[..., :512]; D = 512 or 576."""
+    q, kv = _bf16(q, "q"), _bf16(kv, "kv")
+    idx = _cuda(idx, "idx").to(torch.int32).contiguous()
+    if q.dim() != 3 or kv.dim() != 3 or idx.dim() != 2:
+        raise ValueError("q and kv must be 3-D, idx 2-D")
+    rows, h, d = q.shape
+    nb, n, dk = kv.shape
+    if dk != d or idx.shape[0] != rows or nb == 0 or rows % nb:
+        raise ValueError(f"shapes q {tuple(q.shape)}, kv {tuple(kv.shape)}, idx {tuple(idx.shape)} do not agree")
+    if sink is not None:
+        sink = _f32(sink, "sink")
+        if tuple(sink.shape) != (h,):
+            raise ValueError(f"sink must be [H], got {tuple(sink.shape)}")
+    topk = idx.shape[1]
+    out = torch.empty(rows, h, 512, dtype=torch.bfloat16, device=q.device)
+    nbytes = _lib.lib().mosaic_mla_decode_workspace_bytes(rows, h, topk)
+    ws = (workspace or _DEFAULT_WS).get(nbytes, q.device)
+    _lib.call("mosaic_mla_sparse_decode_bf16", _ptr(q), _ptr(kv), _ptr(sink), _ptr(idx), _ptr(out), rows, h, n, topk,
+              d, rows // nb, float(softmax_scale), _ptr(ws), ws.numel(), _stream())
+    return out

@@ -1,0 +1,141 @@
+"""DSA oracles (numpy) -- TEST INFRASTRUCTURE ONLY, see ``oracle/__init__``.
+
+* ``indexer_scores`` / ``indexer_topk`` (A20): the lightning indexer of
+  ``Indexer.forward`` (``.mosaicvm/source/inference_model.py:408-439``,
+  ``mosaicvm/model/dsa_layers.py:281-321``): per token t,
+  score[t] = sum_h w_h * ReLU(q_h . k_t), then top-k with the causal / length
+  mask and ``+ offset`` on the kept indices (``inference_model.py:432-438``).
+  Here q and k are FP8 e4m3 codes with one fp32 scale per (row, head) and per
+  token (the BASELINE format; the reference feeds bf16 after an fp4
+  simulation), and the arithmetic is pinned to one canonical sequence so the
+  indices can be compared bit for bit:
+
+  1. d = the exact dot of the decoded e4m3 values, rounded once to fp32
+     (every product is a multiple of 2^-18 below 2^17.6, so a 128-term sum is
+     a multiple of 2^-18 below 2^25 and exact in float64);
+  2. a = fp32((fp32(d * q_scale[h])) * k_scale[t]);
+  3. r = a if a > 0 else +0;
+  4. s = sequential fp32 sum over h ascending, from +0, of fp32(r * w_h).
+
+  Top-k lists tokens by descending score, equal scores by ascending index
+  (``torch.topk`` leaves ties open); NaN scores rank lowest.  Tokens at or
+  beyond the row's length are masked; when fewer than k remain the tail is -1.
+* ``mla_sparse_decode`` (A21): ``sparse_attn_ref`` (``mosaicvm/model/dsa.py:214-242``),
+  the math of the upstream ``sparse_attn_kernel``
+  (``.mosaicvm/source/inference_kernel.py:276-352``): gathered KV, scores =
+  q . kv * scale in fp32, masked indices (-1) excluded, softmax with the sink
+  as a denominator-only term exp(sink - max), the value product taken with
+  bf16-rounded probabilities, output bf16.  The KV latent is FP8: e4m3 codes
+  with one fp32 scale per ``scale_block`` latent elements, dequantized to bf16
+  (``act_quant_sim``, ``mosaicvm/model/dsa.py:81-90``); the rope part stays
+  bf16 (``mosaicvm/model/dsa_layers.py:553``).  The value is the latent part.
+
+Pinned by ``tests/test_oracle_dsa.py``: the exact dot against an integer
+(int64) restatement; the scores against an independent float64 formula; the
+top-k against a brute-force full sort with ties; closed forms for the
+attention (one valid token and no sink gives that token's row; equal scores
+give the mean; the sink term checked against its definition).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import codecs as C
+
+
+def f32_order_key(s: np.ndarray) -> np.ndarray:
+    """Order-preserving uint32 key of fp32 values; NaN -> 0 (lowest)."""
+    s = np.asarray(s, dtype=np.float32)
+    u = s.view(np.uint32).astype(np.uint64)
+    key = np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    return np.where(np.isnan(s), 0, key).astype(np.uint32)
+
+
+def exact_dots(q_codes: np.ndarray, k_codes: np.ndarray) -> np.ndarray:
+    """[H, D] x [L, D] e4m3 codes -> exact dots [L, H] rounded once to fp32."""
+    qv = C.e4m3_decode(q_codes).astype(np.float64)
+    kv = C.e4m3_decode(k_codes).astype(np.float64)
+    return (kv @ qv.T).astype(np.float32)
+
+
+def indexer_scores(q, q_s, k, k_s, w) -> np.ndarray:
+    """q [B,H,D] u8, q_s [B,H] f32, k [B,L,D] u8, k_s [B,L] f32, w [B,H] f32 -> [B,L] f32."""
+    b_, h_ = q.shape[0], q.shape[1]
+    out = np.zeros((b_, k.shape[1]), dtype=np.float32)
+    for b in range(b_):
+        d = exact_dots(q[b], k[b])                                   # [L, H]
+        a = (d * q_s[b].astype(np.float32)[None, :]) * k_s[b].astype(np.float32)[:, None]
+        r = np.where(a > 0, a, np.float32(0)).astype(np.float32)
+        term = r * w[b].astype(np.float32)[None, :]
+        s = np.zeros(k.shape[1], dtype=np.float32)
+        for h in range(h_):
+            s = s + term[:, h]
+        out[b] = s
+    return out
+
+
+def topk_from_scores(scores: np.ndarray, topk: int, lengths=None, offset: int = 0) -> np.ndarray:
+    """[B, L] scores -> [B, topk] int32 indices (descending score, ties to the lower index, -1 tail)."""
+    b_, l_ = scores.shape
+    out = np.full((b_, topk), -1, dtype=np.int32)
+    for b in range(b_):
+        n = l_ if lengths is None else int(min(max(lengths[b], 0), l_))
+        key = f32_order_key(scores[b, :n]).astype(np.int64)
+        order = np.lexsort((np.arange(n), -key))
+        kk = min(topk, n)
+        out[b, :kk] = order[:kk].astype(np.int32) + np.int32(offset)
+    return out
+
+
+def indexer_topk(q, q_s, k, k_s, w, topk: int, lengths=None, offset: int = 0) -> np.ndarray:
+    return topk_from_scores(indexer_scores(q, q_s, k, k_s, w), topk, lengths, offset)
+
+
+def quantize_rows_e4m3(x: np.ndarray):
+    """Per-row (last axis) e4m3 quantization with s = amax/448 (the BASELINE
+    'per-token fp32 scale'); returns (codes, scales)."""
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x).max(axis=-1).astype(np.float32)
+    s = np.maximum(amax, np.float32(1e-4)) / np.float32(448.0)
+    return C.e4m3_encode(x / s[..., None]), s.astype(np.float32)
+
+
+def dequant_kv_latent(lat_codes: np.ndarray, lat_scale: np.ndarray, scale_block: int) -> np.ndarray:
+    """[..., Dl] e4m3 codes x [..., Dl/scale_block] f32 -> bf16-valued fp32 [..., Dl]."""
+    v = C.e4m3_decode(lat_codes).astype(np.float32)
+    s = np.repeat(lat_scale.astype(np.float32), scale_block, axis=-1)
+    return C.round_bf16((v * s).astype(np.float32))
+
+
+def sparse_attn(q, kv, sink, idx, softmax_scale: float, dv: int = 512, rows_per_kv: int = 1) -> np.ndarray:
+    """q [R,H,D] (bf16 values), kv [R/rows_per_kv, N, D] (bf16 values), sink [H] or None,
+    idx [R,T] int32 (-1 or >= N masked) -> o [R,H,dv] (bf16 values), V = kv[..., :dv]."""
+    r_, h_, _ = q.shape
+    n_ = kv.shape[1]
+    out = np.zeros((r_, h_, dv), dtype=np.float32)
+    for r in range(r_):
+        ids = np.asarray(idx[r]).astype(np.int64)
+        valid = (ids >= 0) & (ids < n_)
+        if not valid.any():
+            continue
+        g = np.asarray(kv[r // rows_per_kv], dtype=np.float32)[np.where(valid, ids, 0)].astype(np.float64)
+        s = (np.asarray(q[r], dtype=np.float64) @ g.T).astype(np.float32) * np.float32(softmax_scale)
+        s = np.where(valid[None, :], s, np.float32(-np.inf)).astype(np.float32)
+        m = s.max(axis=1)
+        p = np.exp((s - m[:, None]).astype(np.float64)).astype(np.float32)
+        denom = p.astype(np.float64).sum(axis=1)
+        if sink is not None:
+            denom = denom + np.exp((np.asarray(sink, dtype=np.float32) - m).astype(np.float64))
+        pb = C.round_bf16(p).astype(np.float64)
+        o = (pb @ g[:, :dv]) / denom[:, None]
+        out[r] = C.round_bf16(o.astype(np.float32))
+    return out
+
+
+def mla_sparse_decode(q, lat_codes, lat_scale, rope, sink, idx, softmax_scale: float,
+                      scale_block: int = 64) -> np.ndarray:
+    """q [B,H,Dl+Dr] (bf16 values), lat_codes [B,N,Dl] u8, lat_scale [B,N,Dl/sb] f32,
+    rope [B,N,Dr] (bf16 values), sink [H] f32 or None, idx [B,T] int32 -> o [B,H,Dl] (bf16 values)."""
+    lat = dequant_kv_latent(lat_codes, lat_scale, scale_block)
+    kv = np.concatenate([lat, np.asarray(rope, dtype=np.float32)], axis=-1)
+    return sparse_attn(q, kv, sink, idx, softmax_scale, dv=lat_codes.shape[-1])
