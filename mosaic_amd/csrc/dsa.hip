@@ -20,9 +20,15 @@
 //   2. tau = a lower bound of the k-th largest lo (radix digits of its order key).
 //      Any token with hi < tau is beaten by k tokens whose lo >= tau, so the
 //      true top-k lies inside {t : hi >= tau}.  Those candidates (typically
-//      k + a few percent) get the exact score (fp64 accumulation is exact:
-//      products are multiples of 2^-18 below 2^17.6, 128 of them stay below
-//      2^25) and are sorted by (score, -index).
+//      k + a few tens of percent) get the exact score, then the k best are
+//      selected (radix select on unique (score, -index) keys) and ranked.
+// Exact dots on the integer MFMA: every e4m3 value times 512 is an integer X
+// with |X| <= 229376, written X = L2*2^14 + L1*2^7 + L0 with L0, L1 in [0, 127]
+// and L2 in [-14, 14] (three int8 limbs).  The nine limb products accumulate in
+// int32 (v_mfma_i32_16x16x64_i8, exact), grouped by weight into five sums, and
+// their weighted fp64 sum (< 2^43, integer) is 2^18 times the exact dot.  (The
+// fp8 MFMA is not used here: its fp32 accumulation drops low-order bits once the
+// operands span more than about four binades.)
 //
 // MLA decode (sparse_attn_kernel, .mosaicvm/source/inference_kernel.py:276-352;
 // sparse_attn_ref, mosaicvm/model/dsa.py:214-242): per (row, head)
@@ -78,6 +84,20 @@ __device__ __forceinline__ float abs_sum_fp8(const i32x8_t v) {
   return s;
 }
 
+// lanes with `active` add 1 to lh[bin]; lanes that share a bin are merged
+// first, so a wave issues one LDS atomic per distinct bin
+__device__ __forceinline__ void lds_hist_add(uint32_t* lh, uint32_t bin, bool active) {
+  const int lane = threadIdx.x & 63;
+  uint64_t pending = __ballot(active);
+  while (pending) {
+    const int leader = __builtin_ctzll(pending);
+    const uint32_t lb = (uint32_t)__builtin_amdgcn_readlane((int)bin, leader);
+    const uint64_t same = __ballot(bin == lb) & pending;
+    if (lane == leader) atomicAdd(&lh[lb], (uint32_t)__builtin_popcountll(same));
+    pending &= ~same;
+  }
+}
+
 __global__ void dsa_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
@@ -124,9 +144,7 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   const int64_t wave_id = (int64_t)blockIdx.x * 4 + wv, n_waves = (int64_t)gridDim.x * 4;
   const uint8_t* kb = k + (int64_t)b * L * kIdxD;
   const float* ksb = ks + (int64_t)b * L;
-  for (int64_t tile0 = wave_id * U; tile0 < n_tiles; tile0 += n_waves * U) {
-    i32x8_t kv[U];
-    float ksv[U];
+  auto load_group = [&](int64_t tile0, i32x8_t (&kv)[U], float (&ksv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t t = (tile0 + u) * 16 + c;
@@ -134,16 +152,24 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
       kv[u] = ok ? load_fp8_operand_nt(kb + t * kIdxD, 0, qq) : i32x8_t{0, 0, 0, 0, 0, 0, 0, 0};
       ksv[u] = ok ? ksb[t] : 0.f;
     }
+  };
+  const int64_t step = n_waves * U;
+  auto compute_group = [&](int64_t tile0, const i32x8_t (&kv)[U], const float (&ksv)[U]) {
+    f32x4_t d[U][HT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < HT; ++j) {
+        const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+        d[u][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j], kv[u], z, 0, 0, 0, 127, 0, 127);
+      }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float part = 0.f;
 #pragma unroll
-      for (int j = 0; j < HT; ++j) {
-        const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-        const f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa[j], kv[u], z, 0, 0, 0, 127, 0, 127);
+      for (int j = 0; j < HT; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part = fmaf(fmaxf((d[r] * qsv[j][r]) * ksv[u], 0.f), wvv[j][r], part);
-      }
+        for (int r = 0; r < 4; ++r) part = fmaf(fmaxf((d[u][j][r] * qsv[j][r]) * ksv[u], 0.f), wvv[j][r], part);
       part += __shfl_xor(part, 16, 64);
       part += __shfl_xor(part, 32, 64);
       const int64_t t = (tile0 + u) * 16 + c;
@@ -155,6 +181,20 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
         if (hist1) atomicAdd(&lh[key_low_nan(l) >> 21], 1u);
       }
     }
+  };
+  // two register sets in ping-pong: the next group's loads are in flight while
+  // the current one computes
+  i32x8_t ka[U], kb2[U];
+  float sa[U], sb[U];
+  int64_t tile0 = wave_id * U;
+  if (tile0 < n_tiles) load_group(tile0, ka, sa);
+  for (; tile0 < n_tiles; tile0 += 2 * step) {
+    const bool more = tile0 + step < n_tiles;
+    if (more) load_group(tile0 + step, kb2, sb);
+    compute_group(tile0, ka, sa);
+    if (!more) break;
+    if (tile0 + 2 * step < n_tiles) load_group(tile0 + 2 * step, ka, sa);
+    compute_group(tile0 + step, kb2, sb);
   }
   if (hist1) {
     __syncthreads();
@@ -226,181 +266,280 @@ __global__ void __launch_bounds__(256) dsa_hist2_kernel(const float* __restrict_
   }
 }
 
-// Exact canonical score of token t for one row; lanes are heads (lane < H).
-// qw: this lane's 128 q code bytes; returns the score in every lane.
-__device__ __forceinline__ float exact_score(const uint32_t (&qw)[32], const uint8_t* __restrict__ krow, float qs_h,
-                                             float w_h, float ks_t, int H) {
-  const u32x4_t* kp = reinterpret_cast<const u32x4_t*>(krow);
-  double acc = 0.0;
-#pragma unroll 1
-  for (int v = 0; v < 8; ++v) {
-    const u32x4_t kw = kp[v];
+typedef __attribute__((ext_vector_type(4))) int i32x4_v;
+
+// 16 e4m3 codes -> three int8 limb vectors: 512 v = L2 2^14 + L1 2^7 + L0
+__device__ __forceinline__ void e4m3_limbs(const u32x4_t x, i32x4_v (&o)[3]) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const f32x2_t q01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)qw[4 * v + e], false);
-      const f32x2_t q23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)qw[4 * v + e], true);
-      const f32x2_t k01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[e], false);
-      const f32x2_t k23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[e], true);
-      acc = fma((double)q01[0], (double)k01[0], acc);
-      acc = fma((double)q01[1], (double)k01[1], acc);
-      acc = fma((double)q23[0], (double)k23[0], acc);
-      acc = fma((double)q23[1], (double)k23[1], acc);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[i], false);
+    const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[i], true);
+    const int v0 = (int)(a[0] * 512.f), v1 = (int)(a[1] * 512.f);
+    const int v2 = (int)(c[0] * 512.f), v3 = (int)(c[1] * 512.f);
+    o[0][i] = (v0 & 127) | ((v1 & 127) << 8) | ((v2 & 127) << 16) | ((v3 & 127) << 24);
+    o[1][i] = ((v0 >> 7) & 127) | (((v1 >> 7) & 127) << 8) | (((v2 >> 7) & 127) << 16) | (((v3 >> 7) & 127) << 24);
+    o[2][i] = ((v0 >> 14) & 255) | (((v1 >> 14) & 255) << 8) | (((v2 >> 14) & 255) << 16) | ((v3 >> 14) << 24);
   }
-  const float d = (float)acc;
-  const float a = (d * qs_h) * ks_t;
-  const float r = a > 0.f ? a : 0.f;
-  const float term = r * w_h;
-  float s = 0.f;
-  for (int h = 0; h < H; ++h) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term), h));
-  return s;
 }
 
-// Stage 2b: exact scores.  With `hi` set, only tokens whose upper bound reaches
-// tau are scored and appended as 64-bit keys (score key << 32 | ~index) to the
-// row's candidate list; without it every token's score goes to `scores`.
+__device__ __forceinline__ i32x4_v mfma_i8(const i32x4_v a, const i32x4_v b, const i32x4_v c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Stage 2b: exact scores.  A workgroup owns `range` consecutive tokens of one
+// row.  With `hi` set it keeps the tokens whose upper bound reaches tau (LDS
+// list), scores them 16 at a time on the MFMA (lanes = 16 candidates x 4 head
+// groups) and appends 64-bit keys (score key << 32 | ~index) to the row's list;
+// without `hi` it scores every token into `scores`.
+constexpr int kRsMaxRange = 4096;
 __global__ void __launch_bounds__(256) dsa_rescore_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ qs, const uint8_t* __restrict__ k,
     const float* __restrict__ ks, const float* __restrict__ w, const int32_t* __restrict__ lengths,
     const float* __restrict__ hi, const uint32_t* __restrict__ hist1, const uint32_t* __restrict__ hist2,
     uint64_t* __restrict__ keys, uint32_t* __restrict__ counts, float* __restrict__ scores, int64_t L, int H,
-    int topk) {
+    int topk, int range) {
   __shared__ uint32_t lh[kHistBins];
+  __shared__ uint32_t lh2[kHistBins];
   __shared__ uint32_t sh[2];
+  __shared__ int cand[kRsMaxRange];
+  __shared__ uint32_t ncand;
+  __shared__ float terms[4][16][65];
   const int b = blockIdx.y;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c = lane & 15, qd = lane >> 4;
   const int64_t n = row_length(lengths, b, L);
+  const int64_t t_begin = (int64_t)blockIdx.x * range;
+  if (t_begin >= n) return;
+  const int64_t t_end = min(n, t_begin + range);
   uint32_t tau = 0u;
   if (hi && n > topk) {
-    for (int i = threadIdx.x; i < kHistBins; i += 256) lh[i] = hist1[(int64_t)b * kHistBins + i];
+    for (int i = tid; i < kHistBins; i += 256) {
+      lh[i] = hist1[(int64_t)b * kHistBins + i];
+      lh2[i] = hist2[(int64_t)b * kHistBins + i];
+    }
     __syncthreads();
     uint32_t d1, above1, d2, above2;
     find_digit<256>(lh, (uint32_t)topk, sh, d1, above1);
-    for (int i = threadIdx.x; i < kHistBins; i += 256) lh[i] = hist2[(int64_t)b * kHistBins + i];
-    __syncthreads();
-    find_digit<256>(lh, (uint32_t)topk - above1, sh, d2, above2);
+    find_digit<256>(lh2, (uint32_t)topk - above1, sh, d2, above2);
     tau = (d1 << 21) | (d2 << 10);
   }
-  const int hl = lane < H ? lane : 0;
-  uint32_t qw[32];
-  const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((int64_t)b * H + hl) * kIdxD);
-#pragma unroll
-  for (int v = 0; v < 8; ++v) {
-    const u32x4_t x = qrow[v];
-    qw[4 * v] = x[0];
-    qw[4 * v + 1] = x[1];
-    qw[4 * v + 2] = x[2];
-    qw[4 * v + 3] = x[3];
+  if (tid == 0) ncand = 0u;
+  __syncthreads();
+  for (int64_t c0 = t_begin + 64 * wv; c0 < t_end; c0 += 256) {
+    const int64_t t = c0 + lane;
+    bool ok = t < t_end;
+    if (hi && ok) ok = key_high_nan(hi[(int64_t)b * L + t]) >= tau;
+    const uint64_t mask = __ballot(ok);
+    const int nc = __builtin_popcountll(mask);
+    if (nc == 0) continue;
+    uint32_t base = 0u;
+    if (lane == 0) base = atomicAdd(&ncand, (uint32_t)nc);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+    if (ok) cand[base + pos] = (int)t;
   }
-  const float qs_h = qs[(int64_t)b * H + hl];
-  const float w_h = lane < H ? w[(int64_t)b * H + hl] : 0.f;
+  __syncthreads();
+  const int C = (int)ncand;
+  const int HT = H / 16;
+  // A operands (rows = heads 16 j + c) as int8 limbs of dims 64 ch + 16 qd ..+16;
+  // per-lane constants of the D layout (heads 16 j + 4 qd + r)
+  i32x4_v ql[4][2][3];
+  float qsv[4][4], wvv[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int hr = j < HT ? 16 * j + c : 0;
+    const uint8_t* qrow = q + ((int64_t)b * H + hr) * kIdxD + 16 * qd;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) e4m3_limbs(*reinterpret_cast<const u32x4_t*>(qrow + 64 * ch), ql[j][ch]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hd = j < HT ? 16 * j + 4 * qd + r : 0;
+      qsv[j][r] = qs[(int64_t)b * H + hd];
+      wvv[j][r] = w[(int64_t)b * H + hd];
+    }
+  }
   const uint8_t* kb = k + (int64_t)b * L * kIdxD;
   const float* ksb = ks + (int64_t)b * L;
-  const int64_t wave_id = (int64_t)blockIdx.x * 4 + wv, n_waves = (int64_t)gridDim.x * 4;
-  for (int64_t c0 = wave_id * 64; c0 < n; c0 += n_waves * 64) {
-    const int64_t t = c0 + lane;
-    bool cand = t < n;
-    if (hi && cand) cand = key_high_nan(hi[(int64_t)b * L + t]) >= tau;
-    uint64_t mask = __ballot(cand);
-    while (mask) {
-      const int bit = __builtin_ctzll(mask);
-      mask &= mask - 1;
-      const int64_t tc = c0 + bit;
-      const float s = exact_score(qw, kb + tc * kIdxD, qs_h, w_h, ksb[tc], H);
-      if (lane == 0) {
-        if (hi) {
-          const uint32_t pos = atomicAdd(&counts[b], 1u);
-          keys[(int64_t)b * L + pos] = ((uint64_t)key_low_nan(s) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)tc);
-        } else {
-          scores[(int64_t)b * L + tc] = s;
-        }
+  struct Batch {
+    u32x4_t x[2];
+    float ks;
+    int t;
+  };
+  auto load_batch = [&](int bt, Batch& o) {
+    const int i = bt * 16 + c;
+    const bool ok = i < C;
+    o.t = ok ? cand[i] : -1;
+    o.ks = ok ? ksb[o.t] : 0.f;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+      o.x[ch] = ok ? *reinterpret_cast<const u32x4_t*>(kb + (int64_t)o.t * kIdxD + 64 * ch + 16 * qd)
+                   : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  auto score_batch = [&](int bt, const Batch& in) {
+    i32x4_v kl[2][3];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) e4m3_limbs(in.x[ch], kl[ch]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j >= HT) break;
+      i32x4_v g[5];
+#pragma unroll
+      for (int m = 0; m < 5; ++m) g[m] = i32x4_v{0, 0, 0, 0};
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int la = 0; la < 3; ++la)
+#pragma unroll
+          for (int lb = 0; lb < 3; ++lb) g[la + lb] = mfma_i8(ql[j][ch][la], kl[ch][lb], g[la + lb]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        double x = (double)g[4][r];
+        x = fma(x, 128.0, (double)g[3][r]);
+        x = fma(x, 128.0, (double)g[2][r]);
+        x = fma(x, 128.0, (double)g[1][r]);
+        x = fma(x, 128.0, (double)g[0][r]);
+        const float d = (float)(x * 0x1p-18);
+        const float a = (d * qsv[j][r]) * in.ks;
+        const float rr = a > 0.f ? a : 0.f;
+        terms[wv][c][16 * j + 4 * qd + r] = rr * wvv[j][r];
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const int nvalid = min(16, C - bt * 16);
+    uint32_t base = 0u;
+    if (hi && lane == 0) base = atomicAdd(&counts[b], (uint32_t)nvalid);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+    if (qd == 0 && in.t >= 0) {
+      float sc = 0.f;
+      for (int h = 0; h < H; ++h) sc = sc + terms[wv][c][h];
+      if (hi)
+        keys[(int64_t)b * L + base + c] =
+            ((uint64_t)key_low_nan(sc) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)in.t);
+      else
+        scores[(int64_t)b * L + in.t] = sc;
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+  // ping-pong over this wave's batches (bt = wv, wv + 4, ...)
+  Batch ba, bb;
+  int bt = wv;
+  if (bt * 16 < C) load_batch(bt, ba);
+  for (; bt * 16 < C; bt += 8) {
+    const bool more = (bt + 4) * 16 < C;
+    if (more) load_batch(bt + 4, bb);
+    score_batch(bt, ba);
+    if (!more) break;
+    if ((bt + 8) * 16 < C) load_batch(bt + 8, ba);
+    score_batch(bt + 4, bb);
   }
 }
 
-// Stage 3: sort the candidates of one row by key (descending) and write the
-// top-k indices (+offset), -1 past the row's valid count.
-__global__ void __launch_bounds__(1024) dsa_topk_sort_kernel(const uint64_t* __restrict__ keys,
-                                                             const uint32_t* __restrict__ counts,
-                                                             const int32_t* __restrict__ lengths, int64_t L, int topk,
-                                                             int offset, int32_t* __restrict__ idx_out) {
+// Stage 3a: radix-select the kk best keys of one row (keys are unique) and
+// store them, unordered, in sel[b][0..kk).
+__global__ void __launch_bounds__(1024) dsa_select_kernel(const uint64_t* __restrict__ keys,
+                                                          const uint32_t* __restrict__ counts,
+                                                          const int32_t* __restrict__ lengths, int64_t L, int topk,
+                                                          uint64_t* __restrict__ sel) {
   __shared__ uint64_t sk[kSortCap];
   __shared__ uint32_t lh[256];
   __shared__ uint32_t sh[4];
-  const int b = blockIdx.x, tid = threadIdx.x;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const int64_t n = row_length(lengths, b, L);
   const int64_t cnt = min((int64_t)counts[b], n);
   const int kk = (int)min((int64_t)topk, cnt);
   const uint64_t* kb = keys + (int64_t)b * L;
-  int m;  // number of keys placed in sk
-  if (cnt <= kSortCap) {
-    m = (int)cnt;
-    for (int i = tid; i < kSortCap; i += 1024) sk[i] = i < m ? kb[i] : 0ull;
-  } else {
-    // radix select of the kk-th largest 64-bit key (keys are unique), 8 bits a pass
-    uint64_t prefix = 0, pmask = 0;
-    uint32_t rem = (uint32_t)kk;
-    for (int shift = 56; shift >= 0; shift -= 8) {
-      if (tid < 256) lh[tid] = 0u;
-      __syncthreads();
-      for (int64_t i = tid; i < cnt; i += 1024) {
-        const uint64_t key = kb[i];
-        if ((key & pmask) == prefix) atomicAdd(&lh[(key >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t acc = 0;
-        for (int d = 255; d >= 0; --d) {
-          if (acc + lh[d] >= rem) {
-            sh[0] = (uint32_t)d;
-            sh[1] = acc;
-            break;
-          }
-          acc += lh[d];
-        }
-      }
-      __syncthreads();
-      prefix |= (uint64_t)sh[0] << shift;
-      pmask |= 255ull << shift;
-      rem -= sh[1];
-      __syncthreads();
-    }
-    if (tid == 0) sh[2] = 0u;
-    for (int i = tid; i < kSortCap; i += 1024) sk[i] = 0ull;
+  uint64_t* out = sel + (int64_t)b * kSortCap;
+  if (cnt <= kk) {
+    for (int i = tid; i < cnt; i += 1024) out[i] = kb[i];
+    return;
+  }
+  const bool in_lds = cnt <= kSortCap;
+  if (in_lds)
+    for (int i = tid; i < cnt; i += 1024) sk[i] = kb[i];
+  uint64_t prefix = 0, pmask = 0;
+  uint32_t rem = (uint32_t)kk;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    if (tid < 256) lh[tid] = 0u;
     __syncthreads();
     for (int64_t i = tid; i < cnt; i += 1024) {
-      const uint64_t key = kb[i];
-      if (key >= prefix) {
-        const uint32_t pos = atomicAdd(&sh[2], 1u);
-        if (pos < (uint32_t)kSortCap) sk[pos] = key;
+      const uint64_t key = in_lds ? sk[i] : kb[i];
+      if ((key & pmask) == prefix) atomicAdd(&lh[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {  // one wave finds the digit: 4 bins per lane, scanned from the top
+      uint32_t cnt4[4], local = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cnt4[i] = lh[255 - (4 * lane + i)];
+        local += cnt4[i];
+      }
+      uint32_t acc = wave_incl_scan_u32(local) - local;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (acc < rem && rem <= acc + cnt4[i]) {
+          sh[0] = 255u - (uint32_t)(4 * lane + i);
+          sh[1] = acc;
+        }
+        acc += cnt4[i];
       }
     }
     __syncthreads();
-    m = (int)min(sh[2], (uint32_t)kSortCap);
+    prefix |= (uint64_t)sh[0] << shift;
+    pmask |= 255ull << shift;
+    rem -= sh[1];
+    const bool whole = lh[sh[0]] == rem;  // every key with this prefix is selected
+    __syncthreads();
+    if (whole) break;
   }
+  if (tid == 0) sh[2] = 0u;
   __syncthreads();
-  int P = 64;
-  while (P < m) P <<= 1;
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < P / 2; i += 1024) {
-        const int a = 2 * i - (i & (stride - 1));
-        const int c2 = a + stride;
-        const bool desc = (a & size) == 0;
-        const uint64_t x = sk[a], y = sk[c2];
-        if ((x < y) == desc) {
-          sk[a] = y;
-          sk[c2] = x;
-        }
-      }
-      __syncthreads();
+  for (int64_t i = tid; i < cnt; i += 1024) {
+    const uint64_t key = in_lds ? sk[i] : kb[i];
+    if (key >= prefix) {
+      const uint32_t pos = atomicAdd(&sh[2], 1u);
+      if (pos < (uint32_t)kk) out[pos] = key;
     }
   }
-  for (int j = tid; j < topk; j += 1024) {
-    int32_t v = -1;
-    if (j < kk && j < m) v = (int32_t)(0xFFFFFFFFu - (uint32_t)sk[j]) + offset;
-    idx_out[(int64_t)b * topk + j] = v;
+}
+
+// Stage 3b: rank of each selected key among the row's kk selected keys (the
+// number of larger keys) -> output slot.  A workgroup takes 64 slots; its four
+// waves count against four quarters of the keys.
+__global__ void __launch_bounds__(256) dsa_rank_kernel(const uint64_t* __restrict__ sel,
+                                                       const uint32_t* __restrict__ counts,
+                                                       const int32_t* __restrict__ lengths, int64_t L, int topk,
+                                                       int offset, int32_t* __restrict__ idx_out) {
+  __shared__ uint64_t sk[kSortCap];
+  __shared__ uint32_t part[4][64];
+  const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t n = row_length(lengths, b, L);
+  const int kk = (int)min((int64_t)topk, min((int64_t)counts[b], n));
+  const int e0 = blockIdx.x * 64;
+  int32_t* dst = idx_out + (int64_t)b * topk;
+  if (tid < 64 && e0 + tid < topk && e0 + tid >= kk) dst[e0 + tid] = -1;
+  if (e0 >= kk) return;
+  const uint64_t* sb = sel + (int64_t)b * kSortCap;
+  for (int i = tid; i < kk; i += 256) sk[i] = sb[i];
+  __syncthreads();
+  const int e = e0 + lane;
+  const uint64_t mine = e < kk ? sk[e] : ~0ull;
+  const int f0 = (int)((int64_t)kk * wv / 4), f1 = (int)((int64_t)kk * (wv + 1) / 4);
+  uint32_t r = 0;
+  int f = f0;
+  for (; f + 8 <= f1; f += 8) {  // eight keys per step, four independent LDS reads
+    uint64_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = sk[f + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r += v[i] > mine ? 1u : 0u;
+  }
+  for (; f < f1; ++f) r += sk[f] > mine ? 1u : 0u;
+  part[wv][lane] = r;
+  __syncthreads();
+  if (wv == 0 && e < kk) {
+    const uint32_t rank = part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
+    dst[rank] = (int32_t)(0xFFFFFFFFu - (uint32_t)mine) + offset;
   }
 }
 
@@ -438,7 +577,7 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   constexpr int KS = DQK + 8;  // bf16 per K row in LDS: 16-byte reads of 16 rows hit distinct banks
   __shared__ __attribute__((aligned(16))) uint16_t Kt[kMlaBT * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[kMlaDl * kVtStride];
-  __shared__ int tok_ok[kMlaBT];
+  __shared__ int tok_id[kMlaBT];
   const int H = NW * 16 * gridDim.z;
   const int split = blockIdx.x, b = blockIdx.y, S = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -462,13 +601,17 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   const int t_end = min(topk, t_begin + chunk);
   for (int t0 = t_begin; t0 < t_end; t0 += kMlaBT) {
     __syncthreads();
+    if (tid < kMlaBT) {
+      const int ti = t0 + tid;
+      const int id = ti < t_end ? idx[(int64_t)b * topk + ti] : -1;
+      tok_id[tid] = (id >= 0 && (int64_t)id < n) ? id : -1;
+    }
+    __syncthreads();
     // gather: (token, 64-wide latent segment) items -> bf16 rows of Kt and columns of Vt
     for (int item = tid; item < kMlaBT * 8; item += NW * 64) {
       const int tk = item >> 3, seg = item & 7;
-      const int ti = t0 + tk;
-      const int id = ti < t_end ? idx[(int64_t)b * topk + ti] : -1;
-      const bool ok = id >= 0 && (int64_t)id < n;
-      if (seg == 0) tok_ok[tk] = ok ? 1 : 0;
+      const int id = tok_id[tk];
+      const bool ok = id >= 0;
       uint32_t outw[32];
       if (ok) {
         const int64_t row = kvb * n + id;
@@ -514,9 +657,8 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     if constexpr (DR > 0) {
       for (int item = tid; item < kMlaBT * (DR / 8); item += NW * 64) {
         const int tk = item / (DR / 8), pc = item % (DR / 8);
-        const int ti = t0 + tk;
-        const int id = ti < t_end ? idx[(int64_t)b * topk + ti] : -1;
-        const bool ok = id >= 0 && (int64_t)id < n;
+        const int id = tok_id[tk];
+        const bool ok = id >= 0;
         u32x4_t v = {0u, 0u, 0u, 0u};
         if (ok) {
           const int64_t row = kvb * n + id;
@@ -530,19 +672,19 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     // S^T tiles (rows = tokens 16 j + 4 qd + r, column = head c)
     f32x4_t st[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      st[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = Kt + (16 * j + c) * KS + 8 * qd;
+    for (int j = 0; j < 4; ++j) st[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < DQK / 32; ++s) st[j] = mfma_bf16(*reinterpret_cast<const bf16x8_t*>(krow + 32 * s), qb[s], st[j]);
-    }
+    for (int s = 0; s < DQK / 32; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        st[j] = mfma_bf16(*reinterpret_cast<const bf16x8_t*>(Kt + (16 * j + c) * KS + 8 * qd + 32 * s), qb[s], st[j]);
     float sc[4][4];
     float bm = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[j][r] = tok_ok[16 * j + 4 * qd + r] ? st[j][r] * scale : -INFINITY;
+        sc[j][r] = tok_id[16 * j + 4 * qd + r] >= 0 ? st[j][r] * scale : -INFINITY;
         bm = fmaxf(bm, sc[j][r]);
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
@@ -603,40 +745,46 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   }
 }
 
-// Merge the splits of one (row, head) with the sink term and normalize.
+// Merge the splits of one (row, head) with the sink term and normalize: one
+// wave turns the split maxima/sums into weights, then each thread blends
+// four consecutive output columns over the splits.
 __global__ void __launch_bounds__(128) mla_combine_kernel(const float* __restrict__ part_o,
                                                           const float* __restrict__ part_ml,
                                                           const float* __restrict__ sink, uint16_t* __restrict__ out,
                                                           int H, int S) {
+  __shared__ float wgt[64];
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, part_ml[(((int64_t)b * S + s) * H + h) * 2]);
-  uint16_t* dst = out + ((int64_t)b * H + h) * kMlaDl;
-  if (M == -INFINITY) {
-    for (int d = tid; d < kMlaDl; d += 128) dst[d] = 0;
-    return;
+  if (tid < 64) {
+    const bool ok = tid < S;
+    const float m = ok ? part_ml[(((int64_t)b * S + tid) * H + h) * 2] : -INFINITY;
+    const float l = ok ? part_ml[(((int64_t)b * S + tid) * H + h) * 2 + 1] : 0.f;
+    float M = m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const float e = (m == -INFINITY) ? 0.f : __expf(m - M);
+    const float lsum = wave_sum_f32(l * e) + ((sink && M != -INFINITY) ? __expf(sink[h] - M) : 0.f);
+    wgt[tid] = (M == -INFINITY) ? 0.f : e / lsum;
   }
-  float lsum = sink ? __expf(sink[h] - M) : 0.f;
+  __syncthreads();
+  const int d = 4 * tid;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const float* po = part_o + ((int64_t)b * S * H + h) * kMlaDl + d;
+#pragma unroll 8
   for (int s = 0; s < S; ++s) {
-    const float* ml = part_ml + (((int64_t)b * S + s) * H + h) * 2;
-    if (ml[0] != -INFINITY) lsum += ml[1] * __expf(ml[0] - M);
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(po + (int64_t)s * H * kMlaDl);
+    acc += wgt[s] * v;
   }
-  const float inv = 1.0f / lsum;
-  for (int d = tid; d < kMlaDl; d += 128) {
-    float acc = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float ms = part_ml[(((int64_t)b * S + s) * H + h) * 2];
-      if (ms != -INFINITY) acc += part_o[(((int64_t)b * S + s) * H + h) * kMlaDl + d] * __expf(ms - M);
-    }
-    dst[d] = f32_bf16(acc * inv);
-  }
+  uint16_t* dst = out + ((int64_t)b * H + h) * kMlaDl + d;
+  const uint32_t w0 = (uint32_t)f32_bf16(acc[0]) | ((uint32_t)f32_bf16(acc[1]) << 16);
+  const uint32_t w1 = (uint32_t)f32_bf16(acc[2]) | ((uint32_t)f32_bf16(acc[3]) << 16);
+  *reinterpret_cast<uint2*>(dst) = uint2{w0, w1};
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct IndexerWs {
   float *lo, *hi;
-  uint64_t* keys;
+  uint64_t *keys, *sel;
   uint32_t *hist1, *hist2, *counts;
   size_t zero_words;  // hist1 .. counts, contiguous
 };
@@ -651,12 +799,14 @@ static size_t indexer_ws(int64_t b, int64_t l, char* base, IndexerWs* w) {
   float* lo = (float*)take((size_t)b * l * 4);
   float* hi = (float*)take((size_t)b * l * 4);
   uint64_t* keys = (uint64_t*)take((size_t)b * l * 8);
+  uint64_t* sel = (uint64_t*)take((size_t)b * kSortCap * 8);
   const size_t zbytes = (size_t)b * kHistBins * 4 * 2 + (size_t)b * 4;
   uint32_t* z = (uint32_t*)take(zbytes);
   if (w) {
     w->lo = lo;
     w->hi = hi;
     w->keys = keys;
+    w->sel = sel;
     w->hist1 = z;
     w->hist2 = z ? z + (size_t)b * kHistBins : nullptr;
     w->counts = z ? z + (size_t)b * kHistBins * 2 : nullptr;
@@ -702,10 +852,13 @@ static void dispatch_bound(const uint8_t* q, const float* qs, const uint8_t* k, 
   }
 }
 
-static int rescore_grid(int64_t b, int64_t l) {
-  int64_t gx = (1024 + b - 1) / b;
-  gx = std::min<int64_t>(gx, (l + 255) / 256);
-  return (int)std::max<int64_t>(gx, 1);
+// tokens per rescoring workgroup: about 512 workgroups over the batch, a
+// multiple of 64, at most the LDS candidate list
+static int rescore_range(int64_t b, int64_t l) {
+  const int64_t target = std::max<int64_t>(1, 512 / std::max<int64_t>(b, 1));
+  int64_t r = (l + target - 1) / target;
+  r = (r + 63) / 64 * 64;
+  return (int)std::min<int64_t>(std::max<int64_t>(r, 64), kRsMaxRange);
 }
 
 struct MlaWs {
@@ -762,12 +915,15 @@ extern "C" int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const
     const int g2 = std::max(1, std::min<int>((int)((l + 255) / 256), (int)((1024 + b - 1) / b)));
     hipLaunchKernelGGL(dsa_hist2_kernel, dim3((unsigned)g2, (unsigned)b), dim3(256), 0, st, ws.lo, lengths, ws.hist1,
                        ws.hist2, l, (int)topk);
-    hipLaunchKernelGGL(dsa_rescore_kernel, dim3((unsigned)rescore_grid(b, l), (unsigned)b), dim3(256), 0, st, q, q_s,
-                       k, k_s, w, lengths, ws.hi, ws.hist1, ws.hist2, ws.keys, ws.counts, (float*)nullptr, l, (int)h,
-                       (int)topk);
+    const int range = rescore_range(b, l);
+    hipLaunchKernelGGL(dsa_rescore_kernel, dim3((unsigned)((l + range - 1) / range), (unsigned)b), dim3(256), 0, st, q,
+                       q_s, k, k_s, w, lengths, ws.hi, ws.hist1, ws.hist2, ws.keys, ws.counts, (float*)nullptr, l,
+                       (int)h, (int)topk, range);
   }
-  hipLaunchKernelGGL(dsa_topk_sort_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.counts, lengths, l,
-                     (int)topk, (int)offset, idx_out);
+  hipLaunchKernelGGL(dsa_select_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.counts, lengths, l, (int)topk,
+                     ws.sel);
+  hipLaunchKernelGGL(dsa_rank_kernel, dim3((unsigned)((topk + 63) / 64), (unsigned)b), dim3(256), 0, st, ws.sel,
+                     ws.counts, lengths, l, (int)topk, (int)offset, idx_out);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_topk");
 }
 
@@ -778,10 +934,11 @@ extern "C" int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, con
   if (rc) return rc;
   MOSAIC_CHECK_ARG(scores, "dsa_indexer_scores: null output");
   if (b == 0 || l == 0) return kOk;
-  hipLaunchKernelGGL(dsa_rescore_kernel, dim3((unsigned)rescore_grid(b, l), (unsigned)b), dim3(256), 0,
+  const int range = rescore_range(b, l);
+  hipLaunchKernelGGL(dsa_rescore_kernel, dim3((unsigned)((l + range - 1) / range), (unsigned)b), dim3(256), 0,
                      (hipStream_t)stream, q, q_s, k, k_s, w, (const int32_t*)nullptr, (const float*)nullptr,
                      (const uint32_t*)nullptr, (const uint32_t*)nullptr, (uint64_t*)nullptr, (uint32_t*)nullptr,
-                     scores, l, (int)h, 0);
+                     scores, l, (int)h, 0, range);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_scores");
 }
 

@@ -42,6 +42,31 @@ def test_indexer_scores_bit_exact(dev, h):
     np.testing.assert_array_equal(got.view(np.uint32), D.indexer_scores(q, qs, k, ks, w).view(np.uint32))
 
 
+def _finite_codes(rng, shape):
+    c = rng.integers(0, 256, size=shape, dtype=np.uint8)
+    return np.where((c & 0x7F) == 0x7F, c ^ 0x01, c).astype(np.uint8)
+
+
+def test_indexer_scores_bit_exact_full_exponent_range(dev):
+    """Uniformly random finite codes (subnormals to +-448 in one dot), the
+    extremes, and exact cancellation: the exact-dot stage must stay exact."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(99)
+    b, h, l = 2, 64, 2000
+    q, k = _finite_codes(rng, (b, h, 128)), _finite_codes(rng, (b, l, 128))
+    k[0, :32] = 0x7E                     # 448 everywhere
+    k[0, 32:64] = 0x01                   # 2^-9 everywhere
+    k[1, :64, :64] = k[1, :64, 64:] ^ 0x80  # halves cancel against each other
+    q[1, :, 64:] = q[1, :, :64]
+    qs = (rng.random((b, h)) + 0.5).astype(np.float32)
+    ks = (rng.random((b, l)) + 0.5).astype(np.float32)
+    w = rng.standard_normal((b, h)).astype(np.float32)
+    got = ops.dsa_indexer_scores(*_t(dev, q, qs, k, ks, w)).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), D.indexer_scores(q, qs, k, ks, w).view(np.uint32))
+    idx = ops.dsa_indexer_topk(*_t(dev, q, qs, k, ks, w), 256).cpu().numpy()
+    np.testing.assert_array_equal(idx, D.indexer_topk(q, qs, k, ks, w, 256))
+
+
 def test_indexer_bounds_enclose_exact(dev):
     """The fp8-MFMA stage's interval contains every canonical score."""
     from mosaic_amd import ops
