@@ -106,6 +106,161 @@ static void launch_fp8_skinny(const uint8_t* a, const float* as, const uint8_t* 
                      (int)k, out_f32);
 }
 
+// Tiled kernel (M >= 96, MFMA-bound at large M): a workgroup of BM/32 waves
+// owns a BM x 128 block of C (its 128 columns share one b_s row); each wave
+// owns a 64x64 quarter (4x4 MFMA tiles).  The A and B tiles of each 128-K
+// block go global -> LDS directly (global_load_lds_dwordx4, 16 bytes a lane
+// into 1 KB runs) through a ring of three stages, so two blocks are in flight
+// while one is consumed; a_s and b_s of a stage ride along through registers.
+// LDS rows are 128 bytes with their 16-byte chunks XOR-swizzled by
+// (row >> 1) & 7, so the 16 rows one MFMA operand read touches fall in
+// distinct banks.  Stage hand-off uses explicit vmcnt waits and a bare
+// s_barrier (a release fence would wait for the in-flight stages too).
+// Workgroups are remapped so that the ones on one XCD (dispatch goes
+// round-robin over 8) take neighbouring tiles, grouped 8 M-tiles deep.
+constexpr int kTileN = 128, kStages = 3;
+
+__device__ __forceinline__ void tile_coords(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int T = tiles_m * tiles_n;
+  const int full = (T / 8) * 8;
+  const int r = id < full ? (id % 8) * (T / 8) + id / 8 : id;
+  constexpr int GM = 8;
+  const int per_group = GM * tiles_n;
+  const int g = r / per_group;
+  const int first_m = g * GM;
+  const int gm = min(GM, tiles_m - first_m);
+  const int in = r % per_group;
+  tm = first_m + in % gm;
+  tn = in / gm;
+}
+
+__device__ __forceinline__ i32x8_t lds_fp8_operand(const uint8_t* tile, int row, int q) {
+  const int swz = (row >> 1) & 7;
+  const uint8_t* p = tile + row * 128;
+  const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(p + ((q ^ swz) << 4));
+  const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(p + (((q + 4) ^ swz) << 4));
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+template <int BM>
+__global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, void* __restrict__ C, int M, int N, int K, int out_f32) {
+  constexpr int NT = BM * 2;                    // threads
+  constexpr int NW = NT / 64;                   // waves
+  constexpr int STAGE = (BM + kTileN) * 128;    // bytes per stage
+  constexpr int IPW = (BM + kTileN) / 8 / NW;   // 1 KB DMA runs per wave per stage
+  static_assert((BM + kTileN) / 8 % NW == 0, "stage does not split evenly over the waves");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages][STAGE];
+  __shared__ float lsa[kStages][BM];
+  __shared__ float lsb[kStages];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  int tm, tn;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + kTileN - 1) / kTileN, tm, tn);
+  const int m0 = tm * BM, n0 = tn * kTileN;
+  const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
+  const int nkb = K / 128;
+  // this lane's source row and 16-byte chunk for each of the wave's DMA runs
+  const uint8_t* gsrc[IPW];
+  int ldsoff[IPW];
+#pragma unroll
+  for (int ii = 0; ii < IPW; ++ii) {
+    const int i = wv * IPW + ii;
+    const int row = (i < BM / 8 ? 8 * i : 8 * (i - BM / 8)) + (lane >> 3);
+    const int logical = (lane & 7) ^ ((row >> 1) & 7);
+    gsrc[ii] = i < BM / 8 ? A + (int64_t)min(m0 + row, M - 1) * K + logical * 16
+                          : B + (int64_t)min(n0 + row, N - 1) * K + logical * 16;
+    ldsoff[ii] = i * 1024;
+  }
+  // scales: threads < BM take a_s rows, thread BM takes b_s
+  const float* ssrc = tid < BM ? As + (int64_t)min(m0 + tid, M - 1) * nkb
+                               : (tid == BM ? Bs + (int64_t)(n0 / 128) * nkb : As);
+  auto issue_dma = [&](int st, int kb) {
+#pragma unroll
+    for (int ii = 0; ii < IPW; ++ii)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(gsrc[ii] + (int64_t)kb * 128),
+                                       (__attribute__((address_space(3))) void*)(&lds[st][ldsoff[ii]]), 16, 0, 0);
+  };
+  auto keep_scale = [&](int st, float v) {
+    if (tid < BM) lsa[st][tid] = v;
+    else if (tid == BM) lsb[st] = v;
+  };
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // prologue: scales of block 0 in LDS, blocks 0 and 1 in flight
+  keep_scale(0, ssrc[0]);
+  issue_dma(0, 0);
+  float sreg = 0.f;
+  if (nkb > 1) {
+    sreg = ssrc[1];
+    issue_dma(1, 1);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int st = kb % kStages;
+    // block kb landed (and the scales of kb + 1); block kb + 1 may still be in flight
+    if (kb + 1 < nkb) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPW) : "memory");
+      keep_scale((kb + 1) % kStages, sreg);
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kb + 2 < nkb) {
+      sreg = ssrc[kb + 2];
+      issue_dma((kb + 2) % kStages, kb + 2);
+    }
+    const uint8_t* ta = lds[st];
+    const uint8_t* tb = lds[st] + BM * 128;
+    const float sb = lsb[st];
+    i32x8_t bop[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) bop[nt] = lds_fp8_operand(tb, wn + 16 * nt + c, q);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const i32x8_t aop = lds_fp8_operand(ta, wm + 16 * mt + c, q);
+      f32x4_t d[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(aop, bop[nt]);
+      // a_s of this lane's accumulator rows wm + 16 mt + 4 q + r
+      const f32x4_t sa4 = *reinterpret_cast<const f32x4_t*>(&lsa[st][wm + 16 * mt + 4 * q]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float s = sa4[r] * sb;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt][r] = __builtin_fmaf(d[nt][r], s, acc[mt][nt][r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int n = n0 + wn + 16 * nt + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm + 16 * mt + 4 * q + r;
+        if (m < M && n < N) {
+          if (out_f32)
+            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[mt][nt][r];
+          else
+            reinterpret_cast<uint16_t*>(C)[(int64_t)m * N + n] = f32_bf16(acc[mt][nt][r]);
+        }
+      }
+    }
+}
+
+template <int BM>
+static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c,
+                             int64_t m, int64_t n, int64_t k, int out_f32, hipStream_t st) {
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + kTileN - 1) / kTileN);
+  hipLaunchKernelGGL((fp8_gemm_tiled_kernel<BM>), dim3((unsigned)tiles), dim3(BM * 2), 0, st, a, as, b, bs, c, (int)m,
+                     (int)n, (int)k, out_f32);
+}
+
 // w [N, K] e4m3 with one fp32 scale per (bn x bk) block -> bf16 [N, K]
 __global__ void __launch_bounds__(256) fp8_block_dequant_kernel(const uint8_t* __restrict__ w,
                                                                 const float* __restrict__ s,
@@ -154,6 +309,14 @@ extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const u
   hipStream_t st = (hipStream_t)stream;
   const int f32 = out_dtype == MOSAIC_DTYPE_F32;
   const int64_t mt = (m + 15) / 16;
+  if (m >= 256) {
+    launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st);
+    MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
+  }
+  if (m >= 96) {
+    launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st);
+    MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
+  }
   // columns per wave chosen so the grid covers the chip (>= ~2048 waves)
   if (((n + 63) / 64) * mt * 8 >= 4096)
     launch_fp8_skinny<4, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
