@@ -131,17 +131,21 @@ int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, int64_t top
 /* Stable expert sort + uncapped tile list for ids [m, top_k] (+ one shared
  * expert row per token when has_shared, virtual expert id e).
  * Replaces layout_assignments (kernels/moe_layout.py:8-27) and emit_tiles
- * (kernels/w4a16_grouped.py:151-169).  Assignment count m*top_k(+m) <= 4096.
+ * (kernels/w4a16_grouped.py:151-169).  Above 4096 assignments a multi-workgroup path runs
+ * with workspace of mosaic_moe_layout_workspace_bytes() bytes (NULL/0 below).
  * Outputs: counts [e(+1)], offsets [e(+1)+1], perm / perm_token / perm_weight /
  * sorted_ids [A] (by sorted position), inv_pos [A] (by flat assignment),
  * combine_pos [m, top_k(+1)] (each token's sorted positions in ascending
  * expert id, shared last), tile_expert / tile_start / tile_rows / tile_p0
  * [tile_cap], n_tiles [1]. */
+/* Scratch bytes mosaic_moe_layout needs (0 up to 4096 assignments). */
+size_t mosaic_moe_layout_workspace_bytes(int64_t m, int64_t top_k, int64_t e, int has_shared);
+
 int mosaic_moe_layout(const int32_t* ids, const float* weights, int64_t m, int64_t top_k, int64_t e, int has_shared,
                       int block_m, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* perm_token,
                       float* perm_weight, int32_t* sorted_ids, int32_t* inv_pos, int32_t* combine_pos,
                       int32_t* tile_expert, int32_t* tile_start, int32_t* tile_rows, int32_t* tile_p0,
-                      int32_t* n_tiles, int64_t tile_cap, void* stream);
+                      int32_t* n_tiles, int64_t tile_cap, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Tile list from per-expert counts [e] int32: one (expert, m_start, rows)
  * entry per block_m rows, ascending expert order, no per-expert cap.

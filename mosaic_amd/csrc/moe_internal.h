@@ -23,7 +23,16 @@ struct LayoutOut {
   int n_counters;
   int small_ok;          // the caller does not read counts/offsets: A_ext <= 64 may take the
                          // single-wave path, which leaves them unwritten
+  int32_t* chunk_counts; // [layout_chunks(A_ext)][E_ext] scratch of the multi-workgroup path
+  int32_t* chunk_base;   // [layout_chunks(A_ext)][E_ext]
 };
+
+constexpr int kLayoutChunk = 1024;  // assignments per workgroup of the multi-workgroup layout
+inline int64_t layout_chunks(int64_t a_ext) { return (a_ext + kLayoutChunk - 1) / kLayoutChunk; }
+// scratch bytes of the multi-workgroup layout (0 when the single-workgroup path applies)
+inline size_t layout_scratch_bytes(int64_t a_ext, int64_t e_ext) {
+  return a_ext > 4096 ? (size_t)layout_chunks(a_ext) * (size_t)e_ext * 4 * 2 : 0;
+}
 
 // Enqueue routing (when logits != nullptr) + stable layout + tile list.
 int launch_route_layout(const float* logits, const float* bias, const int32_t* ids_in, const float* weights_in,
@@ -48,6 +57,7 @@ struct MoeWorkspace {
   float* xs;       // A8 only: [M, H/128] scales
   uint8_t* zq;     // A8 only: [A, I] e4m3 z
   float* zs;       // A8 only: [A, I/128] scales
+  int32_t *chunk_counts, *chunk_base;
   int64_t tile_cap;
   size_t bytes;
 };
@@ -81,6 +91,9 @@ inline MoeWorkspace carve_moe_workspace(char* base, int64_t M, int64_t H, int64_
   w.tile_rows = (int32_t*)take(4 * w.tile_cap);
   w.tile_p0 = (int32_t*)take(4 * w.tile_cap);
   w.n_tiles = (int32_t*)take(4);
+  const size_t lsb = layout_scratch_bytes(A, Ee);
+  w.chunk_counts = lsb ? (int32_t*)take(lsb / 2) : nullptr;
+  w.chunk_base = lsb ? (int32_t*)take(lsb / 2) : nullptr;
   w.z = (uint16_t*)take(2 * A * I);
   w.yp = (float*)take(4 * A * H);
   if (a8) {

@@ -407,6 +407,149 @@ __global__ void __launch_bounds__(1024) route_layout_small_kernel(
   if (lane == 0) out.n_tiles[0] = (int)total_tiles;
 }
 
+// ------------------------------------------------ multi-workgroup layout ----
+// For more than kRouteMaxAssign assignments: chunks of kLayoutChunk flat
+// assignments (tokens' slots in order, then the shared-expert rows) are
+// counted per expert (one workgroup per chunk), one workgroup turns the counts
+// into expert offsets, per-(chunk, expert) bases and the tile list, and a
+// second pass over the chunks places every assignment at base + its rank
+// among the same expert's assignments earlier in the chunk: the same stable
+// order as the single-workgroup kernel.
+__device__ __forceinline__ int assignment_expert(const int32_t* ids, int a, int A, int A_ext, int E) {
+  if (a >= A_ext) return -1;
+  if (a >= A) return E;
+  const int e = ids[a];
+  return (e < 0 || e >= E) ? -1 : e;
+}
+
+__global__ void __launch_bounds__(kLayoutChunk) layout_count_kernel(const int32_t* __restrict__ ids, int A, int A_ext,
+                                                                    int E, int E_ext, int32_t* chunk_counts,
+                                                                    int32_t* counters, int n_counters) {
+  __shared__ int32_t cnt[kRouteMaxExperts + 2];
+  const int tid = threadIdx.x, ch = blockIdx.x;
+  for (int e = tid; e < E_ext; e += kLayoutChunk) cnt[e] = 0;
+  if (ch == 0)
+    for (int i = tid; i < n_counters; i += kLayoutChunk) counters[i] = 0;
+  __syncthreads();
+  const int e = assignment_expert(ids, ch * kLayoutChunk + tid, A, A_ext, E);
+  if (e >= 0) atomicAdd(&cnt[e], 1);
+  __syncthreads();
+  for (int x = tid; x < E_ext; x += kLayoutChunk) chunk_counts[(int64_t)ch * E_ext + x] = cnt[x];
+}
+
+__global__ void __launch_bounds__(1024) layout_scan_kernel(const int32_t* __restrict__ chunk_counts, int n_chunks,
+                                                           int E_ext, int block_m, int tile_cap, LayoutOut out) {
+  __shared__ int32_t s_cnt[kRouteMaxExperts + 2];
+  __shared__ int32_t s_off[kRouteMaxExperts + 2];
+  __shared__ int32_t s_toff[kRouteMaxExperts + 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E_ext; e += 1024) {
+    int c = 0;
+    for (int ch = 0; ch < n_chunks; ++ch) c += chunk_counts[(int64_t)ch * E_ext + e];
+    s_cnt[e] = c;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t carry = 0, tcarry = 0;
+    for (int base = 0; base < E_ext; base += 64) {
+      const int e = base + lane;
+      const uint32_t c = (e < E_ext) ? (uint32_t)s_cnt[e] : 0u;
+      const uint32_t tc = (c + block_m - 1) / block_m;
+      const uint32_t inc = wave_incl_scan_u32(c), tinc = wave_incl_scan_u32(tc);
+      if (e < E_ext) {
+        s_off[e] = (int)(carry + inc - c);
+        s_toff[e] = (int)(tcarry + tinc - tc);
+      }
+      carry += wave_bcast_u32(inc, 63);
+      tcarry += wave_bcast_u32(tinc, 63);
+    }
+    if (lane == 0) {
+      s_off[E_ext] = (int)carry;
+      s_toff[E_ext] = (int)tcarry;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E_ext; e += 1024) {
+    int run = s_off[e];
+    for (int ch = 0; ch < n_chunks; ++ch) {
+      out.chunk_base[(int64_t)ch * E_ext + e] = run;
+      run += chunk_counts[(int64_t)ch * E_ext + e];
+    }
+    out.counts[e] = s_cnt[e];
+    out.offsets[e] = s_off[e];
+    const int nt = (s_cnt[e] + block_m - 1) / block_m;
+    for (int t = 0; t < nt; ++t) {
+      const int slot = s_toff[e] + t;
+      if (slot < tile_cap) {
+        out.tile_expert[slot] = e;
+        out.tile_start[slot] = t * block_m;
+        out.tile_rows[slot] = min(block_m, s_cnt[e] - t * block_m);
+        out.tile_p0[slot] = s_off[e] + t * block_m;
+      }
+    }
+  }
+  if (tid == 0) {
+    out.offsets[E_ext] = s_off[E_ext];
+    out.n_tiles[0] = min(s_toff[E_ext], tile_cap);
+  }
+}
+
+__global__ void __launch_bounds__(kLayoutChunk) layout_scatter_kernel(const int32_t* __restrict__ ids,
+                                                                      const float* __restrict__ weights, int A,
+                                                                      int A_ext, int E, int E_ext, int K, int W,
+                                                                      LayoutOut out) {
+  constexpr int NW = kLayoutChunk / 64;
+  __shared__ int16_t s_tab[NW][kRouteMaxExperts + 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ch = blockIdx.x;
+  for (int e2 = tid; e2 < E_ext; e2 += kLayoutChunk)
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s_tab[w][e2] = 0;
+  __syncthreads();
+  const int a = ch * kLayoutChunk + tid;
+  const int my = assignment_expert(ids, a, A, A_ext, E);
+  const bool live = my >= 0;
+  const int e = live ? my : 0;
+  int nbits = 1;
+  while ((1 << nbits) <= E_ext) ++nbits;
+  uint64_t mask = __ballot(live);
+  for (int b = 0; b < nbits; ++b) {
+    const uint64_t bb = __ballot(live && ((e >> b) & 1));
+    mask &= ((e >> b) & 1) ? bb : ~bb;
+  }
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int rank_w = __popcll(mask & lt);
+  if (live && rank_w == 0) s_tab[wave][e] = (int16_t)__popcll(mask);
+  __syncthreads();
+  if (a >= A_ext) return;
+  const int t = a < A ? a / K : a - A;
+  int rank;
+  if (a >= A) {
+    rank = K;
+  } else {
+    const int s = a - t * K;
+    int nvalid = 0, below = 0, inv_before = 0;
+    for (int s2 = 0; s2 < K; ++s2) {
+      const int o = assignment_expert(ids, t * K + s2, A, A_ext, E);
+      nvalid += (o >= 0);
+      below += (o >= 0 && my >= 0 && o < my);
+      inv_before += (o < 0 && s2 < s);
+    }
+    rank = my >= 0 ? below : nvalid + inv_before;
+  }
+  int p = -1;
+  if (live) {
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += s_tab[w][e];
+    p = out.chunk_base[(int64_t)ch * E_ext + e] + before + rank_w;
+    out.perm[p] = a;
+    out.sorted_ids[p] = e;
+    out.perm_token[p] = t;
+    out.perm_weight[p] = a < A ? weights[a] : 1.0f;
+  }
+  out.inv_pos[a] = p;
+  out.combine_pos[(int64_t)t * W + rank] = p;
+}
+
 int launch_route_layout(const float* logits, const float* bias, const int32_t* ids_in, const float* weights_in,
                         int32_t* ids_out, float* weights_out, int64_t M, int64_t E, int64_t K, int func, int renorm,
                         float route_scale, int has_shared, int block_m, int64_t tile_cap, const LayoutOut& out,
@@ -417,8 +560,7 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
   MOSAIC_CHECK_ARG(E <= kRouteMaxExperts, "moe layout: E=%lld exceeds %d", (long long)E, kRouteMaxExperts);
   MOSAIC_CHECK_ARG(K <= kRouteMaxTopK && K <= E, "moe layout: top_k=%lld (max %d, <= E)", (long long)K,
                    kRouteMaxTopK);
-  MOSAIC_CHECK_ARG(A_ext <= kRouteMaxAssign, "moe layout: %lld assignments exceed %d", (long long)A_ext,
-                   kRouteMaxAssign);
+  MOSAIC_CHECK_ARG(A_ext < (1ll << 30), "moe layout: %lld assignments", (long long)A_ext);
   MOSAIC_CHECK_ARG(block_m >= 1, "moe layout: block_m=%d", block_m);
   MOSAIC_CHECK_ARG(func >= 0 && func <= 2, "moe layout: score func %d", func);
   MOSAIC_CHECK_ARG(logits ? (ids_out && weights_out) : (ids_in && weights_in), "moe layout: missing ids/weights");
@@ -430,6 +572,28 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
     MOSAIC_RETURN_LAUNCH("moe_route_layout_small");
   }
   MOSAIC_CHECK_ARG(out.counts && out.offsets, "moe layout: counts/offsets required");
+  if (A_ext > kRouteMaxAssign) {
+    MOSAIC_CHECK_ARG(out.chunk_counts && out.chunk_base, "moe layout: %lld assignments need the layout scratch",
+                     (long long)A_ext);
+    const int E_ext = (int)E + (has_shared ? 1 : 0);
+    const int A = (int)(M * K);
+    const int nch = (int)layout_chunks(A_ext);
+    const int32_t* ids = ids_in;
+    const float* wts = weights_in;
+    if (logits) {
+      hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, logits, bias, ids_out,
+                         weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale);
+      ids = ids_out;
+      wts = weights_out;
+    }
+    hipLaunchKernelGGL(layout_count_kernel, dim3((unsigned)nch), dim3(kLayoutChunk), 0, st, ids, A, (int)A_ext,
+                       (int)E, E_ext, out.chunk_counts, out.counters, out.n_counters);
+    hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(1024), 0, st, out.chunk_counts, nch, E_ext, block_m,
+                       (int)tile_cap, out);
+    hipLaunchKernelGGL(layout_scatter_kernel, dim3((unsigned)nch), dim3(kLayoutChunk), 0, st, ids, wts, A,
+                       (int)A_ext, (int)E, E_ext, (int)K, (int)K + (has_shared ? 1 : 0), out);
+    MOSAIC_RETURN_LAUNCH("moe_route_layout_multi");
+  }
   hipLaunchKernelGGL(route_layout_kernel, dim3(1), dim3(kRouteThreads), 0, st, logits, bias, ids_in, weights_in,
                      ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
                      (int)tile_cap, out);
@@ -456,16 +620,27 @@ extern "C" int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, 
   MOSAIC_RETURN_LAUNCH("moe_route_topk");
 }
 
+extern "C" size_t mosaic_moe_layout_workspace_bytes(int64_t m, int64_t top_k, int64_t e, int has_shared) {
+  if (m < 0 || top_k < 0 || e < 0) return 0;
+  return layout_scratch_bytes(m * top_k + (has_shared ? m : 0), e + (has_shared ? 1 : 0));
+}
+
 extern "C" int mosaic_moe_layout(const int32_t* ids, const float* weights, int64_t m, int64_t top_k, int64_t e,
                                  int has_shared, int block_m, int32_t* counts, int32_t* offsets, int32_t* perm,
                                  int32_t* perm_token, float* perm_weight, int32_t* sorted_ids, int32_t* inv_pos,
                                  int32_t* combine_pos, int32_t* tile_expert, int32_t* tile_start, int32_t* tile_rows,
-                                 int32_t* tile_p0, int32_t* n_tiles, int64_t tile_cap, void* stream) {
+                                 int32_t* tile_p0, int32_t* n_tiles, int64_t tile_cap, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   MOSAIC_CHECK_ARG(ids && weights && counts && offsets && perm && perm_token && perm_weight && sorted_ids &&
                        inv_pos && combine_pos && tile_expert && tile_start && tile_rows && tile_p0 && n_tiles,
                    "moe_layout: null pointer");
+  const size_t need = mosaic_moe_layout_workspace_bytes(m, top_k, e, has_shared);
+  MOSAIC_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need), "moe_layout: workspace %zu bytes < %zu",
+                   workspace_bytes, need);
+  int32_t* cc = need ? (int32_t*)workspace : nullptr;
+  int32_t* cb = need ? cc + need / 8 : nullptr;
   LayoutOut out{counts, offsets, perm, perm_token, perm_weight, sorted_ids, inv_pos, combine_pos,
-                tile_expert, tile_start, tile_rows, tile_p0, n_tiles, nullptr, 0, 0};
+                tile_expert, tile_start, tile_rows, tile_p0, n_tiles, nullptr, 0, 0, cc, cb};
   return launch_route_layout(nullptr, nullptr, ids, weights, nullptr, nullptr, m, e, top_k, 0, 0, 1.0f, has_shared,
                              block_m, tile_cap, out, (hipStream_t)stream);
 }

@@ -307,7 +307,8 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
                    w.bytes);
   hipStream_t st = (hipStream_t)stream;
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,
-               w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0, 1};
+               w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0, 1,
+               w.chunk_counts, w.chunk_base};
   int rc = launch_route_layout(logits, route_bias, ids, weights, ids, weights, m, n_experts, top_k, score_func,
                                renorm, route_scale, has_shared, kMoeBlockM, w.tile_cap, lo, st);
   if (rc != 0) return rc;

@@ -314,11 +314,13 @@ def moe_layout(ids: torch.Tensor, weights: torch.Tensor | None, n_experts: int, 
         combine_pos=torch.empty(m, k + int(has_shared), **i32), tile_expert=torch.empty(max(cap, 1), **i32),
         tile_start=torch.empty(max(cap, 1), **i32), tile_rows=torch.empty(max(cap, 1), **i32),
         tile_p0=torch.empty(max(cap, 1), **i32), n_tiles=torch.empty(1, **i32))
+    nbytes = _lib.lib().mosaic_moe_layout_workspace_bytes(m, k, n_experts, int(has_shared))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
     _lib.call("mosaic_moe_layout", _ptr(ids32), _ptr(weights), m, k, n_experts, int(has_shared), block_m,
               _ptr(out["counts"]), _ptr(out["offsets"]), _ptr(out["perm"]), _ptr(out["perm_token"]),
               _ptr(out["perm_weight"]), _ptr(out["sorted_ids"]), _ptr(out["inv_pos"]), _ptr(out["combine_pos"]),
               _ptr(out["tile_expert"]), _ptr(out["tile_start"]), _ptr(out["tile_rows"]), _ptr(out["tile_p0"]),
-              _ptr(out["n_tiles"]), cap, _stream())
+              _ptr(out["n_tiles"]), cap, _ptr(ws), nbytes, _stream())
     out["tile_cap"] = cap
     return out
 

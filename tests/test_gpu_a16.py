@@ -156,7 +156,8 @@ def test_route_topk_vs_oracle(dev, m, e, k, func):
 
 
 @pytest.mark.parametrize("m,k,e,shared", [(1, 8, 256, True), (4, 8, 256, False), (64, 8, 256, True),
-                                          (300, 8, 16, True), (2, 1, 4, False)])
+                                          (300, 8, 16, True), (2, 1, 4, False), (4096, 8, 256, True),
+                                          (700, 8, 16, False), (5000, 1, 4, True)])
 def test_layout_vs_oracle(dev, m, k, e, shared):
     ops = _ops()
     rng = np.random.default_rng(m * 7 + e)
@@ -229,7 +230,7 @@ def _make_bank(rng, e, h, inter):
 
 @pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
     (1, 16, 256, 128, 4, True, 0.0), (3, 16, 256, 128, 4, False, 10.0), (20, 8, 384, 256, 2, True, 0.0),
-    (37, 32, 512, 128, 8, True, 10.0)])
+    (37, 32, 512, 128, 8, True, 10.0), (600, 16, 256, 128, 8, True, 0.0)])
 def test_moe_a16_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     ops = _ops()
     rng = np.random.default_rng(m + e + h)
@@ -271,7 +272,7 @@ def test_moe_a16_given_ids_weight_before_down(dev):
 
 @pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
     (1, 16, 256, 128, 4, False, 10.0), (3, 16, 256, 128, 4, True, 10.0), (20, 8, 384, 256, 2, False, 0.0),
-    (37, 32, 512, 128, 8, True, 10.0)])
+    (37, 32, 512, 128, 8, True, 10.0), (520, 8, 256, 128, 8, True, 10.0)])
 def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     """A8 layer (fused_moe_mxint contract) vs the A8 oracle of identical bytes."""
     ops = _ops()
