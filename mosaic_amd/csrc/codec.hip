@@ -180,6 +180,65 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const T* __restrict__ x,
   if (lane == 0) s_out[row * nb + kb] = s;
 }
 
+// 1x128 blocks, 16 lanes per block, 8 consecutive elements per lane (one
+// 16- or 32-byte load, one 8-byte store); same arithmetic as act_quant_kernel.
+template <typename T>
+__device__ __forceinline__ void load8_f32(const T* p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void load8_f32<uint16_t>(const uint16_t* p, float (&v)[8]) {
+  const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void load8_f32<float>(const float* p, float (&v)[8]) {
+  const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p), b = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = a[i];
+    v[4 + i] = b[i];
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__ x, uint8_t* __restrict__ q,
+                                                           float* __restrict__ s_out, int64_t n_chunks, int mode) {
+  const int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 8-element chunk
+  if (ch >= n_chunks) return;  // n_chunks is a multiple of 16: whole 16-lane groups leave together
+  float v[8];
+  load8_f32<T>(x + ch * 8, v);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  float s;
+  if (mode == 0) {
+    float a = fmaxf(amax, 1e-4f) * 0.002232142925783992f;  // fp32(1/448)
+    uint32_t ab = __float_as_uint(a);
+    int e = (int)((ab >> 23) & 0xFFu) - 127 + ((ab & 0x7FFFFFu) != 0u ? 1 : 0);
+    s = __uint_as_float((uint32_t)(e + 127) << 23);
+  } else if (mode == 1) {
+    s = fmaxf(amax, 1e-4f) * 0.002232142925783992f;
+  } else {
+    s = amax / 448.0f;
+  }
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y = v[i] / s;
+    y = fminf(fmaxf(y, -448.0f), 448.0f);
+    const uint32_t b = e4m3_rne(y);
+    if (i < 4) lo |= b << (8 * i);
+    else hi |= b << (8 * (i - 4));
+  }
+  *reinterpret_cast<uint2*>(q + ch * 8) = uint2{lo, hi};
+  if ((threadIdx.x & 15) == 0) s_out[ch / 16] = s;
+}
+
 __global__ void __launch_bounds__(256) e4m3_decode_kernel(const uint8_t* __restrict__ in, float* __restrict__ out,
                                                           int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -283,6 +342,16 @@ extern "C" int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s
   int64_t waves = m * (k / block);
   if (waves == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
+  if (block == 128 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)q & 7u) == 0) {
+    const int64_t chunks = m * k / 8;
+    const unsigned g = grid1d(chunks, 256);
+    if (x_dtype == MOSAIC_DTYPE_F32)
+      hipLaunchKernelGGL(act_quant128_kernel<float>, dim3(g), dim3(256), 0, st, (const float*)x, q, s, chunks, mode);
+    else
+      hipLaunchKernelGGL(act_quant128_kernel<uint16_t>, dim3(g), dim3(256), 0, st, (const uint16_t*)x, q, s, chunks,
+                         mode);
+    MOSAIC_RETURN_LAUNCH("act_quant");
+  }
   unsigned grid = grid1d(waves * 64, 256);
   if (x_dtype == MOSAIC_DTYPE_F32)
     hipLaunchKernelGGL(act_quant_kernel<float>, dim3(grid), dim3(256), 0, st, (const float*)x, q, s, m, k, block,

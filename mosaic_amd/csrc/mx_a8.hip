@@ -13,6 +13,8 @@
 //      (the 4-bit operand order: one 16-byte load, low nibble first).
 // The activation scale is constant over a super-step, so which lane supplies
 // it for which 32-K block does not matter.
+#include <algorithm>
+
 #include "common.h"
 #include "moe_internal.h"
 #include "../../include/mosaic_amd.h"
@@ -254,6 +256,256 @@ __global__ void __launch_bounds__(KS * 64) moe_a8_down_kernel(
   }
 }
 
+// ------------------------------------------------------ prefill (A8) ------
+// Large batches: tiles of 128 sorted assignment rows of one expert, a
+// workgroup of 4 waves per (tile, 8 weight groups of 16 rows).  Per 128-K step
+// the workgroup stages in LDS, in MFMA operand order: the e4m3 rows of its
+// tokens (two 1 KB runs per 16-row tile), the MXT16 weight blocks (1 KB per
+// group, already in lane order), the weight scale dwords and the rows'
+// activation scales.  Everything moves global -> LDS directly
+// (global_load_lds) through a ring of three stages, two steps ahead of the
+// MFMAs.  The copies are issued from inline asm with explicit vmcnt waits and
+// a bare s_barrier: the compiler then neither waits for the in-flight stages
+// before each LDS read (which it does for copies it knows about) nor needs
+// staging registers.  Each wave owns 64 rows x 4 groups and accumulates
+// straight into its MFMA accumulators: both scales are e8m0 operands of
+// v_mfma_scale, so there is no per-step VALU rescale.
+constexpr int kPfBM = 256;     // sorted rows per tile
+constexpr int kPfWaves = 8;    // 4 row quarters x 2 column halves
+constexpr int kPfStages = 3;
+constexpr int kPfNG = 16;      // weight groups (16 rows each) per workgroup
+constexpr int kPfA = 0, kPfB = 32768, kPfBs = kPfB + kPfNG * 1024, kPfAs = kPfBs + kPfNG * 256;
+constexpr int kPfStage = kPfAs + kPfBM * 4;
+constexpr int kPfOps = 9;  // copies per wave per stage: 4 A runs, 2 weight runs, 2 scale runs, 1 row-scale run
+
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
+
+// Tile coordinates of a 1-D grid of n_col x ceil8(n_tile) workgroups: the
+// dispatcher deals workgroups round-robin to the 8 XCDs, so ids that share
+// id % 8 run on one XCD; all column tiles of a row tile get the same id % 8 and
+// share that XCD's L2 copy of the tile's activation rows.
+__device__ __forceinline__ void pf_coords(int id, int n_col, int& col, int& tile) {
+  col = (id / 8) % n_col;
+  tile = (id % 8) + 8 * (id / (8 * n_col));
+}
+
+// this lane's sources for the wave's copy runs of one stage (add the step offsets)
+struct PfSrc {
+  const uint8_t* a[4];   // A run 4 wv + i: 16-row tile run >> 1, bytes 64 (run & 1) + 16 (lane / 16) of row lane % 16
+  const uint8_t* b[2];   // weight group 2 wv + i, this lane's 16 bytes
+  const uint8_t* bs[2];  // its scale dword
+  const float* as;       // row 64 (wv & 3) + lane: its 1x128 scale row
+};
+
+__device__ __forceinline__ void pf_issue(const PfSrc& src, int S, uint8_t* stage) {
+  const int wv = threadIdx.x >> 6;
+  const uint32_t base = lds_u32(stage);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lds_copy16(src.a[i] + 128 * S, base + kPfA + (4 * wv + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) lds_copy16(src.b[i] + (int64_t)S * 1024, base + kPfB + (2 * wv + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) lds_copy4(src.bs[i] + (int64_t)(S >> 2) * 256, base + kPfBs + (2 * wv + i) * 256);
+  lds_copy4(src.as + S, base + kPfAs + (wv & 3) * 256);
+}
+
+// One wave's MFMAs of one staged step: its 4 row tiles (rows 64 (wv >> 1)) x
+// the 8 staged groups in wg.
+__device__ __forceinline__ void pf_compute(const uint8_t* stage, const int (&wg)[8], int S, f32x4_t (&acc)[4][8]) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15;
+  const int sh = 8 * (S & 3);
+  i32x8_t a[4];
+  int sa[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int mtg = 4 * (wv >> 1) + mt;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + lane * 16);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + 1024 + lane * 16);
+    a[mt] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    sa[mt] = pow2_e8m0(*reinterpret_cast<const float*>(stage + kPfAs + (16 * mtg + c) * 4));
+  }
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const u32x4_t wb = *reinterpret_cast<const u32x4_t*>(stage + kPfB + wg[n] * 1024 + lane * 16);
+    const int sw = (int)((*reinterpret_cast<const uint32_t*>(stage + kPfBs + wg[n] * 256 + lane * 4) >> sh) & 0xFFu);
+    const i32x8_t b = {(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3], 0, 0, 0, 0};
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      acc[mt][n] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mt], b, acc[mt][n], 0, 4, 0, sa[mt], 0, sw);
+  }
+}
+
+__device__ __forceinline__ void pf_kloop(const PfSrc& src, int ns, const int (&wg)[8], f32x4_t (&acc)[4][8]) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[mt][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  pf_issue(src, 0, ring[0]);
+  if (ns > 1) pf_issue(src, 1, ring[1]);
+  for (int S = 0; S < ns; ++S) {
+    // step S landed (every wave's copies: the barrier), step S + 1 may still fly
+    if (S + 1 < ns)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kPfOps) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (S + 2 < ns) pf_issue(src, S + 2, ring[(S + 2) % kPfStages]);
+    pf_compute(ring[S % kPfStages], wg, S, acc);
+  }
+}
+
+// this lane's copy sources; rows past the tile's end read the tile's first row
+// (their results are never stored)
+__device__ __forceinline__ void pf_sources(PfSrc& src, const uint8_t* const (&rowp)[4], const uint8_t* bank_p,
+                                           const uint8_t* bank_s, const int (&groups)[2], int ns, const float* as_row) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) src.a[i] = rowp[i] + 64 * (i & 1) + 16 * (lane >> 4);  // run 4 wv + i: half i & 1
+  const int ns4 = (ns + 3) / 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    src.b[i] = bank_p + ((int64_t)groups[i] * ns) * 1024 + lane * 16;
+    src.bs[i] = bank_s + ((int64_t)groups[i] * ns4) * 256 + lane * 4;
+  }
+  src.as = as_row;
+}
+
+// gate/up + SwiGLU: 1-D grid of (I / 128) x ceil8(tiles); z [A, I] bf16 in
+// sorted order.  Staged groups: 0..7 gate (z columns j0 + 16 g), 8..15 up;
+// wave (rows 64 (wv >> 1), z columns j0 + 64 (wv & 1)) owns gate groups
+// 4 (wv & 1) + n and the matching up groups.
+__global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel(
+    const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ gu_p,
+    const uint8_t* __restrict__ gu_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
+    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
+    const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, const int32_t* __restrict__ perm_token,
+    const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H, int I, int E, float limit) {
+  int colt, tile;
+  pf_coords(blockIdx.x, I / 128, colt, tile);
+  if (tile >= n_tiles[0]) return;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 15, q = lane >> 4;
+  const int j0 = colt * 128;
+  const int ns = H / 128, ns4 = (ns + 3) / 4;
+  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * ebytes;
+  const uint8_t* bsc = (e == E) ? sh_s : gu_s + (int64_t)e * sbytes;
+  const uint8_t* rowp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * ((4 * wv + i) >> 1) + c;
+    rowp[i] = xq + (int64_t)perm_token[p0 + (row < rows ? row : 0)] * H;
+  }
+  int groups[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int g = 2 * wv + i;
+    groups[i] = g < 8 ? j0 / 16 + g : (I + j0) / 16 + g - 8;
+  }
+  const int srow = 64 * (wv & 3) + lane;
+  const float* as_row = xs + (int64_t)perm_token[p0 + (srow < rows ? srow : 0)] * ns;
+  PfSrc src;
+  pf_sources(src, rowp, bp, bsc, groups, ns, as_row);
+  const int hc = wv & 1;
+  int wg[8];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    wg[n] = 4 * hc + n;
+    wg[n + 4] = 8 + 4 * hc + n;
+  }
+  f32x4_t acc[4][8];
+  pf_kloop(src, ns, wg, acc);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
+        if (row < rows) {
+          const int pp = p0 + row;
+          const float gb = bf16_f32(f32_bf16(acc[mt][n][r])), ub = bf16_f32(f32_bf16(acc[mt][n + 4][r]));
+          const float zv = swiglu_f32(gb, ub, limit) * perm_weight[pp];
+          z[(int64_t)pp * I + j0 + 64 * hc + 16 * n + c] = f32_bf16(zv);
+        }
+      }
+}
+
+// down: 1-D grid of (H / 256) x ceil8(tiles); bf16 partial rows yb [A, H] in
+// sorted order.  Wave (rows 64 (wv >> 1), columns h0 + 128 (wv & 1)).
+__global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
+    const uint8_t* __restrict__ zq, const float* __restrict__ zs, const uint8_t* __restrict__ d_p,
+    const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
+    const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
+    const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, uint16_t* __restrict__ yb, int H,
+    int I, int E) {
+  int colt, tile;
+  pf_coords(blockIdx.x, H / 256, colt, tile);
+  if (tile >= n_tiles[0]) return;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 15, q = lane >> 4;
+  const int h0 = colt * 256;
+  const int ns = I / 128, ns4 = (ns + 3) / 4;
+  const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : d_p + (int64_t)e * ebytes;
+  const uint8_t* bsc = (e == E) ? sh_s : d_s + (int64_t)e * sbytes;
+  const uint8_t* rowp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * ((4 * wv + i) >> 1) + c;
+    rowp[i] = zq + (int64_t)(p0 + (row < rows ? row : 0)) * I;
+  }
+  const int groups[2] = {h0 / 16 + 2 * wv, h0 / 16 + 2 * wv + 1};
+  const int srow = 64 * (wv & 3) + lane;
+  const float* as_row = zs + (int64_t)(p0 + (srow < rows ? srow : 0)) * ns;
+  PfSrc src;
+  pf_sources(src, rowp, bp, bsc, groups, ns, as_row);
+  const int hc = wv & 1;
+  int wg[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) wg[n] = 8 * hc + n;
+  f32x4_t acc[4][8];
+  pf_kloop(src, ns, wg, acc);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
+        if (row < rows) yb[(int64_t)(p0 + row) * H + h0 + 128 * hc + 16 * n + c] = f32_bf16(acc[mt][n][r]);
+      }
+}
+
+// y[t][h] = bf16(sum over j of yb[combine_pos[t][j]][h]), bf16 partials
+__global__ void __launch_bounds__(256) moe_combine_bf16_kernel(const uint16_t* __restrict__ yb,
+                                                               const int32_t* __restrict__ combine_pos,
+                                                               uint16_t* __restrict__ y, int M, int W, int H) {
+  const int t = blockIdx.y;
+  const int h = 2 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (t >= M || h >= H) return;
+  float s0 = 0.f, s1 = 0.f;
+  for (int j = 0; j < W; ++j) {
+    const int p = combine_pos[(int64_t)t * W + j];
+    if (p >= 0) {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(yb + (int64_t)p * H + h);
+      s0 += bf16_f32((uint16_t)(v & 0xFFFFu));
+      s1 += bf16_f32((uint16_t)(v >> 16));
+    }
+  }
+  *reinterpret_cast<uint32_t*>(y + (int64_t)t * H + h) = (uint32_t)f32_bf16(s0) | ((uint32_t)f32_bf16(s1) << 16);
+}
+
 }  // namespace mosaic
 
 using namespace mosaic;
@@ -309,23 +561,45 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,
                w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0, 1,
                w.chunk_counts, w.chunk_base};
+  const int64_t A = m * top_k + (has_shared ? m : 0);
+  // large batches (>= 24 assignments per expert on average): 128-row tiles
+  const bool prefill = m * top_k >= 24 * n_experts && hidden % 256 == 0;
+  const int block_m = prefill ? kPfBM : kMoeBlockM;
+  const int64_t e_ext = n_experts + (has_shared ? 1 : 0);
+  const int64_t tcap = prefill ? (A + std::min(A, e_ext) * (kPfBM - 1)) / kPfBM : w.tile_cap;
   int rc = launch_route_layout(logits, route_bias, ids, weights, ids, weights, m, n_experts, top_k, score_func,
-                               renorm, route_scale, has_shared, kMoeBlockM, w.tile_cap, lo, st);
+                               renorm, route_scale, has_shared, block_m, tcap, lo, st);
   if (rc != 0) return rc;
   rc = mosaic_act_quant(x, MOSAIC_DTYPE_BF16, w.xq, w.xs, m, hidden, 128, 0, stream);
   if (rc != 0) return rc;
-  const unsigned tcap = (unsigned)w.tile_cap;
+  if (prefill) {
+    uint16_t* yb = reinterpret_cast<uint16_t*>(w.yp);  // bf16 partials in the fp32 partial buffer
+    const int64_t tcap8 = (tcap + 7) / 8 * 8;
+    hipLaunchKernelGGL(moe_a8_gateup_prefill_kernel, dim3((unsigned)(inter / 128 * tcap8)), dim3(kPfWaves * 64), 0, st,
+                       w.xq, w.xs, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_rows,
+                       w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
+                       (int)n_experts, swiglu_limit);
+    MOSAIC_LAUNCH_CHECK("moe_a8_gateup_prefill");
+    rc = mosaic_act_quant(w.z, MOSAIC_DTYPE_BF16, w.zq, w.zs, A, inter, 128, 0, stream);
+    if (rc != 0) return rc;
+    hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
+                       w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows, w.tile_p0,
+                       w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts);
+    MOSAIC_LAUNCH_CHECK("moe_a8_down_prefill");
+    hipLaunchKernelGGL(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 2 + 255) / 256), (unsigned)m), dim3(256),
+                       0, st, yb, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
+    MOSAIC_RETURN_LAUNCH("moe_a8_combine_bf16");
+  }
   constexpr int GT = 2, GKS = 4, DT = 2, DKS = 4;
-  hipLaunchKernelGGL((moe_a8_gateup_kernel<GT, GKS>), dim3((unsigned)(inter / (8 * GT)), tcap), dim3(GKS * 64), 0,
+  hipLaunchKernelGGL((moe_a8_gateup_kernel<GT, GKS>), dim3((unsigned)(inter / (8 * GT)), (unsigned)tcap), dim3(GKS * 64), 0,
                      st, w.xq, w.xs, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_rows,
                      w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
                      (int)n_experts, swiglu_limit);
   MOSAIC_LAUNCH_CHECK("moe_a8_gateup");
-  const int64_t A = m * top_k + (has_shared ? m : 0);
   // rows of z past the real assignments are never read by the down kernel
   rc = mosaic_act_quant(w.z, MOSAIC_DTYPE_BF16, w.zq, w.zs, A, inter, 128, 0, stream);
   if (rc != 0) return rc;
-  hipLaunchKernelGGL((moe_a8_down_kernel<DT, DKS>), dim3((unsigned)(hidden / (16 * DT)), tcap), dim3(DKS * 64), 0,
+  hipLaunchKernelGGL((moe_a8_down_kernel<DT, DKS>), dim3((unsigned)(hidden / (16 * DT)), (unsigned)tcap), dim3(DKS * 64), 0,
                      st, w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows,
                      w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
   MOSAIC_LAUNCH_CHECK("moe_a8_down");

@@ -272,7 +272,8 @@ def test_moe_a16_given_ids_weight_before_down(dev):
 
 @pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
     (1, 16, 256, 128, 4, False, 10.0), (3, 16, 256, 128, 4, True, 10.0), (20, 8, 384, 256, 2, False, 0.0),
-    (37, 32, 512, 128, 8, True, 10.0), (520, 8, 256, 128, 8, True, 10.0)])
+    (37, 32, 512, 128, 8, True, 10.0), (520, 8, 256, 128, 8, True, 10.0), (300, 16, 384, 256, 4, False, 0.0),
+    (1100, 32, 256, 128, 8, True, 10.0)])
 def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     """A8 layer (fused_moe_mxint contract) vs the A8 oracle of identical bytes."""
     ops = _ops()
