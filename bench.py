@@ -45,6 +45,7 @@ def parse():
     ap.add_argument("--m", type=int, default=1, help="tokens per decode step")
     ap.add_argument("--sweep", default="4,16,64", help="extra M values reported under m_sweep ('' to skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1, 3, 4, 5")
     return ap.parse_args()
 
 
@@ -133,6 +134,141 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     }
 
 
+def _graph_time(torch, fn, calls: int, reps: int = 5) -> float:
+    """Average microseconds per fn() call, replaying a HIP graph of `calls` calls
+    (launch overhead of the Python wrapper excluded)."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * calls)
+
+
+def config1_linear(torch, ops):
+    """BASELINE configs[0]: one MXFP4 linear [2048, 7168] at M=1 (A16, MXT16 weights);
+    ~70 weight copies (> the 256 MB MALL) rotate through the graph."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    n, k = 2048, 7168
+    w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    p, sc = ops.mx_quantize(w, "ceil")
+    copies = [ops.mxt16_prepack(p.clone(), sc.clone()) for _ in range(70)]
+    x = torch.randn(1, k, generator=g, device=dev).to(torch.bfloat16)
+    it = iter(range(10 ** 9))
+    cold = _graph_time(torch, lambda: ops.mxt16_linear_a16(x, copies[next(it) % len(copies)]), len(copies))
+    warm = _graph_time(torch, lambda: ops.mxt16_linear_a16(x, copies[0]), 70)
+    byts = n * (k // 2 + k // 32) + k * 2 + n * 2
+    return {"shape": [1, n, k], "us": round(cold, 3), "GBs": round(byts / cold / 1e3, 1),
+            "hbm_frac": round(byts / cold / 1e3 / HBM_PEAK_GBS, 4), "warm_mall_us": round(warm, 3),
+            "bytes": byts}
+
+
+def config3_fp8(torch, ops):
+    """FP8 block-scaled GEMMs, 5 shapes x M in {1, 16, 128, 4096}."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    out = {}
+    for n, k in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (18432, 7168)]:
+        w = torch.randn(n, k, generator=g, device=dev) * 0.02
+        wb = w.view((n + 127) // 128, 128, k // 128, 128) if n % 128 == 0 else None
+        if wb is None:
+            wp = torch.zeros((n + 127) // 128 * 128, k, device=dev)
+            wp[:n] = w
+            wb = wp.view(-1, 128, k // 128, 128)
+        bs = (wb.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12)
+        bq = (wb / bs[:, None, :, None]).reshape(-1, k)[:n].to(torch.float8_e4m3fn)
+        for m in (1, 16, 128, 4096):
+            x = torch.randn(m, k, generator=g, device=dev)
+            aq, a_s = ops.act_quant(x, 128, "amax")
+            calls = 20 if m < 4096 else 5
+            us = _graph_time(torch, lambda: ops.fp8_block_gemm(aq, a_s, bq, bs), calls, reps=3)
+            fl = 2 * m * n * k
+            byts = m * k + 4 * m * (k // 128) + n * k + 4 * bs.numel() + 2 * m * n
+            out[f"m{m}_n{n}_k{k}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                                      "mfma_frac": round(fl / us / 1e6 / 5000.0, 4),
+                                      "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def config4_prefill(torch, ops, bank, m: int = 4096, seed: int = 13):
+    """MoE prefill at M=4096 with Zipf(1.1) expert popularity over a
+    seeded permutation (8 experts pinned to zero), Gumbel-top-8, A8 contract."""
+    import math
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    perm = torch.randperm(E, generator=g, device=dev)
+    logp = torch.tensor([-1.1 * math.log(r + 1) for r in range(E)], device=dev)[torch.argsort(perm)]
+    logp[perm[-8:]] = -1e4
+    u = torch.rand(m, E, generator=g, device=dev).clamp(1e-9, 1 - 1e-9)
+    logits = logp[None, :] - torch.log(-torch.log(u))
+    x = torch.randn(m, H, generator=g, device=dev).to(torch.bfloat16)
+    ws = ops.MoEWorkspace()
+    fn = lambda: ops.moe_a8_forward(x, bank["gu"], bank["dn"], logits=logits, top_k=K, shared=bank["shared"],
+                                    workspace=ws)
+    _, ids, _ = fn()
+    us = _graph_time(torch, fn, 3, reps=3)
+    counts = torch.bincount(ids.flatten().long(), minlength=E)
+    used = int((counts > 0).sum().item())
+    fl = 2 * m * (K + 1) * 3 * H * I
+    byts = (used + 1) * EXPERT_BYTES + m * H * 2 * 2
+    return {"tokens": m, "us": round(us, 1), "tokens_per_s": round(m / us * 1e6, 1),
+            "TFLOPs": round(fl / us / 1e6, 1), "mfma_frac": round(fl / us / 1e6 / 5000.0, 4),
+            "hbm_GBs": round(byts / us / 1e3, 1), "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
+            "experts_used": used, "max_expert_rows": int(counts.max().item()), "contract": "A8 (fused_moe_mxint)"}
+
+
+def config5_dsa(torch, ops):
+    """FP8 lightning indexer + top-2048 and MLA decode over the picks."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(14)
+    out = {}
+    ws = ops.MoEWorkspace()
+    for b, l in [(1, 32768), (8, 131072)]:
+        q8 = lambda *sh: (torch.randn(*sh, generator=g, device=dev) * 60).clamp(-448, 448).to(torch.float8_e4m3fn)
+        nrot = max(1, (512 << 20) // (b * l * 132) + 1)
+        ks = [q8(b, l, 128) for _ in range(nrot)]
+        kss = [torch.rand(b, l, generator=g, device=dev) * 0.01 + 1e-3 for _ in range(nrot)]
+        q, qs = q8(b, 64, 128), torch.rand(b, 64, generator=g, device=dev) * 0.01 + 1e-3
+        w = torch.randn(b, 64, generator=g, device=dev) * 0.01
+        it = iter(range(10 ** 9))
+
+        def idx_fn():
+            i = next(it) % nrot
+            return ops.dsa_indexer_topk(q, qs, ks[i], kss[i], w, 2048, workspace=ws)
+        us = _graph_time(torch, idx_fn, nrot, reps=3)
+        byts = b * l * 132 + b * 64 * 136
+        out[f"indexer_b{b}_l{l}"] = {"us": round(us, 1), "GBs": round(byts / us / 1e3, 1),
+                                     "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del ks, kss
+    for b in (1, 8):
+        n = 65536
+        qh = torch.randn(b, 128, 576, generator=g, device=dev).to(torch.bfloat16)
+        lat = (torch.randn(b, n, 512, generator=g, device=dev) * 60).clamp(-448, 448).to(torch.float8_e4m3fn)
+        ls = torch.rand(b, n, 8, generator=g, device=dev) * 0.01
+        rope = torch.randn(b, n, 64, generator=g, device=dev).to(torch.bfloat16)
+        idx = torch.stack([torch.randperm(n, generator=g, device=dev)[:2048] for _ in range(b)]).int()
+        sink = torch.randn(128, generator=g, device=dev)
+        us = _graph_time(torch, lambda: ops.mla_sparse_decode(qh, lat, ls, rope, idx, 576 ** -0.5, sink,
+                                                              workspace=ws), 10, reps=3)
+        fl = 2 * b * 128 * 2048 * (576 + 512)
+        out[f"mla_b{b}"] = {"us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 2)}
+    return out
+
+
 def cpu_baseline(torch, ops, bank, tokens: int = 8, seed: int = 7):
     """Oracle (numpy A16 dequant-then-matmul) on ``tokens`` single-token decode
     steps of the same layer (each token routed on its own, its 8 routed + the
@@ -187,6 +323,14 @@ def main():
             sweep[str(mv)] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()
                               if k in ("us_per_layer", "gbs", "distinct_experts_avg")}
             sweep[str(mv)]["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    configs = {}
+    if not args.no_configs:
+        for name, fn in [("config1_linear_m1", lambda: config1_linear(torch, ops)),
+                         ("config3_fp8_gemm", lambda: config3_fp8(torch, ops)),
+                         ("config4_moe_prefill", lambda: config4_prefill(torch, ops, banks[0])),
+                         ("config5_dsa", lambda: config5_dsa(torch, ops))]:
+            print(f"bench.py: {name}", file=sys.stderr, flush=True)
+            configs[name] = fn()
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch, ops, banks[0])
     gu_gbs = main_r["gateup_gbs"]
     line = {
@@ -216,6 +360,7 @@ def main():
                      "algorithmic_bytes_per_launch": round(main_r["gateup_bytes_per_launch"])},
         "cpu_baseline": cpu,
         "m_sweep": sweep,
+        "configs": configs,
     }
     print(json.dumps(line))
 
