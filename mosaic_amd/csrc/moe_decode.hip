@@ -1,0 +1,428 @@
+// Batch-1 decode MoE layer (A16 contract) in two launches.
+//
+// 1. moe_dec1_gateup_kernel: every workgroup of a routed tile routes the token
+//    itself (route_token.h, the same arithmetic as the layout kernel, so ids
+//    and weights are identical), sorts the picks by expert id and takes the
+//    tile-th one; shared-expert workgroups skip routing.  A workgroup owns 16 z
+//    columns of one tile (gate row group j and up row group I/16 + j); its KS
+//    waves split K into equal parts and each wave streams its part through a
+//    register ring of D super-steps (weights + scale dwords loaded D steps
+//    ahead, no branches in the steady state), with the x part it needs staged
+//    in wave-private LDS.  The parts meet in LDS; SwiGLU and the route weight
+//    are applied and z row `tile` is written (the shared expert's row is K).
+// 2. moe_dec1_down_kernel: a workgroup owns 16 hidden columns and walks every
+//    tile (experts in ascending id, the shared expert last); its waves again
+//    split K (= inter) and stream (tile, super-step) entries through a ring, with
+//    the z parts staged in wave-private LDS.  Each expert's partial (a fresh
+//    MFMA chain) is added to the running fp32 sum in tile order, so the combine
+//    of the reference (ascending expert id, shared last, fp32) happens in
+//    registers and y is written directly: no partial buffer, no combine launch.
+//
+// Rows: the decode batch has one token, so the x / z operand is row 0 in every
+// lane (all 16 MFMA rows carry the same data and only row 0 is stored).
+#include <algorithm>
+
+#include "common.h"
+#include "moe_internal.h"
+#include "route_token.h"
+#include "../../include/mosaic_amd.h"
+
+namespace mosaic {
+
+constexpr int kDecXVMax = 8;   // x vectors (16 B) per lane staged by a gate/up wave: part <= 32 super-steps
+constexpr int kDecZVMax = 20;  // z vectors per lane staged by a down wave
+
+__device__ __forceinline__ bf16x8_t dec_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// MXT16 addresses of row group g for this lane: its 16 B code block of super-step 0
+// and its scale dword of super-steps 0..3 (add S * 1024 and (S / 4) * 256)
+__device__ __forceinline__ void dec_ptrs(const uint8_t* pt, const uint8_t* st, int64_t g, int ns, int lane,
+                                         const uint8_t*& w, const uint8_t*& s) {
+  const int ns4 = (ns + 3) / 4;
+  w = pt + (g * ns * 64 + lane) * 16;
+  s = st + (g * ns4 * 64 + lane) * 4;
+}
+
+// 16 B of E2M1 (one lane's MX block) x 32 bf16 of x at the same K -> acc
+__device__ __forceinline__ void dec_mfma(const u32x4_t w, uint32_t sbyte, const u32x4_t (&xv)[4], f32x4_t& acc) {
+  bf16x8_t wb[4];
+  mx_block_to_bf16(w, e8m0_f32(sbyte), wb);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dec_bf16x8(xv[s]), wb[s], acc, 0, 0, 0);
+}
+
+// x operand of super-step s of a part staged at xs (row-major, 128 bf16 per step)
+__device__ __forceinline__ void dec_x(const uint8_t* xs, int s, int q, u32x4_t (&xv)[4]) {
+  const u32x4_t* p = reinterpret_cast<const u32x4_t*>(xs + s * 256 + q * 64);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) xv[k] = p[k];
+}
+
+// Route the token in this wave (or read the given ids) and sort the picks by
+// (expert id, slot), all in registers: lane i < K ends with pick i (rank order)
+// in me/mw and its sorted position in rank; invalid picks (given ids out of
+// range) have me = -1 and sort last.  Returns the number of valid picks.
+__device__ __forceinline__ int dec1_route(const float* __restrict__ logits, const float* __restrict__ bias,
+                                          const int32_t* __restrict__ ids_in, const float* __restrict__ w_in, int E,
+                                          int K, int func, int renorm, float scale, int& me, float& mw, int& rank) {
+  const int lane = threadIdx.x & 63;
+  if (logits) {
+    route_token_any(logits, E, K, func, renorm, scale, bias, me, mw);
+  } else {
+    const int e = lane < K ? ids_in[lane] : -1;
+    me = (e < 0 || e >= E) ? -1 : e;
+    mw = lane < K ? w_in[lane] : 0.f;
+  }
+  const int km = me >= 0 ? me : 0x7FFF;
+  rank = 0;
+  for (int jj = 0; jj < K; ++jj) {
+    const int o = __builtin_amdgcn_readlane(me, jj);
+    const int ko = o >= 0 ? o : 0x7FFF;
+    rank += (ko < km || (ko == km && jj < lane)) ? 1 : 0;
+  }
+  return __builtin_popcountll(__ballot(lane < K && me >= 0));
+}
+
+// grid (I/16, K + has_shared), KS waves; dynamic LDS = H * 2 bytes (the x row, split in parts);
+// XV >= the x vectors per lane of a part (nsp / 4)
+template <int KS, int D, int XV>
+__global__ void __launch_bounds__(KS * 64) moe_dec1_gateup_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ logits, const float* __restrict__ bias,
+    const int32_t* __restrict__ ids_in, const float* __restrict__ w_in, int32_t* __restrict__ ids_out,
+    float* __restrict__ w_out, const uint8_t* __restrict__ gu_p, const uint8_t* __restrict__ gu_s,
+    const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s, uint16_t* __restrict__ z,
+    int32_t* __restrict__ tile_expert, int32_t* __restrict__ n_tiles, int H, int I, int E, int K, int func,
+    int renorm, float route_scale, float limit) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dec_smem[];
+  __shared__ float red[KS][2][16];
+  __shared__ int s_tile_e;
+  __shared__ float s_tile_w;
+  const int tile = blockIdx.y;
+  const bool is_shared = tile == K;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int j = blockIdx.x;
+  const int ns = H / 128, nsp = ns / KS, sbase = w * nsp, ns4 = (ns + 3) / 4;
+  // 1. this wave's x part -> registers (clamped: every lane loads, lanes past the part do not store)
+  const int nvec = nsp * 16;
+  u32x4_t xst[XV];
+#pragma unroll
+  for (int v = 0; v < XV; ++v) {
+    const int i = min(lane + 64 * v, nvec - 1);
+    xst[v] = reinterpret_cast<const u32x4_t*>(x + (int64_t)sbase * 128)[i];
+  }
+  // 2. routing (routed tiles): wave 0 routes (one wave per workgroup, not
+  //    per wave: the DPP rounds would otherwise compete for every SIMD) and
+  //    publishes this tile's expert and route weight
+  int e = E;
+  float rw = 1.0f;
+  if (!is_shared) {
+    if (w == 0) {
+      int me, rank;
+      float mw;
+      const int nv = dec1_route(logits, bias, ids_in, w_in, E, K, func, renorm, route_scale, me, mw, rank);
+      if (blockIdx.x == 0 && tile == 0 && lane < K) {  // outputs + the tile list of the down kernel
+        if (logits) {
+          ids_out[lane] = me;
+          w_out[lane] = mw;
+        }
+        if (me >= 0) tile_expert[rank] = me;
+        if (lane == 0) n_tiles[0] = nv;
+      }
+      const uint64_t src = __ballot(lane < K && me >= 0 && rank == tile);
+      const int sl = src ? __builtin_ctzll(src) : 0;
+      const int te = __builtin_amdgcn_readlane(me, sl);
+      const float tw = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(mw), sl));
+      if (lane == 0) {
+        s_tile_e = src ? te : -1;
+        s_tile_w = tw;
+      }
+    }
+    __syncthreads();
+    e = s_tile_e;
+    rw = s_tile_w;
+    if (e < 0) return;  // tile >= valid picks (uniform over the workgroup)
+  }
+  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
+  const uint8_t* bp = is_shared ? sh_p : gu_p + (int64_t)e * ebytes;
+  const uint8_t* bs = is_shared ? sh_s : gu_s + (int64_t)e * sbytes;
+  const uint8_t* wt[2];
+  const uint8_t* st[2];
+  dec_ptrs(bp, bs, j, ns, lane, wt[0], st[0]);
+  dec_ptrs(bp, bs, I / 16 + j, ns, lane, wt[1], st[1]);
+  // 3. ring prologue: steps [0, D) of the part (padded steps past the part load step 0 and get scale 0)
+  const int nchunks = (nsp + D - 1) / D;
+  u32x4_t rw_w[D][2];
+  uint32_t rw_s[D][2];
+  auto load_step = [&](int n, u32x4_t (&wv)[2], uint32_t (&sv)[2]) {
+    const int S = sbase + (n < nsp ? n : 0);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      wv[t] = load_nt_u32x4(wt[t] + (int64_t)S * 1024);
+      sv[t] = *reinterpret_cast<const uint32_t*>(st[t] + (int64_t)(S >> 2) * 256);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) load_step(s, rw_w[s], rw_s[s]);
+  // 4. x part -> wave-private LDS (the wave reads only what it wrote)
+  uint8_t* xs = dec_smem + (size_t)w * nsp * 256;
+#pragma unroll
+  for (int v = 0; v < XV; ++v) {
+    const int i = lane + 64 * v;
+    if (i < nvec) reinterpret_cast<u32x4_t*>(xs)[i] = xst[v];
+  }
+  f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+  auto chunk = [&](int ch, auto more) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int n = ch * D + s;
+      const int S = sbase + n;
+      const bool real = n < nsp;
+      u32x4_t xv[4];
+      dec_x(xs, real ? n : 0, q, xv);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t sb = real ? (rw_s[s][t] >> (8 * (S & 3))) & 0xFFu : 0u;  // padded step: scale 0 -> W = 0
+        dec_mfma(rw_w[s][t], sb, xv, acc[t]);
+      }
+      if constexpr (decltype(more)::value) load_step(n + D, rw_w[s], rw_s[s]);
+    }
+  };
+  for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
+  chunk(nchunks - 1, std::false_type{});
+  // 5. parts meet in LDS (row 0 only: lanes 0..15, element 0)
+  if (q == 0) {
+    red[w][0][c] = acc[0][0];
+    red[w][1][c] = acc[1][0];
+  }
+  __syncthreads();
+  if (w == 0 && q == 0) {
+    float g = red[0][0][c], u = red[0][1][c];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) {
+      g += red[k2][0][c];
+      u += red[k2][1][c];
+    }
+    const float zv = swiglu_f32(g, u, limit) * rw;
+    z[(int64_t)tile * I + 16 * j + c] = f32_bf16(zv);
+  }
+}
+
+// grid (H/16), KS waves; dynamic LDS = (K + has_shared) * I * 2 bytes (z rows, split in parts);
+// ZV >= the z vectors per lane of a part ((K + has_shared) * nsp / 4)
+template <int KS, int D, int ZV>
+__global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
+    const uint16_t* __restrict__ z, const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ n_tiles,
+    const uint8_t* __restrict__ d_p, const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p,
+    const uint8_t* __restrict__ sh_s, uint16_t* __restrict__ y, int H, int I, int E, int K, int has_shared) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dec_smem[];
+  __shared__ float red[KS][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int g = blockIdx.x;
+  const int ns = I / 128, nsp = ns / KS, sbase = w * nsp, ns4 = (ns + 3) / 4;
+  const int nz = K + has_shared;  // z rows (row K = shared expert)
+  // 1. z parts of every row -> registers (row r, part steps [sbase, sbase + nsp))
+  const int pvec = nsp * 16, nvec = nz * pvec;
+  u32x4_t zst[ZV];
+#pragma unroll
+  for (int v = 0; v < ZV; ++v) {
+    const int i = min(lane + 64 * v, nvec - 1);
+    const int r = i / pvec, o = i - r * pvec;
+    zst[v] = reinterpret_cast<const u32x4_t*>(z + (int64_t)r * I + (int64_t)sbase * 128)[o];
+  }
+  // 2. tiles: routed ones (ascending expert id) then the shared expert; lane t holds tile t's bases
+  const int nv = n_tiles[0];
+  const int le = lane < K ? tile_expert[lane] : 0;  // issued with n_tiles (no dependence on it)
+  const int nt = nv + has_shared;
+  const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
+  const bool lsh = lane >= nv;
+  const uint8_t* lw = lsh ? sh_p : d_p + (int64_t)le * ebytes;
+  const uint8_t* ls = lsh ? sh_s : d_s + (int64_t)le * sbytes;
+  const int lrow = lsh ? K : lane;
+  const uint64_t lw_u = reinterpret_cast<uint64_t>(lw), ls_u = reinterpret_cast<uint64_t>(ls);
+  auto tile_base = [&](int t, const uint8_t*& wp, const uint8_t*& sp) {
+    const uint32_t wlo = __builtin_amdgcn_readlane((int)(uint32_t)lw_u, t);
+    const uint32_t whi = __builtin_amdgcn_readlane((int)(uint32_t)(lw_u >> 32), t);
+    const uint32_t slo = __builtin_amdgcn_readlane((int)(uint32_t)ls_u, t);
+    const uint32_t shi = __builtin_amdgcn_readlane((int)(uint32_t)(ls_u >> 32), t);
+    wp = reinterpret_cast<const uint8_t*>(((uint64_t)whi << 32) | wlo) + ((int64_t)g * ns * 64 + lane) * 16;
+    sp = reinterpret_cast<const uint8_t*>(((uint64_t)shi << 32) | slo) + ((int64_t)g * ns4 * 64 + lane) * 4;
+  };
+  const int N = nt * nsp;
+  const int nchunks = (N + D - 1) / D;
+  u32x4_t r_w[D];
+  uint32_t r_s[D];
+  auto load_entry = [&](int n, u32x4_t& wv, uint32_t& sv) {
+    const int nn = n < N ? n : 0;  // padded entries reload entry 0 and get scale 0
+    const int t = nn / nsp, S = sbase + (nn - t * nsp);
+    const uint8_t* wp;
+    const uint8_t* sp;
+    tile_base(t, wp, sp);
+    wv = load_nt_u32x4(wp + (int64_t)S * 1024);
+    sv = *reinterpret_cast<const uint32_t*>(sp + (int64_t)(S >> 2) * 256);
+  };
+  if (N > 0) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) load_entry(s, r_w[s], r_s[s]);
+  }
+  // 3. z parts -> wave-private LDS: row r at zs + r * nsp * 256
+  uint8_t* zs = dec_smem + (size_t)w * nz * nsp * 256;
+#pragma unroll
+  for (int v = 0; v < ZV; ++v) {
+    const int i = lane + 64 * v;
+    if (i < nvec) reinterpret_cast<u32x4_t*>(zs)[i] = zst[v];
+  }
+  f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+  float ysum = 0.f;
+  auto chunk = [&](int ch, auto more) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int n = ch * D + s;
+      const bool real = n < N;
+      const int nn = real ? n : 0;
+      const int t = nn / nsp, sl = nn - t * nsp;
+      const int row = __builtin_amdgcn_readlane(lrow, t);
+      u32x4_t xv[4];
+      dec_x(zs + (size_t)row * nsp * 256, sl, q, xv);
+      const int S = sbase + sl;
+      const uint32_t sb = real ? (r_s[s] >> (8 * (S & 3))) & 0xFFu : 0u;
+      dec_mfma(r_w[s], sb, xv, part);
+      // last step of this expert: fold its partial into the sum (selects, no branch)
+      const bool fold = real && sl == nsp - 1;
+      ysum += fold ? part[0] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[r] = fold ? 0.f : part[r];
+      if constexpr (decltype(more)::value) load_entry(n + D, r_w[s], r_s[s]);
+    }
+  };
+  if (N > 0) {
+    for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
+    chunk(nchunks - 1, std::false_type{});
+  }
+  if (q == 0) red[w][c] = ysum;
+  __syncthreads();
+  if (w == 0 && q == 0) {
+    float v = red[0][c];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][c];
+    y[16 * g + c] = f32_bf16(v);
+  }
+}
+
+// ring depth of a part of n super-steps: 8, 7 or 4 when it divides n, else the
+// largest of 8, 4, 2, 1 not above n (the last chunk is then padded)
+static int dec_depth(int n) {
+  for (int d : {8, 7, 4})
+    if (n % d == 0) return d;
+  return n >= 8 ? 8 : (n >= 4 ? 4 : (n >= 2 ? 2 : 1));
+}
+
+template <int KS, int XV>
+static void launch_dec1_gateup_x(int D, dim3 grid, size_t lds, hipStream_t st, const uint16_t* x, const float* logits,
+                                 const float* bias, const int32_t* ids_in, const float* w_in, int32_t* ids_out,
+                                 float* w_out, const uint8_t* gu_p, const uint8_t* gu_s, const uint8_t* sh_p,
+                                 const uint8_t* sh_s, uint16_t* z, int32_t* te, int32_t* nt, int H, int I, int E,
+                                 int K, int func, int renorm, float scale, float limit) {
+#define DEC_GU(DV)                                                                                                \
+  hipLaunchKernelGGL((moe_dec1_gateup_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, st, x, logits, bias, ids_in, \
+                     w_in, ids_out, w_out, gu_p, gu_s, sh_p, sh_s, z, te, nt, H, I, E, K, func, renorm, scale, limit)
+  switch (D) {
+    case 8: DEC_GU(8); break;
+    case 7: DEC_GU(7); break;
+    case 4: DEC_GU(4); break;
+    case 2: DEC_GU(2); break;
+    default: DEC_GU(1); break;
+  }
+#undef DEC_GU
+}
+
+template <int KS, int ZV>
+static void launch_dec1_down_z(int D, dim3 grid, size_t lds, hipStream_t st, const uint16_t* z, const int32_t* te,
+                               const int32_t* nt, const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_p,
+                               const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared) {
+#define DEC_DN(DV)                                                                                                 \
+  hipLaunchKernelGGL((moe_dec1_down_kernel<KS, DV, ZV>), grid, dim3(KS * 64), lds, st, z, te, nt, d_p, d_s, sh_p, \
+                     sh_s, y, H, I, E, K, has_shared)
+  switch (D) {
+    case 6: DEC_DN(6); break;
+    case 4: DEC_DN(4); break;
+    case 3: DEC_DN(3); break;
+    default: DEC_DN(2); break;
+  }
+#undef DEC_DN
+}
+
+constexpr int kDecGuKS = 2;   // gate/up: waves (K parts) per workgroup (all workgroups resident: routing latency paid once)
+// down: waves (K parts) per workgroup, 8 when inter / 128 allows it, else 4
+static int dec_dn_ks(int64_t nsi) { return nsi % 8 == 0 ? 8 : (nsi % 4 == 0 ? 4 : 0); }
+
+bool moe_decode1_supported(int64_t m, int64_t hidden, int64_t inter, int64_t top_k, int has_shared) {
+  if (m != 1 || top_k < 1 || top_k > kRouteMaxTopK) return false;
+  const int64_t nsh = hidden / 128, nsi = inter / 128;
+  if (hidden % 128 || inter % 128 || nsh % kDecGuKS || dec_dn_ks(nsi) == 0) return false;
+  const int64_t gu_part = nsh / kDecGuKS, dn_part = nsi / dec_dn_ks(nsi);
+  if (gu_part * 16 > 64 * kDecXVMax) return false;                        // x staging registers
+  if ((top_k + has_shared) * dn_part * 16 > 64 * kDecZVMax) return false;  // z staging registers
+  if ((size_t)(top_k + has_shared) * inter * 2 > 64 * 1024) return false;
+  return true;
+}
+
+int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias, const int32_t* ids_in,
+                       const float* w_in, int32_t* ids_out, float* w_out, const uint8_t* gu_p, const uint8_t* gu_s,
+                       const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_gu_p, const uint8_t* sh_gu_s,
+                       const uint8_t* sh_d_p, const uint8_t* sh_d_s, uint16_t* y, int64_t H, int64_t I, int64_t E,
+                       int64_t K, int has_shared, int func, int renorm, float route_scale, float limit, uint16_t* z,
+                       int32_t* tile_expert, int32_t* n_tiles, void* const* marks, hipStream_t st) {
+  MOSAIC_CHECK_ARG(E >= 1 && E <= kRouteMaxExperts && K <= E, "moe decode: E=%lld top_k=%lld", (long long)E,
+                   (long long)K);
+  MOSAIC_CHECK_ARG(func >= 0 && func <= 2, "moe decode: score func %d", func);
+  auto mark = [&](int i) {
+    if (marks && marks[i]) (void)hipEventRecord((hipEvent_t)marks[i], st);
+  };
+  mark(1);  // routing runs inside the gate/up launch: the layout stage is empty
+  const int dn_ks = dec_dn_ks(I / 128);
+  const int gu_part = (int)(H / 128 / kDecGuKS), dn_part = (int)(I / 128 / dn_ks);
+  const int nz = (int)K + has_shared;
+  const int gd = dec_depth(gu_part);
+  const int xv = (gu_part * 16 + 63) / 64;
+  const dim3 ggrid((unsigned)(I / 16), (unsigned)nz);
+#define GU_ARGS gd, ggrid, (size_t)H * 2, st, x, logits, bias, ids_in, w_in, ids_out, w_out, gu_p, gu_s, sh_gu_p, \
+                sh_gu_s, z, tile_expert, n_tiles, (int)H, (int)I, (int)E, (int)K, func, renorm, route_scale, limit
+  if (xv <= 2)
+    launch_dec1_gateup_x<kDecGuKS, 2>(GU_ARGS);
+  else if (xv <= 4)
+    launch_dec1_gateup_x<kDecGuKS, 4>(GU_ARGS);
+  else
+    launch_dec1_gateup_x<kDecGuKS, 8>(GU_ARGS);
+#undef GU_ARGS
+  MOSAIC_LAUNCH_CHECK("moe_decode1_gateup");
+  mark(2);
+  const int ndn = nz * dn_part;
+  const int dd = ndn % 6 == 0 ? 6 : (ndn % 4 == 0 ? 4 : (ndn % 3 == 0 ? 3 : 2));
+  const int zv = (ndn * 16 + 63) / 64;
+#define DN_ARGS dd, dim3((unsigned)(H / 16)), (size_t)nz * I * 2, st, z, tile_expert, n_tiles, d_p, d_s, sh_d_p, \
+                sh_d_s, y, (int)H, (int)I, (int)E, (int)K, has_shared
+  if (dn_ks == 8) {
+    if (zv <= 5)
+      launch_dec1_down_z<8, 5>(DN_ARGS);
+    else if (zv <= 10)
+      launch_dec1_down_z<8, 10>(DN_ARGS);
+    else
+      launch_dec1_down_z<8, kDecZVMax>(DN_ARGS);
+  } else {
+    if (zv <= 5)
+      launch_dec1_down_z<4, 5>(DN_ARGS);
+    else if (zv <= 10)
+      launch_dec1_down_z<4, 10>(DN_ARGS);
+    else
+      launch_dec1_down_z<4, kDecZVMax>(DN_ARGS);
+  }
+#undef DN_ARGS
+  MOSAIC_LAUNCH_CHECK("moe_decode1_down");
+  mark(3);
+  mark(4);
+  return kOk;
+}
+
+}  // namespace mosaic

@@ -106,4 +106,14 @@ inline MoeWorkspace carve_moe_workspace(char* base, int64_t M, int64_t H, int64_
   return w;
 }
 
+// Batch-1 decode layer in two launches (moe_decode.hip): routing + gate/up +
+// SwiGLU, then down + combine.  `supported` says whether the shapes fit it.
+bool moe_decode1_supported(int64_t m, int64_t hidden, int64_t inter, int64_t top_k, int has_shared);
+int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias, const int32_t* ids_in,
+                       const float* w_in, int32_t* ids_out, float* w_out, const uint8_t* gu_p, const uint8_t* gu_s,
+                       const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_gu_p, const uint8_t* sh_gu_s,
+                       const uint8_t* sh_d_p, const uint8_t* sh_d_s, uint16_t* y, int64_t H, int64_t I, int64_t E,
+                       int64_t K, int has_shared, int func, int renorm, float route_scale, float limit, uint16_t* z,
+                       int32_t* tile_expert, int32_t* n_tiles, void* const* marks, hipStream_t st);
+
 }  // namespace mosaic

@@ -7,6 +7,7 @@
 // Everything stays on the device; nothing is read back by the host.
 #include "common.h"
 #include "moe_internal.h"
+#include "route_token.h"
 #include "../../include/mosaic_amd.h"
 
 namespace mosaic {
@@ -14,128 +15,6 @@ namespace mosaic {
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
 constexpr int kRouteMaxAssign = 4096;   // A_ext limit of the single-workgroup path
-constexpr int kRouteMaxExperts = 512;   // routed experts (+1 virtual shared expert)
-constexpr int kRouteMaxTopK = 16;
-
-// fp32 -> unsigned key with the same order (NaN -> smallest)
-__device__ __forceinline__ uint32_t order_key(float f) {
-  if (f != f) return 0u;
-  uint32_t u = __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float score_of(float logit, int func) {
-  if (func == MOSAIC_SCORE_SIGMOID) return 1.0f / (1.0f + expf(-logit));
-  if (func == MOSAIC_SCORE_SQRTSOFTPLUS) {
-    float sp = logit > 20.f ? logit : log1pf(expf(logit));
-    return sqrtf(sp);
-  }
-  return logit;  // softmax handled by the caller
-}
-
-// One wave routes one token; logits stay in registers (PER per lane, E <=
-// 64*PER).  Selection key: the logit when there is no bias (every score
-// function is monotone), else score + bias.  Ties -> lower index.  Each round
-// is two 32-bit DPP max-reductions over (key, ~index); lane r then computes
-// the score of pick r, and lane 0 renormalizes.  Picks go to s_ids/s_w
-// (workgroup scratch) and to the global outputs.
-template <int PER>
-__device__ __forceinline__ void route_one_token_t(const float* __restrict__ lg, int E, int K, int func, int renorm,
-                                                  float scale, const float* __restrict__ bias, int16_t* s_ids,
-                                                  float* s_w, int32_t* ids_out, float* w_out) {
-  const int lane = threadIdx.x & 63;
-  float lv[PER];
-  uint32_t khi[PER], klo[PER];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int e = lane + 64 * j;
-    lv[j] = (e < E) ? lg[e] : -INFINITY;
-    mx = fmaxf(mx, lv[j]);
-  }
-  float denom = 1.f;
-  if (func == MOSAIC_SCORE_SOFTMAX) {
-    mx = wave_max_f32(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (lane + 64 * j < E) sum += expf(lv[j] - mx);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    denom = sum;
-  }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int e = lane + 64 * j;
-    float k = lv[j];
-    if (bias && e < E) {
-      const float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(lv[j] - mx) / denom : score_of(lv[j], func);
-      k = sc + bias[e];
-    }
-    khi[j] = (e < E) ? order_key(k) : 0u;  // absent experts sort below every real one
-    klo[j] = (e < E) ? 0xFFFFFFFFu - (uint32_t)e : 0u;
-  }
-  int my_pick = -1;
-  float my_logit = 0.f;
-  for (int r = 0; r < K; ++r) {
-    uint32_t bh = 0u, bl = 0u;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const bool better = khi[j] > bh || (khi[j] == bh && klo[j] > bl);
-      bh = better ? khi[j] : bh;
-      bl = better ? klo[j] : bl;
-    }
-    const uint32_t hi = wave_max_u32(bh);
-    const uint32_t lo = wave_max_u32(bh == hi ? bl : 0u);
-    const int e = (int)(0xFFFFFFFFu - lo);
-    float mine = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const bool own = (lane + 64 * j) == e;
-      mine = own ? lv[j] : mine;
-      khi[j] = own ? 0u : khi[j];
-      klo[j] = own ? 0u : klo[j];
-    }
-    const float l = __uint_as_float(wave_bcast_u32(__float_as_uint(mine), e & 63));
-    if (lane == r) {
-      my_pick = e;
-      my_logit = l;
-    }
-  }
-  if (lane < K) {
-    const float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(my_logit - mx) / denom : score_of(my_logit, func);
-    s_ids[lane] = (int16_t)my_pick;
-    s_w[lane] = sc;
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane == 0) {
-    float sum = 0.f;
-    for (int r = 0; r < K; ++r) sum += s_w[r];
-    for (int r = 0; r < K; ++r) {
-      float w = s_w[r];
-      if (renorm && func != MOSAIC_SCORE_SOFTMAX) w = w / sum;
-      w = w * scale;
-      s_w[r] = w;
-      w_out[r] = w;
-      ids_out[r] = s_ids[r];
-    }
-  }
-}
-
-__device__ __forceinline__ void route_one_token(const float* __restrict__ lg, int E, int K, int func, int renorm,
-                                                float scale, const float* __restrict__ bias, int16_t* s_ids,
-                                                float* s_w, int32_t* ids_out, float* w_out) {
-  if (E <= 64)
-    route_one_token_t<1>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
-  else if (E <= 128)
-    route_one_token_t<2>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
-  else if (E <= 256)
-    route_one_token_t<4>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
-  else
-    route_one_token_t<8>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
-}
 
 // Flat assignment a < M*K is (token a/K, slot a%K); a >= M*K is the shared
 // expert's row for token a - M*K (virtual expert id E, weight 1).
@@ -230,7 +109,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_layout_kernel(
         for (int s2 = 0; s2 < K; ++s2) {
           const int o = s_ids[t * K + s2];
           nvalid += (o >= 0);
-          below += (o >= 0 && my >= 0 && o < my);
+          below += (o >= 0 && my >= 0 && (o < my || (o == my && s2 < s)));  // repeated ids: slot order
           inv_before += (o < 0 && s2 < s);
         }
         rank = my >= 0 ? below : nvalid + inv_before;
@@ -373,7 +252,7 @@ __global__ void __launch_bounds__(1024) route_layout_small_kernel(
     cnt += (vb && eb == e);
     const bool same_tok = tb == t;
     tok_valid += (same_tok && vb);
-    tok_less += (same_tok && vb && eb < e);
+    tok_less += (same_tok && vb && (eb < e || (eb == e && b < a)));  // repeated ids: slot order
     tok_inv_before += (same_tok && !vb && b < a);
   }
   // tile count of a's expert if a heads its expert segment, else 0
@@ -531,7 +410,7 @@ __global__ void __launch_bounds__(kLayoutChunk) layout_scatter_kernel(const int3
     for (int s2 = 0; s2 < K; ++s2) {
       const int o = assignment_expert(ids, t * K + s2, A, A_ext, E);
       nvalid += (o >= 0);
-      below += (o >= 0 && my >= 0 && o < my);
+      below += (o >= 0 && my >= 0 && (o < my || (o == my && s2 < s)));  // repeated ids: slot order
       inv_before += (o < 0 && s2 < s);
     }
     rank = my >= 0 ? below : nvalid + inv_before;

@@ -401,6 +401,11 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
     if (stage_events && stage_events[i]) (void)hipEventRecord((hipEvent_t)stage_events[i], st);
   };
   mark(0);
+  if (moe_decode1_supported(m, hidden, inter, top_k, has_shared))
+    return launch_moe_decode1(x, logits, route_bias, ids, weights, ids, weights, gu_packed, gu_scale, d_packed,
+                              d_scale, sh_gu_packed, sh_gu_scale, sh_d_packed, sh_d_scale, y, hidden, inter, n_experts,
+                              top_k, has_shared, score_func, renorm, route_scale, swiglu_limit, w.z, w.tile_expert,
+                              w.n_tiles, stage_events, st);
   // counts/offsets are not read by the MoE kernels, so small decode batches may
   // take the single-wave layout path
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,

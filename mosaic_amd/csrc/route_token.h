@@ -1,0 +1,177 @@
+// Per-token router shared by the layout kernels and the fused decode kernels:
+// scores, top-k with ties to the lower expert index, renormalization.
+#pragma once
+#include "common.h"
+#include "../../include/mosaic_amd.h"
+
+namespace mosaic {
+
+constexpr int kRouteMaxExperts = 512;   // routed experts (+1 virtual shared expert)
+constexpr int kRouteMaxTopK = 16;
+
+// fp32 -> unsigned key with the same order (NaN -> smallest)
+__device__ __forceinline__ uint32_t order_key(float f) {
+  if (f != f) return 0u;
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float score_of(float logit, int func) {
+  if (func == MOSAIC_SCORE_SIGMOID) return 1.0f / (1.0f + expf(-logit));
+  if (func == MOSAIC_SCORE_SQRTSOFTPLUS) {
+    float sp = logit > 20.f ? logit : log1pf(expf(logit));
+    return sqrtf(sp);
+  }
+  return logit;  // softmax handled by the caller
+}
+
+// One wave routes one token; logits stay in registers (PER per lane, E <=
+// 64*PER).  Selection key: the logit when there is no bias (every score
+// function is monotone), else score + bias.  Ties -> lower index.  Each round
+// is two 32-bit DPP max-reductions over (key, ~index).  On return lane r < K
+// holds pick r (rank order) and its weight: score / (fp32 sum of the K scores
+// in rank order) when renormalizing (not softmax), times `scale`; other lanes
+// hold -1 and 0.  Everything stays in registers (readlane broadcasts).
+template <int PER>
+__device__ __forceinline__ void route_token_regs(const float* __restrict__ lg, int E, int K, int func, int renorm,
+                                                 float scale, const float* __restrict__ bias, int& pick,
+                                                 float& weight) {
+  const int lane = threadIdx.x & 63;
+  float lv[PER];
+  uint32_t khi[PER], klo[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + 64 * j;
+    lv[j] = (e < E) ? lg[e] : -INFINITY;
+    mx = fmaxf(mx, lv[j]);
+  }
+  float denom = 1.f;
+  if (func == MOSAIC_SCORE_SOFTMAX) {
+    mx = wave_max_f32(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (lane + 64 * j < E) sum += expf(lv[j] - mx);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    denom = sum;
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + 64 * j;
+    float k = lv[j];
+    if (bias && e < E) {
+      const float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(lv[j] - mx) / denom : score_of(lv[j], func);
+      k = sc + bias[e];
+    }
+    khi[j] = (e < E) ? order_key(k) : 0u;  // absent experts sort below every real one
+    klo[j] = (e < E) ? 0xFFFFFFFFu - (uint32_t)e : 0u;
+  }
+  // sort this lane's PER candidates by (key, lower index) descending once; a
+  // round then reduces only the lane heads and the winning lane shifts its list
+  float lgv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) lgv[j] = lv[j];
+  auto cex = [&](int i, int j) {  // order candidates i < j descending
+    const bool sw = khi[j] > khi[i] || (khi[j] == khi[i] && klo[j] > klo[i]);
+    const uint32_t hi_i = sw ? khi[j] : khi[i], hi_j = sw ? khi[i] : khi[j];
+    const uint32_t lo_i = sw ? klo[j] : klo[i], lo_j = sw ? klo[i] : klo[j];
+    const float l_i = sw ? lgv[j] : lgv[i], l_j = sw ? lgv[i] : lgv[j];
+    khi[i] = hi_i; khi[j] = hi_j; klo[i] = lo_i; klo[j] = lo_j; lgv[i] = l_i; lgv[j] = l_j;
+  };
+  if constexpr (PER == 2) {
+    cex(0, 1);
+  } else if constexpr (PER == 4) {
+    cex(0, 1); cex(2, 3); cex(0, 2); cex(1, 3); cex(1, 2);
+  } else if constexpr (PER == 8) {  // Batcher odd-even merge sort
+    cex(0, 1); cex(2, 3); cex(4, 5); cex(6, 7);
+    cex(0, 2); cex(1, 3); cex(4, 6); cex(5, 7); cex(1, 2); cex(5, 6);
+    cex(0, 4); cex(1, 5); cex(2, 6); cex(3, 7); cex(2, 4); cex(3, 5); cex(1, 2); cex(3, 4); cex(5, 6);
+  }
+  int my_pick = -1;
+  float my_logit = 0.f;
+  for (int r = 0; r < K; ++r) {
+    const uint32_t hi = wave_max_u32(khi[0]);
+    // the index reduction is needed only when several lanes hold the winning key
+    const uint64_t at_max = __ballot(khi[0] == hi);
+    const uint32_t lo = (__builtin_popcountll(at_max) == 1)
+                            ? wave_bcast_u32(klo[0], __builtin_ctzll(at_max))
+                            : wave_max_u32(khi[0] == hi ? klo[0] : 0u);
+    const int e = (int)(0xFFFFFFFFu - lo);
+    const int src = e & 63;  // expert e lives in lane e % 64
+    const float l = __uint_as_float(wave_bcast_u32(__float_as_uint(lgv[0]), src));
+    const bool win = lane == src;
+#pragma unroll
+    for (int j = 0; j < PER - 1; ++j) {
+      khi[j] = win ? khi[j + 1] : khi[j];
+      klo[j] = win ? klo[j + 1] : klo[j];
+      lgv[j] = win ? lgv[j + 1] : lgv[j];
+    }
+    khi[PER - 1] = win ? 0u : khi[PER - 1];
+    klo[PER - 1] = win ? 0u : klo[PER - 1];
+    if (lane == r) {
+      my_pick = e;
+      my_logit = l;
+    }
+  }
+  const float sc = (lane < K) ? ((func == MOSAIC_SCORE_SOFTMAX) ? expf(my_logit - mx) / denom
+                                                               : score_of(my_logit, func))
+                              : 0.f;
+  float sum = 0.f;
+  for (int r = 0; r < K; ++r) sum += __uint_as_float(wave_bcast_u32(__float_as_uint(sc), r));  // rank order
+  float w = sc;
+  if (renorm && func != MOSAIC_SCORE_SOFTMAX) w = w / sum;
+  w = w * scale;
+  pick = lane < K ? my_pick : -1;
+  weight = lane < K ? w : 0.f;
+}
+
+// route_token_regs, then picks/weights to s_ids/s_w (workgroup scratch; the
+// caller synchronizes before reading them) and to ids_out/w_out when given.
+template <int PER>
+__device__ __forceinline__ void route_one_token_t(const float* __restrict__ lg, int E, int K, int func, int renorm,
+                                                  float scale, const float* __restrict__ bias, int16_t* s_ids,
+                                                  float* s_w, int32_t* ids_out, float* w_out) {
+  const int lane = threadIdx.x & 63;
+  int pick;
+  float w;
+  route_token_regs<PER>(lg, E, K, func, renorm, scale, bias, pick, w);
+  if (lane < K) {
+    s_ids[lane] = (int16_t)pick;
+    s_w[lane] = w;
+    if (w_out) {
+      w_out[lane] = w;
+      ids_out[lane] = pick;
+    }
+  }
+}
+
+// picks in registers (see route_token_regs), E <= 512
+__device__ __forceinline__ void route_token_any(const float* __restrict__ lg, int E, int K, int func, int renorm,
+                                                float scale, const float* __restrict__ bias, int& pick,
+                                                float& weight) {
+  if (E <= 64)
+    route_token_regs<1>(lg, E, K, func, renorm, scale, bias, pick, weight);
+  else if (E <= 128)
+    route_token_regs<2>(lg, E, K, func, renorm, scale, bias, pick, weight);
+  else if (E <= 256)
+    route_token_regs<4>(lg, E, K, func, renorm, scale, bias, pick, weight);
+  else
+    route_token_regs<8>(lg, E, K, func, renorm, scale, bias, pick, weight);
+}
+
+__device__ __forceinline__ void route_one_token(const float* __restrict__ lg, int E, int K, int func, int renorm,
+                                                float scale, const float* __restrict__ bias, int16_t* s_ids,
+                                                float* s_w, int32_t* ids_out, float* w_out) {
+  if (E <= 64)
+    route_one_token_t<1>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+  else if (E <= 128)
+    route_one_token_t<2>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+  else if (E <= 256)
+    route_one_token_t<4>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+  else
+    route_one_token_t<8>(lg, E, K, func, renorm, scale, bias, s_ids, s_w, ids_out, w_out);
+}
+
+}  // namespace mosaic

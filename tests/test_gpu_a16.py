@@ -270,6 +270,109 @@ def test_moe_a16_given_ids_weight_before_down(dev):
     assert not np.allclose(y.float().cpu().numpy(), unit, atol=1e-3)
 
 
+# ---- batch-1 decode path (fused routing + gate/up, fused down + combine) ----
+# It is taken for M == 1 when hidden and inter are multiples of 512.
+@pytest.mark.parametrize("e,h,inter,k,shared,limit,func", [
+    (16, 512, 512, 4, True, 0.0, "sigmoid"), (32, 1024, 512, 8, False, 10.0, "sigmoid"),
+    (64, 2048, 1024, 6, True, 10.0, "softmax"), (8, 512, 1024, 8, True, 0.0, "sqrtsoftplus"),
+    (16, 1536, 2048, 1, True, 0.0, "sigmoid")])
+def test_moe_a16_decode1_vs_oracle(dev, e, h, inter, k, shared, limit, func):
+    ops = _ops()
+    rng = np.random.default_rng(e * 7 + h + inter + k)
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    sh = _make_bank(rng, 1, h, inter) if shared else None
+    x = _bf16(rng.standard_normal((1, h)))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    gu_b, d_b = ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds))
+    shb = None if sh is None else (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])),
+                                   ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    for rep in range(2):  # two calls in a row with different routing reuse the workspace
+        logits = rng.standard_normal((1, e)).astype(np.float32)
+        y, ids, w = ops.moe_a16_forward(x.to(dev), gu_b, d_b, logits=T(logits), top_k=k, shared=shb,
+                                        swiglu_limit=limit, score_func=func)
+        ids_ref, w_ref = MO.route_topk(logits, k, func)
+        np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+        np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=1e-6, atol=1e-7)
+        ref = MO.moe_layer_a16(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds,
+                               shared=None if sh is None else tuple(t[0] for t in sh), swiglu_limit=limit)
+        assert_close(y.float().cpu().numpy(), ref, what=f"moe a16 decode1 call {rep}")
+
+
+def test_moe_a16_decode1_given_ids_drop_and_duplicate(dev):
+    """ids given: an out-of-range id is dropped, a repeated id counts twice."""
+    ops = _ops()
+    rng = np.random.default_rng(21)
+    e, h, inter, k = 8, 512, 512, 4
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    sh = _make_bank(rng, 1, h, inter)
+    x = _bf16(rng.standard_normal((1, h)) * 3.0)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ids = np.array([[5, -1, 2, 5]])
+    w = np.array([[0.5, 0.7, 0.25, 0.125]], dtype=np.float32)
+    shb = (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])), ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    y, _, _ = ops.moe_a16_forward(x.to(dev), ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds)),
+                                  ids=T(ids.astype(np.int32)), weights=T(w), shared=shb, swiglu_limit=10.0)
+    keep = ids[0] >= 0
+    ref = MO.moe_layer_a16(x.float().numpy(), ids[:, keep], w[:, keep], gp, gs, dp, ds,
+                           shared=tuple(t[0] for t in sh), swiglu_limit=10.0)
+    assert_close(y.float().cpu().numpy(), ref, what="moe decode1 given ids")
+
+
+@pytest.mark.parametrize("a8", [False, True])
+def test_moe_given_ids_repeated_and_dropped_multi_token(dev, a8):
+    """Layout path (M > 1): a repeated expert id in one token counts once per
+    slot (slot order inside the expert), an out-of-range id is dropped."""
+    ops = _ops()
+    rng = np.random.default_rng(33)
+    e, h, inter, m, k = 8, 256, 128, 3, 4
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    x = _bf16(rng.standard_normal((m, h)) * 2.0)
+    ids = np.array([[5, -1, 2, 5], [1, 1, 1, 7], [0, 3, 9, 3]])
+    w = rng.uniform(0.1, 1.0, size=(m, k)).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    fwd = ops.moe_a8_forward if a8 else ops.moe_a16_forward
+    y, _, _ = fwd(x.to(dev), ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds)),
+                  ids=T(ids.astype(np.int32)), weights=T(w), swiglu_limit=10.0)
+    oracle = MO.moe_layer_a8 if a8 else MO.moe_layer_a16
+    for t in range(m):
+        keep = (ids[t] >= 0) & (ids[t] < e)
+        ref = oracle(x[t:t + 1].float().numpy(), ids[t:t + 1, keep], w[t:t + 1, keep], gp, gs, dp, ds,
+                     swiglu_limit=10.0)
+        assert_close(y[t:t + 1].float().cpu().numpy(), ref, what=f"moe repeated ids token {t}")
+
+
+def test_moe_a16_decode1_baseline_geometry(dev):
+    """BASELINE configs[1] geometry (hidden 7168, inter 2048, top-8, shared) on a
+    32-expert bank quantized on the device; oracle over the experts actually used."""
+    ops = _ops()
+    e, h, inter, k = 32, 7168, 2048, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    gp = torch.empty(e + 1, 2 * inter, h // 2, dtype=torch.uint8, device=dev)
+    gs = torch.empty(e + 1, 2 * inter, h // 32, dtype=torch.uint8, device=dev)
+    dp = torch.empty(e + 1, h, inter // 2, dtype=torch.uint8, device=dev)
+    ds = torch.empty(e + 1, h, inter // 32, dtype=torch.uint8, device=dev)
+    for i in range(e + 1):
+        p, s = ops.mx_quantize((torch.randn(2 * inter, h, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        gp[i].copy_(p)
+        gs[i].copy_(s)
+        p, s = ops.mx_quantize((torch.randn(h, inter, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        dp[i].copy_(p)
+        ds[i].copy_(s)
+    x = torch.randn(1, h, generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.randn(1, e, generator=g, device=dev)
+    y, ids, w = ops.moe_a16_forward(x, ops.mxt16_prepack(gp[:e], gs[:e]), ops.mxt16_prepack(dp[:e], ds[:e]),
+                                    logits=logits, top_k=k,
+                                    shared=(ops.mxt16_prepack(gp[e], gs[e]), ops.mxt16_prepack(dp[e], ds[e])))
+    ids_ref, w_ref = MO.route_topk(logits.cpu().numpy(), k, "sigmoid")
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    host = lambda t: (lambda i: t[i].cpu().numpy())
+    ref = MO.moe_layer_a16(x.float().cpu().numpy(), ids_ref, w_ref, host(gp), host(gs), host(dp), host(ds),
+                           shared=(gp[e].cpu().numpy(), gs[e].cpu().numpy(), dp[e].cpu().numpy(),
+                                   ds[e].cpu().numpy()))
+    assert_close(y.float().cpu().numpy(), ref, what="moe decode1 baseline geometry")
+
+
 @pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
     (1, 16, 256, 128, 4, False, 10.0), (3, 16, 256, 128, 4, True, 10.0), (20, 8, 384, 256, 2, False, 0.0),
     (37, 32, 512, 128, 8, True, 10.0), (520, 8, 256, 128, 8, True, 10.0), (300, 16, 384, 256, 4, False, 0.0),
