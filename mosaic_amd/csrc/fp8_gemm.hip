@@ -108,16 +108,19 @@ static void launch_fp8_skinny(const uint8_t* a, const float* as, const uint8_t* 
 
 // Tiled kernel (M >= 96, MFMA-bound at large M): a workgroup of BM/32 waves
 // owns a BM x 128 block of C (its 128 columns share one b_s row); each wave
-// owns a 64x64 quarter (4x4 MFMA tiles).  The A and B tiles of each 128-K
-// block go global -> LDS directly (global_load_lds_dwordx4, 16 bytes a lane
-// into 1 KB runs) through a ring of three stages, so two blocks are in flight
-// while one is consumed; a_s and b_s of a stage ride along through registers.
-// LDS rows are 128 bytes with their 16-byte chunks XOR-swizzled by
-// (row >> 1) & 7, so the 16 rows one MFMA operand read touches fall in
-// distinct banks.  Stage hand-off uses explicit vmcnt waits and a bare
-// s_barrier (a release fence would wait for the in-flight stages too).
-// Workgroups are remapped so that the ones on one XCD (dispatch goes
-// round-robin over 8) take neighbouring tiles, grouped 8 M-tiles deep.
+// owns a 64x64 quarter (4x4 MFMA tiles).  Each 128-K block's A and B tiles and
+// its scales (BM a_s values, one b_s) go global -> LDS directly
+// (global_load_lds, 16 bytes a lane into 1 KB runs, 4 bytes a lane for the
+// scales) through a ring of three stages, two blocks ahead of the MFMAs.  All
+// copies in the loop are issued from inline asm so the compiler neither waits
+// for the in-flight stages before each LDS read (as it does for copies it can
+// see) nor needs staging registers; every wave issues the same number of
+// copies per stage, so `s_waitcnt vmcnt(ops)` + a bare s_barrier hands a stage
+// over.  LDS rows are 128 bytes with their 16-byte chunks XOR-swizzled by
+// (row >> 1) & 7 (applied on the global side of the copy), so the 16 rows one
+// MFMA operand read touches fall in distinct banks.  Workgroups are remapped so
+// that the ones on one XCD (dispatch goes round-robin over 8) take
+// neighbouring tiles, grouped 8 M-tiles deep.
 constexpr int kTileN = 128, kStages = 3;
 
 __device__ __forceinline__ void tile_coords(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -142,18 +145,41 @@ __device__ __forceinline__ i32x8_t lds_fp8_operand(const uint8_t* tile, int row,
   return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
+__device__ __forceinline__ uint32_t fp8_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// one 16-byte (resp. 4-byte) global -> LDS copy per lane; the LDS address of
+// lane i is base + 16 i (resp. 4 i)
+__device__ __forceinline__ void fp8_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void fp8_copy4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
+
+template <int BM>
+struct Fp8Tile {
+  static constexpr int NT = BM * 2;                   // threads
+  static constexpr int NW = NT / 64;                  // waves
+  static constexpr int AB = (BM + kTileN) * 128;      // A and B bytes of a stage
+  static constexpr int SA = AB;                       // a_s: BM floats
+  static constexpr int SB = SA + BM * 4;              // b_s: 64 copies of one float
+  static constexpr int STAGE = SB + 256;
+  static constexpr int RUNS = AB / 1024 / NW;         // 1 KB A/B runs per wave per stage
+  static constexpr int SRUNS = BM / 64;               // 256-byte a_s runs per stage
+  static constexpr int OPS = RUNS + 1;                // copies per wave per stage
+  static_assert(AB / 1024 % NW == 0, "stage does not split evenly over the waves");
+  static_assert(SRUNS + 1 <= NW, "one scale copy per wave");
+};
+
 template <int BM>
 __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, void* __restrict__ C, int M, int N, int K, int out_f32) {
-  constexpr int NT = BM * 2;                    // threads
-  constexpr int NW = NT / 64;                   // waves
-  constexpr int STAGE = (BM + kTileN) * 128;    // bytes per stage
-  constexpr int IPW = (BM + kTileN) / 8 / NW;   // 1 KB DMA runs per wave per stage
-  static_assert((BM + kTileN) / 8 % NW == 0, "stage does not split evenly over the waves");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages][STAGE];
-  __shared__ float lsa[kStages][BM];
-  __shared__ float lsb[kStages];
+  using TT = Fp8Tile<BM>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages][TT::STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int c = lane & 15, q = lane >> 4;
   int tm, tn;
@@ -161,61 +187,53 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
   const int m0 = tm * BM, n0 = tn * kTileN;
   const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
   const int nkb = K / 128;
-  // this lane's source row and 16-byte chunk for each of the wave's DMA runs
-  const uint8_t* gsrc[IPW];
-  int ldsoff[IPW];
+  // this lane's source row and 16-byte chunk for each of the wave's A/B runs
+  const uint8_t* gsrc[TT::RUNS];
+  int ldsoff[TT::RUNS];
 #pragma unroll
-  for (int ii = 0; ii < IPW; ++ii) {
-    const int i = wv * IPW + ii;
+  for (int ii = 0; ii < TT::RUNS; ++ii) {
+    const int i = wv * TT::RUNS + ii;
     const int row = (i < BM / 8 ? 8 * i : 8 * (i - BM / 8)) + (lane >> 3);
     const int logical = (lane & 7) ^ ((row >> 1) & 7);
     gsrc[ii] = i < BM / 8 ? A + (int64_t)min(m0 + row, M - 1) * K + logical * 16
                           : B + (int64_t)min(n0 + row, N - 1) * K + logical * 16;
     ldsoff[ii] = i * 1024;
   }
-  // scales: threads < BM take a_s rows, thread BM takes b_s
-  const float* ssrc = tid < BM ? As + (int64_t)min(m0 + tid, M - 1) * nkb
-                               : (tid == BM ? Bs + (int64_t)(n0 / 128) * nkb : As);
-  auto issue_dma = [&](int st, int kb) {
+  // the wave's scale copy: waves < SRUNS take 64 a_s rows each, wave SRUNS the
+  // b_s value (every lane the same), the others repeat it into the same slot
+  const float* ssrc;
+  int sdst;
+  if (wv < TT::SRUNS) {
+    ssrc = As + (int64_t)min(m0 + 64 * wv + lane, M - 1) * nkb;
+    sdst = TT::SA + 256 * wv;
+  } else {
+    ssrc = Bs + (int64_t)(n0 / 128) * nkb;
+    sdst = TT::SB;
+  }
+  auto issue = [&](int st, int kb) {
+    const uint32_t base = fp8_lds_addr(lds[st]);
 #pragma unroll
-    for (int ii = 0; ii < IPW; ++ii)
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(gsrc[ii] + (int64_t)kb * 128),
-                                       (__attribute__((address_space(3))) void*)(&lds[st][ldsoff[ii]]), 16, 0, 0);
-  };
-  auto keep_scale = [&](int st, float v) {
-    if (tid < BM) lsa[st][tid] = v;
-    else if (tid == BM) lsb[st] = v;
+    for (int ii = 0; ii < TT::RUNS; ++ii) fp8_copy16(gsrc[ii] + (int64_t)kb * 128, base + ldsoff[ii]);
+    fp8_copy4(ssrc + kb, base + sdst);
   };
   f32x4_t acc[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // prologue: scales of block 0 in LDS, blocks 0 and 1 in flight
-  keep_scale(0, ssrc[0]);
-  issue_dma(0, 0);
-  float sreg = 0.f;
-  if (nkb > 1) {
-    sreg = ssrc[1];
-    issue_dma(1, 1);
-  }
+  issue(0, 0);
+  if (nkb > 1) issue(1, 1);
   for (int kb = 0; kb < nkb; ++kb) {
-    const int st = kb % kStages;
-    // block kb landed (and the scales of kb + 1); block kb + 1 may still be in flight
-    if (kb + 1 < nkb) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(IPW) : "memory");
-      keep_scale((kb + 1) % kStages, sreg);
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kb + 2 < nkb) {
-      sreg = ssrc[kb + 2];
-      issue_dma((kb + 2) % kStages, kb + 2);
-    }
-    const uint8_t* ta = lds[st];
-    const uint8_t* tb = lds[st] + BM * 128;
-    const float sb = lsb[st];
+    // block kb landed for every wave (its copies, then the barrier); kb + 1 may still fly
+    if (kb + 1 < nkb)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(TT::OPS) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kb + 2 < nkb) issue((kb + 2) % kStages, kb + 2);
+    const uint8_t* stg = lds[kb % kStages];
+    const uint8_t* ta = stg;
+    const uint8_t* tb = stg + BM * 128;
+    const float sb = *reinterpret_cast<const float*>(stg + TT::SB);
     i32x8_t bop[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) bop[nt] = lds_fp8_operand(tb, wn + 16 * nt + c, q);
@@ -226,7 +244,7 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(aop, bop[nt]);
       // a_s of this lane's accumulator rows wm + 16 mt + 4 q + r
-      const f32x4_t sa4 = *reinterpret_cast<const f32x4_t*>(&lsa[st][wm + 16 * mt + 4 * q]);
+      const f32x4_t sa4 = *reinterpret_cast<const f32x4_t*>(stg + TT::SA + 4 * (wm + 16 * mt + 4 * q));
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float s = sa4[r] * sb;
@@ -313,7 +331,9 @@ extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const u
     launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st);
     MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
   }
-  if (m >= 96) {
+  // 96 <= M < 256: 128x128 tiles when there are enough of them to spread over
+  // the chip, else the skinny kernel (K split over 8 waves, one grid row per 16 tokens)
+  if (m >= 96 && ((m + 127) / 128) * ((n + 127) / 128) >= 32) {
     launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st);
     MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
   }

@@ -25,7 +25,8 @@ def _case(rng, m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 1536, 7168), (16, 576, 7168), (3, 200, 384), (37, 130, 256),
                                    (128, 256, 1536), (1, 24576, 1536), (64, 7168, 512),
-                                   (256, 128, 128), (300, 576, 1024), (1024, 1536, 2048), (513, 700, 384)])
+                                   (256, 128, 128), (300, 576, 1024), (1024, 1536, 2048), (513, 700, 384),
+                                   (129, 8200, 512), (200, 640, 1536), (96, 1536, 7168)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
     from mosaic_amd import ops
@@ -37,5 +38,12 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
     got = c.float().cpu().numpy()
     err = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
     assert err.max() <= 2e-2, f"max scaled err {err.max()}"
-    if out == "f32":  # fp32 output: only summation order differs from the oracle
-        assert err.max() <= 1e-4, f"f32 max scaled err {err.max()}"
+    if out == "f32":
+        # fp32 output: only the order of the fp32 additions differs from the
+        # oracle (MFMA inner sums, K slices summed across waves), so
+        # |got - ref| <= gamma_n * sum |terms| with n = K/128 block partials +
+        # 128 products per block (gamma_n ~ n * 2^-24; factor 2 for the scale products)
+        abs_sum = L.fp8_block_gemm(aq & 0x7F, a_s, bq & 0x7F, np.abs(bs), out_bf16=False)
+        bound = 2.0 * (k // 128 + 128) * 2.0 ** -24 * abs_sum + 1e-30
+        viol = np.abs(got - ref) - bound
+        assert viol.max() <= 0, f"f32 reassociation bound exceeded by {viol.max()} (max scaled err {err.max()})"
