@@ -310,6 +310,74 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
   }
 }
 
+// Single A16 linear at one token (y [1, N] = x [1, K] . W^T, W MXT16): a
+// workgroup owns one 16-row group of W; its KS waves split K into equal parts,
+// each streaming its part through a register ring of D super-steps with its x
+// part staged in wave-private LDS; the parts meet in LDS.
+template <int KS, int D, int XV>
+__global__ void __launch_bounds__(KS * 64) mx_dec1_linear_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint8_t* __restrict__ packed_t,
+                                                                 const uint8_t* __restrict__ scale_t,
+                                                                 uint16_t* __restrict__ y, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dec_smem[];
+  __shared__ float red[KS][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int g = blockIdx.x;
+  const int ns = K / 128, nsp = ns / KS, sbase = w * nsp;
+  const int nvec = nsp * 16;
+  u32x4_t xst[XV];
+#pragma unroll
+  for (int v = 0; v < XV; ++v) {
+    const int i = min(lane + 64 * v, nvec - 1);
+    xst[v] = reinterpret_cast<const u32x4_t*>(x + (int64_t)sbase * 128)[i];
+  }
+  const uint8_t* wt;
+  const uint8_t* st;
+  dec_ptrs(packed_t, scale_t, g, ns, lane, wt, st);
+  const int nchunks = (nsp + D - 1) / D;
+  u32x4_t r_w[D];
+  uint32_t r_s[D];
+  auto load_step = [&](int n, u32x4_t& wv, uint32_t& sv) {
+    const int S = sbase + (n < nsp ? n : 0);
+    wv = load_nt_u32x4(wt + (int64_t)S * 1024);
+    sv = *reinterpret_cast<const uint32_t*>(st + (int64_t)(S >> 2) * 256);
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) load_step(s, r_w[s], r_s[s]);
+  uint8_t* xs = dec_smem + (size_t)w * nsp * 256;
+#pragma unroll
+  for (int v = 0; v < XV; ++v) {
+    const int i = lane + 64 * v;
+    if (i < nvec) reinterpret_cast<u32x4_t*>(xs)[i] = xst[v];
+  }
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  auto chunk = [&](int ch, auto more) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int n = ch * D + s;
+      const int S = sbase + n;
+      const bool real = n < nsp;
+      u32x4_t xv[4];
+      dec_x(xs, real ? n : 0, q, xv);
+      const uint32_t sb = real ? (r_s[s] >> (8 * (S & 3))) & 0xFFu : 0u;
+      dec_mfma(r_w[s], sb, xv, acc);
+      if constexpr (decltype(more)::value) load_step(n + D, r_w[s], r_s[s]);
+    }
+  };
+  for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
+  chunk(nchunks - 1, std::false_type{});
+  if (q == 0) red[w][c] = acc[0];
+  __syncthreads();
+  if (w == 0 && q == 0) {
+    float v = red[0][c];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][c];
+    const int n = 16 * g + c;
+    if (n < N) y[n] = f32_bf16(v);
+  }
+}
+
 // ring depth of a part of n super-steps: 8, 7 or 4 when it divides n, else the
 // largest of 8, 4, 2, 1 not above n (the last chunk is then padded)
 static int dec_depth(int n) {
@@ -351,6 +419,41 @@ static void launch_dec1_down_z(int D, dim3 grid, size_t lds, hipStream_t st, con
     default: DEC_DN(2); break;
   }
 #undef DEC_DN
+}
+
+template <int KS, int XV>
+static void launch_dec1_linear_x(int D, const uint16_t* x, const uint8_t* pt, const uint8_t* st, uint16_t* y,
+                                 int64_t n, int64_t k, hipStream_t s) {
+  const dim3 grid((unsigned)(n / 16));
+  const size_t lds = (size_t)k * 2;
+#define DEC_LIN(DV) \
+  hipLaunchKernelGGL((mx_dec1_linear_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, s, x, pt, st, y, (int)n, (int)k)
+  switch (D) {
+    case 8: DEC_LIN(8); break;
+    case 7: DEC_LIN(7); break;
+    case 4: DEC_LIN(4); break;
+    case 2: DEC_LIN(2); break;
+    default: DEC_LIN(1); break;
+  }
+#undef DEC_LIN
+}
+
+bool linear_decode1_supported(int64_t m, int64_t n, int64_t k) {
+  return m == 1 && n % 16 == 0 && k % 1024 == 0 && (k / 128 / 8) * 16 <= 64 * kDecXVMax;
+}
+
+// K split over 8 waves: every wave's part is loaded in one ring fill at K <= 8192
+void launch_linear_decode1(const uint16_t* x, const uint8_t* pt, const uint8_t* st, uint16_t* y, int64_t n, int64_t k,
+                           hipStream_t s) {
+  const int part = (int)(k / 128 / 8);
+  const int d = dec_depth(part);
+  const int xv = (part * 16 + 63) / 64;
+  if (xv <= 2)
+    launch_dec1_linear_x<8, 2>(d, x, pt, st, y, n, k, s);
+  else if (xv <= 4)
+    launch_dec1_linear_x<8, 4>(d, x, pt, st, y, n, k, s);
+  else
+    launch_dec1_linear_x<8, 8>(d, x, pt, st, y, n, k, s);
 }
 
 constexpr int kDecGuKS = 2;   // gate/up: waves (K parts) per workgroup (all workgroups resident: routing latency paid once)

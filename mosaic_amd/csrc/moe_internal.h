@@ -116,4 +116,9 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
                        int64_t K, int has_shared, int func, int renorm, float route_scale, float limit, uint16_t* z,
                        int32_t* tile_expert, int32_t* n_tiles, void* const* marks, hipStream_t st);
 
+// Single MXT16 A16 linear at one token (moe_decode.hip).
+bool linear_decode1_supported(int64_t m, int64_t n, int64_t k);
+void launch_linear_decode1(const uint16_t* x, const uint8_t* pt, const uint8_t* st, uint16_t* y, int64_t n, int64_t k,
+                           hipStream_t s);
+
 }  // namespace mosaic

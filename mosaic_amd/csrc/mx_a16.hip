@@ -364,7 +364,10 @@ extern "C" int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_
   MOSAIC_CHECK_ARG(m >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
                    "mxt16_linear_a16: shape out of range");
   if (m == 0) return kOk;
-  dispatch_linear<true>(x, packed_t, scale_t, y, m, n, k, (hipStream_t)stream);
+  if (linear_decode1_supported(m, n, k))
+    launch_linear_decode1(x, packed_t, scale_t, y, n, k, (hipStream_t)stream);
+  else
+    dispatch_linear<true>(x, packed_t, scale_t, y, m, n, k, (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("mxt16_linear_a16");
 }
 

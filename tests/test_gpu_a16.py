@@ -92,7 +92,8 @@ def test_mxt16_prepack_bitexact_roundtrip(dev, n, k):
     np.testing.assert_array_equal(s2.cpu().numpy(), scale)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 2048, 7168), (3, 48, 640), (16, 64, 1024), (20, 7168, 2048)])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 2048, 7168), (3, 48, 640), (16, 64, 1024), (20, 7168, 2048),
+                                   (1, 528, 3072), (1, 64, 8192), (1, 4096, 1024)])
 def test_mxt16_linear_a16_vs_oracle(dev, m, n, k):
     ops = _ops()
     rng = np.random.default_rng(m * 31 + n + k)
