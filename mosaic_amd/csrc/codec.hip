@@ -25,32 +25,6 @@ __device__ __forceinline__ uint32_t e2m1_code_rne(float q) {
   return c | sign;
 }
 
-// fp32 -> e4m3fn byte, round to nearest even; beyond 448 after rounding, inf
-// and NaN give 0x7F | sign (the behaviour of torch's float8_e4m3fn cast).
-__device__ __forceinline__ uint32_t e4m3_rne(float v) {
-  uint32_t u = __float_as_uint(v);
-  uint32_t sign = (u >> 24) & 0x80u;
-  float a = fabsf(v);
-  if (!(a < 464.0f)) {
-    if (a == 464.0f) return sign | 0x7Eu;  // tie between 448 and 480: even -> 448
-    return sign | 0x7Fu;                   // overflow, inf, NaN
-  }
-  if (a < 0.015625f) {  // below 2^-6: subnormal step 2^-9
-    float q = rintf(a * 512.0f);
-    return sign | (uint32_t)q;
-  }
-  uint32_t au = __float_as_uint(a);
-  int e = (int)(au >> 23) - 127;
-  uint32_t mant = au & 0x7FFFFFu;
-  uint32_t m3 = mant >> 20;
-  uint32_t rem = mant & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3++;
-  if (m3 == 8u) { m3 = 0; e++; }
-  uint32_t code = ((uint32_t)(e + 7) << 3) | m3;
-  if (code > 0x7Eu) code = 0x7Fu;
-  return sign | code;
-}
-
 template <typename T> __device__ __forceinline__ float load_as_f32(const T* p, int64_t i);
 template <> __device__ __forceinline__ float load_as_f32<float>(const float* p, int64_t i) { return p[i]; }
 template <> __device__ __forceinline__ float load_as_f32<uint16_t>(const uint16_t* p, int64_t i) {
@@ -163,10 +137,7 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const T* __restrict__ x,
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
   float s;
   if (mode == 0) {
-    float a = fmaxf(amax, 1e-4f) * 0.002232142925783992f;  // fp32(1/448)
-    uint32_t ab = __float_as_uint(a);
-    int e = (int)((ab >> 23) & 0xFFu) - 127 + ((ab & 0x7FFFFFu) != 0u ? 1 : 0);
-    s = __uint_as_float((uint32_t)(e + 127) << 23);
+    s = act_scale_pow2(amax);
   } else if (mode == 1) {
     s = fmaxf(amax, 1e-4f) * 0.002232142925783992f;
   } else {
@@ -217,10 +188,7 @@ __global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__
   for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
   float s;
   if (mode == 0) {
-    float a = fmaxf(amax, 1e-4f) * 0.002232142925783992f;  // fp32(1/448)
-    uint32_t ab = __float_as_uint(a);
-    int e = (int)((ab >> 23) & 0xFFu) - 127 + ((ab & 0x7FFFFFu) != 0u ? 1 : 0);
-    s = __uint_as_float((uint32_t)(e + 127) << 23);
+    s = act_scale_pow2(amax);
   } else if (mode == 1) {
     s = fmaxf(amax, 1e-4f) * 0.002232142925783992f;
   } else {

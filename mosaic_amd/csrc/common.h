@@ -110,6 +110,41 @@ __device__ __forceinline__ void mx_block_to_bf16(const u32x4_t w, float scale, b
   }
 }
 
+// fp32 -> e4m3fn byte, round to nearest even; beyond 448 after rounding, inf
+// and NaN give 0x7F | sign (the behaviour of torch's float8_e4m3fn cast).
+__device__ __forceinline__ uint32_t e4m3_rne(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  float a = fabsf(v);
+  if (!(a < 464.0f)) {
+    if (a == 464.0f) return sign | 0x7Eu;  // tie between 448 and 480: even -> 448
+    return sign | 0x7Fu;                   // overflow, inf, NaN
+  }
+  if (a < 0.015625f) {  // below 2^-6: subnormal step 2^-9
+    float q = rintf(a * 512.0f);
+    return sign | (uint32_t)q;
+  }
+  uint32_t au = __float_as_uint(a);
+  int e = (int)(au >> 23) - 127;
+  uint32_t mant = au & 0x7FFFFFu;
+  uint32_t m3 = mant >> 20;
+  uint32_t rem = mant & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3++;
+  if (m3 == 8u) { m3 = 0; e++; }
+  uint32_t code = ((uint32_t)(e + 7) << 3) | m3;
+  if (code > 0x7Eu) code = 0x7Fu;
+  return sign | code;
+}
+
+// power-of-two 1x128 activation scale: 2^ceil(log2(max(amax, 1e-4) * fp32(1/448)))
+// by IEEE bits (act_quant_ref, kernels/fp4_source.py:110-129)
+__device__ __forceinline__ float act_scale_pow2(float amax) {
+  const float a = fmaxf(amax, 1e-4f) * 0.002232142925783992f;  // fp32(1/448)
+  const uint32_t ab = __float_as_uint(a);
+  const int e = (int)((ab >> 23) & 0xFFu) - 127 + ((ab & 0x7FFFFFu) != 0u ? 1 : 0);
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
 // ---------------------------------------------------- DPP wave primitives ----
 // gfx9 DPP controls: quad_perm [1,0,3,2] / [2,3,0,1], row_half_mirror,
 // row_mirror, row_shr:n, row_bcast:15, row_bcast:31.

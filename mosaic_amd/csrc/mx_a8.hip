@@ -319,15 +319,17 @@ __device__ __forceinline__ void pf_issue(const PfSrc& src, int S, uint8_t* stage
   lds_copy4(src.as + S, base + kPfAs + (wv & 3) * 256);
 }
 
-// One wave's MFMAs of one staged step: its 4 row tiles (rows 64 (wv >> 1)) x
-// the 8 staged groups in wg.
+// One wave's MFMAs of one staged step: its row tiles (rows 64 (wv >> 1) + 16 mt,
+// the first MT of them: the tiles past the workgroup's valid rows are skipped)
+// x the 8 staged groups in wg.
+template <int MT>
 __device__ __forceinline__ void pf_compute(const uint8_t* stage, const int (&wg)[8], int S, f32x4_t (&acc)[4][8]) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15;
   const int sh = 8 * (S & 3);
-  i32x8_t a[4];
-  int sa[4];
+  i32x8_t a[MT];
+  int sa[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     const int mtg = 4 * (wv >> 1) + mt;
     const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + lane * 16);
     const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + 1024 + lane * 16);
@@ -340,19 +342,21 @@ __device__ __forceinline__ void pf_compute(const uint8_t* stage, const int (&wg)
     const int sw = (int)((*reinterpret_cast<const uint32_t*>(stage + kPfBs + wg[n] * 256 + lane * 4) >> sh) & 0xFFu);
     const i32x8_t b = {(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3], 0, 0, 0, 0};
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
       acc[mt][n] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mt], b, acc[mt][n], 0, 4, 0, sa[mt], 0, sw);
   }
 }
 
-__device__ __forceinline__ void pf_kloop(const PfSrc& src, int ns, const int (&wg)[8], f32x4_t (&acc)[4][8]) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int n = 0; n < 8; ++n) acc[mt][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  pf_issue(src, 0, ring[0]);
-  if (ns > 1) pf_issue(src, 1, ring[1]);
+// row tiles of this wave that hold valid rows (0..4), uniform over the wave
+__device__ __forceinline__ int pf_live_tiles(int rows) {
+  const int wv = threadIdx.x >> 6;
+  const int r = rows - 64 * (wv >> 1);
+  return r <= 0 ? 0 : (r >= 64 ? 4 : (r + 15) / 16);
+}
+
+template <int LIVE>
+__device__ __forceinline__ void pf_kloop_t(const PfSrc& src, int ns, const int (&wg)[8], f32x4_t (&acc)[4][8],
+                                           uint8_t (*ring)[kPfStage]) {
   for (int S = 0; S < ns; ++S) {
     // step S landed (every wave's copies: the barrier), step S + 1 may still fly
     if (S + 1 < ns)
@@ -360,7 +364,25 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& src, int ns, const int (&w
     else
       asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (S + 2 < ns) pf_issue(src, S + 2, ring[(S + 2) % kPfStages]);
-    pf_compute(ring[S % kPfStages], wg, S, acc);
+    if constexpr (LIVE > 0) pf_compute<LIVE>(ring[S % kPfStages], wg, S, acc);
+  }
+}
+
+__device__ __forceinline__ void pf_kloop(const PfSrc& src, int ns, int rows, const int (&wg)[8],
+                                         f32x4_t (&acc)[4][8], uint8_t (*ring)[kPfStage]) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[mt][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  pf_issue(src, 0, ring[0]);
+  if (ns > 1) pf_issue(src, 1, ring[1]);
+  // the wave's row tiles past the valid rows are skipped (one loop per count)
+  switch (pf_live_tiles(rows)) {
+    case 4: pf_kloop_t<4>(src, ns, wg, acc, ring); break;
+    case 3: pf_kloop_t<3>(src, ns, wg, acc, ring); break;
+    case 2: pf_kloop_t<2>(src, ns, wg, acc, ring); break;
+    case 1: pf_kloop_t<1>(src, ns, wg, acc, ring); break;
+    default: pf_kloop_t<0>(src, ns, wg, acc, ring); break;
   }
 }
 
@@ -389,7 +411,9 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
     const uint8_t* __restrict__ gu_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
     const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, const int32_t* __restrict__ perm_token,
-    const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H, int I, int E, float limit) {
+    const float* __restrict__ perm_weight, uint8_t* __restrict__ zq, float* __restrict__ zs, int H, int I, int E,
+    float limit) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
   int colt, tile;
   pf_coords(blockIdx.x, I / 128, colt, tile);
   if (tile >= n_tiles[0]) return;
@@ -424,21 +448,61 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
     wg[n + 4] = 8 + 4 * hc + n;
   }
   f32x4_t acc[4][8];
-  pf_kloop(src, ns, wg, acc);
+  pf_kloop(src, ns, rows, wg, acc, ring);
+  // z = bf16(SwiGLU(bf16 gate, bf16 up) * route weight) in acc[mt][n][r], and
+  // the amax of each row over this wave's 64 columns (DPP max over the 16
+  // lanes of the row, on the bits of non-negative floats)
+  uint32_t rmax[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int r = 0; r < 4; ++r) {
+      const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
+      const float wgt = perm_weight[p0 + (row < rows ? row : 0)];
+      float m = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
-        if (row < rows) {
-          const int pp = p0 + row;
-          const float gb = bf16_f32(f32_bf16(acc[mt][n][r])), ub = bf16_f32(f32_bf16(acc[mt][n + 4][r]));
-          const float zv = swiglu_f32(gb, ub, limit) * perm_weight[pp];
-          z[(int64_t)pp * I + j0 + 64 * hc + 16 * n + c] = f32_bf16(zv);
-        }
+      for (int n = 0; n < 4; ++n) {
+        const float gb = bf16_f32(f32_bf16(acc[mt][n][r])), ub = bf16_f32(f32_bf16(acc[mt][n + 4][r]));
+        const float zb = bf16_f32(f32_bf16(swiglu_f32(gb, ub, limit) * wgt));
+        acc[mt][n][r] = zb;
+        m = fmaxf(m, fabsf(zb));
       }
+      uint32_t u = __float_as_uint(m);
+      u = max(u, MOSAIC_DPP(0u, u, 0xB1, 0xF));
+      u = max(u, MOSAIC_DPP(0u, u, 0x4E, 0xF));
+      u = max(u, MOSAIC_DPP(0u, u, 0x141, 0xF));
+      u = max(u, MOSAIC_DPP(0u, u, 0x140, 0xF));
+      rmax[mt][r] = u;
+    }
+  // the 1x128 quantization block of a row spans this wave's columns and those
+  // of wave wv ^ 1: exchange the row maxima through the (now idle) ring
+  __syncthreads();
+  uint32_t* pam = reinterpret_cast<uint32_t*>(&ring[0][0]);  // [8 waves][64 rows]
+  if (c == 0) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pam[wv * 64 + 16 * mt + 4 * q + r] = rmax[mt][r];
+  }
+  __syncthreads();
+  const int nbk = I / 128;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
+      const float amax = __uint_as_float(max(rmax[mt][r], pam[(wv ^ 1) * 64 + 16 * mt + 4 * q + r]));
+      const float sc = act_scale_pow2(amax);
+      if (row < rows) {
+        const int64_t pp = p0 + row;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const float y = fminf(fmaxf(acc[mt][n][r] / sc, -448.0f), 448.0f);
+          zq[pp * I + j0 + 64 * hc + 16 * n + c] = (uint8_t)e4m3_rne(y);
+        }
+        if (hc == 0 && c == 0) zs[pp * nbk + j0 / 128] = sc;
+      }
+    }
 }
 
 // down: 1-D grid of (H / 256) x ceil8(tiles); bf16 partial rows yb [A, H] in
@@ -449,6 +513,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
     const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, uint16_t* __restrict__ yb, int H,
     int I, int E) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
   int colt, tile;
   pf_coords(blockIdx.x, H / 256, colt, tile);
   if (tile >= n_tiles[0]) return;
@@ -475,7 +540,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
 #pragma unroll
   for (int n = 0; n < 8; ++n) wg[n] = 8 * hc + n;
   f32x4_t acc[4][8];
-  pf_kloop(src, ns, wg, acc);
+  pf_kloop(src, ns, rows, wg, acc, ring);
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -487,23 +552,30 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
       }
 }
 
-// y[t][h] = bf16(sum over j of yb[combine_pos[t][j]][h]), bf16 partials
-__global__ void __launch_bounds__(256) moe_combine_bf16_kernel(const uint16_t* __restrict__ yb,
+// y[t][h] = bf16(sum over j of yb[combine_pos[t][j]][h]), bf16 partials; a
+// thread sums 8 consecutive columns (16-byte loads), in ascending j
+__global__ void __launch_bounds__(128) moe_combine_bf16_kernel(const uint16_t* __restrict__ yb,
                                                                const int32_t* __restrict__ combine_pos,
                                                                uint16_t* __restrict__ y, int M, int W, int H) {
   const int t = blockIdx.y;
-  const int h = 2 * (blockIdx.x * blockDim.x + threadIdx.x);
+  const int h = 8 * (blockIdx.x * blockDim.x + threadIdx.x);
   if (t >= M || h >= H) return;
-  float s0 = 0.f, s1 = 0.f;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < W; ++j) {
     const int p = combine_pos[(int64_t)t * W + j];
     if (p >= 0) {
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(yb + (int64_t)p * H + h);
-      s0 += bf16_f32((uint16_t)(v & 0xFFFFu));
-      s1 += bf16_f32((uint16_t)(v >> 16));
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(yb + (int64_t)p * H + h);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[2 * i] += bf16_f32((uint16_t)(v[i] & 0xFFFFu));
+        s[2 * i + 1] += bf16_f32((uint16_t)(v[i] >> 16));
+      }
     }
   }
-  *reinterpret_cast<uint32_t*>(y + (int64_t)t * H + h) = (uint32_t)f32_bf16(s0) | ((uint32_t)f32_bf16(s1) << 16);
+  u32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (uint32_t)f32_bf16(s[2 * i]) | ((uint32_t)f32_bf16(s[2 * i + 1]) << 16);
+  *reinterpret_cast<u32x4_t*>(y + (int64_t)t * H + h) = o;
 }
 
 }  // namespace mosaic
@@ -575,18 +647,17 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
   if (prefill) {
     uint16_t* yb = reinterpret_cast<uint16_t*>(w.yp);  // bf16 partials in the fp32 partial buffer
     const int64_t tcap8 = (tcap + 7) / 8 * 8;
+    // the gate/up epilogue writes z already quantized (1x128 pow2 e4m3, as act_quant mode 0)
     hipLaunchKernelGGL(moe_a8_gateup_prefill_kernel, dim3((unsigned)(inter / 128 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.xq, w.xs, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_rows,
-                       w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
+                       w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.zq, w.zs, (int)hidden, (int)inter,
                        (int)n_experts, swiglu_limit);
     MOSAIC_LAUNCH_CHECK("moe_a8_gateup_prefill");
-    rc = mosaic_act_quant(w.z, MOSAIC_DTYPE_BF16, w.zq, w.zs, A, inter, 128, 0, stream);
-    if (rc != 0) return rc;
     hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows, w.tile_p0,
                        w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts);
     MOSAIC_LAUNCH_CHECK("moe_a8_down_prefill");
-    hipLaunchKernelGGL(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 2 + 255) / 256), (unsigned)m), dim3(256),
+    hipLaunchKernelGGL(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 8 + 127) / 128), (unsigned)m), dim3(128),
                        0, st, yb, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
     MOSAIC_RETURN_LAUNCH("moe_a8_combine_bf16");
   }
