@@ -209,8 +209,11 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_gateup_kernel(
 }
 
 // grid (H/16), KS waves; dynamic LDS = (K + has_shared) * I * 2 bytes (z rows, split in parts);
-// ZV >= the z vectors per lane of a part ((K + has_shared) * nsp / 4)
-template <int KS, int D, int ZV>
+// ZV >= the z vectors per lane of a part ((K + has_shared) * NSP / 4).  A wave's
+// part of K is NSP super-steps (inter / 128 = KS * NSP, NSP <= 4, and the part
+// starts at a multiple of NSP so its scale bytes sit in one dword); the ring
+// holds DT tiles, each NSP code blocks + one scale dword.
+template <int KS, int NSP, int DT, int ZV>
 __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
     const uint16_t* __restrict__ z, const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ n_tiles,
     const uint8_t* __restrict__ d_p, const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p,
@@ -220,10 +223,10 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
   const int g = blockIdx.x;
-  const int ns = I / 128, nsp = ns / KS, sbase = w * nsp, ns4 = (ns + 3) / 4;
+  const int ns = I / 128, sbase = w * NSP, ns4 = (ns + 3) / 4;
   const int nz = K + has_shared;  // z rows (row K = shared expert)
-  // 1. z parts of every row -> registers (row r, part steps [sbase, sbase + nsp))
-  const int pvec = nsp * 16, nvec = nz * pvec;
+  // 1. z parts of every row -> registers (row r, part steps [sbase, sbase + NSP))
+  const int pvec = NSP * 16, nvec = nz * pvec;
   u32x4_t zst[ZV];
 #pragma unroll
   for (int v = 0; v < ZV; ++v) {
@@ -231,43 +234,40 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
     const int r = i / pvec, o = i - r * pvec;
     zst[v] = reinterpret_cast<const u32x4_t*>(z + (int64_t)r * I + (int64_t)sbase * 128)[o];
   }
-  // 2. tiles: routed ones (ascending expert id) then the shared expert; lane t holds tile t's bases
+  // 2. tiles: routed ones (ascending expert id) then the shared expert; lane t
+  //    holds tile t's code and scale addresses for this row group and part
   const int nv = n_tiles[0];
   const int le = lane < K ? tile_expert[lane] : 0;  // issued with n_tiles (no dependence on it)
   const int nt = nv + has_shared;
   const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
   const bool lsh = lane >= nv;
-  const uint8_t* lw = lsh ? sh_p : d_p + (int64_t)le * ebytes;
-  const uint8_t* ls = lsh ? sh_s : d_s + (int64_t)le * sbytes;
+  // lane-independent part of tile t's addresses (broadcast by readlane; each lane adds its own offset)
+  const uint8_t* lw = (lsh ? sh_p : d_p + (int64_t)le * ebytes) + (int64_t)g * ns * 64 * 16 + (int64_t)sbase * 1024;
+  const uint8_t* ls = (lsh ? sh_s : d_s + (int64_t)le * sbytes) + (int64_t)g * ns4 * 64 * 4 +
+                      (int64_t)(sbase >> 2) * 256;
   const int lrow = lsh ? K : lane;
   const uint64_t lw_u = reinterpret_cast<uint64_t>(lw), ls_u = reinterpret_cast<uint64_t>(ls);
-  auto tile_base = [&](int t, const uint8_t*& wp, const uint8_t*& sp) {
-    const uint32_t wlo = __builtin_amdgcn_readlane((int)(uint32_t)lw_u, t);
-    const uint32_t whi = __builtin_amdgcn_readlane((int)(uint32_t)(lw_u >> 32), t);
-    const uint32_t slo = __builtin_amdgcn_readlane((int)(uint32_t)ls_u, t);
-    const uint32_t shi = __builtin_amdgcn_readlane((int)(uint32_t)(ls_u >> 32), t);
-    wp = reinterpret_cast<const uint8_t*>(((uint64_t)whi << 32) | wlo) + ((int64_t)g * ns * 64 + lane) * 16;
-    sp = reinterpret_cast<const uint8_t*>(((uint64_t)shi << 32) | slo) + ((int64_t)g * ns4 * 64 + lane) * 4;
-  };
-  const int N = nt * nsp;
-  const int nchunks = (N + D - 1) / D;
-  u32x4_t r_w[D];
-  uint32_t r_s[D];
-  auto load_entry = [&](int n, u32x4_t& wv, uint32_t& sv) {
-    const int nn = n < N ? n : 0;  // padded entries reload entry 0 and get scale 0
-    const int t = nn / nsp, S = sbase + (nn - t * nsp);
-    const uint8_t* wp;
-    const uint8_t* sp;
-    tile_base(t, wp, sp);
-    wv = load_nt_u32x4(wp + (int64_t)S * 1024);
-    sv = *reinterpret_cast<const uint32_t*>(sp + (int64_t)(S >> 2) * 256);
-  };
-  if (N > 0) {
+  const int nchunks = (nt + DT - 1) / DT;
+  u32x4_t r_w[DT][NSP];
+  uint32_t r_s[DT];
+  auto load_tile = [&](int t, u32x4_t (&wv)[NSP], uint32_t& sv) {
+    const int tt = t < nt ? t : 0;  // padded tiles reload tile 0 and get scale 0
+    const uint8_t* wp = reinterpret_cast<const uint8_t*>(
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lw_u >> 32), tt) << 32) |
+        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lw_u, tt));
+    const uint8_t* sp = reinterpret_cast<const uint8_t*>(
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ls_u >> 32), tt) << 32) |
+        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ls_u, tt));
 #pragma unroll
-    for (int s = 0; s < D; ++s) load_entry(s, r_w[s], r_s[s]);
+    for (int u = 0; u < NSP; ++u) wv[u] = load_nt_u32x4(wp + lane * 16 + u * 1024);
+    sv = *reinterpret_cast<const uint32_t*>(sp + lane * 4);
+  };
+  if (nt > 0) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) load_tile(d, r_w[d], r_s[d]);
   }
-  // 3. z parts -> wave-private LDS: row r at zs + r * nsp * 256
-  uint8_t* zs = dec_smem + (size_t)w * nz * nsp * 256;
+  // 3. z parts -> wave-private LDS: row r at zs + r * NSP * 256
+  uint8_t* zs = dec_smem + (size_t)w * nz * NSP * 256;
 #pragma unroll
   for (int v = 0; v < ZV; ++v) {
     const int i = lane + 64 * v;
@@ -277,26 +277,25 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
   float ysum = 0.f;
   auto chunk = [&](int ch, auto more) {
 #pragma unroll
-    for (int s = 0; s < D; ++s) {
-      const int n = ch * D + s;
-      const bool real = n < N;
-      const int nn = real ? n : 0;
-      const int t = nn / nsp, sl = nn - t * nsp;
-      const int row = __builtin_amdgcn_readlane(lrow, t);
-      u32x4_t xv[4];
-      dec_x(zs + (size_t)row * nsp * 256, sl, q, xv);
-      const int S = sbase + sl;
-      const uint32_t sb = real ? (r_s[s] >> (8 * (S & 3))) & 0xFFu : 0u;
-      dec_mfma(r_w[s], sb, xv, part);
-      // last step of this expert: fold its partial into the sum (selects, no branch)
-      const bool fold = real && sl == nsp - 1;
-      ysum += fold ? part[0] : 0.f;
+    for (int d = 0; d < DT; ++d) {
+      const int t = ch * DT + d;
+      const bool real = t < nt;
+      const int row = __builtin_amdgcn_readlane(lrow, real ? t : 0);
+      const uint8_t* zr = zs + (size_t)row * NSP * 256;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) part[r] = fold ? 0.f : part[r];
-      if constexpr (decltype(more)::value) load_entry(n + D, r_w[s], r_s[s]);
+      for (int u = 0; u < NSP; ++u) {
+        u32x4_t xv[4];
+        dec_x(zr, u, q, xv);
+        const uint32_t sb = real ? (r_s[d] >> (8 * ((sbase + u) & 3))) & 0xFFu : 0u;
+        dec_mfma(r_w[d][u], sb, xv, part);
+      }
+      // this expert's partial is complete: fold it into the sum (selects, no branch)
+      ysum += real ? part[0] : 0.f;
+      part = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (decltype(more)::value) load_tile(t + DT, r_w[d], r_s[d]);
     }
   };
-  if (N > 0) {
+  if (nt > 0) {
     for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
     chunk(nchunks - 1, std::false_type{});
   }
@@ -405,18 +404,18 @@ static void launch_dec1_gateup_x(int D, dim3 grid, size_t lds, hipStream_t st, c
 #undef DEC_GU
 }
 
-template <int KS, int ZV>
-static void launch_dec1_down_z(int D, dim3 grid, size_t lds, hipStream_t st, const uint16_t* z, const int32_t* te,
+template <int KS, int NSP, int ZV>
+static void launch_dec1_down_z(int DT, dim3 grid, size_t lds, hipStream_t st, const uint16_t* z, const int32_t* te,
                                const int32_t* nt, const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_p,
                                const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared) {
-#define DEC_DN(DV)                                                                                                 \
-  hipLaunchKernelGGL((moe_dec1_down_kernel<KS, DV, ZV>), grid, dim3(KS * 64), lds, st, z, te, nt, d_p, d_s, sh_p, \
-                     sh_s, y, H, I, E, K, has_shared)
-  switch (D) {
-    case 6: DEC_DN(6); break;
+#define DEC_DN(DV)                                                                                           \
+  hipLaunchKernelGGL((moe_dec1_down_kernel<KS, NSP, DV, ZV>), grid, dim3(KS * 64), lds, st, z, te, nt, d_p, \
+                     d_s, sh_p, sh_s, y, H, I, E, K, has_shared)
+  switch (DT) {
     case 4: DEC_DN(4); break;
     case 3: DEC_DN(3); break;
-    default: DEC_DN(2); break;
+    case 2: DEC_DN(2); break;
+    default: DEC_DN(1); break;
   }
 #undef DEC_DN
 }
@@ -457,8 +456,14 @@ void launch_linear_decode1(const uint16_t* x, const uint8_t* pt, const uint8_t* 
 }
 
 constexpr int kDecGuKS = 2;   // gate/up: waves (K parts) per workgroup (all workgroups resident: routing latency paid once)
-// down: waves (K parts) per workgroup, 8 when inter / 128 allows it, else 4
-static int dec_dn_ks(int64_t nsi) { return nsi % 8 == 0 ? 8 : (nsi % 4 == 0 ? 4 : 0); }
+// down: K parts per workgroup and super-steps per part (a part must sit inside
+// one 4-step scale dword): 4 waves of 1, 2 or 4 (inter 512, 1024, 2048), 8 of
+// 4 (4096); 0 = not handled
+static int dec_dn_ks(int64_t nsi) {
+  if (nsi == 32) return 8;
+  if (nsi == 4 || nsi == 8 || nsi == 16) return 4;
+  return 0;
+}
 
 bool moe_decode1_supported(int64_t m, int64_t hidden, int64_t inter, int64_t top_k, int has_shared) {
   if (m != 1 || top_k < 1 || top_k > kRouteMaxTopK) return false;
@@ -501,26 +506,28 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
 #undef GU_ARGS
   MOSAIC_LAUNCH_CHECK("moe_decode1_gateup");
   mark(2);
-  const int ndn = nz * dn_part;
-  const int dd = ndn % 6 == 0 ? 6 : (ndn % 4 == 0 ? 4 : (ndn % 3 == 0 ? 3 : 2));
-  const int zv = (ndn * 16 + 63) / 64;
-#define DN_ARGS dd, dim3((unsigned)(H / 16)), (size_t)nz * I * 2, st, z, tile_expert, n_tiles, d_p, d_s, sh_d_p, \
+  // ring of 3 tiles (DT * NSP super-steps in flight), 4 when a part is one step
+  const int dt = dn_part == 1 ? 4 : 3;
+  const int zv = (nz * dn_part * 16 + 63) / 64;
+#define DN_ARGS dt, dim3((unsigned)(H / 16)), (size_t)nz * I * 2, st, z, tile_expert, n_tiles, d_p, d_s, sh_d_p, \
                 sh_d_s, y, (int)H, (int)I, (int)E, (int)K, has_shared
+#define DN_Z(KSV, NSPV)                                  \
+  if (zv <= 5)                                           \
+    launch_dec1_down_z<KSV, NSPV, 5>(DN_ARGS);           \
+  else if (zv <= 10)                                     \
+    launch_dec1_down_z<KSV, NSPV, 10>(DN_ARGS);          \
+  else                                                   \
+    launch_dec1_down_z<KSV, NSPV, kDecZVMax>(DN_ARGS);
   if (dn_ks == 8) {
-    if (zv <= 5)
-      launch_dec1_down_z<8, 5>(DN_ARGS);
-    else if (zv <= 10)
-      launch_dec1_down_z<8, 10>(DN_ARGS);
-    else
-      launch_dec1_down_z<8, kDecZVMax>(DN_ARGS);
+    DN_Z(8, 4)
+  } else if (dn_part == 4) {
+    DN_Z(4, 4)
+  } else if (dn_part == 2) {
+    DN_Z(4, 2)
   } else {
-    if (zv <= 5)
-      launch_dec1_down_z<4, 5>(DN_ARGS);
-    else if (zv <= 10)
-      launch_dec1_down_z<4, 10>(DN_ARGS);
-    else
-      launch_dec1_down_z<4, kDecZVMax>(DN_ARGS);
+    DN_Z(4, 1)
   }
+#undef DN_Z
 #undef DN_ARGS
   MOSAIC_LAUNCH_CHECK("moe_decode1_down");
   mark(3);
