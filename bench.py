@@ -35,6 +35,13 @@ GU_BYTES = 2 * I * (H // 2 + H // 32)   # gate+up codes and scales of one expert
 DN_BYTES = H * (I // 2 + I // 32)       # down codes and scales of one expert
 EXPERT_BYTES = GU_BYTES + DN_BYTES      # 23,396,352
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of moe_dec1_gateup_kernel (the M = 1 roofline kernel),
+# from two rocprofv3 --pmc passes over this script (FETCH_SIZE, then
+# WRITE_SIZE, KiB per dispatch, averaged over the timed dispatches), each
+# scaled by what the same counter reads for --calibration-copy-mib 256:
+# FETCH_SIZE x 2.0, WRITE_SIZE x 1.0.  The profile summary
+# profiles/moe_decode_m1_traffic.md holds the commands and raw figures.
+GATEUP_M1_TRAFFIC_BYTES = (68782 * 2.0 + 36.1) * 1024
 METRIC = "MXFP4 MoE-layer decode µs & HBM GB/s % peak; FP8/MXFP4 GEMM TFLOPS % peak"
 
 
@@ -47,6 +54,9 @@ def parse():
     ap.add_argument("--sweep", default="4,16,64", help="extra M values reported under m_sweep ('' to skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1, 3, 4, 5")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after the line is printed, copy a buffer of this many MiB device to device three times "
+                         "(a plain copy of known size that scales FETCH_SIZE / WRITE_SIZE counter passes)")
     return ap.parse_args()
 
 
@@ -358,13 +368,21 @@ def main():
         "roofline": {"kernel": "moe_dec1_gateup_kernel" if args.m == 1 else "moe_a16_gateup_kernel", "bound": "hbm",
                      "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_launch_us": round(main_r["gateup_us"], 2),
+                     "traffic": round(GATEUP_M1_TRAFFIC_BYTES) if args.m == 1 else None,
+                     "avg_launch_us": round(main_r["gateup_us"], 2),
                      "algorithmic_bytes_per_launch": round(main_r["gateup_bytes_per_launch"])},
         "cpu_baseline": cpu,
         "m_sweep": sweep,
         "configs": configs,
     }
-    print(json.dumps(line))
+    print(json.dumps(line), flush=True)
+    if args.calibration_copy_mib > 0:
+        src = torch.ones(args.calibration_copy_mib << 18, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
