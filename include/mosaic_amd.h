@@ -216,7 +216,7 @@ size_t mosaic_dsa_indexer_workspace_bytes(int64_t b, int64_t l);
  *   ascending); idx_out [b, topk] int32 = tokens by descending score, ties to
  *   the lower index, + offset; tokens t >= lengths[b] (lengths NULL = all l)
  *   are masked and missing slots are -1.  d == 128, h in {16, 32, 48, 64},
- *   topk <= 4096.  Non-finite q/k codes or scales give unspecified indices. */
+ *   topk <= 4096, l <= 2^24.  Non-finite q/k codes or scales give unspecified indices. */
 int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
                             const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h, int64_t d, int64_t l,
                             int64_t topk, int32_t offset, void* workspace, size_t workspace_bytes, void* stream);

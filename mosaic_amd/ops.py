@@ -506,7 +506,7 @@ def dsa_indexer_scores(q, q_s, k, k_s, w) -> torch.Tensor:
 
 
 def dsa_indexer_bounds(q, q_s, k, k_s, w) -> tuple[torch.Tensor, torch.Tensor]:
-    """The fp8-MFMA stage: (lo, hi) [B, L] f32 enclosing every canonical score."""
+    """The bound stage: (lo, hi) [B, L] f32 enclosing every canonical score."""
     q, q_s, k, k_s, w, b, h, d, l_ = _indexer_args(q, q_s, k, k_s, w)
     lo = torch.empty(b, l_, dtype=torch.float32, device=q.device)
     hi = torch.empty_like(lo)

@@ -81,6 +81,33 @@ def test_indexer_bounds_enclose_exact(dev):
     assert np.median(hi - lo) < 0.2 * s.std()  # tight enough to prune
 
 
+def test_indexer_bounds_enclose_wide_product_spans(dev):
+    """Dots whose products span many binades inside every run of 8 K: one
+    448 x 448 product next to seven products of 7.875 (0.017578 x 448), so a
+    sum kept to ~14 bits below the largest product would drop all seven.  Also
+    uniformly random finite codes (products from 2^-18 to 2^17.6).  The
+    interval must contain the canonical score for every token."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(21)
+    b, h, l = 2, 64, 4096
+    big, small = C.e4m3_encode(np.array([448.0, 0.017578125], np.float32))
+    q = np.full((b, h, 128), small, dtype=np.uint8)
+    q[:, :, ::8] = big
+    k = np.full((b, l, 128), big, dtype=np.uint8)
+    k[1] = _finite_codes(rng, (l, 128))
+    q[1, 32:] = _finite_codes(rng, (h - 32, 128))
+    k[0, l // 2:, 1::8] ^= 0x80     # negative small products in half the rows
+    qs = (rng.random((b, h)) + 0.5).astype(np.float32)
+    ks = (rng.random((b, l)) + 0.5).astype(np.float32)
+    w = np.abs(rng.standard_normal((b, h))).astype(np.float32)
+    lo, hi = ops.dsa_indexer_bounds(*_t(dev, q, qs, k, ks, w))
+    lo, hi = lo.cpu().numpy(), hi.cpu().numpy()
+    s = D.indexer_scores(q, qs, k, ks, w)
+    assert np.all(lo <= s) and np.all(s <= hi), f"{int((lo > s).sum() + (s > hi).sum())} scores outside their interval"
+    idx = ops.dsa_indexer_topk(*_t(dev, q, qs, k, ks, w), 512).cpu().numpy()
+    np.testing.assert_array_equal(idx, D.indexer_topk(q, qs, k, ks, w, 512))
+
+
 @pytest.mark.parametrize("b,l,topk", [(2, 32768, 2048), (1, 5000, 512), (3, 1000, 2048), (1, 64, 16)])
 def test_indexer_topk_bit_exact(dev, b, l, topk):
     from mosaic_amd import ops
