@@ -91,6 +91,15 @@ __device__ __forceinline__ float abs_sum_fp8(const i32x8_t v) {
   return s;
 }
 
+// Sum over the four lanes c, c + 16, c + 32, c + 48 of a 16-column MFMA result
+// (v_permlane16/32_swap: no LDS round trip), the same value in all four.
+__device__ __forceinline__ float sum_lane_quad(float x) {
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
 // The 32 e4m3 codes of one fp8 MFMA operand lane -> 4 x 8 bf16 (exact), chunk
 // kc = code bytes [8 kc, 8 kc + 8); `neg` flips every sign.
 __device__ __forceinline__ void fp8x32_to_bf16(const i32x8_t v, bf16x8_t (&out)[4], bool neg) {
@@ -149,14 +158,14 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     float* __restrict__ lo, float* __restrict__ hi, uint32_t* __restrict__ hist1, int64_t L) {
   constexpr int H = HT * 16;
   constexpr int GT = 16 * U;  // tokens per group
-  __shared__ uint32_t lh[kHistBins + 64];  // + one dummy bin per lane
+  __shared__ uint32_t lh[kHistBins];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int c = lane & 15, qq = lane >> 4;
   const int64_t n = row_length(lengths, b, L);
   if (hist1) {
-    for (int i = threadIdx.x; i < kHistBins + 64; i += 256) lh[i] = 0u;
+    for (int i = threadIdx.x; i < kHistBins; i += 256) lh[i] = 0u;
     __syncthreads();
   }
   const uint8_t* qb = q + (int64_t)b * H * kIdxD;
@@ -198,13 +207,15 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     const int nt = group_tokens(g);
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kb + g * GT * kIdxD, nt * kIdxD);
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(ksb + g * GT, nt * 4);
+    // the scales first: the wait for a group's codes then covers them too
+#pragma unroll
+    for (int u = 0; u < U; ++u) sr[s][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (16 * u + c) * 4, 0, 0));
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int off = (16 * u + c) * kIdxD + 16 * qq;
       const u32x4_t a0 = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
       const u32x4_t a1 = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64, 0, 0);
       kr[s][u] = i32x8_t{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-      sr[s][u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (16 * u + c) * 4, 0, 0));
     }
   };
   auto compute = [&](int s, int64_t i) {
@@ -229,18 +240,22 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     for (int u = 0; u < U; ++u) {
       // with d' = d sign(q_scale): max(d q_scale k_scale, 0) w
       //   = |q_scale k_scale| w (|d'| + sign(k_scale) d') / 2
-      float sa = 0.f, sb = 0.f;
+      // partial sums per head row r (independent chains), then across r and lanes
+      float pa[4], pb[4];
 #pragma unroll
-      for (int j = 0; j < HT; ++j)
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = cw[0][r] * fabsf(d[u][0][r]);
+        pb[r] = cw[0][r] * d[u][0][r];
+      }
+#pragma unroll
+      for (int j = 1; j < HT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          sa = fmaf(cw[j][r], fabsf(d[u][j][r]), sa);
-          sb = fmaf(cw[j][r], d[u][j][r], sb);
+          pa[r] = fmaf(cw[j][r], fabsf(d[u][j][r]), pa[r]);
+          pb[r] = fmaf(cw[j][r], d[u][j][r], pb[r]);
         }
-      sa += __shfl_xor(sa, 16, 64);
-      sa += __shfl_xor(sa, 32, 64);
-      sb += __shfl_xor(sb, 16, 64);
-      sb += __shfl_xor(sb, 32, 64);
+      const float sa = sum_lane_quad((pa[0] + pa[1]) + (pa[2] + pa[3]));
+      const float sb = sum_lane_quad((pb[0] + pb[1]) + (pb[2] + pb[3]));
       const float ksu = sr[s][u];
       const float part = 0.5f * fabsf(ksu) * (ksu < 0.f ? sa - sb : sa + sb);
       const float e = fabsf(sr[s][u]) * qbound;
@@ -249,10 +264,7 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
       const int off = qq == 0 ? (16 * u + c) * 4 : 0x40000000;
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l), rl, off, 0, 0);
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h), rh, off, 0, 0);
-      if (hist1) {
-        const bool real = qq == 0 && 16 * u + c < nt;
-        atomicAdd(&lh[real ? key_low_nan(l) >> kHistShift : kHistBins + lane], real ? 1u : 0u);
-      }
+      if (hist1 && qq == 0 && 16 * u + c < nt) atomicAdd(&lh[key_low_nan(l) >> kHistShift], 1u);
     }
   };
   if (iters > 0) {
@@ -974,14 +986,15 @@ static size_t indexer_ws(int64_t b, int64_t l, char* base, IndexerWs* w) {
   return off;
 }
 
-// Bound kernel shape: U = 2 tiles per group; about 2048 resident waves (its
-// register use leaves two waves per SIMD on 256 CUs) spread over the rows, at
-// least one group per wave; the ring depth D is the per-wave group count, capped at 4.
-constexpr int kBoundU = 2;
+// Bound kernel shape: one 16-token tile per group, a ring of up to 4 groups
+// (its registers then leave three waves per SIMD: about 3072 resident waves on
+// 256 CUs) spread over the rows, and at least one full ring per wave where the
+// rows are short (each workgroup merges its whole histogram once).
+constexpr int kBoundU = 1;
 static void bound_shape(int64_t b, int64_t l, int& gx, int& depth) {
   const int64_t groups = (l + 16 * kBoundU - 1) / (16 * kBoundU);
-  int64_t g = (512 + b - 1) / b;
-  g = std::min<int64_t>(g, (groups + 3) / 4);
+  int64_t g = (768 + b - 1) / b;
+  g = std::min<int64_t>(g, (groups + 15) / 16);
   gx = (int)std::max<int64_t>(g, 1);
   const int64_t iters = (groups + 4 * gx - 1) / (4 * gx);
   depth = iters >= 4 ? 4 : (iters >= 2 ? 2 : 1);
