@@ -279,6 +279,118 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
                      (int)n, (int)k, out_f32);
 }
 
+// Large tiled kernel (enough 256 x 256 tiles to fill the chip): a workgroup
+// of 8 waves owns a 256 x 256 block of C; wave w owns rows 128 (w >> 2) and
+// columns 64 (w & 3) of it (8 x 4 MFMA tiles, 128 accumulators).  Twice the
+// columns of the 256 x 128 kernel for the same A block: 262 instead of 175
+// flops per byte copied into LDS, and 0.75 instead of 1 KB of LDS operand
+// reads per MFMA.  A stage (A and B blocks, 256 a_s values, the two b_s values
+// of the block's column halves) is 66.8 KB, so the ring holds two stages, one
+// K-block ahead; copies, swizzle and XCD grouping as in the kernel above.
+struct Fp8Big {
+  static constexpr int BM = 256, BN = 256, NT = 512, NW = 8;
+  static constexpr int AB = (BM + BN) * 128;    // A and B bytes of a stage
+  static constexpr int SA = AB;                  // a_s: 256 floats
+  static constexpr int SB = SA + BM * 4;         // b_s: 32 copies of each column half's value
+  static constexpr int STAGE = SB + 256;
+  static constexpr int RUNS = AB / 1024 / NW;    // 8 one-KB A/B runs per wave per stage
+  static constexpr int SRUNS = BM / 64;          // 4 a_s runs of 256 bytes
+  static constexpr int OPS = RUNS + 1;
+};
+
+__global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __restrict__ A,
+                                                              const float* __restrict__ As,
+                                                              const uint8_t* __restrict__ B,
+                                                              const float* __restrict__ Bs, void* __restrict__ C,
+                                                              int M, int N, int K, int out_f32) {
+  using TT = Fp8Big;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][TT::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  int tm, tn;
+  tile_coords(blockIdx.x, (M + TT::BM - 1) / TT::BM, (N + TT::BN - 1) / TT::BN, tm, tn);
+  const int m0 = tm * TT::BM, n0 = tn * TT::BN;
+  const int wm = (wv >> 2) * 128, wn = (wv & 3) * 64;
+  const int nkb = K / 128;
+  const uint8_t* gsrc[TT::RUNS];
+  int ldsoff[TT::RUNS];
+#pragma unroll
+  for (int ii = 0; ii < TT::RUNS; ++ii) {
+    const int i = wv * TT::RUNS + ii;  // run i: 8 rows of A (i < 32) or of B
+    const int row = (i < TT::BM / 8 ? 8 * i : 8 * (i - TT::BM / 8)) + (lane >> 3);
+    const int logical = (lane & 7) ^ ((row >> 1) & 7);
+    gsrc[ii] = i < TT::BM / 8 ? A + (int64_t)min(m0 + row, M - 1) * K + logical * 16
+                              : B + (int64_t)min(n0 + row, N - 1) * K + logical * 16;
+    ldsoff[ii] = i * 1024;
+  }
+  // scale copies: waves 0..3 take 64 a_s rows each; the others copy the two
+  // b_s values of the block (lanes 0..31 the first column half, 32..63 the second)
+  const float* ssrc;
+  int sdst;
+  if (wv < TT::SRUNS) {
+    ssrc = As + (int64_t)min(m0 + 64 * wv + lane, M - 1) * nkb;
+    sdst = TT::SA + 256 * wv;
+  } else {
+    const int nb = min(n0 / 128 + (lane >> 5), (N - 1) / 128);
+    ssrc = Bs + (int64_t)nb * nkb;
+    sdst = TT::SB;
+  }
+  auto issue = [&](int st, int kb) {
+    const uint32_t base = fp8_lds_addr(lds[st]);
+#pragma unroll
+    for (int ii = 0; ii < TT::RUNS; ++ii) fp8_copy16(gsrc[ii] + (int64_t)kb * 128, base + ldsoff[ii]);
+    fp8_copy4(ssrc + kb, base + sdst);
+  };
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  issue(0, 0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    // block kb landed for every wave, and every wave is done with block kb - 1
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kb + 1 < nkb) issue((kb + 1) & 1, kb + 1);
+    const uint8_t* stg = lds[kb & 1];
+    const uint8_t* ta = stg;
+    const uint8_t* tb = stg + TT::BM * 128;
+    const float sb = *reinterpret_cast<const float*>(stg + TT::SB + (wn >= 128 ? 128 : 0));
+    i32x8_t bop[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) bop[nt] = lds_fp8_operand(tb, wn + 16 * nt + c, q);
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const i32x8_t aop = lds_fp8_operand(ta, wm + 16 * mt + c, q);
+      f32x4_t d[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(aop, bop[nt]);
+      const f32x4_t sa4 = *reinterpret_cast<const f32x4_t*>(stg + TT::SA + 4 * (wm + 16 * mt + 4 * q));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float s = sa4[r] * sb;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt][r] = __builtin_fmaf(d[nt][r], s, acc[mt][nt][r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int n = n0 + wn + 16 * nt + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm + 16 * mt + 4 * q + r;
+        if (m < M && n < N) {
+          if (out_f32)
+            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[mt][nt][r];
+          else
+            reinterpret_cast<uint16_t*>(C)[(int64_t)m * N + n] = f32_bf16(acc[mt][nt][r]);
+        }
+      }
+    }
+}
+
 // w [N, K] e4m3 with one fp32 scale per (bn x bk) block -> bf16 [N, K]
 __global__ void __launch_bounds__(256) fp8_block_dequant_kernel(const uint8_t* __restrict__ w,
                                                                 const float* __restrict__ s,
@@ -328,6 +440,12 @@ extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const u
   const int f32 = out_dtype == MOSAIC_DTYPE_F32;
   const int64_t mt = (m + 15) / 16;
   if (m >= 256) {
+    const int64_t big_tiles = ((m + 255) / 256) * ((n + 255) / 256);
+    if (big_tiles >= 256) {
+      hipLaunchKernelGGL(fp8_gemm_big_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a, a_s, b, b_s, c, (int)m,
+                         (int)n, (int)k, f32);
+      MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
+    }
     launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st);
     MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
   }
