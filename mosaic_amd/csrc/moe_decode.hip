@@ -11,12 +11,13 @@
 //    in wave-private LDS.  The parts meet in LDS; SwiGLU and the route weight
 //    are applied and z row `tile` is written (the shared expert's row is K).
 // 2. moe_dec1_down_kernel: a workgroup owns 16 hidden columns and walks every
-//    tile (experts in ascending id, the shared expert last); its waves again
+//    tile (the shared expert first, then the experts in ascending id); its waves again
 //    split K (= inter) and stream (tile, super-step) entries through a ring, with
 //    the z parts staged in wave-private LDS.  Each expert's partial (a fresh
-//    MFMA chain) is added to the running fp32 sum in tile order, so the combine
-//    of the reference (ascending expert id, shared last, fp32) happens in
-//    registers and y is written directly: no partial buffer, no combine launch.
+//    MFMA chain) is added to the running fp32 sum of the routed tiles in order,
+//    and the shared partial after it, so the combine of the reference
+//    (ascending expert id, shared last, fp32) happens in registers and y is
+//    written directly: no partial buffer, no combine launch.
 //
 // Rows: the decode batch has one token, so the x / z operand is row 0 in every
 // lane (all 16 MFMA rows carry the same data and only row 0 is stored).
@@ -234,37 +235,47 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
     const int r = i / pvec, o = i - r * pvec;
     zst[v] = reinterpret_cast<const u32x4_t*>(z + (int64_t)r * I + (int64_t)sbase * 128)[o];
   }
-  // 2. tiles: routed ones (ascending expert id) then the shared expert; lane t
-  //    holds tile t's code and scale addresses for this row group and part
-  const int nv = n_tiles[0];
-  const int le = lane < K ? tile_expert[lane] : 0;  // issued with n_tiles (no dependence on it)
-  const int nt = nv + has_shared;
+  // 2. tiles: the shared expert first (its addresses need no tile list, so its
+  //    loads go out at once), then the routed ones in ascending expert id; lane
+  //    r holds routed tile r's code and scale addresses for this row group and
+  //    part.  The shared partial is kept apart and added after the routed sum,
+  //    so the fp32 combine order is still ascending id, shared last.
   const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
-  const bool lsh = lane >= nv;
-  // lane-independent part of tile t's addresses (broadcast by readlane; each lane adds its own offset)
-  const uint8_t* lw = (lsh ? sh_p : d_p + (int64_t)le * ebytes) + (int64_t)g * ns * 64 * 16 + (int64_t)sbase * 1024;
-  const uint8_t* ls = (lsh ? sh_s : d_s + (int64_t)le * sbytes) + (int64_t)g * ns4 * 64 * 4 +
-                      (int64_t)(sbase >> 2) * 256;
-  const int lrow = lsh ? K : lane;
-  const uint64_t lw_u = reinterpret_cast<uint64_t>(lw), ls_u = reinterpret_cast<uint64_t>(ls);
-  const int nchunks = (nt + DT - 1) / DT;
+  const int64_t woff = (int64_t)g * ns * 64 * 16 + (int64_t)sbase * 1024;
+  const int64_t soff = (int64_t)g * ns4 * 64 * 4 + (int64_t)(sbase >> 2) * 256;
   u32x4_t r_w[DT][NSP];
   uint32_t r_s[DT];
+  if (has_shared) {
+#pragma unroll
+    for (int u = 0; u < NSP; ++u) r_w[0][u] = load_nt_u32x4(sh_p + woff + lane * 16 + u * 1024);
+    r_s[0] = *reinterpret_cast<const uint32_t*>(sh_s + soff + lane * 4);
+  }
+  const int nv = n_tiles[0];
+  const int le = lane < nv ? tile_expert[lane] : 0;  // lanes past the valid tiles: expert 0 (valid memory)
+  const int nt = nv + has_shared;
+  const uint8_t* lw = d_p + (int64_t)le * ebytes + woff;
+  const uint8_t* ls = d_s + (int64_t)le * sbytes + soff;
+  const uint64_t lw_u = reinterpret_cast<uint64_t>(lw), ls_u = reinterpret_cast<uint64_t>(ls);
+  const int nchunks = (nt + DT - 1) / DT;
+  // ring entry t >= has_shared is routed tile t - has_shared; padded entries
+  // (t >= nt) reload lane 0's tile and get scale 0 (selects only: the ring
+  // issues its loads without branches)
   auto load_tile = [&](int t, u32x4_t (&wv)[NSP], uint32_t& sv) {
-    const int tt = t < nt ? t : 0;  // padded tiles reload tile 0 and get scale 0
+    const int rt = t < nt ? t - has_shared : 0;
     const uint8_t* wp = reinterpret_cast<const uint8_t*>(
-        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lw_u >> 32), tt) << 32) |
-        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lw_u, tt));
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lw_u >> 32), rt) << 32) |
+        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lw_u, rt));
     const uint8_t* sp = reinterpret_cast<const uint8_t*>(
-        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ls_u >> 32), tt) << 32) |
-        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ls_u, tt));
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ls_u >> 32), rt) << 32) |
+        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ls_u, rt));
 #pragma unroll
     for (int u = 0; u < NSP; ++u) wv[u] = load_nt_u32x4(wp + lane * 16 + u * 1024);
     sv = *reinterpret_cast<const uint32_t*>(sp + lane * 4);
   };
   if (nt > 0) {
 #pragma unroll
-    for (int d = 0; d < DT; ++d) load_tile(d, r_w[d], r_s[d]);
+    for (int d = 0; d < DT; ++d)
+      if (d > 0 || !has_shared) load_tile(d, r_w[d], r_s[d]);
   }
   // 3. z parts -> wave-private LDS: row r at zs + r * NSP * 256
   uint8_t* zs = dec_smem + (size_t)w * nz * NSP * 256;
@@ -274,13 +285,14 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
     if (i < nvec) reinterpret_cast<u32x4_t*>(zs)[i] = zst[v];
   }
   f32x4_t part = {0.f, 0.f, 0.f, 0.f};
-  float ysum = 0.f;
+  float ysum = 0.f, ysh = 0.f;
   auto chunk = [&](int ch, auto more) {
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
       const int t = ch * DT + d;
       const bool real = t < nt;
-      const int row = __builtin_amdgcn_readlane(lrow, real ? t : 0);
+      const bool shared_t = has_shared && t == 0;
+      const int row = shared_t ? K : (real ? t - has_shared : 0);
       const uint8_t* zr = zs + (size_t)row * NSP * 256;
 #pragma unroll
       for (int u = 0; u < NSP; ++u) {
@@ -289,8 +301,9 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
         const uint32_t sb = real ? (r_s[d] >> (8 * ((sbase + u) & 3))) & 0xFFu : 0u;
         dec_mfma(r_w[d][u], sb, xv, part);
       }
-      // this expert's partial is complete: fold it into the sum (selects, no branch)
-      ysum += real ? part[0] : 0.f;
+      // this expert's partial is complete: fold it in (selects, no branch)
+      ysh = shared_t ? part[0] : ysh;
+      ysum += (real && !shared_t) ? part[0] : 0.f;
       part = f32x4_t{0.f, 0.f, 0.f, 0.f};
       if constexpr (decltype(more)::value) load_tile(t + DT, r_w[d], r_s[d]);
     }
@@ -299,6 +312,7 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
     for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
     chunk(nchunks - 1, std::false_type{});
   }
+  ysum += ysh;
   if (q == 0) red[w][c] = ysum;
   __syncthreads();
   if (w == 0 && q == 0) {
