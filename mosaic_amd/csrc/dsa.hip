@@ -717,9 +717,9 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
 }
 
 // ===================================================================== MLA
-constexpr int kMlaBT = 64;        // tokens per online-softmax block
+constexpr int kMlaBT = 32;        // tokens per online-softmax block
 constexpr int kMlaDl = 512;       // latent (value) width
-constexpr int kVtStride = 72;     // bf16 per V^T row (64 tokens + 8)
+constexpr int kVtStride = 40;     // bf16 per V^T row (32 tokens + 8)
 
 __device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t a, const bf16x8_t b, const f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -741,16 +741,27 @@ struct MlaKv {
 // One split (a contiguous slice of the selected tokens) of one query row and
 // one group of 16*NW heads: partial (m, l, O) per head.  Waves own 16 heads;
 // with at most 4 waves a workgroup runs one wave per SIMD, which leaves room
-// for each wave's 16x512 fp32 O tile in accumulation registers.
+// for each wave's 16x512 fp32 O tile in accumulation registers.  Blocks of
+// kMlaBT tokens go through two LDS buffers: while block i is multiplied out of
+// one, block i + 1's raw KV rows are already in registers (loaded before the
+// math) and are converted into the other after it; the token ids are read two
+// blocks ahead.  A thread gathers one (token, 64-wide latent segment) item and
+// one 16-byte rope chunk per block.
 template <int NW, bool FP8, int DR>
 __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     const uint16_t* __restrict__ q, const MlaKv kv, const int32_t* __restrict__ idx, float* __restrict__ part_o,
     float* __restrict__ part_ml, int topk, float scale, int chunk) {
   constexpr int DQK = kMlaDl + DR;
   constexpr int KS = DQK + 8;  // bf16 per K row in LDS: 16-byte reads of 16 rows hit distinct banks
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[kMlaBT * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kMlaDl * kVtStride];
-  __shared__ int tok_id[kMlaBT];
+  constexpr int NT = NW * 64;
+  constexpr int ITEMS = kMlaBT * 8;               // (token, segment) items per block
+  constexpr int IPT = (ITEMS + NT - 1) / NT;      // items per thread
+  constexpr int RCH = kMlaBT * (DR / 8);          // 16-byte rope chunks per block
+  constexpr int RPT = DR > 0 ? (RCH + NT - 1) / NT : 0;
+  constexpr int RAWV = FP8 ? 4 : 8;               // 16-byte vectors per item
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[2][kMlaBT * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kMlaDl * kVtStride];
+  __shared__ int tok_id[2][kMlaBT];
   const int H = NW * 16 * gridDim.z;
   const int split = blockIdx.x, b = blockIdx.y, S = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -759,6 +770,9 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   const int head = 16 * hw + c;
   const int64_t n = kv.n;
   const int64_t kvb = b / kv.rows_per_kv;
+  const int t_begin = split * chunk;
+  const int t_end = min(topk, t_begin + chunk);
+  const int nblk = t_end > t_begin ? (t_end - t_begin + kMlaBT - 1) / kMlaBT : 0;
   // q as the B operand of S^T = K Q^T: lane (c, qd) holds q[head][32 s + 8 qd .. +8]
   bf16x8_t qb[DQK / 32];
   {
@@ -766,98 +780,158 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
 #pragma unroll
     for (int s = 0; s < DQK / 32; ++s) qb[s] = *reinterpret_cast<const bf16x8_t*>(qrow + 32 * s + 8 * qd);
   }
-  f32x4_t o[kMlaDl / 16];
+  // token id of a block's slot (-1: masked or past the split)
+  auto token = [&](int blk, int slot) -> int {
+    const int ti = t_begin + blk * kMlaBT + slot;
+    const int id = (blk < nblk && ti < t_end) ? idx[(int64_t)b * topk + ti] : -1;
+    return (id >= 0 && (int64_t)id < n) ? id : -1;
+  };
+  // this thread's items: latent (token it % kMlaBT, segment it / kMlaBT) and rope chunk
+  int iid[IPT], rid[RPT > 0 ? RPT : 1];
+  u32x4_t raw[IPT][RAWV];
+  float rsc[IPT][4];
+  u32x4_t rrope[RPT > 0 ? RPT : 1];
+  auto load_ids = [&](int blk, int (&ii)[IPT], int (&ri)[RPT > 0 ? RPT : 1]) {
 #pragma unroll
-  for (int i = 0; i < kMlaDl / 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  const int t_begin = split * chunk;
-  const int t_end = min(topk, t_begin + chunk);
-  for (int t0 = t_begin; t0 < t_end; t0 += kMlaBT) {
-    __syncthreads();
-    if (tid < kMlaBT) {
-      const int ti = t0 + tid;
-      const int id = ti < t_end ? idx[(int64_t)b * topk + ti] : -1;
-      tok_id[tid] = (id >= 0 && (int64_t)id < n) ? id : -1;
+    for (int k = 0; k < IPT; ++k) {
+      const int it = tid + NT * k;
+      ii[k] = it < ITEMS ? token(blk, it % kMlaBT) : -1;
     }
-    __syncthreads();
-    // gather: (token, 64-wide latent segment) items -> bf16 rows of Kt and columns of Vt
-    for (int item = tid; item < kMlaBT * 8; item += NW * 64) {
-      const int tk = item >> 3, seg = item & 7;
-      const int id = tok_id[tk];
-      const bool ok = id >= 0;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int it = tid + NT * k;
+      ri[k] = it < RCH ? token(blk, it / (DR / 8)) : -1;
+    }
+  };
+  auto issue = [&](const int (&ii)[IPT], const int (&ri)[RPT > 0 ? RPT : 1]) {
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+      const int it = tid + NT * k, seg = it / kMlaBT;
+      const int64_t row = kvb * n + (ii[k] >= 0 ? ii[k] : 0);
+      if constexpr (FP8) {
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(kv.lat) + row * kMlaDl + seg * 64;
+        const float* ssrc = kv.lat_s + row * (kMlaDl >> kv.sb_shift);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          raw[k][v] = *reinterpret_cast<const u32x4_t*>(src + 16 * v);
+          rsc[k][v] = ssrc[(seg * 64 + 16 * v) >> kv.sb_shift];
+        }
+      } else {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(kv.lat) + row * DQK + seg * 64;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) raw[k][v] = *reinterpret_cast<const u32x4_t*>(src + 8 * v);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int it = tid + NT * k, pc = it % (DR / 8);
+      const int64_t row = kvb * n + (ri[k] >= 0 ? ri[k] : 0);
+      const uint16_t* src = FP8 ? kv.rope + row * DR : reinterpret_cast<const uint16_t*>(kv.lat) + row * DQK + kMlaDl;
+      rrope[k] = *reinterpret_cast<const u32x4_t*>(src + 8 * pc);
+    }
+  };
+  // raw registers -> bf16 rows of Kt and columns of Vt of buffer bf
+  auto fill = [&](int bf, const int (&ii)[IPT], const int (&ri)[RPT > 0 ? RPT : 1]) {
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+      const int it = tid + NT * k;
+      if (it >= ITEMS) continue;
+      const int tk = it % kMlaBT, seg = it / kMlaBT;
+      const bool ok = ii[k] >= 0;
       uint32_t outw[32];
-      if (ok) {
-        const int64_t row = kvb * n + id;
-        if constexpr (FP8) {
-          const uint8_t* src = reinterpret_cast<const uint8_t*>(kv.lat) + row * kMlaDl + seg * 64;
-          const float* ssrc = kv.lat_s + row * (kMlaDl >> kv.sb_shift);
+      if constexpr (FP8) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(src + 16 * v);
-            const float sc = ssrc[(seg * 64 + 16 * v) >> kv.sb_shift];
+        for (int v = 0; v < 4; ++v) {
+          const float sc = rsc[k][v];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[e], false);
-              const f32x2_t bb = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[e], true);
-              outw[8 * v + 2 * e] = (uint32_t)f32_bf16(a[0] * sc) | ((uint32_t)f32_bf16(a[1] * sc) << 16);
-              outw[8 * v + 2 * e + 1] = (uint32_t)f32_bf16(bb[0] * sc) | ((uint32_t)f32_bf16(bb[1] * sc) << 16);
-            }
-          }
-        } else {
-          const uint16_t* src = reinterpret_cast<const uint16_t*>(kv.lat) + row * DQK + seg * 64;
-#pragma unroll
-          for (int v = 0; v < 8; ++v) {
-            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(src + 8 * v);
-            outw[4 * v] = x[0];
-            outw[4 * v + 1] = x[1];
-            outw[4 * v + 2] = x[2];
-            outw[4 * v + 3] = x[3];
+          for (int e2 = 0; e2 < 4; ++e2) {
+            // exact e4m3 -> fp32, fp32 product with the scale, one RNE rounding to bf16
+            f32x2_t a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw[k][v][e2], false);
+            f32x2_t b2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw[k][v][e2], true);
+            a2[0] *= sc;
+            a2[1] *= sc;
+            b2[0] *= sc;
+            b2[1] *= sc;
+            outw[8 * v + 2 * e2] = __builtin_bit_cast(uint32_t, __builtin_convertvector(a2, bf16x2_t));
+            outw[8 * v + 2 * e2 + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(b2, bf16x2_t));
           }
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) outw[i] = 0u;
+        for (int v = 0; v < 8; ++v)
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) outw[4 * v + e2] = raw[k][v][e2];
       }
-      u32x4_t* kdst = reinterpret_cast<u32x4_t*>(Kt + tk * KS + seg * 64);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) outw[i] = ok ? outw[i] : 0u;
+      u32x4_t* kdst = reinterpret_cast<u32x4_t*>(&Kt[bf][tk * KS + seg * 64]);
 #pragma unroll
       for (int v = 0; v < 8; ++v) kdst[v] = u32x4_t{outw[4 * v], outw[4 * v + 1], outw[4 * v + 2], outw[4 * v + 3]};
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
-        Vt[(seg * 64 + 2 * i) * kVtStride + tk] = (uint16_t)(outw[i] & 0xFFFFu);
-        Vt[(seg * 64 + 2 * i + 1) * kVtStride + tk] = (uint16_t)(outw[i] >> 16);
+        Vt[bf][(seg * 64 + 2 * i) * kVtStride + tk] = (uint16_t)(outw[i] & 0xFFFFu);
+        Vt[bf][(seg * 64 + 2 * i + 1) * kVtStride + tk] = (uint16_t)(outw[i] >> 16);
       }
+      if (seg == 0) tok_id[bf][tk] = ii[k];
     }
-    if constexpr (DR > 0) {
-      for (int item = tid; item < kMlaBT * (DR / 8); item += NW * 64) {
-        const int tk = item / (DR / 8), pc = item % (DR / 8);
-        const int id = tok_id[tk];
-        const bool ok = id >= 0;
-        u32x4_t v = {0u, 0u, 0u, 0u};
-        if (ok) {
-          const int64_t row = kvb * n + id;
-          const uint16_t* src = FP8 ? kv.rope + row * DR : reinterpret_cast<const uint16_t*>(kv.lat) + row * DQK + kMlaDl;
-          v = *reinterpret_cast<const u32x4_t*>(src + 8 * pc);
-        }
-        *reinterpret_cast<u32x4_t*>(Kt + tk * KS + kMlaDl + 8 * pc) = v;
-      }
-    }
-    __syncthreads();
-    // S^T tiles (rows = tokens 16 j + 4 qd + r, column = head c)
-    f32x4_t st[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < RPT; ++k) {
+      const int it = tid + NT * k;
+      if (it >= RCH) continue;
+      const int tk = it / (DR / 8), pc = it % (DR / 8);
+      const u32x4_t v = ri[k] >= 0 ? rrope[k] : u32x4_t{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(&Kt[bf][tk * KS + kMlaDl + 8 * pc]) = v;
+    }
+  };
+  f32x4_t o[kMlaDl / 16];
+#pragma unroll
+  for (int i = 0; i < kMlaDl / 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  int nid[IPT], nrid[RPT > 0 ? RPT : 1];  // ids of the block after the next
+  if (nblk > 0) {
+    int ii0[IPT], ri0[RPT > 0 ? RPT : 1];
+    load_ids(0, ii0, ri0);
+    issue(ii0, ri0);
+    load_ids(1, nid, nrid);
+    fill(0, ii0, ri0);
+  }
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int bf = blk & 1;
+    __syncthreads();  // buffer bf is filled; buffer bf ^ 1 is no longer read
+    int cid[IPT], crid[RPT > 0 ? RPT : 1];
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) cid[k] = nid[k];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) crid[k] = nrid[k];
+    const bool more = blk + 1 < nblk;
+    if (more) {
+      issue(cid, crid);             // block blk + 1 flies while block blk is multiplied out
+      load_ids(blk + 2, nid, nrid);
+    }
+    // S^T tiles (rows = tokens 16 j + 4 qd + r, column = head c); two
+    // accumulators per tile (even and odd K steps) halve the dependent MFMA chain
+    f32x4_t st[kMlaBT / 16], st2[kMlaBT / 16];
+#pragma unroll
+    for (int j = 0; j < kMlaBT / 16; ++j) st[j] = st2[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < DQK / 32; ++s)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        st[j] = mfma_bf16(*reinterpret_cast<const bf16x8_t*>(Kt + (16 * j + c) * KS + 8 * qd + 32 * s), qb[s], st[j]);
-    float sc[4][4];
+      for (int j = 0; j < kMlaBT / 16; ++j) {
+        const bf16x8_t kop = *reinterpret_cast<const bf16x8_t*>(&Kt[bf][(16 * j + c) * KS + 8 * qd + 32 * s]);
+        if (s & 1)
+          st2[j] = mfma_bf16(kop, qb[s], st2[j]);
+        else
+          st[j] = mfma_bf16(kop, qb[s], st[j]);
+      }
+#pragma unroll
+    for (int j = 0; j < kMlaBT / 16; ++j) st[j] += st2[j];
+    float sc[kMlaBT / 16][4];
     float bm = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kMlaBT / 16; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[j][r] = tok_id[16 * j + 4 * qd + r] >= 0 ? st[j][r] * scale : -INFINITY;
+        sc[j][r] = tok_id[bf][16 * j + 4 * qd + r] >= 0 ? st[j][r] * scale : -INFINITY;
         bm = fmaxf(bm, sc[j][r]);
       }
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
@@ -866,9 +940,9 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     const bool none = m_new == -INFINITY;
     const float alpha = none ? 1.f : __expf(m_run - m_new);
     float psum = 0.f;
-    float p[4][4];
+    float p[kMlaBT / 16][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kMlaBT / 16; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         p[j][r] = none ? 0.f : __expf(sc[j][r] - m_new);
@@ -878,17 +952,20 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // rescale O rows (heads 4 qd + r of this wave) by their alpha
-    float al[4];
+    // rescale O rows (heads 4 qd + r of this wave) by their alpha, unless no
+    // head's running maximum moved (then every alpha is 1)
+    if (__ballot(alpha != 1.f)) {
+      float al[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * qd + r, 64);
+      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * qd + r, 64);
 #pragma unroll
-    for (int dt = 0; dt < kMlaDl / 16; ++dt)
+      for (int dt = 0; dt < kMlaDl / 16; ++dt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[dt][r] *= al[r];
+        for (int r = 0; r < 4; ++r) o[dt][r] *= al[r];
+    }
     // O += P V: k index 8 qd + j <-> token 32 s2 + 4 qd + j (j < 4), 32 s2 + 16 + 4 qd + j - 4 (j >= 4)
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
+    for (int s2 = 0; s2 < kMlaBT / 32; ++s2) {
       bf16x8_t pa;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -897,13 +974,14 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
       }
 #pragma unroll
       for (int dt = 0; dt < kMlaDl / 16; ++dt) {
-        const uint16_t* vrow = Vt + (16 * dt + c) * kVtStride + 32 * s2 + 4 * qd;
+        const uint16_t* vrow = &Vt[bf][(16 * dt + c) * kVtStride + 32 * s2 + 4 * qd];
         const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
         const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
         const u32x4_t vv = {v0.x, v0.y, v1.x, v1.y};
         o[dt] = mfma_bf16(pa, __builtin_bit_cast(bf16x8_t, vv), o[dt]);
       }
     }
+    if (more) fill(bf ^ 1, cid, crid);
   }
   // partials: O rows are heads 16 hw + 4 qd + r, columns 16 dt + c
   float* po = part_o + (((int64_t)b * S + split) * H) * kMlaDl;
@@ -1083,14 +1161,15 @@ struct MlaWs {
   float *part_o, *part_ml;
 };
 
+// splits per row: about 256 workgroups over the batch (two head groups per
+// row), at most one per block and at most 32
 static int mla_splits(int64_t b, int64_t topk) {
   const int64_t blocks = (topk + kMlaBT - 1) / kMlaBT;
-  int64_t s = (256 + b - 1) / b;
+  int64_t s = (128 + b - 1) / b;
   s = std::min<int64_t>(s, blocks);
   s = std::min<int64_t>(s, 32);
   return (int)std::max<int64_t>(s, 1);
 }
-
 static size_t mla_ws(int64_t b, int64_t h, int64_t topk, char* base, MlaWs* w) {
   const int64_t S = mla_splits(b, topk);
   const size_t ob = align256((size_t)b * S * h * kMlaDl * 4);

@@ -443,7 +443,7 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
   MOSAIC_CHECK_ARG(block_m >= 1, "moe layout: block_m=%d", block_m);
   MOSAIC_CHECK_ARG(func >= 0 && func <= 2, "moe layout: score func %d", func);
   MOSAIC_CHECK_ARG(logits ? (ids_out && weights_out) : (ids_in && weights_in), "moe layout: missing ids/weights");
-  if (out.small_ok && A_ext <= kSmallAssign && M <= 16) {
+  if (out.small_ok && A_ext <= kSmallAssign && M <= 2) {  // single-wave layout: faster only for one or two tokens
     const unsigned threads = (unsigned)(64 * (logits ? (M > 1 ? M : 1) : 1));
     hipLaunchKernelGGL(route_layout_small_kernel, dim3(1), dim3(threads), 0, st, logits, bias, ids_in, weights_in,
                        ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
