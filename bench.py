@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--sweep", default="4,16,64", help="extra M values reported under m_sweep ('' to skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1, 3, 4, 5")
+    ap.add_argument("--configs", default="",
+                    help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config4_moe_prefill, "
+                         "config5_dsa to run (default: all)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the line is printed, copy a buffer of this many MiB device to device three times "
                          "(a plain copy of known size that scales FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -340,6 +343,8 @@ def main():
                          ("config3_fp8_gemm", lambda: config3_fp8(torch, ops)),
                          ("config4_moe_prefill", lambda: config4_prefill(torch, ops, banks[0])),
                          ("config5_dsa", lambda: config5_dsa(torch, ops))]:
+            if args.configs and name not in args.configs.split(","):
+                continue
             print(f"bench.py: {name}", file=sys.stderr, flush=True)
             configs[name] = fn()
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch, ops, banks[0])

@@ -281,22 +281,48 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
 
 // Large tiled kernel (enough 256 x 256 tiles to fill the chip): a workgroup
 // of 8 waves owns a 256 x 256 block of C; wave w owns rows 128 (w >> 2) and
-// columns 64 (w & 3) of it (8 x 4 MFMA tiles, 128 accumulators).  Twice the
-// columns of the 256 x 128 kernel for the same A block: 262 instead of 175
-// flops per byte copied into LDS, and 0.75 instead of 1 KB of LDS operand
-// reads per MFMA.  A stage (A and B blocks, 256 a_s values, the two b_s values
-// of the block's column halves) is 66.8 KB, so the ring holds two stages, one
-// K-block ahead; copies, swizzle and XCD grouping as in the kernel above.
+// columns 64 (w & 3) of it.  Twice the columns of the 256 x 128 kernel for
+// the same A block: 256 instead of 171 flops per byte copied into LDS.  A
+// stage (A and B blocks of one K-block) is 64 KB, so the ring holds two
+// stages, one K-block ahead.  Copies use a wave-uniform base (SGPR pair) plus
+// per-lane 32-bit offsets.
+//
+// Scales: a stage copy waits for its slowest load, and a per-block gather of
+// 256 a_s values (one per A row, 256 cache lines) was the slowest.  a_s and
+// b_s are instead staged for 8 K-blocks at a time ([8 blocks][256 rows] and
+// [8][2] floats, two chunk buffers): one 16-byte load per thread (a row's 8
+// consecutive a_s values are 32 contiguous bytes), issued one block after a
+// chunk starts and written to LDS after the next barrier, 6 blocks before use.
+//
+// MFMA roles are transposed (B rows are the MFMA rows, A rows the columns):
+// a lane's 16 x 16 tile entries then share one A row, hence one a_s value per
+// tile, and 4 consecutive C columns, stored as one 8- or 16-byte write.  The
+// a_s values of a block are laid out so that lane c reads its 8 tiles' values
+// as two 16-byte words.  A tile's fp32 rescale (acc += d * a_s * b_s) is
+// issued after the next tile's MFMAs, so the MFMA results are not waited on;
+// the next A fragment is read from LDS while the current MFMAs run.
 struct Fp8Big {
   static constexpr int BM = 256, BN = 256, NT = 512, NW = 8;
-  static constexpr int AB = (BM + BN) * 128;    // A and B bytes of a stage
-  static constexpr int SA = AB;                  // a_s: 256 floats
-  static constexpr int SB = SA + BM * 4;         // b_s: 32 copies of each column half's value
-  static constexpr int STAGE = SB + 256;
-  static constexpr int RUNS = AB / 1024 / NW;    // 8 one-KB A/B runs per wave per stage
-  static constexpr int SRUNS = BM / 64;          // 4 a_s runs of 256 bytes
-  static constexpr int OPS = RUNS + 1;
+  static constexpr int STAGE = (BM + BN) * 128;  // A and B bytes of a stage
+  static constexpr int RUNS = STAGE / 1024 / NW;  // 8 one-KB A/B runs per wave per stage
+  static constexpr int CHUNK = 8;                 // K-blocks per scale chunk
 };
+
+// a_s slot of tile row m (0..255): (m / 128) * 128 + (m % 16) * 8 + (m % 128) / 16,
+// so that rows wm + 16 mt + c (mt = 0..7) of one wave sit at slots wm + 8 c + mt
+__device__ __forceinline__ int fp8_big_slot_row(int s) {
+  const int t = s & 127;
+  return (s & ~127) + (t & 7) * 16 + (t >> 3);
+}
+
+__device__ __forceinline__ void fp8_copy16_so(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(off), "s"(base) : "memory", "m0");
+}
+__device__ __forceinline__ void fp8_copy4_so(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(off), "s"(base) : "memory", "m0");
+}
 
 __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __restrict__ A,
                                                               const float* __restrict__ As,
@@ -305,90 +331,142 @@ __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __r
                                                               int M, int N, int K, int out_f32) {
   using TT = Fp8Big;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][TT::STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  __shared__ __attribute__((aligned(16))) float sc_a[2][TT::CHUNK][TT::BM];  // [chunk buf][block][a_s slot]
+  __shared__ float sc_b[2][TT::CHUNK][2];                                    // [chunk buf][block][column half]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, q = lane >> 4;
   int tm, tn;
   tile_coords(blockIdx.x, (M + TT::BM - 1) / TT::BM, (N + TT::BN - 1) / TT::BN, tm, tn);
   const int m0 = tm * TT::BM, n0 = tn * TT::BN;
   const int wm = (wv >> 2) * 128, wn = (wv & 3) * 64;
   const int nkb = K / 128;
-  const uint8_t* gsrc[TT::RUNS];
-  int ldsoff[TT::RUNS];
+  // waves 0..3 copy A rows 64 w .. 64 w + 63 of the tile, waves 4..7 B rows
+  // 64 (w - 4) ..; run ii is 8 rows (1 KB, its 16-byte chunks XOR-swizzled)
+  const bool is_a = wv < 4;
+  const uint8_t* obase = is_a ? A : B;
+  const int r0 = is_a ? m0 : n0, lim = (is_a ? M : N) - 1, rb = 64 * (wv & 3);
+  uint32_t voff[TT::RUNS];
 #pragma unroll
   for (int ii = 0; ii < TT::RUNS; ++ii) {
-    const int i = wv * TT::RUNS + ii;  // run i: 8 rows of A (i < 32) or of B
-    const int row = (i < TT::BM / 8 ? 8 * i : 8 * (i - TT::BM / 8)) + (lane >> 3);
+    const int row = rb + 8 * ii + (lane >> 3);
     const int logical = (lane & 7) ^ ((row >> 1) & 7);
-    gsrc[ii] = i < TT::BM / 8 ? A + (int64_t)min(m0 + row, M - 1) * K + logical * 16
-                              : B + (int64_t)min(n0 + row, N - 1) * K + logical * 16;
-    ldsoff[ii] = i * 1024;
-  }
-  // scale copies: waves 0..3 take 64 a_s rows each; the others copy the two
-  // b_s values of the block (lanes 0..31 the first column half, 32..63 the second)
-  const float* ssrc;
-  int sdst;
-  if (wv < TT::SRUNS) {
-    ssrc = As + (int64_t)min(m0 + 64 * wv + lane, M - 1) * nkb;
-    sdst = TT::SA + 256 * wv;
-  } else {
-    const int nb = min(n0 / 128 + (lane >> 5), (N - 1) / 128);
-    ssrc = Bs + (int64_t)nb * nkb;
-    sdst = TT::SB;
+    voff[ii] = (uint32_t)min(r0 + row, lim) * (uint32_t)K + (uint32_t)(logical * 16);
   }
   auto issue = [&](int st, int kb) {
     const uint32_t base = fp8_lds_addr(lds[st]);
+    const uint8_t* ob = obase + (int64_t)kb * 128;
 #pragma unroll
-    for (int ii = 0; ii < TT::RUNS; ++ii) fp8_copy16(gsrc[ii] + (int64_t)kb * 128, base + ldsoff[ii]);
-    fp8_copy4(ssrc + kb, base + sdst);
+    for (int ii = 0; ii < TT::RUNS; ++ii) fp8_copy16_so(ob, voff[ii], base + (uint32_t)((wv * TT::RUNS + ii) * 1024));
+  };
+  // scale chunk loads: thread t takes a_s slot t / 2, blocks 4 (t % 2) .. + 3 of
+  // the chunk; threads 0..15 also take b_s (block t % 8, column half t / 8)
+  const int slot = tid >> 1, half = tid & 1;
+  const float* arow = As + (int64_t)min(m0 + fp8_big_slot_row(slot), M - 1) * nkb;
+  const float* brow = Bs + (int64_t)min(n0 / 128 + ((tid >> 3) & 1), (N - 1) / 128) * nkb;
+  const bool vec_as = (nkb & 3) == 0;  // 16-byte aligned a_s rows
+  auto load_chunk = [&](int ch, f32x4_t& va, float& vb) {
+    const int k0 = ch * TT::CHUNK + 4 * half;
+    if (vec_as && k0 + 3 < nkb) {
+      va = *reinterpret_cast<const f32x4_t*>(arow + k0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) va[i] = arow[min(k0 + i, nkb - 1)];
+    }
+    vb = tid < 16 ? brow[min(ch * TT::CHUNK + (tid & 7), nkb - 1)] : 0.f;
+  };
+  auto store_chunk = [&](int ch, const f32x4_t& va, float vb) {
+    const int bf = ch & 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc_a[bf][4 * half + i][slot] = va[i];
+    if (tid < 16) sc_b[bf][tid & 7][tid >> 3] = vb;
   };
   f32x4_t acc[8][4];
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x4_t dp[4];  // product of the previous tile, rescaled one tile later
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) dp[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float sp = 0.f;
+  f32x4_t pend_a;  // the next scale chunk, between its load and its LDS write
+  float pend_b;
+  load_chunk(0, pend_a, pend_b);
+  store_chunk(0, pend_a, pend_b);
   issue(0, 0);
   for (int kb = 0; kb < nkb; ++kb) {
     // block kb landed for every wave, and every wave is done with block kb - 1
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int ch = kb / TT::CHUNK, kc = kb % TT::CHUNK;
+    const bool next_chunk = (ch + 1) * TT::CHUNK < nkb;
+    if (kc == 2 && next_chunk) store_chunk(ch + 1, pend_a, pend_b);  // its loads completed at the wait above
     if (kb + 1 < nkb) issue((kb + 1) & 1, kb + 1);
+    if (kc == 1 && next_chunk) load_chunk(ch + 1, pend_a, pend_b);
     const uint8_t* stg = lds[kb & 1];
     const uint8_t* ta = stg;
     const uint8_t* tb = stg + TT::BM * 128;
-    const float sb = *reinterpret_cast<const float*>(stg + TT::SB + (wn >= 128 ? 128 : 0));
+    const float sb = sc_b[ch & 1][kc][wn >= 128 ? 1 : 0];
+    const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(&sc_a[ch & 1][kc][wm + 8 * c]);
+    const f32x4_t s1 = *reinterpret_cast<const f32x4_t*>(&sc_a[ch & 1][kc][wm + 8 * c + 4]);
     i32x8_t bop[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) bop[nt] = lds_fp8_operand(tb, wn + 16 * nt + c, q);
+    i32x8_t aop[2];
+    aop[0] = lds_fp8_operand(ta, wm + c, q);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
-      const i32x8_t aop = lds_fp8_operand(ta, wm + 16 * mt + c, q);
+      if (mt + 1 < 8) aop[(mt + 1) & 1] = lds_fp8_operand(ta, wm + 16 * (mt + 1) + c, q);
       f32x4_t d[4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(aop, bop[nt]);
-      const f32x4_t sa4 = *reinterpret_cast<const f32x4_t*>(stg + TT::SA + 4 * (wm + 16 * mt + 4 * q));
+      for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(bop[nt], aop[mt & 1]);
+      const int pm = mt == 0 ? 7 : mt - 1;  // the previous tile (tile 7 of block kb - 1 at mt == 0)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float s = sa4[r] * sb;
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[mt][nt][r] = __builtin_fmaf(d[nt][r], s, acc[mt][nt][r]);
-      }
+        for (int r = 0; r < 4; ++r) acc[pm][nt][r] = __builtin_fmaf(dp[nt][r], sp, acc[pm][nt][r]);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) dp[nt] = d[nt];
+      sp = (mt < 4 ? s0[mt & 3] : s1[mt & 3]) * sb;
     }
   }
 #pragma unroll
-  for (int mt = 0; mt < 8; ++mt)
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[7][nt][r] = __builtin_fmaf(dp[nt][r], sp, acc[7][nt][r]);
+  // lane (c, q) of tile (mt, nt) holds C[m0 + wm + 16 mt + c][n .. n + 3], n = n0 + wn + 16 nt + 4 q
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    const int m = m0 + wm + 16 * mt + c;
+    if (m >= M) continue;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      const int n = n0 + wn + 16 * nt + c;
+      const int n = n0 + wn + 16 * nt + 4 * q;
+      const f32x4_t v = acc[mt][nt];
+      if (out_f32) {
+        float* o = reinterpret_cast<float*>(C) + (int64_t)m * N + n;
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<f32x4_t*>(o) = v;
+        } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + 16 * mt + 4 * q + r;
-        if (m < M && n < N) {
-          if (out_f32)
-            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[mt][nt][r];
-          else
-            reinterpret_cast<uint16_t*>(C)[(int64_t)m * N + n] = f32_bf16(acc[mt][nt][r]);
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) o[r] = v[r];
+        }
+      } else {
+        uint16_t* o = reinterpret_cast<uint16_t*>(C) + (int64_t)m * N + n;
+        if (vec && n + 3 < N) {
+          const uint32_t lo = (uint32_t)f32_bf16(v[0]) | ((uint32_t)f32_bf16(v[1]) << 16);
+          const uint32_t hi = (uint32_t)f32_bf16(v[2]) | ((uint32_t)f32_bf16(v[3]) << 16);
+          *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) o[r] = f32_bf16(v[r]);
         }
       }
     }
+  }
 }
 
 // w [N, K] e4m3 with one fp32 scale per (bn x bk) block -> bf16 [N, K]
@@ -441,7 +519,8 @@ extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const u
   const int64_t mt = (m + 15) / 16;
   if (m >= 256) {
     const int64_t big_tiles = ((m + 255) / 256) * ((n + 255) / 256);
-    if (big_tiles >= 256) {
+    // the big kernel addresses A and B with 32-bit offsets
+    if (big_tiles >= 256 && m * k < (1ll << 32) && n * k < (1ll << 32)) {
       hipLaunchKernelGGL(fp8_gemm_big_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a, a_s, b, b_s, c, (int)m,
                          (int)n, (int)k, f32);
       MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
