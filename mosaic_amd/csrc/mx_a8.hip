@@ -274,9 +274,16 @@ constexpr int kPfBM = 256;     // sorted rows per tile
 constexpr int kPfWaves = 8;    // 4 row quarters x 2 column halves
 constexpr int kPfStages = 3;
 constexpr int kPfNG = 16;      // weight groups (16 rows each) per workgroup
-constexpr int kPfA = 0, kPfB = 32768, kPfBs = kPfB + kPfNG * 1024, kPfAs = kPfBs + kPfNG * 256;
-constexpr int kPfStage = kPfAs + kPfBM * 4;
-constexpr int kPfOps = 9;  // copies per wave per stage: 4 A runs, 2 weight runs, 2 scale runs, 1 row-scale run
+constexpr int kPfA = 0, kPfB = 32768;
+constexpr int kPfStage = kPfB + kPfNG * 1024;  // A rows and weight blocks of one step
+// Scales move per 4 steps ("chunk", two buffers): the weight scale dwords
+// (one dword per lane and group covers 4 steps) and the rows' 1x128 scales,
+// 16 bytes (4 steps) per row, so the row-scale gather touches each row's
+// line once per 4 steps instead of once per step.
+constexpr int kPfCBs = 0, kPfCAs = kPfNG * 256, kPfChunk = kPfCAs + kPfBM * 16;
+// copies per wave per step: 2 A runs per valid 16-row tile of the wave's two
+// (0, 2 or 4) and 2 weight runs; on steps 4c also the chunk: 2 weight-scale
+// runs and (waves 0..3) one 16-byte row-scale run
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -304,26 +311,37 @@ struct PfSrc {
   const uint8_t* a[4];   // A run 4 wv + i: 16-row tile run >> 1, bytes 64 (run & 1) + 16 (lane / 16) of row lane % 16
   const uint8_t* b[2];   // weight group 2 wv + i, this lane's 16 bytes
   const uint8_t* bs[2];  // its scale dword
-  const float* as;       // row 64 (wv & 3) + lane: its 1x128 scale row
+  const float* as;       // row 64 (wv & 3) + lane: its 1x128 scale row (waves 0..3)
 };
 
-__device__ __forceinline__ void pf_issue(const PfSrc& src, int S, uint8_t* stage) {
-  const int wv = threadIdx.x >> 6;
+// copies of one step by this wave (see pf_issue)
+__device__ __forceinline__ int pf_ops(int S, int n_a, int wv) { return n_a + 2 + ((S & 3) == 0 ? (wv < 4 ? 3 : 2) : 0); }
+
+// A runs 4 wv + i of 16-row tiles past the tile's rows are not copied (no
+// wave computes on them); n_a is 0, 2 or 4, uniform over the wave.  Steps 4c
+// also copy chunk c (into chunk buffer c & 1).
+__device__ __forceinline__ void pf_issue(const PfSrc& src, int S, uint8_t* stage, uint8_t* chunk, int n_a) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t base = lds_u32(stage);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lds_copy16(src.a[i] + 128 * S, base + kPfA + (4 * wv + i) * 1024);
+  for (int i = 0; i < 4; ++i)
+    if (i < n_a) lds_copy16(src.a[i] + 128 * S, base + kPfA + (4 * wv + i) * 1024);
 #pragma unroll
   for (int i = 0; i < 2; ++i) lds_copy16(src.b[i] + (int64_t)S * 1024, base + kPfB + (2 * wv + i) * 1024);
+  if ((S & 3) == 0) {
+    const uint32_t cb = lds_u32(chunk + ((S >> 2) & 1) * kPfChunk);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) lds_copy4(src.bs[i] + (int64_t)(S >> 2) * 256, base + kPfBs + (2 * wv + i) * 256);
-  lds_copy4(src.as + S, base + kPfAs + (wv & 3) * 256);
+    for (int i = 0; i < 2; ++i) lds_copy4(src.bs[i] + (int64_t)(S >> 2) * 256, cb + kPfCBs + (2 * wv + i) * 256);
+    if (wv < 4) lds_copy16(src.as + S, cb + kPfCAs + wv * 1024);
+  }
 }
 
 // One wave's MFMAs of one staged step: its row tiles (rows 64 (wv >> 1) + 16 mt,
 // the first MT of them: the tiles past the workgroup's valid rows are skipped)
 // x the 8 staged groups in wg.
 template <int MT>
-__device__ __forceinline__ void pf_compute(const uint8_t* stage, const int (&wg)[8], int S, f32x4_t (&acc)[4][8]) {
+__device__ __forceinline__ void pf_compute(const uint8_t* stage, const uint8_t* chunk, const int (&wg)[8], int S,
+                                           f32x4_t (&acc)[4][8]) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15;
   const int sh = 8 * (S & 3);
   i32x8_t a[MT];
@@ -334,12 +352,12 @@ __device__ __forceinline__ void pf_compute(const uint8_t* stage, const int (&wg)
     const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + lane * 16);
     const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + 1024 + lane * 16);
     a[mt] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-    sa[mt] = pow2_e8m0(*reinterpret_cast<const float*>(stage + kPfAs + (16 * mtg + c) * 4));
+    sa[mt] = pow2_e8m0(*reinterpret_cast<const float*>(chunk + kPfCAs + (16 * mtg + c) * 16 + (S & 3) * 4));
   }
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     const u32x4_t wb = *reinterpret_cast<const u32x4_t*>(stage + kPfB + wg[n] * 1024 + lane * 16);
-    const int sw = (int)((*reinterpret_cast<const uint32_t*>(stage + kPfBs + wg[n] * 256 + lane * 4) >> sh) & 0xFFu);
+    const int sw = (int)((*reinterpret_cast<const uint32_t*>(chunk + kPfCBs + wg[n] * 256 + lane * 4) >> sh) & 0xFFu);
     const i32x8_t b = {(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3], 0, 0, 0, 0};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -354,35 +372,55 @@ __device__ __forceinline__ int pf_live_tiles(int rows) {
   return r <= 0 ? 0 : (r >= 64 ? 4 : (r + 15) / 16);
 }
 
+// wait until this wave has at most `ops` copies in flight, then the workgroup barrier
+template <int N>
+__device__ __forceinline__ void pf_wait_n() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void pf_wait_ops(int ops) {
+  switch (ops) {
+    case 9: pf_wait_n<9>(); break;
+    case 8: pf_wait_n<8>(); break;
+    case 7: pf_wait_n<7>(); break;
+    case 6: pf_wait_n<6>(); break;
+    case 5: pf_wait_n<5>(); break;
+    case 4: pf_wait_n<4>(); break;
+    case 3: pf_wait_n<3>(); break;
+    case 2: pf_wait_n<2>(); break;
+    case 1: pf_wait_n<1>(); break;
+    default: pf_wait_n<0>(); break;
+  }
+}
+
 template <int LIVE>
 __device__ __forceinline__ void pf_kloop_t(const PfSrc& src, int ns, const int (&wg)[8], f32x4_t (&acc)[4][8],
-                                           uint8_t (*ring)[kPfStage]) {
+                                           uint8_t (*ring)[kPfStage], uint8_t* chunk, int n_a, int wv) {
   for (int S = 0; S < ns; ++S) {
     // step S landed (every wave's copies: the barrier), step S + 1 may still fly
-    if (S + 1 < ns)
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kPfOps) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (S + 2 < ns) pf_issue(src, S + 2, ring[(S + 2) % kPfStages]);
-    if constexpr (LIVE > 0) pf_compute<LIVE>(ring[S % kPfStages], wg, S, acc);
+    pf_wait_ops(S + 1 < ns ? pf_ops(S + 1, n_a, wv) : 0);
+    if (S + 2 < ns) pf_issue(src, S + 2, ring[(S + 2) % kPfStages], chunk, n_a);
+    if constexpr (LIVE > 0) pf_compute<LIVE>(ring[S % kPfStages], chunk + ((S >> 2) & 1) * kPfChunk, wg, S, acc);
   }
 }
 
 __device__ __forceinline__ void pf_kloop(const PfSrc& src, int ns, int rows, const int (&wg)[8],
-                                         f32x4_t (&acc)[4][8], uint8_t (*ring)[kPfStage]) {
+                                         f32x4_t (&acc)[4][8], uint8_t (*ring)[kPfStage], uint8_t* chunk) {
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[mt][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  pf_issue(src, 0, ring[0]);
-  if (ns > 1) pf_issue(src, 1, ring[1]);
+  // A runs of this wave: its 16-row tiles 2 wv and 2 wv + 1, two runs each if valid
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n_a = (32 * wv < rows ? 2 : 0) + (32 * wv + 16 < rows ? 2 : 0);
+  pf_issue(src, 0, ring[0], chunk, n_a);
+  if (ns > 1) pf_issue(src, 1, ring[1], chunk, n_a);
   // the wave's row tiles past the valid rows are skipped (one loop per count)
   switch (pf_live_tiles(rows)) {
-    case 4: pf_kloop_t<4>(src, ns, wg, acc, ring); break;
-    case 3: pf_kloop_t<3>(src, ns, wg, acc, ring); break;
-    case 2: pf_kloop_t<2>(src, ns, wg, acc, ring); break;
-    case 1: pf_kloop_t<1>(src, ns, wg, acc, ring); break;
-    default: pf_kloop_t<0>(src, ns, wg, acc, ring); break;
+    case 4: pf_kloop_t<4>(src, ns, wg, acc, ring, chunk, n_a, wv); break;
+    case 3: pf_kloop_t<3>(src, ns, wg, acc, ring, chunk, n_a, wv); break;
+    case 2: pf_kloop_t<2>(src, ns, wg, acc, ring, chunk, n_a, wv); break;
+    case 1: pf_kloop_t<1>(src, ns, wg, acc, ring, chunk, n_a, wv); break;
+    default: pf_kloop_t<0>(src, ns, wg, acc, ring, chunk, n_a, wv); break;
   }
 }
 
@@ -393,6 +431,113 @@ __device__ __forceinline__ void pf_sources(PfSrc& src, const uint8_t* const (&ro
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < 4; ++i) src.a[i] = rowp[i] + 64 * (i & 1) + 16 * (lane >> 4);  // run 4 wv + i: half i & 1
+  const int ns4 = (ns + 3) / 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    src.b[i] = bank_p + ((int64_t)groups[i] * ns) * 1024 + lane * 16;
+    src.bs[i] = bank_s + ((int64_t)groups[i] * ns4) * 256 + lane * 4;
+  }
+  src.as = as_row;
+}
+
+// ---- light tiles (at most 64 rows): weight streaming -------------------------
+// A tile of <= 64 rows does a quarter of the MFMAs of a full one for the same
+// weight bytes, so its time is the weight stream's: what matters is how many
+// weight bytes are in flight.  Such tiles stage only their 64 rows (8 KB) with
+// the 16 weight groups (16 KB) and scales: a 28.3 KB stage, five stages, four
+// steps ahead (64 KB of weights in flight per CU instead of 32 KB).  Every wave
+// then owns two staged groups and the tile's (up to 4) 16-row tiles.
+constexpr int kPfLStages = 5;
+constexpr int kPfLA = 0, kPfLB = 8192, kPfLBs = kPfLB + kPfNG * 1024, kPfLAs = kPfLBs + kPfNG * 256;
+constexpr int kPfLStage = kPfLAs + 256;
+// copies per wave per stage: 1 A run, 2 weight runs, 2 scale runs, and (wave 0) 1 row-scale run
+static_assert(kPfLStages * kPfLStage <= kPfStages * kPfStage, "light ring must fit the prefill ring");
+
+struct PfLSrc {
+  const uint8_t* a;      // A run wv: 16-row tile wv >> 1, bytes 64 (wv & 1) + 16 (lane / 16) of row lane % 16
+  const uint8_t* b[2];   // weight group 2 wv + i, this lane's 16 bytes
+  const uint8_t* bs[2];  // its scale dword
+  const float* as;       // row lane: its 1x128 scale row
+};
+
+__device__ __forceinline__ void pfl_issue(const PfLSrc& src, int S, uint8_t* stage) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t base = lds_u32(stage);
+  lds_copy16(src.a + 128 * S, base + kPfLA + wv * 1024);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) lds_copy16(src.b[i] + (int64_t)S * 1024, base + kPfLB + (2 * wv + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) lds_copy4(src.bs[i] + (int64_t)(S >> 2) * 256, base + kPfLBs + (2 * wv + i) * 256);
+  if (wv == 0) lds_copy4(src.as + S, base + kPfLAs);  // wave 0 copies the 64 row scales
+}
+
+// wait until this wave has `ahead` later stages in flight, then the barrier
+__device__ __forceinline__ void pfl_wait(int ahead, int wv) {
+  if (wv == 0) {
+    if (ahead >= 3) pf_wait_n<18>(); else if (ahead == 2) pf_wait_n<12>(); else if (ahead == 1) pf_wait_n<6>(); else pf_wait_n<0>();
+  } else {
+    if (ahead >= 3) pf_wait_n<15>(); else if (ahead == 2) pf_wait_n<10>(); else if (ahead == 1) pf_wait_n<5>(); else pf_wait_n<0>();
+  }
+}
+
+// one wave's MFMAs of one staged step: 16-row tiles 0..MT-1 x staged groups ga, gb
+template <int MT>
+__device__ __forceinline__ void pfl_compute(const uint8_t* stage, int ga, int gb, int S, f32x4_t (&acc)[4][2]) {
+  const int lane = threadIdx.x & 63, c = lane & 15;
+  const int sh = 8 * (S & 3);
+  i32x8_t a[MT];
+  int sa[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(stage + kPfLA + mt * 2048 + lane * 16);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(stage + kPfLA + mt * 2048 + 1024 + lane * 16);
+    a[mt] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    sa[mt] = pow2_e8m0(*reinterpret_cast<const float*>(stage + kPfLAs + (16 * mt + c) * 4));
+  }
+#pragma unroll
+  for (int gi = 0; gi < 2; ++gi) {
+    const int g = gi ? gb : ga;
+    const u32x4_t wb = *reinterpret_cast<const u32x4_t*>(stage + kPfLB + g * 1024 + lane * 16);
+    const int sw = (int)((*reinterpret_cast<const uint32_t*>(stage + kPfLBs + g * 256 + lane * 4) >> sh) & 0xFFu);
+    const i32x8_t b = {(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3], 0, 0, 0, 0};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      acc[mt][gi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mt], b, acc[mt][gi], 0, 4, 0, sa[mt], 0, sw);
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void pfl_kloop_t(const PfLSrc& src, int ns, int ga, int gb, f32x4_t (&acc)[4][2],
+                                            uint8_t* ring) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int S = 0; S < ns; ++S) {
+    pfl_wait(min(kPfLStages - 2, ns - 1 - S), wv);  // step S landed, later issued steps may fly
+    if (S + kPfLStages - 1 < ns)
+      pfl_issue(src, S + kPfLStages - 1, ring + ((S + kPfLStages - 1) % kPfLStages) * kPfLStage);
+    pfl_compute<MT>(ring + (S % kPfLStages) * kPfLStage, ga, gb, S, acc);
+  }
+}
+
+__device__ __forceinline__ void pfl_kloop(const PfLSrc& src, int ns, int rows, int ga, int gb, f32x4_t (&acc)[4][2],
+                                          uint8_t* ring) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) acc[mt][0] = acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int st = 0; st < kPfLStages - 1 && st < ns; ++st) pfl_issue(src, st, ring + st * kPfLStage);
+  switch ((rows + 15) / 16) {
+    case 4: pfl_kloop_t<4>(src, ns, ga, gb, acc, ring); break;
+    case 3: pfl_kloop_t<3>(src, ns, ga, gb, acc, ring); break;
+    case 2: pfl_kloop_t<2>(src, ns, ga, gb, acc, ring); break;
+    default: pfl_kloop_t<1>(src, ns, ga, gb, acc, ring); break;
+  }
+}
+
+// light-tile copy sources: A run wv is row 16 (wv >> 1) + lane % 16 (rows past
+// the tile's end read its first row; their results are never stored)
+__device__ __forceinline__ void pfl_sources(PfLSrc& src, const uint8_t* rowp, const uint8_t* bank_p,
+                                            const uint8_t* bank_s, const int (&groups)[2], int ns,
+                                            const float* as_row) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  src.a = rowp + 64 * (wv & 1) + 16 * (lane >> 4);
   const int ns4 = (ns + 3) / 4;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -414,6 +559,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
     const float* __restrict__ perm_weight, uint8_t* __restrict__ zq, float* __restrict__ zs, int H, int I, int E,
     float limit) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
+  __shared__ __attribute__((aligned(16))) uint8_t chunk[2 * kPfChunk];
   int colt, tile;
   pf_coords(blockIdx.x, I / 128, colt, tile);
   if (tile >= n_tiles[0]) return;
@@ -424,17 +570,72 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
   const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
   const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * ebytes;
   const uint8_t* bsc = (e == E) ? sh_s : gu_s + (int64_t)e * sbytes;
-  const uint8_t* rowp[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * ((4 * wv + i) >> 1) + c;
-    rowp[i] = xq + (int64_t)perm_token[p0 + (row < rows ? row : 0)] * H;
-  }
   int groups[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int g = 2 * wv + i;
     groups[i] = g < 8 ? j0 / 16 + g : (I + j0) / 16 + g - 8;
+  }
+  const int nbk = I / 128;
+  if (rows <= 64) {
+    // light tile: wave wv owns gate group wv and up group 8 + wv (z columns j0 + 16 wv)
+    const int arow = 16 * (wv >> 1) + c;
+    PfLSrc lsrc;
+    pfl_sources(lsrc, xq + (int64_t)perm_token[p0 + (arow < rows ? arow : 0)] * H, bp, bsc, groups, ns,
+                xs + (int64_t)perm_token[p0 + (lane < rows ? lane : 0)] * ns);
+    f32x4_t lacc[4][2];
+    uint8_t* lring = &ring[0][0];
+    pfl_kloop(lsrc, ns, rows, wv, 8 + wv, lacc, lring);
+    uint32_t lmax[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mt + 4 * q + r;
+        const float wgt = perm_weight[p0 + (row < rows ? row : 0)];
+        const float gb = bf16_f32(f32_bf16(lacc[mt][0][r])), ub = bf16_f32(f32_bf16(lacc[mt][1][r]));
+        const float zb = bf16_f32(f32_bf16(swiglu_f32(gb, ub, limit) * wgt));
+        lacc[mt][0][r] = zb;
+        uint32_t u = __float_as_uint(fabsf(zb));
+        u = max(u, MOSAIC_DPP(0u, u, 0xB1, 0xF));
+        u = max(u, MOSAIC_DPP(0u, u, 0x4E, 0xF));
+        u = max(u, MOSAIC_DPP(0u, u, 0x141, 0xF));
+        u = max(u, MOSAIC_DPP(0u, u, 0x140, 0xF));
+        lmax[mt][r] = u;
+      }
+    // the 1x128 block of a row spans the 8 waves' 16 columns: row maxima through the idle ring
+    __syncthreads();
+    uint32_t* pam = reinterpret_cast<uint32_t*>(lring);  // [8 waves][64 rows]
+    if (c == 0) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pam[wv * 64 + 16 * mt + 4 * q + r] = lmax[mt][r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mt + 4 * q + r;
+        uint32_t um = pam[row];
+#pragma unroll
+        for (int w2 = 1; w2 < 8; ++w2) um = max(um, pam[w2 * 64 + row]);
+        const float sc = act_scale_pow2(__uint_as_float(um));
+        if (row < rows) {
+          const int64_t pp = p0 + row;
+          const float y = fminf(fmaxf(lacc[mt][0][r] / sc, -448.0f), 448.0f);
+          zq[pp * I + j0 + 16 * wv + c] = (uint8_t)e4m3_rne(y);
+          if (wv == 0 && c == 0) zs[pp * nbk + j0 / 128] = sc;
+        }
+      }
+    return;
+  }
+  const uint8_t* rowp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * ((4 * wv + i) >> 1) + c;
+    rowp[i] = xq + (int64_t)perm_token[p0 + (row < rows ? row : 0)] * H;
   }
   const int srow = 64 * (wv & 3) + lane;
   const float* as_row = xs + (int64_t)perm_token[p0 + (srow < rows ? srow : 0)] * ns;
@@ -448,7 +649,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
     wg[n + 4] = 8 + 4 * hc + n;
   }
   f32x4_t acc[4][8];
-  pf_kloop(src, ns, rows, wg, acc, ring);
+  pf_kloop(src, ns, rows, wg, acc, ring, chunk);
   // z = bf16(SwiGLU(bf16 gate, bf16 up) * route weight) in acc[mt][n][r], and
   // the amax of each row over this wave's 64 columns (DPP max over the 16
   // lanes of the row, on the bits of non-negative floats)
@@ -485,7 +686,6 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
       for (int r = 0; r < 4; ++r) pam[wv * 64 + 16 * mt + 4 * q + r] = rmax[mt][r];
   }
   __syncthreads();
-  const int nbk = I / 128;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -514,6 +714,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
     const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, uint16_t* __restrict__ yb, int H,
     int I, int E) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
+  __shared__ __attribute__((aligned(16))) uint8_t chunk[2 * kPfChunk];
   int colt, tile;
   pf_coords(blockIdx.x, H / 256, colt, tile);
   if (tile >= n_tiles[0]) return;
@@ -524,13 +725,32 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
   const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
   const uint8_t* bp = (e == E) ? sh_p : d_p + (int64_t)e * ebytes;
   const uint8_t* bsc = (e == E) ? sh_s : d_s + (int64_t)e * sbytes;
+  const int groups[2] = {h0 / 16 + 2 * wv, h0 / 16 + 2 * wv + 1};
+  if (rows <= 64) {
+    // light tile: wave wv owns staged groups 2 wv and 2 wv + 1 (columns h0 + 32 wv)
+    const int arow = 16 * (wv >> 1) + c;
+    PfLSrc lsrc;
+    pfl_sources(lsrc, zq + (int64_t)(p0 + (arow < rows ? arow : 0)) * I, bp, bsc, groups, ns,
+                zs + (int64_t)(p0 + (lane < rows ? lane : 0)) * ns);
+    f32x4_t lacc[4][2];
+    pfl_kloop(lsrc, ns, rows, 2 * wv, 2 * wv + 1, lacc, &ring[0][0]);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mt + 4 * q + r;
+          if (row < rows) yb[(int64_t)(p0 + row) * H + h0 + 32 * wv + 16 * gi + c] = f32_bf16(lacc[mt][gi][r]);
+        }
+    return;
+  }
   const uint8_t* rowp[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 16 * ((4 * wv + i) >> 1) + c;
     rowp[i] = zq + (int64_t)(p0 + (row < rows ? row : 0)) * I;
   }
-  const int groups[2] = {h0 / 16 + 2 * wv, h0 / 16 + 2 * wv + 1};
   const int srow = 64 * (wv & 3) + lane;
   const float* as_row = zs + (int64_t)(p0 + (srow < rows ? srow : 0)) * ns;
   PfSrc src;
@@ -540,7 +760,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
 #pragma unroll
   for (int n = 0; n < 8; ++n) wg[n] = 8 * hc + n;
   f32x4_t acc[4][8];
-  pf_kloop(src, ns, rows, wg, acc, ring);
+  pf_kloop(src, ns, rows, wg, acc, ring, chunk);
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -635,7 +855,8 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
                w.chunk_counts, w.chunk_base};
   const int64_t A = m * top_k + (has_shared ? m : 0);
   // large batches (>= 24 assignments per expert on average): 128-row tiles
-  const bool prefill = m * top_k >= 24 * n_experts && hidden % 256 == 0;
+  // the prefill kernels copy 4 row scales (16 bytes) at a time: H / 128 and I / 128 multiples of 4
+  const bool prefill = m * top_k >= 24 * n_experts && hidden % 512 == 0 && inter % 512 == 0;
   const int block_m = prefill ? kPfBM : kMoeBlockM;
   const int64_t e_ext = n_experts + (has_shared ? 1 : 0);
   const int64_t tcap = prefill ? (A + std::min(A, e_ext) * (kPfBM - 1)) / kPfBM : w.tile_cap;

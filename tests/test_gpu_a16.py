@@ -377,7 +377,9 @@ def test_moe_a16_decode1_baseline_geometry(dev):
 @pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
     (1, 16, 256, 128, 4, False, 10.0), (3, 16, 256, 128, 4, True, 10.0), (20, 8, 384, 256, 2, False, 0.0),
     (37, 32, 512, 128, 8, True, 10.0), (520, 8, 256, 128, 8, True, 10.0), (300, 16, 384, 256, 4, False, 0.0),
-    (1100, 32, 256, 128, 8, True, 10.0)])
+    (1100, 32, 256, 128, 8, True, 10.0),
+    # prefill kernels (H, I multiples of 512): full and partial 256-row tiles, light (<= 64-row) tiles
+    (600, 8, 512, 512, 8, True, 10.0), (130, 32, 512, 512, 8, True, 0.0), (300, 16, 1024, 512, 8, False, 10.0)])
 def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     """A8 layer (fused_moe_mxint contract) vs the A8 oracle of identical bytes."""
     ops = _ops()
