@@ -316,8 +316,8 @@ __global__ void __launch_bounds__(KS * 64) mx_linear_a16_kernel(const uint16_t* 
   }
 }
 
-constexpr int kGuT = 2, kGuKS = 4;   // gate/up: 16 z outputs per workgroup
-constexpr int kDnT = 2, kDnKS = 4;   // down: 32 hidden rows per workgroup
+constexpr int kGuT = 4, kGuKS = 4;   // gate/up: 32 z outputs per workgroup
+constexpr int kDnT = 2, kDnKS = 2;   // down: 32 hidden rows per workgroup, K in two halves
 
 template <int T, int KS, bool TILED>
 static void launch_linear(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
