@@ -21,8 +21,8 @@ struct LayoutOut {
   int32_t* n_tiles;      // [1]
   int32_t* counters;     // [n_counters] zeroed by the layout kernel (arrival counters of later kernels)
   int n_counters;
-  int small_ok;          // the caller does not read counts/offsets: A_ext <= 64 may take the
-                         // single-wave path, which leaves them unwritten
+  int small_ok;          // the caller does not read counts/offsets: small batches may take the
+                         // small-batch path, which leaves them unwritten
   int32_t* chunk_counts; // [layout_chunks(A_ext)][E_ext] scratch of the multi-workgroup path
   int32_t* chunk_base;   // [layout_chunks(A_ext)][E_ext]
 };

@@ -204,86 +204,136 @@ __global__ void __launch_bounds__(1024) emit_tiles_kernel(const int32_t* __restr
   if (tid == 0) n_tiles[0] = min(s_toff[E], tile_cap);
 }
 
-// Small-layout fast path (A_ext <= 64, M <= 16) for the MoE forward: one wave
-// routes each token, then wave 0 lays out every assignment (lane a = flat
-// assignment a) with two passes over the <= 64 ids.  Writes what the MoE
-// kernels read (perm / perm_token / perm_weight / sorted_ids / inv_pos /
-// combine_pos / tile list); counts and offsets are left untouched.
-constexpr int kSmallAssign = 64;
+// Small-batch fast path for the MoE forward (A_ext <= 256, M <= 16): one
+// wave per token routes (all tokens at once), then four waves lay out every
+// assignment (lane a = flat assignment a) by the same rule as
+// route_layout_kernel: in-wave exact-match ballot ranks, per-wave counts for
+// the ranks across waves, one scan of the expert counts.  Three barriers in
+// all.  Writes what the MoE kernels read (perm / perm_token / perm_weight /
+// sorted_ids / inv_pos / combine_pos / tile list); counts and offsets are left
+// untouched.
+constexpr int kSmallAssign = 256;
+constexpr int kSmallTokens = 16;
 __global__ void __launch_bounds__(1024) route_layout_small_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, const int32_t* ids_in,
     const float* weights_in, int32_t* ids_out, float* weights_out, int M, int E, int K, int func, int renorm,
     float route_scale, int has_shared, int block_m, LayoutOut out) {
   __shared__ int16_t s_ids[kSmallAssign];
   __shared__ float s_w[kSmallAssign];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ int32_t s_cnt[kRouteMaxExperts + 2];
+  __shared__ int32_t s_off[kRouteMaxExperts + 2];
+  __shared__ int32_t s_toff[kRouteMaxExperts + 2];
+  __shared__ int16_t s_wc[4][kRouteMaxExperts + 2];  // per layout wave: its assignments of each expert
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nthr = blockDim.x;
   const int A = M * K;
   const int A_ext = A + (has_shared ? M : 0);
+  const int E_ext = E + (has_shared ? 1 : 0);
   const int W = K + (has_shared ? 1 : 0);
+  for (int i = tid; i < out.n_counters; i += nthr) out.counters[i] = 0;
+  // 1. routing (wave t routes token t) or the given ids
   if (logits) {
     if (wave < M)
       route_one_token(logits + (int64_t)wave * E, E, K, func, renorm, route_scale, bias, s_ids + wave * K,
                       s_w + wave * K, ids_out + (int64_t)wave * K, weights_out + (int64_t)wave * K);
-  } else if (wave == 0) {
-    for (int a = lane; a < A; a += 64) {
+  } else {
+    for (int a = tid; a < A; a += nthr) {
       const int e = ids_in[a];
       s_ids[a] = (int16_t)((e < 0 || e >= E) ? -1 : e);
       s_w[a] = weights_in[a];
     }
   }
-  if (wave == 0)
-    for (int a = A + lane; a < A_ext; a += 64) { s_ids[a] = (int16_t)E; s_w[a] = 1.0f; }
+  for (int a = A + tid; a < A_ext; a += nthr) {
+    s_ids[a] = (int16_t)E;
+    s_w[a] = 1.0f;
+  }
+  for (int e = tid; e < E_ext; e += nthr) {
+    s_cnt[e] = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s_wc[w][e] = 0;
+  }
   __syncthreads();
-  if (wave != 0) return;
-  // every lane holds its assignment's (expert, token); the passes over all
-  // assignments broadcast them with readlane (no memory round trips)
-  const int a = lane;
-  const bool in = a < A_ext;
-  const int e = in ? s_ids[a] : 0x7FFF;
-  const bool live = in && e >= 0;
-  const int t = a < A ? a / K : a - A;
-  int less = 0, eq_before = 0, cnt = 0, tok_less = 0, tok_inv_before = 0, tok_valid = 0;
-  for (int b = 0; b < A_ext; ++b) {
-    const int eb = __builtin_amdgcn_readlane(e, b);
-    const int tb = __builtin_amdgcn_readlane(t, b);
-    const bool vb = eb >= 0;
-    less += (vb && eb < e);
-    eq_before += (vb && eb == e && b < a);
-    cnt += (vb && eb == e);
-    const bool same_tok = tb == t;
-    tok_valid += (same_tok && vb);
-    tok_less += (same_tok && vb && (eb < e || (eb == e && b < a)));  // repeated ids: slot order
-    tok_inv_before += (same_tok && !vb && b < a);
+  // 2. waves 0..3: in-wave ranks (exact-match ballots on the id bits) and counts
+  int nbits = 1;
+  while ((1 << nbits) <= E_ext) ++nbits;
+  const int a = tid;
+  const bool in = wave < 4 && a < A_ext;
+  const int e = in ? s_ids[a] : -1;
+  const bool live = e >= 0;
+  int rank_w = 0;
+  if (wave < 4) {
+    uint64_t mask = __ballot(live);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t bb = __ballot(live && ((e >> b) & 1));
+      mask &= ((e >> b) & 1) ? bb : ~bb;
+    }
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    rank_w = __popcll(mask & lt);
+    if (live && rank_w == 0) {
+      s_wc[wave][e] = (int16_t)__popcll(mask);
+      atomicAdd(&s_cnt[e], (int)__popcll(mask));
+    }
   }
-  // tile count of a's expert if a heads its expert segment, else 0
-  const int my_tiles = (live && eq_before == 0) ? (cnt + block_m - 1) / block_m : 0;
-  int tiles_before = 0;
-  for (int b = 0; b < A_ext; ++b) {
-    const int eb = __builtin_amdgcn_readlane(e, b);
-    const int nb = __builtin_amdgcn_readlane(my_tiles, b);
-    tiles_before += (eb >= 0 && eb < e) ? nb : 0;
+  __syncthreads();
+  // 3. exclusive scans of the counts and of the tile counts (wave 0)
+  if (wave == 0) {
+    uint32_t carry = 0, tcarry = 0;
+    for (int base = 0; base < E_ext; base += 64) {
+      const int x = base + lane;
+      const uint32_t c = (x < E_ext) ? (uint32_t)s_cnt[x] : 0u;
+      const uint32_t tc = (c + block_m - 1) / block_m;
+      const uint32_t inc = wave_incl_scan_u32(c), tinc = wave_incl_scan_u32(tc);
+      if (x < E_ext) {
+        s_off[x] = (int)(carry + inc - c);
+        s_toff[x] = (int)(tcarry + tinc - tc);
+      }
+      carry += wave_bcast_u32(inc, 63);
+      tcarry += wave_bcast_u32(tinc, 63);
+    }
+    if (lane == 0) s_toff[E_ext] = (int)tcarry;
   }
-  const uint32_t total_tiles = wave_bcast_u32(wave_incl_scan_u32((uint32_t)my_tiles), 63);
+  __syncthreads();
+  // 4. place every assignment; the first of each expert emits the expert's tiles
   if (in) {
-    const int p = live ? less + eq_before : -1;
+    const int t = a < A ? a / K : a - A;
+    int rank;
+    if (a >= A) {
+      rank = K;
+    } else {
+      const int sl = a - t * K;
+      int nvalid = 0, below = 0, inv_before = 0;
+      for (int s2 = 0; s2 < K; ++s2) {
+        const int o = s_ids[t * K + s2];
+        nvalid += (o >= 0);
+        below += (o >= 0 && live && (o < e || (o == e && s2 < sl)));  // repeated ids: slot order
+        inv_before += (o < 0 && s2 < sl);
+      }
+      rank = live ? below : nvalid + inv_before;
+    }
+    int p = -1;
     if (live) {
+      int before = 0;
+      for (int w = 0; w < wave; ++w) before += s_wc[w][e];
+      p = s_off[e] + before + rank_w;
       out.perm[p] = a;
       out.sorted_ids[p] = e;
       out.perm_token[p] = t;
       out.perm_weight[p] = s_w[a];
+      if (p == s_off[e]) {
+        const int cnt = s_cnt[e];
+        for (int j = 0; j * block_m < cnt; ++j) {
+          const int slot = s_toff[e] + j;
+          out.tile_expert[slot] = e;
+          out.tile_start[slot] = j * block_m;
+          out.tile_rows[slot] = min(block_m, cnt - j * block_m);
+          out.tile_p0[slot] = s_off[e] + j * block_m;
+        }
+      }
     }
     out.inv_pos[a] = p;
-    const int rank = a >= A ? K : (live ? tok_less : tok_valid + tok_inv_before);
     out.combine_pos[(int64_t)t * W + rank] = p;
-    for (int j = 0; j < my_tiles; ++j) {  // head lane emits its expert's tiles
-      const int slot = tiles_before + j;
-      out.tile_expert[slot] = e;
-      out.tile_start[slot] = j * block_m;
-      out.tile_rows[slot] = min(block_m, cnt - j * block_m);
-      out.tile_p0[slot] = less + j * block_m;
-    }
   }
-  if (lane == 0) out.n_tiles[0] = (int)total_tiles;
+  if (tid == 0) out.n_tiles[0] = s_toff[E_ext];
 }
 
 // ------------------------------------------------ multi-workgroup layout ----
@@ -443,8 +493,8 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
   MOSAIC_CHECK_ARG(block_m >= 1, "moe layout: block_m=%d", block_m);
   MOSAIC_CHECK_ARG(func >= 0 && func <= 2, "moe layout: score func %d", func);
   MOSAIC_CHECK_ARG(logits ? (ids_out && weights_out) : (ids_in && weights_in), "moe layout: missing ids/weights");
-  if (out.small_ok && A_ext <= kSmallAssign && M <= 2) {  // single-wave layout: faster only for one or two tokens
-    const unsigned threads = (unsigned)(64 * (logits ? (M > 1 ? M : 1) : 1));
+  if (out.small_ok && A_ext <= kSmallAssign && M <= kSmallTokens) {
+    const unsigned threads = logits ? 1024u : 256u;
     hipLaunchKernelGGL(route_layout_small_kernel, dim3(1), dim3(threads), 0, st, logits, bias, ids_in, weights_in,
                        ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
                        out);

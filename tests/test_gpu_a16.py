@@ -231,7 +231,9 @@ def _make_bank(rng, e, h, inter):
 
 @pytest.mark.parametrize("m,e,h,inter,k,shared,limit", [
     (1, 16, 256, 128, 4, True, 0.0), (3, 16, 256, 128, 4, False, 10.0), (20, 8, 384, 256, 2, True, 0.0),
-    (37, 32, 512, 128, 8, True, 10.0), (600, 16, 256, 128, 8, True, 0.0)])
+    (37, 32, 512, 128, 8, True, 10.0), (600, 16, 256, 128, 8, True, 0.0),
+    # small-batch layout kernel: up to 16 tokens x (8 + shared) assignments, 256 experts
+    (16, 64, 256, 128, 8, True, 0.0), (9, 256, 256, 128, 8, True, 10.0), (16, 256, 256, 128, 15, True, 0.0)])
 def test_moe_a16_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     ops = _ops()
     rng = np.random.default_rng(m + e + h)
@@ -379,7 +381,8 @@ def test_moe_a16_decode1_baseline_geometry(dev):
     (37, 32, 512, 128, 8, True, 10.0), (520, 8, 256, 128, 8, True, 10.0), (300, 16, 384, 256, 4, False, 0.0),
     (1100, 32, 256, 128, 8, True, 10.0),
     # prefill kernels (H, I multiples of 512): full and partial 256-row tiles, light (<= 64-row) tiles
-    (600, 8, 512, 512, 8, True, 10.0), (130, 32, 512, 512, 8, True, 0.0), (300, 16, 1024, 512, 8, False, 10.0)])
+    (600, 8, 512, 512, 8, True, 10.0), (130, 32, 512, 512, 8, True, 0.0), (300, 16, 1024, 512, 8, False, 10.0),
+    (16, 32, 256, 128, 8, True, 10.0)])
 def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     """A8 layer (fused_moe_mxint contract) vs the A8 oracle of identical bytes."""
     ops = _ops()
