@@ -344,6 +344,31 @@ def test_moe_given_ids_repeated_and_dropped_multi_token(dev, a8):
         assert_close(y[t:t + 1].float().cpu().numpy(), ref, what=f"moe repeated ids token {t}")
 
 
+def test_moe_a8_prefill_tile_boundaries(dev):
+    """Prefill kernels (A8) at the tile-shape boundaries, with given ids: experts
+    with 1, 64 (last light tile), 65 (first full-tile path), 256 (one full tile)
+    and 257 rows (a full tile plus a one-row light tile), plus the shared expert."""
+    ops = _ops()
+    rng = np.random.default_rng(61)
+    e, h, inter = 5, 512, 512
+    rows = [1, 64, 65, 256, 257]
+    ids = np.concatenate([np.full(r, i) for i, r in enumerate(rows)])
+    rng.shuffle(ids)
+    m = ids.size
+    ids = ids.reshape(m, 1).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, size=(m, 1)).astype(np.float32)
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    sh = _make_bank(rng, 1, h, inter)
+    x = _bf16(rng.standard_normal((m, h)))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    shb = (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])), ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    y, _, _ = ops.moe_a8_forward(x.to(dev), ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds)),
+                                 ids=T(ids), weights=T(w), shared=shb, swiglu_limit=10.0)
+    ref = MO.moe_layer_a8(x.float().numpy(), ids, w, gp, gs, dp, ds, swiglu_limit=10.0,
+                          shared=tuple(t[0] for t in sh))
+    assert_close(y.float().cpu().numpy(), ref, what="moe a8 prefill tile boundaries")
+
+
 def test_moe_a16_decode1_baseline_geometry(dev):
     """BASELINE configs[1] geometry (hidden 7168, inter 2048, top-8, shared) on a
     32-expert bank quantized on the device; oracle over the experts actually used."""
