@@ -122,9 +122,10 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = ev0.elapsed_time(ev1)
-    # instrumented pass over the same steps: HIP events recorded on the kernels'
-    # stream at the stage boundaries (they cost a few us of dispatch overlap, so
-    # the headline above is timed without them)
+    # instrumented pass over the same steps: HIP events at the stage boundaries,
+    # on the kernels' stream (at M = 1 the gate/up and down dispatches record
+    # them, so they bracket those kernels' execution); the headline above is
+    # timed without them
     stage = [ops.StageEvents() for _ in range(steps)]
     torch.cuda.synchronize()
     for i in range(steps):

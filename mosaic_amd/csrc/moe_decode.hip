@@ -23,6 +23,8 @@
 // lane (all 16 MFMA rows carry the same data and only row 0 is stored).
 #include <algorithm>
 
+#include <hip/hip_ext.h>
+
 #include "common.h"
 #include "moe_internal.h"
 #include "route_token.h"
@@ -404,10 +406,14 @@ static void launch_dec1_gateup_x(int D, dim3 grid, size_t lds, hipStream_t st, c
                                  const float* bias, const int32_t* ids_in, const float* w_in, int32_t* ids_out,
                                  float* w_out, const uint8_t* gu_p, const uint8_t* gu_s, const uint8_t* sh_p,
                                  const uint8_t* sh_s, uint16_t* z, int32_t* te, int32_t* nt, int H, int I, int E,
-                                 int K, int func, int renorm, float scale, float limit) {
-#define DEC_GU(DV)                                                                                                \
-  hipLaunchKernelGGL((moe_dec1_gateup_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, st, x, logits, bias, ids_in, \
-                     w_in, ids_out, w_out, gu_p, gu_s, sh_p, sh_s, z, te, nt, H, I, E, K, func, renorm, scale, limit)
+                                 int K, int func, int renorm, float scale, float limit, hipEvent_t ev_start,
+                                 hipEvent_t ev_stop) {
+  // the events (stage timing, may be null) are recorded by the dispatch itself:
+  // they bracket the kernel's execution, not the launch around it
+#define DEC_GU(DV)                                                                                              \
+  hipExtLaunchKernelGGL((moe_dec1_gateup_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, st, ev_start, ev_stop, \
+                        0u, x, logits, bias, ids_in, w_in, ids_out, w_out, gu_p, gu_s, sh_p, sh_s, z, te, nt, H,  \
+                        I, E, K, func, renorm, scale, limit)
   switch (D) {
     case 8: DEC_GU(8); break;
     case 7: DEC_GU(7); break;
@@ -421,10 +427,11 @@ static void launch_dec1_gateup_x(int D, dim3 grid, size_t lds, hipStream_t st, c
 template <int KS, int NSP, int ZV>
 static void launch_dec1_down_z(int DT, dim3 grid, size_t lds, hipStream_t st, const uint16_t* z, const int32_t* te,
                                const int32_t* nt, const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_p,
-                               const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared) {
-#define DEC_DN(DV)                                                                                           \
-  hipLaunchKernelGGL((moe_dec1_down_kernel<KS, NSP, DV, ZV>), grid, dim3(KS * 64), lds, st, z, te, nt, d_p, \
-                     d_s, sh_p, sh_s, y, H, I, E, K, has_shared)
+                               const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared,
+                               hipEvent_t ev_stop) {
+#define DEC_DN(DV)                                                                                              \
+  hipExtLaunchKernelGGL((moe_dec1_down_kernel<KS, NSP, DV, ZV>), grid, dim3(KS * 64), lds, st, nullptr, ev_stop, \
+                        0u, z, te, nt, d_p, d_s, sh_p, sh_s, y, H, I, E, K, has_shared)
   switch (DT) {
     case 4: DEC_DN(4); break;
     case 3: DEC_DN(3); break;
@@ -502,7 +509,9 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
   auto mark = [&](int i) {
     if (marks && marks[i]) (void)hipEventRecord((hipEvent_t)marks[i], st);
   };
-  mark(1);  // routing runs inside the gate/up launch: the layout stage is empty
+  auto ev = [&](int i) { return marks ? (hipEvent_t)marks[i] : (hipEvent_t) nullptr; };
+  // routing runs inside the gate/up launch (the layout stage is the dispatch
+  // latency); marks 1 and 2 are the gate/up kernel's own start and end
   const int dn_ks = dec_dn_ks(I / 128);
   const int gu_part = (int)(H / 128 / kDecGuKS), dn_part = (int)(I / 128 / dn_ks);
   const int nz = (int)K + has_shared;
@@ -510,7 +519,8 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
   const int xv = (gu_part * 16 + 63) / 64;
   const dim3 ggrid((unsigned)(I / 16), (unsigned)nz);
 #define GU_ARGS gd, ggrid, (size_t)H * 2, st, x, logits, bias, ids_in, w_in, ids_out, w_out, gu_p, gu_s, sh_gu_p, \
-                sh_gu_s, z, tile_expert, n_tiles, (int)H, (int)I, (int)E, (int)K, func, renorm, route_scale, limit
+                sh_gu_s, z, tile_expert, n_tiles, (int)H, (int)I, (int)E, (int)K, func, renorm, route_scale, limit, \
+                ev(1), ev(2)
   if (xv <= 2)
     launch_dec1_gateup_x<kDecGuKS, 2>(GU_ARGS);
   else if (xv <= 4)
@@ -519,12 +529,11 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
     launch_dec1_gateup_x<kDecGuKS, 8>(GU_ARGS);
 #undef GU_ARGS
   MOSAIC_LAUNCH_CHECK("moe_decode1_gateup");
-  mark(2);
   // ring of 3 tiles (DT * NSP super-steps in flight), 4 when a part is one step
   const int dt = dn_part == 1 ? 4 : 3;
   const int zv = (nz * dn_part * 16 + 63) / 64;
 #define DN_ARGS dt, dim3((unsigned)(H / 16)), (size_t)nz * I * 2, st, z, tile_expert, n_tiles, d_p, d_s, sh_d_p, \
-                sh_d_s, y, (int)H, (int)I, (int)E, (int)K, has_shared
+                sh_d_s, y, (int)H, (int)I, (int)E, (int)K, has_shared, ev(3)
 #define DN_Z(KSV, NSPV)                                  \
   if (zv <= 5)                                           \
     launch_dec1_down_z<KSV, NSPV, 5>(DN_ARGS);           \
@@ -544,8 +553,7 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
 #undef DN_Z
 #undef DN_ARGS
   MOSAIC_LAUNCH_CHECK("moe_decode1_down");
-  mark(3);
-  mark(4);
+  mark(4);  // mark 3 is the down kernel's end; the combine is fused into it
   return kOk;
 }
 
