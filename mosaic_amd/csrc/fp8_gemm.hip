@@ -353,11 +353,31 @@ __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __r
     const int logical = (lane & 7) ^ ((row >> 1) & 7);
     voff[ii] = (uint32_t)min(r0 + row, lim) * (uint32_t)K + (uint32_t)(logical * 16);
   }
+  // Copy issue: a wave stalls at a copy until the address unit takes it, and
+  // 64 one-KB copies per stage keep it busy for ~1000 cycles.  In interior
+  // tiles one half of the waves (0..3 on even blocks, 4..7 on odd) issues the
+  // whole stage, A and B rows through the same lane offsets (the base moved by
+  // n0 - m0 rows), so the other wave of each SIMD keeps its MFMAs going; edge
+  // tiles, whose clamped rows differ between A and B, copy their own operand.
+  const bool interior = m0 + TT::BM <= M && n0 + TT::BN <= N;
+  const uint8_t* base_a = is_a ? A : A + (int64_t)(m0 - n0) * K;
+  const uint8_t* base_b = is_a ? B + (int64_t)(n0 - m0) * K : B;
   auto issue = [&](int st, int kb) {
     const uint32_t base = fp8_lds_addr(lds[st]);
-    const uint8_t* ob = obase + (int64_t)kb * 128;
+    if (interior) {
+      if ((wv >> 2) == (kb & 1)) {
+        const int wq = wv & 3;
 #pragma unroll
-    for (int ii = 0; ii < TT::RUNS; ++ii) fp8_copy16_so(ob, voff[ii], base + (uint32_t)((wv * TT::RUNS + ii) * 1024));
+        for (int ii = 0; ii < TT::RUNS; ++ii) {
+          fp8_copy16_so(base_a + (int64_t)kb * 128, voff[ii], base + (uint32_t)((wq * TT::RUNS + ii) * 1024));
+          fp8_copy16_so(base_b + (int64_t)kb * 128, voff[ii], base + (uint32_t)(((wq + 4) * TT::RUNS + ii) * 1024));
+        }
+      }
+    } else {
+      const uint8_t* ob = obase + (int64_t)kb * 128;
+#pragma unroll
+      for (int ii = 0; ii < TT::RUNS; ++ii) fp8_copy16_so(ob, voff[ii], base + (uint32_t)((wv * TT::RUNS + ii) * 1024));
+    }
   };
   // scale chunk loads: thread t takes a_s slot t / 2, blocks 4 (t % 2) .. + 3 of
   // the chunk; threads 0..15 also take b_s (block t % 8, column half t / 8)
@@ -401,7 +421,6 @@ __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __r
     const int ch = kb / TT::CHUNK, kc = kb % TT::CHUNK;
     const bool next_chunk = (ch + 1) * TT::CHUNK < nkb;
     if (kc == 2 && next_chunk) store_chunk(ch + 1, pend_a, pend_b);  // its loads completed at the wait above
-    if (kb + 1 < nkb) issue((kb + 1) & 1, kb + 1);
     if (kc == 1 && next_chunk) load_chunk(ch + 1, pend_a, pend_b);
     const uint8_t* stg = lds[kb & 1];
     const uint8_t* ta = stg;
@@ -416,6 +435,8 @@ __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __r
     aop[0] = lds_fp8_operand(ta, wm + c, q);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
+      // block kb + 1's copies, once the first tile's MFMAs are issued
+      if (mt == 1 && kb + 1 < nkb) issue((kb + 1) & 1, kb + 1);
       if (mt + 1 < 8) aop[(mt + 1) & 1] = lds_fp8_operand(ta, wm + 16 * (mt + 1) + c, q);
       f32x4_t d[4];
 #pragma unroll
