@@ -113,6 +113,21 @@ int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* pa
 int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
                           int out_dtype, int64_t m, int64_t n, int64_t k, void* stream);
 
+/* Bytes of the fp32 partials workspace that mosaic_fp8_block_gemm_ws uses to
+ * split K over up to 8 slices when the output tiles cover fewer than half of
+ * the GPU (0: the shape is not split).  No counterpart in the reference, whose
+ * fp8_gemm launches allocate nothing; it serves the same call sites. */
+size_t mosaic_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/* mosaic_fp8_block_gemm with a caller-provided workspace of workspace_bytes
+ * (>= mosaic_fp8_block_gemm_workspace_bytes(m, n, k) to split K; with less,
+ * or NULL, it runs unsplit).  The slices' fp32 partials are summed in slice
+ * order.  Same call sites as mosaic_fp8_block_gemm (fp8_gemm,
+ * .mosaicvm/source/inference_kernel.py:203-273). */
+int mosaic_fp8_block_gemm_ws(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
+                             int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* e4m3 [n, k] with one f32 scale per block_n x block_k block -> bf16 [n, k].
  * Replaces dequant_fp8 (runtime/fp8.py:52-64), dsa.dequant_weight
  * (model/dsa.py:72-78) and fp8_core's dequant_kernel (bench/fp8_core.py:60-91). */

@@ -174,10 +174,14 @@ struct Fp8Tile {
   static_assert(SRUNS + 1 <= NW, "one scale copy per wave");
 };
 
+// Split-K (blockIdx.y = K slice of kps blocks): with `part` the slice writes its
+// fp32 partial tile to part[slice][M][N] (fp8_splitk_reduce_kernel sums the
+// slices in order); without it the tile goes to C.
 template <int BM>
 __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
-    const float* __restrict__ Bs, void* __restrict__ C, int M, int N, int K, int out_f32) {
+    const float* __restrict__ Bs, void* __restrict__ C, int M, int N, int K, int out_f32, int kps,
+    float* __restrict__ part) {
   using TT = Fp8Tile<BM>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kStages][TT::STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -221,16 +225,17 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  issue(0, 0);
-  if (nkb > 1) issue(1, 1);
-  for (int kb = 0; kb < nkb; ++kb) {
-    // block kb landed for every wave (its copies, then the barrier); kb + 1 may still fly
-    if (kb + 1 < nkb)
+  const int kb0 = (int)blockIdx.y * kps, cnt = min(nkb, kb0 + kps) - kb0;
+  issue(0, kb0);
+  if (cnt > 1) issue(1, kb0 + 1);
+  for (int i = 0; i < cnt; ++i) {
+    // block kb0 + i landed for every wave (its copies, then the barrier); the next may still fly
+    if (i + 1 < cnt)
       asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(TT::OPS) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kb + 2 < nkb) issue((kb + 2) % kStages, kb + 2);
-    const uint8_t* stg = lds[kb % kStages];
+    if (i + 2 < cnt) issue((i + 2) % kStages, kb0 + i + 2);
+    const uint8_t* stg = lds[i % kStages];
     const uint8_t* ta = stg;
     const uint8_t* tb = stg + BM * 128;
     const float sb = *reinterpret_cast<const float*>(stg + TT::SB);
@@ -262,7 +267,9 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm + 16 * mt + 4 * q + r;
         if (m < M && n < N) {
-          if (out_f32)
+          if (part)
+            part[((int64_t)blockIdx.y * M + m) * N + n] = acc[mt][nt][r];
+          else if (out_f32)
             reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[mt][nt][r];
           else
             reinterpret_cast<uint16_t*>(C)[(int64_t)m * N + n] = f32_bf16(acc[mt][nt][r]);
@@ -271,12 +278,36 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
     }
 }
 
+// C = sum over the S slices of part, in slice order; 4 elements per thread
+__global__ void __launch_bounds__(256) fp8_splitk_reduce_kernel(const float* __restrict__ part, int S, int64_t mn,
+                                                                void* __restrict__ C, int out_f32) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = i0 + j;
+    if (i >= mn) break;
+    float v = part[i];
+    for (int sl = 1; sl < S; ++sl) v += part[(int64_t)sl * mn + i];
+    if (out_f32)
+      reinterpret_cast<float*>(C)[i] = v;
+    else
+      reinterpret_cast<uint16_t*>(C)[i] = f32_bf16(v);
+  }
+}
+
 template <int BM>
 static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c,
-                             int64_t m, int64_t n, int64_t k, int out_f32, hipStream_t st) {
+                             int64_t m, int64_t n, int64_t k, int out_f32, hipStream_t st, int S = 1,
+                             float* part = nullptr) {
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((fp8_gemm_tiled_kernel<BM>), dim3((unsigned)tiles), dim3(BM * 2), 0, st, a, as, b, bs, c, (int)m,
-                     (int)n, (int)k, out_f32);
+  const int nkb = (int)(k / 128), kps = (nkb + S - 1) / S;
+  hipLaunchKernelGGL((fp8_gemm_tiled_kernel<BM>), dim3((unsigned)tiles, (unsigned)S), dim3(BM * 2), 0, st, a, as, b,
+                     bs, c, (int)m, (int)n, (int)k, out_f32, kps, S > 1 ? part : nullptr);
+  if (S > 1) {
+    const int64_t mn = m * n;
+    hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, part, S, mn,
+                       c, out_f32);
+  }
 }
 
 // Large tiled kernel (enough 256 x 256 tiles to fill the chip): a workgroup
@@ -509,10 +540,6 @@ __global__ void __launch_bounds__(256) fp8_block_dequant_kernel(const uint8_t* _
   o[3] = f32_bf16(hi[1] * sc);
 }
 
-}  // namespace mosaic
-
-using namespace mosaic;
-
 extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16_t* out, int64_t n, int64_t k,
                                         int block_n, int block_k, void* stream) {
   MOSAIC_CHECK_ARG(w && s && out, "fp8_block_dequant: null pointer");
@@ -525,8 +552,40 @@ extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16
   MOSAIC_RETURN_LAUNCH("fp8_block_dequant");
 }
 
-extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
-                                     int out_dtype, int64_t m, int64_t n, int64_t k, void* stream) {
+// Kernel choice of the block GEMM.  kind 0: skinny, 1: tiled<128>, 2: tiled<256>,
+// 3: big tiles.  The tiled kernels split K into S slices (S > 1 needs the
+// S * M * N * 4-byte partials workspace) when their tiles cover fewer than
+// half of the 256 CUs: S = min(8, 256 / tiles, K-blocks / 4).
+struct Fp8Plan {
+  int kind, S;
+};
+static Fp8Plan fp8_plan(int64_t m, int64_t n, int64_t k) {
+  const int64_t nkb = k / 128;
+  auto split = [&](int64_t tiles) {
+    int64_t s = std::min<int64_t>(8, std::min<int64_t>(256 / std::max<int64_t>(tiles, 1), nkb / 4));
+    return tiles * 2 <= 256 && s >= 2 ? (int)s : 1;
+  };
+  if (m >= 256) {
+    const int64_t big_tiles = ((m + 255) / 256) * ((n + 255) / 256);
+    // the big kernel addresses A and B with 32-bit offsets
+    if (big_tiles >= 256 && m * k < (1ll << 32) && n * k < (1ll << 32)) return {3, 1};
+    return {2, split(((m + 255) / 256) * ((n + 127) / 128))};
+  }
+  if (m >= 96) {
+    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+    const int s = split(tiles);
+    if (tiles * s >= 32) return {1, s};
+  }
+  return {0, 1};
+}
+
+}  // namespace mosaic
+
+using namespace mosaic;
+
+static int fp8_block_gemm_impl(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
+                               int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   MOSAIC_CHECK_ARG(a && a_s && b && b_s && c, "fp8_block_gemm: null pointer");
   MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "fp8_block_gemm: K=%lld must be a positive multiple of 128",
                    (long long)k);
@@ -537,30 +596,47 @@ extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const u
   if (m == 0 || n == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
   const int f32 = out_dtype == MOSAIC_DTYPE_F32;
+  Fp8Plan plan = fp8_plan(m, n, k);
+  if (plan.S > 1 && (!workspace || workspace_bytes < (size_t)plan.S * m * n * 4)) {
+    // no partials workspace: the whole K in one slice (the kernels of the plan without split)
+    plan = plan.kind == 1 && ((m + 127) / 128) * ((n + 127) / 128) < 32 ? Fp8Plan{0, 1} : Fp8Plan{plan.kind, 1};
+  }
+  float* part = reinterpret_cast<float*>(workspace);
   const int64_t mt = (m + 15) / 16;
-  if (m >= 256) {
-    const int64_t big_tiles = ((m + 255) / 256) * ((n + 255) / 256);
-    // the big kernel addresses A and B with 32-bit offsets
-    if (big_tiles >= 256 && m * k < (1ll << 32) && n * k < (1ll << 32)) {
+  switch (plan.kind) {
+    case 3: {
+      const int64_t big_tiles = ((m + 255) / 256) * ((n + 255) / 256);
       hipLaunchKernelGGL(fp8_gemm_big_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a, a_s, b, b_s, c, (int)m,
                          (int)n, (int)k, f32);
-      MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
+      break;
     }
-    launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st);
-    MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
+    case 2: launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
+    case 1: launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
+    default:
+      // columns per wave chosen so the grid covers the chip (>= ~2048 waves)
+      if (((n + 63) / 64) * mt * 8 >= 4096)
+        launch_fp8_skinny<4, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      else if (((n + 31) / 32) * mt * 8 >= 4096)
+        launch_fp8_skinny<2, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      else
+        launch_fp8_skinny<1, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
   }
-  // 96 <= M < 256: 128x128 tiles when there are enough of them to spread over
-  // the chip, else the skinny kernel (K split over 8 waves, one grid row per 16 tokens)
-  if (m >= 96 && ((m + 127) / 128) * ((n + 127) / 128) >= 32) {
-    launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st);
-    MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
-  }
-  // columns per wave chosen so the grid covers the chip (>= ~2048 waves)
-  if (((n + 63) / 64) * mt * 8 >= 4096)
-    launch_fp8_skinny<4, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
-  else if (((n + 31) / 32) * mt * 8 >= 4096)
-    launch_fp8_skinny<2, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
-  else
-    launch_fp8_skinny<1, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
   MOSAIC_RETURN_LAUNCH("fp8_block_gemm");
+}
+
+extern "C" int mosaic_fp8_block_gemm(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s, void* c,
+                                     int out_dtype, int64_t m, int64_t n, int64_t k, void* stream) {
+  return fp8_block_gemm_impl(a, a_s, b, b_s, c, out_dtype, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" size_t mosaic_fp8_block_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 128) return 0;
+  const Fp8Plan plan = fp8_plan(m, n, k);
+  return plan.S > 1 ? (size_t)plan.S * (size_t)m * (size_t)n * 4 : 0;
+}
+
+extern "C" int mosaic_fp8_block_gemm_ws(const uint8_t* a, const float* a_s, const uint8_t* b, const float* b_s,
+                                        void* c, int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return fp8_block_gemm_impl(a, a_s, b, b_s, c, out_dtype, m, n, k, workspace, workspace_bytes, stream);
 }

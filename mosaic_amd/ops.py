@@ -247,8 +247,11 @@ def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: tor
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"out_dtype {out_dtype}")
     c = torch.empty(m, n, dtype=out_dtype, device=a.device)
-    _lib.call("mosaic_fp8_block_gemm", _ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(c),
-              DT_F32 if out_dtype == torch.float32 else DT_BF16, m, n, k, _stream())
+    # partials of the split-K plan (shapes whose tiles cover under half the GPU)
+    nbytes = _lib.lib().mosaic_fp8_block_gemm_workspace_bytes(m, n, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
+    _lib.call("mosaic_fp8_block_gemm_ws", _ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(c),
+              DT_F32 if out_dtype == torch.float32 else DT_BF16, m, n, k, _ptr(ws), nbytes, _stream())
     return c
 
 

@@ -27,7 +27,9 @@ def _case(rng, m, n, k):
                                    (128, 256, 1536), (1, 24576, 1536), (64, 7168, 512),
                                    (256, 128, 128), (300, 576, 1024), (1024, 1536, 2048), (513, 700, 384),
                                    (129, 8200, 512), (200, 640, 1536), (96, 1536, 7168), (2304, 7200, 384),
-                                   (1024, 16384, 384), (1024, 16384, 2304)])
+                                   (1024, 16384, 384), (1024, 16384, 2304),
+                                   # split K (tiles under half the GPU): tiled<128> x 8 / x 4, tiled<256> x 3
+                                   (128, 576, 7168), (128, 7168, 4096), (4096, 576, 7168)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
     from mosaic_amd import ops
