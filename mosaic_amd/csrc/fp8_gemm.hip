@@ -120,7 +120,10 @@ static void launch_fp8_skinny(const uint8_t* a, const float* as, const uint8_t* 
 // (row >> 1) & 7 (applied on the global side of the copy), so the 16 rows one
 // MFMA operand read touches fall in distinct banks.  Workgroups are remapped so
 // that the ones on one XCD (dispatch goes round-robin over 8) take
-// neighbouring tiles, grouped 8 M-tiles deep.
+// neighbouring tiles, grouped 8 M-tiles deep.  The K loop has the big kernel's
+// schedule: transposed MFMA roles (one a_s per lane and tile, 4 consecutive C
+// columns per lane), the next A fragment read during the MFMAs, each tile's
+// rescale issued after the next tile's MFMAs.
 constexpr int kTileN = 128, kStages = 3;
 
 __device__ __forceinline__ void tile_coords(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -225,6 +228,10 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x4_t dp[4];  // product of the previous tile, rescaled one tile later
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) dp[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float sp = 0.f;
   const int kb0 = (int)blockIdx.y * kps, cnt = min(nkb, kb0 + kps) - kb0;
   issue(0, kb0);
   if (cnt > 1) issue(1, kb0 + 1);
@@ -242,40 +249,62 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
     i32x8_t bop[4];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) bop[nt] = lds_fp8_operand(tb, wn + 16 * nt + c, q);
+    i32x8_t aop[2];
+    aop[0] = lds_fp8_operand(ta, wm + c, q);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const i32x8_t aop = lds_fp8_operand(ta, wm + 16 * mt + c, q);
+      if (mt + 1 < 4) aop[(mt + 1) & 1] = lds_fp8_operand(ta, wm + 16 * (mt + 1) + c, q);
+      // transposed roles: rows are B rows (n), columns A rows (m = wm + 16 mt + c)
       f32x4_t d[4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(aop, bop[nt]);
-      // a_s of this lane's accumulator rows wm + 16 mt + 4 q + r
-      const f32x4_t sa4 = *reinterpret_cast<const f32x4_t*>(stg + TT::SA + 4 * (wm + 16 * mt + 4 * q));
+      for (int nt = 0; nt < 4; ++nt) d[nt] = mfma_fp8_block(bop[nt], aop[mt & 1]);
+      const int pm = mt == 0 ? 3 : mt - 1;  // the previous tile (tile 3 of the previous block at mt == 0)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float s = sa4[r] * sb;
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[mt][nt][r] = __builtin_fmaf(d[nt][r], s, acc[mt][nt][r]);
-      }
+        for (int r = 0; r < 4; ++r) acc[pm][nt][r] = __builtin_fmaf(dp[nt][r], sp, acc[pm][nt][r]);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) dp[nt] = d[nt];
+      sp = *reinterpret_cast<const float*>(stg + TT::SA + 4 * (wm + 16 * mt + c)) * sb;
     }
   }
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[3][nt][r] = __builtin_fmaf(dp[nt][r], sp, acc[3][nt][r]);
+  // lane (c, q) of tile (mt, nt) holds C[m0 + wm + 16 mt + c][n .. n + 3], n = n0 + wn + 16 nt + 4 q
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int m = m0 + wm + 16 * mt + c;
+    if (m >= M) continue;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-      const int n = n0 + wn + 16 * nt + c;
+      const int n = n0 + wn + 16 * nt + 4 * q;
+      const f32x4_t v = acc[mt][nt];
+      if (part || out_f32) {
+        float* o = part ? part + ((int64_t)blockIdx.y * M + m) * N + n : reinterpret_cast<float*>(C) + (int64_t)m * N + n;
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<f32x4_t*>(o) = v;
+        } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm + 16 * mt + 4 * q + r;
-        if (m < M && n < N) {
-          if (part)
-            part[((int64_t)blockIdx.y * M + m) * N + n] = acc[mt][nt][r];
-          else if (out_f32)
-            reinterpret_cast<float*>(C)[(int64_t)m * N + n] = acc[mt][nt][r];
-          else
-            reinterpret_cast<uint16_t*>(C)[(int64_t)m * N + n] = f32_bf16(acc[mt][nt][r]);
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) o[r] = v[r];
+        }
+      } else {
+        uint16_t* o = reinterpret_cast<uint16_t*>(C) + (int64_t)m * N + n;
+        if (vec && n + 3 < N) {
+          const uint32_t lo = (uint32_t)f32_bf16(v[0]) | ((uint32_t)f32_bf16(v[1]) << 16);
+          const uint32_t hi = (uint32_t)f32_bf16(v[2]) | ((uint32_t)f32_bf16(v[3]) << 16);
+          *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) o[r] = f32_bf16(v[r]);
         }
       }
     }
+  }
 }
 
 // C = sum over the S slices of part, in slice order; 4 elements per thread
