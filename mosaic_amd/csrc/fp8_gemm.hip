@@ -98,6 +98,122 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemm_skinny_kernel(
   }
 }
 
+// Decode-shaped GEMM (M <= 16, wide N): MFMA roles transposed (rows are 16 B
+// rows, columns the M tokens, so a lane's column has one a_s per K-block); a
+// workgroup owns 16 T columns of C and its KS waves split K.  Each wave streams
+// its K-blocks through a register ring of D entries (the T tiles' B operands,
+// the A operand, a_s and the T b_s values of one block), issued D blocks ahead
+// with buffer loads: B rows past N and A rows past M read zeros, entries past
+// the wave's range reload its last block and are scaled by 0, so the loop has
+// no branches.  The K parts meet in LDS in wave order.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fp8_rsrc(const void* base, int64_t records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)records, 0x00020000);
+}
+
+template <int T, int KS, int D>
+__global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __restrict__ A, const float* __restrict__ As,
+                                                           const uint8_t* __restrict__ B,
+                                                           const float* __restrict__ Bs, void* __restrict__ C, int M,
+                                                           int N, int K, int out_f32) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16 * T;
+  const int nkb = K / 128;
+  const int kb0 = nkb * ks / KS, nb = nkb * (ks + 1) / KS - kb0;
+  const __amdgpu_buffer_rsrc_t rb = fp8_rsrc(B + (int64_t)n0 * K, (int64_t)min(N - n0, 16 * T) * K);
+  const __amdgpu_buffer_rsrc_t ra = fp8_rsrc(A, (int64_t)M * K);
+  const __amdgpu_buffer_rsrc_t rs = fp8_rsrc(As, (int64_t)M * nkb * 4);
+  const uint32_t a_row = c < M ? (uint32_t)(c * K) + 16u * q : 0x80000000u;  // rows past M: out of range
+  const uint32_t s_row = c < M ? (uint32_t)(c * nkb) * 4u : 0x80000000u;
+  const float* bs_row[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) bs_row[t] = Bs + (int64_t)(min(n0 + 16 * t, N - 1) / 128) * nkb;
+  u32x4_t rbv[D][T][2], rav[D][2];
+  float rsa[D], rsb[D][T];
+  auto load = [&](int s, int i) {
+    const int kb = kb0 + (i < nb ? i : nb - 1);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t off = (uint32_t)((16 * t + c) * K + kb * 128 + 16 * q);
+      rbv[s][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
+      rbv[s][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(off + 64), 0, 0);
+      rsb[s][t] = bs_row[t][kb];
+    }
+    rav[s][0] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_row + kb * 128), 0, 0);
+    rav[s][1] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_row + kb * 128 + 64), 0, 0);
+    rsa[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(s_row + kb * 4), 0, 0));
+  };
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int s, int i) {
+    const i32x8_t a = {(int)rav[s][0][0], (int)rav[s][0][1], (int)rav[s][0][2], (int)rav[s][0][3],
+                       (int)rav[s][1][0], (int)rav[s][1][1], (int)rav[s][1][2], (int)rav[s][1][3]};
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const i32x8_t bo = {(int)rbv[s][t][0][0], (int)rbv[s][t][0][1], (int)rbv[s][t][0][2], (int)rbv[s][t][0][3],
+                          (int)rbv[s][t][1][0], (int)rbv[s][t][1][1], (int)rbv[s][t][1][2], (int)rbv[s][t][1][3]};
+      const f32x4_t d = mfma_fp8_block(bo, a);
+      const float sc = i < nb ? rsa[s] * rsb[s][t] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(d[r], sc, acc[t][r]);
+    }
+  };
+  const int nchunks = (nb + D - 1) / D;
+  if (nb > 0) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) load(s, s);
+    for (int ch = 0; ch + 1 < nchunks; ++ch) {
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        compute(s, ch * D + s);
+        load(s, ch * D + s + D);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s) compute(s, (nchunks - 1) * D + s);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T && c < M) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+    // lane (c, q): C[c][n .. n + 3], n = n0 + 16 t + 4 q
+    const int n = n0 + 16 * t + 4 * q;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (n + r < N) {
+        if (out_f32)
+          reinterpret_cast<float*>(C)[(int64_t)c * N + n + r] = v[r];
+        else
+          reinterpret_cast<uint16_t*>(C)[(int64_t)c * N + n + r] = f32_bf16(v[r]);
+      }
+    }
+  }
+}
+
+template <int T, int KS>
+static void launch_fp8_gemv(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c, int64_t m,
+                            int64_t n, int64_t k, int out_f32, hipStream_t st) {
+  const int nb = (int)(k / 128 / KS);
+  const dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)));
+#define FP8_GEMV(DV) \
+  hipLaunchKernelGGL((fp8_gemv_kernel<T, KS, DV>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, out_f32)
+  if (nb % 8 == 0)
+    FP8_GEMV(8);
+  else if (nb % 7 == 0)
+    FP8_GEMV(7);
+  else if (nb % 6 == 0)
+    FP8_GEMV(6);
+  else
+    FP8_GEMV(4);
+#undef FP8_GEMV
+}
+
 template <int T, int KS>
 static void launch_fp8_skinny(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c,
                               int64_t m, int64_t n, int64_t k, int out_f32, hipStream_t st) {
@@ -582,7 +698,7 @@ extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16
 }
 
 // Kernel choice of the block GEMM.  kind 0: skinny, 1: tiled<128>, 2: tiled<256>,
-// 3: big tiles.  The tiled kernels split K into S slices (S > 1 needs the
+// 3: big tiles, 4: decode ring (M <= 16, wide N).  The tiled kernels split K into S slices (S > 1 needs the
 // S * M * N * 4-byte partials workspace) when their tiles cover fewer than
 // half of the 256 CUs: S = min(8, 256 / tiles, K-blocks / 4).
 struct Fp8Plan {
@@ -605,6 +721,8 @@ static Fp8Plan fp8_plan(int64_t m, int64_t n, int64_t k) {
     const int s = split(tiles);
     if (tiles * s >= 32) return {1, s};
   }
+  // decode shapes with wide N: the ring kernel (>= 128 workgroups of 32 columns, >= 4 blocks per K part)
+  if (m <= 16 && n >= 4096 && nkb >= 8 && (int64_t)n * k < (1ll << 31)) return {4, 1};
   return {0, 1};
 }
 
@@ -639,6 +757,7 @@ static int fp8_block_gemm_impl(const uint8_t* a, const float* a_s, const uint8_t
                          (int)n, (int)k, f32);
       break;
     }
+    case 4: launch_fp8_gemv<2, 2>(a, a_s, b, b_s, c, m, n, k, f32, st); break;
     case 2: launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     case 1: launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     default:
