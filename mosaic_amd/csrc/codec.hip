@@ -143,8 +143,11 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const T* __restrict__ x,
   } else {
     s = amax / 448.0f;
   }
+  // a power-of-two scale (mode 0) has an exact reciprocal: x * (1 / s) == x / s
+  const float inv = mode == 0 ? 1.0f / s : 0.f;
   for (int i = lane; i < block; i += 64) {
-    float y = load_as_f32<T>(x, base + i) / s;
+    const float xv = load_as_f32<T>(x, base + i);
+    float y = mode == 0 ? xv * inv : xv / s;
     y = fminf(fmaxf(y, -448.0f), 448.0f);
     q[base + i] = (uint8_t)e4m3_rne(y);
   }
@@ -194,10 +197,12 @@ __global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__
   } else {
     s = amax / 448.0f;
   }
+  // a power-of-two scale (mode 0) has an exact reciprocal: v * (1 / s) == v / s
+  const float inv = mode == 0 ? 1.0f / s : 0.f;
   uint32_t lo = 0, hi = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float y = v[i] / s;
+    float y = mode == 0 ? v[i] * inv : v[i] / s;
     y = fminf(fmaxf(y, -448.0f), 448.0f);
     const uint32_t b = e4m3_rne(y);
     if (i < 4) lo |= b << (8 * i);

@@ -624,7 +624,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
         const float sc = act_scale_pow2(__uint_as_float(um));
         if (row < rows) {
           const int64_t pp = p0 + row;
-          const float y = fminf(fmaxf(lacc[mt][0][r] / sc, -448.0f), 448.0f);
+          const float y = fminf(fmaxf(lacc[mt][0][r] * (1.0f / sc), -448.0f), 448.0f);  // sc = 2^e: exact
           zq[pp * I + j0 + 16 * wv + c] = (uint8_t)e4m3_rne(y);
           if (wv == 0 && c == 0) zs[pp * nbk + j0 / 128] = sc;
         }
@@ -697,7 +697,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
         const int64_t pp = p0 + row;
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          const float y = fminf(fmaxf(acc[mt][n][r] / sc, -448.0f), 448.0f);
+          const float y = fminf(fmaxf(acc[mt][n][r] * (1.0f / sc), -448.0f), 448.0f);  // sc = 2^e: exact
           zq[pp * I + j0 + 64 * hc + 16 * n + c] = (uint8_t)e4m3_rne(y);
         }
         if (hc == 0 && c == 0) zs[pp * nbk + j0 / 128] = sc;
