@@ -389,7 +389,8 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[3][nt][r] = __builtin_fmaf(dp[nt][r], sp, acc[3][nt][r]);
   // lane (c, q) of tile (mt, nt) holds C[m0 + wm + 16 mt + c][n .. n + 3], n = n0 + wn + 16 nt + 4 q
-  const bool vec = (N & 3) == 0;
+  // 4-column vector stores: N % 4 == 0 and an output base aligned for them (16 B covers both widths)
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(part ? (const void*)part : C) & 15) == 0;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const int m = m0 + wm + 16 * mt + c;
@@ -560,7 +561,7 @@ __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __r
   const int slot = tid >> 1, half = tid & 1;
   const float* arow = As + (int64_t)min(m0 + fp8_big_slot_row(slot), M - 1) * nkb;
   const float* brow = Bs + (int64_t)min(n0 / 128 + ((tid >> 3) & 1), (N - 1) / 128) * nkb;
-  const bool vec_as = (nkb & 3) == 0;  // 16-byte aligned a_s rows
+  const bool vec_as = (nkb & 3) == 0 && (reinterpret_cast<uintptr_t>(As) & 15) == 0;  // 16-byte aligned a_s rows
   auto load_chunk = [&](int ch, f32x4_t& va, float& vb) {
     const int k0 = ch * TT::CHUNK + 4 * half;
     if (vec_as && k0 + 3 < nkb) {
@@ -632,7 +633,8 @@ __global__ void __launch_bounds__(512, 1) fp8_gemm_big_kernel(const uint8_t* __r
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[7][nt][r] = __builtin_fmaf(dp[nt][r], sp, acc[7][nt][r]);
   // lane (c, q) of tile (mt, nt) holds C[m0 + wm + 16 mt + c][n .. n + 3], n = n0 + wn + 16 nt + 4 q
-  const bool vec = (N & 3) == 0;
+  // 4-column vector stores: N % 4 == 0 and an output base aligned for them (16 B covers both widths)
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) {
     const int m = m0 + wm + 16 * mt + c;
