@@ -398,8 +398,10 @@ __device__ __forceinline__ void pf_kloop_t(const PfSrc& src, int ns, const int (
   for (int S = 0; S < ns; ++S) {
     // step S landed (every wave's copies: the barrier), step S + 1 may still fly
     pf_wait_ops(S + 1 < ns ? pf_ops(S + 1, n_a, wv) : 0);
-    if (S + 2 < ns) pf_issue(src, S + 2, ring[(S + 2) % kPfStages], chunk, n_a);
+    // the step's MFMAs first, then step S + 2's copies (slot (S + 2) % 3 was
+    // step S - 1's, which every wave finished before the barrier above)
     if constexpr (LIVE > 0) pf_compute<LIVE>(ring[S % kPfStages], chunk + ((S >> 2) & 1) * kPfChunk, wg, S, acc);
+    if (S + 2 < ns) pf_issue(src, S + 2, ring[(S + 2) % kPfStages], chunk, n_a);
   }
 }
 
@@ -512,9 +514,11 @@ __device__ __forceinline__ void pfl_kloop_t(const PfLSrc& src, int ns, int ga, i
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   for (int S = 0; S < ns; ++S) {
     pfl_wait(min(kPfLStages - 2, ns - 1 - S), wv);  // step S landed, later issued steps may fly
+    // the step's MFMAs go out first: a wave stalls at a copy until the address
+    // unit takes it, and issued MFMAs keep running meanwhile
+    pfl_compute<MT>(ring + (S % kPfLStages) * kPfLStage, ga, gb, S, acc);
     if (S + kPfLStages - 1 < ns)
       pfl_issue(src, S + kPfLStages - 1, ring + ((S + kPfLStages - 1) % kPfLStages) * kPfLStage);
-    pfl_compute<MT>(ring + (S % kPfLStages) * kPfLStage, ga, gb, S, acc);
   }
 }
 
