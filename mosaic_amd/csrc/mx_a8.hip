@@ -257,19 +257,21 @@ __global__ void __launch_bounds__(KS * 64) moe_a8_down_kernel(
 }
 
 // ------------------------------------------------------ prefill (A8) ------
-// Large batches: tiles of 128 sorted assignment rows of one expert, a
-// workgroup of 4 waves per (tile, 8 weight groups of 16 rows).  Per 128-K step
-// the workgroup stages in LDS, in MFMA operand order: the e4m3 rows of its
-// tokens (two 1 KB runs per 16-row tile), the MXT16 weight blocks (1 KB per
-// group, already in lane order), the weight scale dwords and the rows'
-// activation scales.  Everything moves global -> LDS directly
+// Large batches: tiles of 256 sorted assignment rows of one expert, a
+// workgroup of 8 waves per (tile, 16 weight groups of 16 rows).  Per 128-K
+// step the workgroup stages in LDS the e4m3 rows of its tokens (256 rows of
+// 128 bytes, 16-byte chunks XOR-swizzled by (row >> 1) & 7, copied as runs of
+// 8 whole rows) and the MXT16 weight blocks (1 KB per group, already in lane
+// order); the weight scale dwords and the rows' activation scales move once
+// per 4 steps into two chunk buffers.  Everything moves global -> LDS directly
 // (global_load_lds) through a ring of three stages, two steps ahead of the
 // MFMAs.  The copies are issued from inline asm with explicit vmcnt waits and
 // a bare s_barrier: the compiler then neither waits for the in-flight stages
 // before each LDS read (which it does for copies it knows about) nor needs
-// staging registers.  Each wave owns 64 rows x 4 groups and accumulates
+// staging registers.  Each wave owns 64 rows x 8 groups and accumulates
 // straight into its MFMA accumulators: both scales are e8m0 operands of
-// v_mfma_scale, so there is no per-step VALU rescale.
+// v_mfma_scale, so there is no per-step VALU rescale.  Tiles of at most 64
+// rows take the light-tile path below.
 constexpr int kPfBM = 256;     // sorted rows per tile
 constexpr int kPfWaves = 8;    // 4 row quarters x 2 column halves
 constexpr int kPfStages = 3;
@@ -281,9 +283,9 @@ constexpr int kPfStage = kPfB + kPfNG * 1024;  // A rows and weight blocks of on
 // 16 bytes (4 steps) per row, so the row-scale gather touches each row's
 // line once per 4 steps instead of once per step.
 constexpr int kPfCBs = 0, kPfCAs = kPfNG * 256, kPfChunk = kPfCAs + kPfBM * 16;
-// copies per wave per step: 2 A runs per valid 16-row tile of the wave's two
-// (0, 2 or 4) and 2 weight runs; on steps 4c also the chunk: 2 weight-scale
-// runs and (waves 0..3) one 16-byte row-scale run
+// copies per wave per step: its A runs holding tile rows (0..4, 8 rows each)
+// and 2 weight runs; on steps 4c also the chunk: 2 weight-scale runs and
+// (waves 0..3) one 16-byte row-scale run
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -308,7 +310,7 @@ __device__ __forceinline__ void pf_coords(int id, int n_col, int& col, int& tile
 
 // this lane's sources for the wave's copy runs of one stage (add the step offsets)
 struct PfSrc {
-  const uint8_t* a[4];   // A run 4 wv + i: 16-row tile run >> 1, bytes 64 (run & 1) + 16 (lane / 16) of row lane % 16
+  const uint8_t* a[4];   // A run 4 wv + i: rows 8 (4 wv + i) .. + 7, this lane's 16-byte chunk (swizzled)
   const uint8_t* b[2];   // weight group 2 wv + i, this lane's 16 bytes
   const uint8_t* bs[2];  // its scale dword
   const float* as;       // row 64 (wv & 3) + lane: its 1x128 scale row (waves 0..3)
@@ -317,9 +319,9 @@ struct PfSrc {
 // copies of one step by this wave (see pf_issue)
 __device__ __forceinline__ int pf_ops(int S, int n_a, int wv) { return n_a + 2 + ((S & 3) == 0 ? (wv < 4 ? 3 : 2) : 0); }
 
-// A runs 4 wv + i of 16-row tiles past the tile's rows are not copied (no
-// wave computes on them); n_a is 0, 2 or 4, uniform over the wave.  Steps 4c
-// also copy chunk c (into chunk buffer c & 1).
+// A runs 4 wv + i (8 rows each) past the tile's rows are not copied (no wave
+// computes on them); n_a is 0..4, uniform over the wave.  Steps 4c also copy
+// chunk c (into chunk buffer c & 1).
 __device__ __forceinline__ void pf_issue(const PfSrc& src, int S, uint8_t* stage, uint8_t* chunk, int n_a) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t base = lds_u32(stage);
@@ -349,8 +351,11 @@ __device__ __forceinline__ void pf_compute(const uint8_t* stage, const uint8_t* 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int mtg = 4 * (wv >> 1) + mt;
-    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + lane * 16);
-    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(stage + kPfA + mtg * 2048 + 1024 + lane * 16);
+    // row r of the tile is 128 bytes at r * 128, its 16-byte chunks XOR-swizzled by (r >> 1) & 7
+    const int row = 16 * mtg + c, swz = (row >> 1) & 7, q = lane >> 4;
+    const uint8_t* rp = stage + kPfA + row * 128;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(rp + ((q ^ swz) << 4));
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(rp + (((q + 4) ^ swz) << 4));
     a[mt] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     sa[mt] = pow2_e8m0(*reinterpret_cast<const float*>(chunk + kPfCAs + (16 * mtg + c) * 16 + (S & 3) * 4));
   }
@@ -411,9 +416,9 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& src, int ns, int rows, con
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[mt][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // A runs of this wave: its 16-row tiles 2 wv and 2 wv + 1, two runs each if valid
+  // A runs of this wave: rows 32 wv + 8 i .. + 7 (i < 4), those holding tile rows
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n_a = (32 * wv < rows ? 2 : 0) + (32 * wv + 16 < rows ? 2 : 0);
+  const int n_a = min(4, max(0, (rows - 32 * wv + 7) / 8));
   pf_issue(src, 0, ring[0], chunk, n_a);
   if (ns > 1) pf_issue(src, 1, ring[1], chunk, n_a);
   // the wave's row tiles past the valid rows are skipped (one loop per count)
@@ -432,7 +437,10 @@ __device__ __forceinline__ void pf_sources(PfSrc& src, const uint8_t* const (&ro
                                            const uint8_t* bank_s, const int (&groups)[2], int ns, const float* as_row) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) src.a[i] = rowp[i] + 64 * (i & 1) + 16 * (lane >> 4);  // run 4 wv + i: half i & 1
+  for (int i = 0; i < 4; ++i) {  // run 4 wv + i: row rowp[i] (row 32 wv + 8 i + lane / 8), chunk swizzled
+    const int row = 32 * (threadIdx.x >> 6) + 8 * i + (lane >> 3);
+    src.a[i] = rowp[i] + 16 * ((lane & 7) ^ ((row >> 1) & 7));
+  }
   const int ns4 = (ns + 3) / 4;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -638,7 +646,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
   const uint8_t* rowp[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 16 * ((4 * wv + i) >> 1) + c;
+    const int row = 32 * wv + 8 * i + (lane >> 3);
     rowp[i] = xq + (int64_t)perm_token[p0 + (row < rows ? row : 0)] * H;
   }
   const int srow = 64 * (wv & 3) + lane;
@@ -752,7 +760,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
   const uint8_t* rowp[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 16 * ((4 * wv + i) >> 1) + c;
+    const int row = 32 * wv + 8 * i + (lane >> 3);
     rowp[i] = zq + (int64_t)(p0 + (row < rows ? row : 0)) * I;
   }
   const int srow = 64 * (wv & 3) + lane;
