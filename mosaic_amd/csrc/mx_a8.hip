@@ -464,7 +464,7 @@ constexpr int kPfLStage = kPfLAs + 256;
 static_assert(kPfLStages * kPfLStage <= kPfStages * kPfStage, "light ring must fit the prefill ring");
 
 struct PfLSrc {
-  const uint8_t* a;      // A run wv: 16-row tile wv >> 1, bytes 64 (wv & 1) + 16 (lane / 16) of row lane % 16
+  const uint8_t* a;      // A run wv: rows 8 wv .. + 7 (row 8 wv + lane / 8), this lane's 16-byte chunk (swizzled)
   const uint8_t* b[2];   // weight group 2 wv + i, this lane's 16 bytes
   const uint8_t* bs[2];  // its scale dword
   const float* as;       // row lane: its 1x128 scale row
@@ -499,8 +499,11 @@ __device__ __forceinline__ void pfl_compute(const uint8_t* stage, int ga, int gb
   int sa[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(stage + kPfLA + mt * 2048 + lane * 16);
-    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(stage + kPfLA + mt * 2048 + 1024 + lane * 16);
+    // row r at r * 128, 16-byte chunks XOR-swizzled by (r >> 1) & 7
+    const int row = 16 * mt + c, swz = (row >> 1) & 7, q = lane >> 4;
+    const uint8_t* rp = stage + kPfLA + row * 128;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(rp + ((q ^ swz) << 4));
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(rp + (((q + 4) ^ swz) << 4));
     a[mt] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     sa[mt] = pow2_e8m0(*reinterpret_cast<const float*>(stage + kPfLAs + (16 * mt + c) * 4));
   }
@@ -543,13 +546,14 @@ __device__ __forceinline__ void pfl_kloop(const PfLSrc& src, int ns, int rows, i
   }
 }
 
-// light-tile copy sources: A run wv is row 16 (wv >> 1) + lane % 16 (rows past
-// the tile's end read its first row; their results are never stored)
+// light-tile copy sources: A run wv is rows 8 wv .. + 7, lane l row 8 wv + l / 8
+// (rows past the tile's end read its first row; their results are never stored)
 __device__ __forceinline__ void pfl_sources(PfLSrc& src, const uint8_t* rowp, const uint8_t* bank_p,
                                             const uint8_t* bank_s, const int (&groups)[2], int ns,
                                             const float* as_row) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  src.a = rowp + 64 * (wv & 1) + 16 * (lane >> 4);
+  const int row = 8 * wv + (lane >> 3);
+  src.a = rowp + 16 * ((lane & 7) ^ ((row >> 1) & 7));
   const int ns4 = (ns + 3) / 4;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -591,7 +595,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
   const int nbk = I / 128;
   if (rows <= 64) {
     // light tile: wave wv owns gate group wv and up group 8 + wv (z columns j0 + 16 wv)
-    const int arow = 16 * (wv >> 1) + c;
+    const int arow = 8 * wv + (lane >> 3);
     PfLSrc lsrc;
     pfl_sources(lsrc, xq + (int64_t)perm_token[p0 + (arow < rows ? arow : 0)] * H, bp, bsc, groups, ns,
                 xs + (int64_t)perm_token[p0 + (lane < rows ? lane : 0)] * ns);
@@ -740,7 +744,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
   const int groups[2] = {h0 / 16 + 2 * wv, h0 / 16 + 2 * wv + 1};
   if (rows <= 64) {
     // light tile: wave wv owns staged groups 2 wv and 2 wv + 1 (columns h0 + 32 wv)
-    const int arow = 16 * (wv >> 1) + c;
+    const int arow = 8 * wv + (lane >> 3);
     PfLSrc lsrc;
     pfl_sources(lsrc, zq + (int64_t)(p0 + (arow < rows ? arow : 0)) * I, bp, bsc, groups, ns,
                 zs + (int64_t)(p0 + (lane < rows ? lane : 0)) * ns);
