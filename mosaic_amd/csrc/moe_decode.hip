@@ -10,10 +10,10 @@
 //    ahead, no branches in the steady state), with the x part it needs staged
 //    in wave-private LDS.  The parts meet in LDS; SwiGLU and the route weight
 //    are applied and z row `tile` is written (the shared expert's row is K).
-// 2. moe_dec1_down_kernel: a workgroup owns 16 hidden columns and walks every
-//    tile (the shared expert first, then the experts in ascending id); its waves again
-//    split K (= inter) and stream (tile, super-step) entries through a ring, with
-//    the z parts staged in wave-private LDS.  Each expert's partial (a fresh
+// 2. moe_dec1_down_kernel: a workgroup owns 16 (or 8) hidden columns and walks
+//    every tile (the shared expert first, then the experts in ascending id);
+//    its waves again split K (= inter) and stream (tile, super-step) entries
+//    through a ring, with z staged in LDS.  Each expert's partial (a fresh
 //    MFMA chain) is added to the running fp32 sum of the routed tiles in order,
 //    and the shared partial after it, so the combine of the reference
 //    (ascending expert id, shared last, fp32) happens in registers and y is
@@ -211,81 +211,86 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_gateup_kernel(
   }
 }
 
-// grid (H/16), KS waves; dynamic LDS = (K + has_shared) * I * 2 bytes (z rows, split in parts);
-// ZV >= the z vectors per lane of a part ((K + has_shared) * NSP / 4).  A wave's
-// part of K is NSP super-steps (inter / 128 = KS * NSP, NSP <= 4, and the part
-// starts at a multiple of NSP so its scale bytes sit in one dword); the ring
-// holds DT tiles, each NSP code blocks + one scale dword.
+// grid H / cpw, KS waves; dynamic LDS = (K + has_shared) * I * 2 bytes (the z
+// rows, stored part by part).  A workgroup owns cpw = 16 or 8 consecutive
+// hidden columns: 8 when H / 16 would leave CUs idle, which keeps every
+// window on whole 128-byte lines (a line is 8 rows of one K quarter); lanes of
+// rows past the window load its last row and are not stored.  Its waves take
+// one K part each: a part is NSP super-steps (inter / 128 = KS * NSP, NSP <= 4,
+// and the part starts at a multiple of NSP so its scale bytes sit in one
+// dword); the ring holds DT expert tiles, each NSP code blocks + one scale dword.
 template <int KS, int NSP, int DT, int ZV>
 __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
     const uint16_t* __restrict__ z, const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ n_tiles,
     const uint8_t* __restrict__ d_p, const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p,
-    const uint8_t* __restrict__ sh_s, uint16_t* __restrict__ y, int H, int I, int E, int K, int has_shared) {
+    const uint8_t* __restrict__ sh_s, uint16_t* __restrict__ y, int H, int I, int E, int K, int has_shared,
+    int cpw) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dec_smem[];
   __shared__ float red[KS][16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int g = blockIdx.x;
+  const int col0 = blockIdx.x * cpw;
   const int ns = I / 128, sbase = w * NSP, ns4 = (ns + 3) / 4;
   const int nz = K + has_shared;  // z rows (row K = shared expert)
-  // 1. z parts of every row -> registers (row r, part steps [sbase, sbase + NSP))
-  const int pvec = NSP * 16, nvec = nz * pvec;
+  // 1. the tile list (scalar loads: they do not wait behind the vector loads
+  //    below), then the workgroup's share of z -> registers: 16-byte vector i
+  //    is part p, row r, vector o of the LDS layout [part][row][NSP * 16]
+  const int nv = n_tiles[0];
+  const int nt = nv + has_shared;
+  const int pvec = NSP * 16, rvec = nz * pvec, nvec = KS * rvec;
   u32x4_t zst[ZV];
 #pragma unroll
   for (int v = 0; v < ZV; ++v) {
-    const int i = min(lane + 64 * v, nvec - 1);
-    const int r = i / pvec, o = i - r * pvec;
-    zst[v] = reinterpret_cast<const u32x4_t*>(z + (int64_t)r * I + (int64_t)sbase * 128)[o];
+    const int i = min((int)threadIdx.x + KS * 64 * v, nvec - 1);
+    const int p = i / rvec, rem = i - p * rvec;
+    const int r = rem / pvec, o = rem - r * pvec;
+    zst[v] = reinterpret_cast<const u32x4_t*>(z + (int64_t)r * I + (int64_t)p * NSP * 128)[o];
   }
-  // 2. tiles: the shared expert first (its addresses need no tile list, so its
-  //    loads go out at once), then the routed ones in ascending expert id; lane
-  //    r holds routed tile r's code and scale addresses for this row group and
-  //    part.  The shared partial is kept apart and added after the routed sum,
-  //    so the fp32 combine order is still ascending id, shared last.
+  // 2. this lane's weight row and its offsets inside an expert's down matrix
+  const bool row_ok = c < cpw;
+  const int row = col0 + (row_ok ? c : cpw - 1);
+  const int gr = row >> 4, l = q * 16 + (row & 15);
+  const uint32_t woff = (uint32_t)gr * ns * 1024u + (uint32_t)sbase * 1024u + (uint32_t)l * 16u;
+  const uint32_t soff = (uint32_t)gr * ns4 * 256u + (uint32_t)(sbase >> 2) * 256u + (uint32_t)l * 4u;
+  // 3. tiles: the shared expert first (its addresses need no tile list), then
+  //    the routed ones in ascending expert id.  The shared partial is kept
+  //    apart and added after the routed sum, so the fp32 combine order is
+  //    ascending id, shared last.
   const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
-  const int64_t woff = (int64_t)g * ns * 64 * 16 + (int64_t)sbase * 1024;
-  const int64_t soff = (int64_t)g * ns4 * 64 * 4 + (int64_t)(sbase >> 2) * 256;
   u32x4_t r_w[DT][NSP];
   uint32_t r_s[DT];
-  if (has_shared) {
-#pragma unroll
-    for (int u = 0; u < NSP; ++u) r_w[0][u] = load_nt_u32x4(sh_p + woff + lane * 16 + u * 1024);
-    r_s[0] = *reinterpret_cast<const uint32_t*>(sh_s + soff + lane * 4);
-  }
-  const int nv = n_tiles[0];
-  const int le = lane < nv ? tile_expert[lane] : 0;  // lanes past the valid tiles: expert 0 (valid memory)
-  const int nt = nv + has_shared;
-  const uint8_t* lw = d_p + (int64_t)le * ebytes + woff;
-  const uint8_t* ls = d_s + (int64_t)le * sbytes + soff;
-  const uint64_t lw_u = reinterpret_cast<uint64_t>(lw), ls_u = reinterpret_cast<uint64_t>(ls);
-  const int nchunks = (nt + DT - 1) / DT;
   // ring entry t >= has_shared is routed tile t - has_shared; padded entries
-  // (t >= nt) reload lane 0's tile and get scale 0 (selects only: the ring
+  // (t >= nt) reload routed tile 0 and get scale 0 (selects only: the ring
   // issues its loads without branches)
-  auto load_tile = [&](int t, u32x4_t (&wv)[NSP], uint32_t& sv) {
-    const int rt = t < nt ? t - has_shared : 0;
-    const uint8_t* wp = reinterpret_cast<const uint8_t*>(
-        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lw_u >> 32), rt) << 32) |
-        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lw_u, rt));
-    const uint8_t* sp = reinterpret_cast<const uint8_t*>(
-        ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(ls_u >> 32), rt) << 32) |
-        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)ls_u, rt));
+  auto load_tile = [&](int t, u32x4_t (&wt)[NSP], uint32_t& sv) {
+    const uint8_t* wp;
+    const uint8_t* sp;
+    if (has_shared && t == 0) {
+      wp = sh_p;
+      sp = sh_s;
+    } else {
+      const int rt = t < nt ? t - has_shared : 0;
+      const int e = nv > 0 ? tile_expert[rt] : 0;
+      wp = d_p + (int64_t)e * ebytes;
+      sp = d_s + (int64_t)e * sbytes;
+    }
 #pragma unroll
-    for (int u = 0; u < NSP; ++u) wv[u] = load_nt_u32x4(wp + lane * 16 + u * 1024);
-    sv = *reinterpret_cast<const uint32_t*>(sp + lane * 4);
+    for (int u = 0; u < NSP; ++u) wt[u] = load_nt_u32x4(wp + woff + u * 1024);
+    sv = *reinterpret_cast<const uint32_t*>(sp + soff);
   };
+  const int nchunks = (nt + DT - 1) / DT;
   if (nt > 0) {
 #pragma unroll
-    for (int d = 0; d < DT; ++d)
-      if (d > 0 || !has_shared) load_tile(d, r_w[d], r_s[d]);
+    for (int d = 0; d < DT; ++d) load_tile(d, r_w[d], r_s[d]);
   }
-  // 3. z parts -> wave-private LDS: row r at zs + r * NSP * 256
-  uint8_t* zs = dec_smem + (size_t)w * nz * NSP * 256;
+  // 4. z -> LDS; this wave's part: row r at zs + r * NSP * 256
 #pragma unroll
   for (int v = 0; v < ZV; ++v) {
-    const int i = lane + 64 * v;
-    if (i < nvec) reinterpret_cast<u32x4_t*>(zs)[i] = zst[v];
+    const int i = (int)threadIdx.x + KS * 64 * v;
+    if (i < nvec) reinterpret_cast<u32x4_t*>(dec_smem)[i] = zst[v];
   }
+  __syncthreads();
+  const uint8_t* zs = dec_smem + (size_t)w * nz * NSP * 256;
   f32x4_t part = {0.f, 0.f, 0.f, 0.f};
   float ysum = 0.f, ysh = 0.f;
   auto chunk = [&](int ch, auto more) {
@@ -294,8 +299,8 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
       const int t = ch * DT + d;
       const bool real = t < nt;
       const bool shared_t = has_shared && t == 0;
-      const int row = shared_t ? K : (real ? t - has_shared : 0);
-      const uint8_t* zr = zs + (size_t)row * NSP * 256;
+      const int zrow = shared_t ? K : (real ? t - has_shared : 0);
+      const uint8_t* zr = zs + (size_t)zrow * NSP * 256;
 #pragma unroll
       for (int u = 0; u < NSP; ++u) {
         u32x4_t xv[4];
@@ -317,11 +322,11 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
   ysum += ysh;
   if (q == 0) red[w][c] = ysum;
   __syncthreads();
-  if (w == 0 && q == 0) {
+  if (w == 0 && q == 0 && row_ok) {
     float v = red[0][c];
 #pragma unroll
     for (int k2 = 1; k2 < KS; ++k2) v += red[k2][c];
-    y[16 * g + c] = f32_bf16(v);
+    y[row] = f32_bf16(v);
   }
 }
 
@@ -427,11 +432,11 @@ static void launch_dec1_gateup_x(int D, dim3 grid, size_t lds, hipStream_t st, c
 template <int KS, int NSP, int ZV>
 static void launch_dec1_down_z(int DT, dim3 grid, size_t lds, hipStream_t st, const uint16_t* z, const int32_t* te,
                                const int32_t* nt, const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_p,
-                               const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared,
+                               const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared, int cpw,
                                hipEvent_t ev_stop) {
 #define DEC_DN(DV)                                                                                              \
   hipExtLaunchKernelGGL((moe_dec1_down_kernel<KS, NSP, DV, ZV>), grid, dim3(KS * 64), lds, st, nullptr, ev_stop, \
-                        0u, z, te, nt, d_p, d_s, sh_p, sh_s, y, H, I, E, K, has_shared)
+                        0u, z, te, nt, d_p, d_s, sh_p, sh_s, y, H, I, E, K, has_shared, cpw)
   switch (DT) {
     case 4: DEC_DN(4); break;
     case 3: DEC_DN(3); break;
@@ -492,7 +497,7 @@ bool moe_decode1_supported(int64_t m, int64_t hidden, int64_t inter, int64_t top
   if (hidden % 128 || inter % 128 || nsh % kDecGuKS || dec_dn_ks(nsi) == 0) return false;
   const int64_t gu_part = nsh / kDecGuKS, dn_part = nsi / dec_dn_ks(nsi);
   if (gu_part * 16 > 64 * kDecXVMax) return false;                        // x staging registers
-  if ((top_k + has_shared) * dn_part * 16 > 64 * kDecZVMax) return false;  // z staging registers
+  if ((top_k + has_shared) * dn_part * 16 > 64 * kDecZVMax) return false;  // z staging registers (one wave's share or less)
   if ((size_t)(top_k + has_shared) * inter * 2 > 64 * 1024) return false;
   return true;
 }
@@ -529,11 +534,14 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
     launch_dec1_gateup_x<kDecGuKS, 8>(GU_ARGS);
 #undef GU_ARGS
   MOSAIC_LAUNCH_CHECK("moe_decode1_gateup");
-  // ring of 3 tiles (DT * NSP super-steps in flight), 4 when a part is one step
+  // ring of 3 tiles (DT * NSP super-steps in flight), 4 when a part is one step;
+  // 8 columns per workgroup when 16 would give fewer workgroups than CUs
   const int dt = dn_part == 1 ? 4 : 3;
-  const int zv = (nz * dn_part * 16 + 63) / 64;
-#define DN_ARGS dt, dim3((unsigned)(H / 16)), (size_t)nz * I * 2, st, z, tile_expert, n_tiles, d_p, d_s, sh_d_p, \
-                sh_d_s, y, (int)H, (int)I, (int)E, (int)K, has_shared, ev(3)
+  const int cpw = H / 16 >= 256 ? 16 : 8;
+  const int zv = (int)(((int64_t)nz * I / 8 + dn_ks * 64 - 1) / (dn_ks * 64));
+  const dim3 dgrid((unsigned)(H / cpw));
+#define DN_ARGS dt, dgrid, (size_t)nz * I * 2, st, z, tile_expert, n_tiles, d_p, d_s, sh_d_p, sh_d_s, y, (int)H, \
+                (int)I, (int)E, (int)K, has_shared, cpw, ev(3)
 #define DN_Z(KSV, NSPV)                                  \
   if (zv <= 5)                                           \
     launch_dec1_down_z<KSV, NSPV, 5>(DN_ARGS);           \

@@ -278,7 +278,8 @@ def test_moe_a16_given_ids_weight_before_down(dev):
 @pytest.mark.parametrize("e,h,inter,k,shared,limit,func", [
     (16, 512, 512, 4, True, 0.0, "sigmoid"), (32, 1024, 512, 8, False, 10.0, "sigmoid"),
     (64, 2048, 1024, 6, True, 10.0, "softmax"), (8, 512, 1024, 8, True, 0.0, "sqrtsoftplus"),
-    (16, 1536, 2048, 1, True, 0.0, "sigmoid")])
+    (16, 1536, 2048, 1, True, 0.0, "sigmoid"), (8, 5120, 512, 4, True, 0.0, "sigmoid"),
+    (8, 1024, 4096, 2, True, 10.0, "sigmoid")])
 def test_moe_a16_decode1_vs_oracle(dev, e, h, inter, k, shared, limit, func):
     ops = _ops()
     rng = np.random.default_rng(e * 7 + h + inter + k)
