@@ -27,6 +27,9 @@ struct LayoutOut {
   int32_t* chunk_base;   // [layout_chunks(A_ext)][E_ext]
 };
 
+// combine_pos row width bound: top_k (<= kRouteMaxTopK = 16) + the shared expert
+constexpr int kCombineMaxW = 17;
+
 constexpr int kLayoutChunk = 1024;  // assignments per workgroup of the multi-workgroup layout
 inline int64_t layout_chunks(int64_t a_ext) { return (a_ext + kLayoutChunk - 1) / kLayoutChunk; }
 // scratch bytes of the multi-workgroup layout (0 when the single-workgroup path applies)

@@ -12,6 +12,8 @@
 
 namespace mosaic {
 
+static_assert(kCombineMaxW == kRouteMaxTopK + 1, "combine width covers top_k + shared");
+
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
 constexpr int kRouteMaxAssign = 4096;   // A_ext limit of the single-workgroup path

@@ -250,18 +250,27 @@ __global__ void __launch_bounds__(KS * 64) moe_a16_down_kernel(
 
 // ------------------------------------------------------------ combine ------
 // y[t][h] = bf16( sum over j of yp[combine_pos[t][j]][h] ): the token's expert
-// partials in ascending expert id, the shared expert last.
+// partials in ascending expert id, the shared expert last.  W <= kCombineMaxW:
+// every partial load is issued before the in-order sum (a loop over W would
+// wait for each position and partial in turn).
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ yp,
                                                           const int32_t* __restrict__ combine_pos,
                                                           uint16_t* __restrict__ y, int M, int W, int H) {
   const int t = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= M || h >= H) return;
-  float sum = 0.f;
-  for (int j = 0; j < W; ++j) {
-    const int p = combine_pos[(int64_t)t * W + j];
-    if (p >= 0) sum += yp[(int64_t)p * H + h];
+  float v[kCombineMaxW];
+  bool ok[kCombineMaxW];
+#pragma unroll
+  for (int j = 0; j < kCombineMaxW; ++j) {
+    const int p = j < W ? combine_pos[(int64_t)t * W + j] : -1;
+    ok[j] = p >= 0;
+    v[j] = ok[j] ? yp[(int64_t)p * H + h] : 0.f;
   }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < kCombineMaxW; ++j)
+    if (ok[j]) sum += v[j];
   y[(int64_t)t * H + h] = f32_bf16(sum);
 }
 

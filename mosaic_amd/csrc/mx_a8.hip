@@ -789,23 +789,30 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
 }
 
 // y[t][h] = bf16(sum over j of yb[combine_pos[t][j]][h]), bf16 partials; a
-// thread sums 8 consecutive columns (16-byte loads), in ascending j
+// thread sums 8 consecutive columns (16-byte loads), in ascending j.  W <=
+// kCombineMaxW: every partial load is issued before the in-order sum.
 __global__ void __launch_bounds__(128) moe_combine_bf16_kernel(const uint16_t* __restrict__ yb,
                                                                const int32_t* __restrict__ combine_pos,
                                                                uint16_t* __restrict__ y, int M, int W, int H) {
   const int t = blockIdx.y;
   const int h = 8 * (blockIdx.x * blockDim.x + threadIdx.x);
   if (t >= M || h >= H) return;
-  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < W; ++j) {
-    const int p = combine_pos[(int64_t)t * W + j];
-    if (p >= 0) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(yb + (int64_t)p * H + h);
+  u32x4_t pv[kCombineMaxW];
+  bool ok[kCombineMaxW];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[2 * i] += bf16_f32((uint16_t)(v[i] & 0xFFFFu));
-        s[2 * i + 1] += bf16_f32((uint16_t)(v[i] >> 16));
-      }
+  for (int j = 0; j < kCombineMaxW; ++j) {
+    const int p = j < W ? combine_pos[(int64_t)t * W + j] : -1;
+    ok[j] = p >= 0;
+    pv[j] = ok[j] ? *reinterpret_cast<const u32x4_t*>(yb + (int64_t)p * H + h) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kCombineMaxW; ++j) {
+    if (!ok[j]) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[2 * i] += bf16_f32((uint16_t)(pv[j][i] & 0xFFFFu));
+      s[2 * i + 1] += bf16_f32((uint16_t)(pv[j][i] >> 16));
     }
   }
   u32x4_t o;
