@@ -168,29 +168,6 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     for (int i = threadIdx.x; i < kHistBins; i += 256) lh[i] = 0u;
     __syncthreads();
   }
-  const uint8_t* qb = q + (int64_t)b * H * kIdxD;
-  const float* qsb = qs + (int64_t)b * H;
-  const float* wb = w + (int64_t)b * H;
-  // A operands: head rows 16 j + c as bf16, in 4 chunks of 8 of this lane's 32
-  // code bytes (the same byte order as the k operand, so every K pairs once),
-  // negated where q_scale < 0; per-lane weights c = w |q_scale| of the D rows
-  // (heads 16 j + 4 qq + r)
-  bf16x8_t qa[HT][4];
-  float cw[HT][4];
-  float bound = 0.f;
-#pragma unroll
-  for (int j = 0; j < HT; ++j) {
-    const i32x8_t raw = load_fp8_operand(qb + (int64_t)(16 * j + c) * kIdxD, 0, qq);
-    float l1 = abs_sum_fp8(raw);
-    l1 += __shfl_xor(l1, 16, 64);
-    l1 += __shfl_xor(l1, 32, 64);
-    const float qsr = qsb[16 * j + c];
-    if (qq == 0) bound += fabsf(wb[16 * j + c]) * fabsf(qsr) * l1;
-    fp8x32_to_bf16(raw, qa[j], qsr < 0.f);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) cw[j][r] = wb[16 * j + 4 * qq + r] * fabsf(qsb[16 * j + 4 * qq + r]);
-  }
-  const float qbound = wave_sum_f32(bound) * kBoundFactor;
   const int64_t n_groups = (n + GT - 1) / GT;
   const int64_t nw = (int64_t)gridDim.x * 4, wid = (int64_t)blockIdx.x * 4 + wv;
   const int64_t iters = wid < n_groups ? (n_groups - 1 - wid) / nw + 1 : 0;
@@ -218,6 +195,45 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
       kr[s][u] = i32x8_t{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
     }
   };
+  // the ring's first groups go out before the q setup below, so their latency
+  // overlaps it (the k stream does not depend on q)
+  if (iters > 0) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) load(s, s);
+  }
+  const uint8_t* qb = q + (int64_t)b * H * kIdxD;
+  const float* qsb = qs + (int64_t)b * H;
+  const float* wb = w + (int64_t)b * H;
+  // A operands: head rows 16 j + c as bf16, in 4 chunks of 8 of this lane's 32
+  // code bytes (the same byte order as the k operand, so every K pairs once),
+  // negated where q_scale < 0; per-lane weights c = w |q_scale| of the D rows
+  // (heads 16 j + 4 qq + r)
+  // every load first (one round trip for the whole setup), then the math
+  bf16x8_t qa[HT][4];
+  float cw[HT][4];
+  i32x8_t raw[HT];
+  float qsr[HT], wr[HT], cq[HT][4], cwr[HT][4];
+#pragma unroll
+  for (int j = 0; j < HT; ++j) {
+    raw[j] = load_fp8_operand(qb + (int64_t)(16 * j + c) * kIdxD, 0, qq);
+    qsr[j] = qsb[16 * j + c];
+    wr[j] = wb[16 * j + c];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      cq[j][r] = qsb[16 * j + 4 * qq + r];
+      cwr[j][r] = wb[16 * j + 4 * qq + r];
+    }
+  }
+  float bound = 0.f;
+#pragma unroll
+  for (int j = 0; j < HT; ++j) {
+    const float l1 = sum_lane_quad(abs_sum_fp8(raw[j]));  // |q| sum of head row 16 j + c over the 4 lanes
+    bound += qq == 0 ? fabsf(wr[j]) * fabsf(qsr[j]) * l1 : 0.f;
+    fp8x32_to_bf16(raw[j], qa[j], qsr[j] < 0.f);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) cw[j][r] = cwr[j][r] * fabsf(cq[j][r]);
+  }
+  const float qbound = wave_sum_f32(bound) * kBoundFactor;
   auto compute = [&](int s, int64_t i) {
     const int64_t g = wid + i * nw;
     const int nt = group_tokens(g);
@@ -268,8 +284,6 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     }
   };
   if (iters > 0) {
-#pragma unroll
-    for (int s = 0; s < D; ++s) load(s, s);
     int64_t i0 = 0;
     for (; i0 + D < iters; i0 += D) {
 #pragma unroll
