@@ -788,17 +788,31 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   const int t_end = min(topk, t_begin + chunk);
   const int nblk = t_end > t_begin ? (t_end - t_begin + kMlaBT - 1) / kMlaBT : 0;
   // q as the B operand of S^T = K Q^T: lane (c, qd) holds q[head][32 s + 8 qd .. +8]
+  // (kept in registers: the empty asm stops the compiler from re-loading q in
+  // every block, where those loads would queue behind the next block's gather
+  // and the QK products would wait for the whole gather)
   bf16x8_t qb[DQK / 32];
   {
     const uint16_t* qrow = q + ((int64_t)b * H + head) * DQK;
 #pragma unroll
     for (int s = 0; s < DQK / 32; ++s) qb[s] = *reinterpret_cast<const bf16x8_t*>(qrow + 32 * s + 8 * qd);
+#pragma unroll
+    for (int s = 0; s < DQK / 32; ++s) asm volatile("" : "+v"(qb[s]));
   }
-  // token id of a block's slot (-1: masked or past the split)
-  auto token = [&](int blk, int slot) -> int {
+  // Token ids of a block's slots in two steps: token_raw loads the index
+  // unconditionally (clamped to the row), token_fix turns it into the id or -1
+  // (masked or past the split).  The ids of block i + 2 are loaded behind block
+  // i + 1's gather and fixed only in the next iteration: a branch around the
+  // load, or math on it right away, would make the compiler wait for every
+  // load in flight, the gather included.
+  auto token_raw = [&](int blk, int slot) -> int {
     const int ti = t_begin + blk * kMlaBT + slot;
-    const int id = (blk < nblk && ti < t_end) ? idx[(int64_t)b * topk + ti] : -1;
-    return (id >= 0 && (int64_t)id < n) ? id : -1;
+    return idx[(int64_t)b * topk + min(ti, topk - 1)];
+  };
+  auto token_fix = [&](int blk, int slot, int raw) -> int {
+    const int ti = t_begin + blk * kMlaBT + slot;
+    const bool live = blk < nblk && ti < t_end && raw >= 0 && (int64_t)raw < n;
+    return live ? raw : -1;
   };
   // this thread's items: latent (token it % kMlaBT, segment it / kMlaBT) and rope chunk
   int iid[IPT], rid[RPT > 0 ? RPT : 1];
@@ -807,14 +821,20 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   u32x4_t rrope[RPT > 0 ? RPT : 1];
   auto load_ids = [&](int blk, int (&ii)[IPT], int (&ri)[RPT > 0 ? RPT : 1]) {
 #pragma unroll
+    for (int k = 0; k < IPT; ++k) ii[k] = token_raw(blk, (tid + NT * k) % kMlaBT);
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) ri[k] = token_raw(blk, ((tid + NT * k) / (DR / 8)) % kMlaBT);
+  };
+  auto fix_ids = [&](int blk, int (&ii)[IPT], int (&ri)[RPT > 0 ? RPT : 1]) {
+#pragma unroll
     for (int k = 0; k < IPT; ++k) {
       const int it = tid + NT * k;
-      ii[k] = it < ITEMS ? token(blk, it % kMlaBT) : -1;
+      ii[k] = it < ITEMS ? token_fix(blk, it % kMlaBT, ii[k]) : -1;
     }
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
       const int it = tid + NT * k;
-      ri[k] = it < RCH ? token(blk, it / (DR / 8)) : -1;
+      ri[k] = it < RCH ? token_fix(blk, it / (DR / 8), ri[k]) : -1;
     }
   };
   auto issue = [&](const int (&ii)[IPT], const int (&ri)[RPT > 0 ? RPT : 1]) {
@@ -905,6 +925,7 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
   if (nblk > 0) {
     int ii0[IPT], ri0[RPT > 0 ? RPT : 1];
     load_ids(0, ii0, ri0);
+    fix_ids(0, ii0, ri0);
     issue(ii0, ri0);
     load_ids(1, nid, nrid);
     fill(0, ii0, ri0);
@@ -919,6 +940,7 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     for (int k = 0; k < RPT; ++k) crid[k] = nrid[k];
     const bool more = blk + 1 < nblk;
     if (more) {
+      fix_ids(blk + 1, cid, crid);
       issue(cid, crid);             // block blk + 1 flies while block blk is multiplied out
       load_ids(blk + 2, nid, nrid);
     }
@@ -927,16 +949,37 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     f32x4_t st[kMlaBT / 16], st2[kMlaBT / 16];
 #pragma unroll
     for (int j = 0; j < kMlaBT / 16; ++j) st[j] = st2[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // K fragments in batches of KB steps, double-buffered: batch i + 1's LDS
+    // reads are issued before batch i's products (the scheduling barriers keep
+    // the compiler from interleaving them into a read-wait-multiply chain)
+    constexpr int KB = 3, NSQ = DQK / 32, NKB = (NSQ + KB - 1) / KB;
+    bf16x8_t kop[2][KB][kMlaBT / 16];
+    auto read_k = [&](int kb2, bf16x8_t (&dst)[KB][kMlaBT / 16]) {
 #pragma unroll
-    for (int s = 0; s < DQK / 32; ++s)
+      for (int ss = 0; ss < KB; ++ss)
 #pragma unroll
-      for (int j = 0; j < kMlaBT / 16; ++j) {
-        const bf16x8_t kop = *reinterpret_cast<const bf16x8_t*>(&Kt[bf][(16 * j + c) * KS + 8 * qd + 32 * s]);
-        if (s & 1)
-          st2[j] = mfma_bf16(kop, qb[s], st2[j]);
-        else
-          st[j] = mfma_bf16(kop, qb[s], st[j]);
-      }
+        for (int j = 0; j < kMlaBT / 16; ++j)
+          if (kb2 * KB + ss < NSQ)
+            dst[ss][j] = *reinterpret_cast<const bf16x8_t*>(&Kt[bf][(16 * j + c) * KS + 8 * qd + 32 * (kb2 * KB + ss)]);
+    };
+    read_k(0, kop[0]);
+#pragma unroll
+    for (int kb2 = 0; kb2 < NKB; ++kb2) {
+      if (kb2 + 1 < NKB) read_k(kb2 + 1, kop[(kb2 + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ss = 0; ss < KB; ++ss)
+#pragma unroll
+        for (int j = 0; j < kMlaBT / 16; ++j) {
+          const int s = kb2 * KB + ss;
+          if (s >= NSQ) continue;
+          if (s & 1)
+            st2[j] = mfma_bf16(kop[kb2 & 1][ss][j], qb[s], st2[j]);
+          else
+            st[j] = mfma_bf16(kop[kb2 & 1][ss][j], qb[s], st[j]);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int j = 0; j < kMlaBT / 16; ++j) st[j] += st2[j];
     float sc[kMlaBT / 16][4];
@@ -967,8 +1010,9 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
     l_run = l_run * alpha + psum;
     m_run = m_new;
     // rescale O rows (heads 4 qd + r of this wave) by their alpha, unless no
-    // head's running maximum moved (then every alpha is 1)
-    if (__ballot(alpha != 1.f)) {
+    // head's running maximum moved (then every alpha is 1) or O is still zero
+    // (the first block)
+    if (blk > 0 && __ballot(alpha != 1.f)) {
       float al[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * qd + r, 64);
@@ -986,13 +1030,27 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
         pa[r] = __builtin_bit_cast(__bf16, f32_bf16(p[2 * s2][r]));
         pa[4 + r] = __builtin_bit_cast(__bf16, f32_bf16(p[2 * s2 + 1][r]));
       }
+      // V fragments in batches of VB column tiles, double-buffered like K
+      constexpr int VB = 8, NVB = kMlaDl / 16 / VB;
+      u32x4_t vv[2][VB];
+      auto read_v = [&](int vb2, u32x4_t (&dst)[VB]) {
 #pragma unroll
-      for (int dt = 0; dt < kMlaDl / 16; ++dt) {
-        const uint16_t* vrow = &Vt[bf][(16 * dt + c) * kVtStride + 32 * s2 + 4 * qd];
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
-        const u32x4_t vv = {v0.x, v0.y, v1.x, v1.y};
-        o[dt] = mfma_bf16(pa, __builtin_bit_cast(bf16x8_t, vv), o[dt]);
+        for (int dd = 0; dd < VB; ++dd) {
+          const uint16_t* vrow = &Vt[bf][(16 * (vb2 * VB + dd) + c) * kVtStride + 32 * s2 + 4 * qd];
+          const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
+          const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
+          dst[dd] = u32x4_t{v0.x, v0.y, v1.x, v1.y};
+        }
+      };
+      read_v(0, vv[0]);
+#pragma unroll
+      for (int vb2 = 0; vb2 < NVB; ++vb2) {
+        if (vb2 + 1 < NVB) read_v(vb2 + 1, vv[(vb2 + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int dd = 0; dd < VB; ++dd)
+          o[vb2 * VB + dd] = mfma_bf16(pa, __builtin_bit_cast(bf16x8_t, vv[vb2 & 1][dd]), o[vb2 * VB + dd]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (more) fill(bf ^ 1, cid, crid);
