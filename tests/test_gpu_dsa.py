@@ -187,7 +187,8 @@ def _mla(rng, b, h, n, t, sb, masked=0.0):
 @pytest.mark.parametrize("b,h,n,t,sb,sink,masked", [(1, 128, 4096, 2048, 64, True, 0.0),
                                                      (2, 128, 3000, 2048, 512, False, 0.1),
                                                      (3, 64, 500, 300, 64, True, 0.3),
-                                                     (1, 16, 100, 64, 128, True, 0.0)])
+                                                     (1, 16, 100, 64, 128, True, 0.0),
+                                                     (2, 32, 80, 20, 64, True, 0.2)])
 def test_mla_fp8_vs_oracle(dev, b, h, n, t, sb, sink, masked):
     from mosaic_amd import ops
     rng = np.random.default_rng(b * 1000 + t)
