@@ -759,7 +759,26 @@ static int fp8_block_gemm_impl(const uint8_t* a, const float* a_s, const uint8_t
                          (int)n, (int)k, f32);
       break;
     }
-    case 4: launch_fp8_gemv<2, 2>(a, a_s, b, b_s, c, m, n, k, f32, st); break;
+    case 4: {
+      // few rows: one 16-column tile per workgroup (more workgroups), K split
+      // wider where there are few column tiles; more rows: two tiles share each
+      // A fragment, except where that leaves under 192 workgroups (measured
+      // with the weights cold in HBM, M = 1 and 16, N = 4096..24576)
+      const int64_t t16 = (n + 15) / 16;
+      if (m <= 4) {
+        if (t16 <= 256)
+          launch_fp8_gemv<1, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
+        else if (t16 <= 1152)
+          launch_fp8_gemv<1, 4>(a, a_s, b, b_s, c, m, n, k, f32, st);
+        else
+          launch_fp8_gemv<1, 2>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      } else if ((n + 31) / 32 < 192) {
+        launch_fp8_gemv<1, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      } else {
+        launch_fp8_gemv<2, 2>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      }
+      break;
+    }
     case 2: launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     case 1: launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     default:

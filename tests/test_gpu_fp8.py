@@ -30,8 +30,9 @@ def _case(rng, m, n, k):
                                    (1024, 16384, 384), (1024, 16384, 2304),
                                    # split K (tiles under half the GPU): tiled<128> x 8 / x 4, tiled<256> x 3
                                    (128, 576, 7168), (128, 7168, 4096), (4096, 576, 7168),
-                                   # decode ring kernel (M <= 16, N >= 4096): full rows, ragged N, uneven K parts
-                                   (16, 7168, 4096), (3, 4100, 1024), (7, 5000, 2176)])
+                                   # decode ring kernel (M <= 16, N >= 4096): full rows, ragged N, uneven K parts;
+                                   # tiles x K parts 2x2, 1x4, 1x8 (M > 4), 1x8 (M <= 4), 1x2
+                                   (16, 7168, 4096), (3, 4100, 1024), (7, 5000, 2176), (2, 4096, 1152)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
     from mosaic_amd import ops
