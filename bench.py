@@ -278,15 +278,26 @@ def config5_dsa(torch, ops):
     for b in (1, 8):
         n = 65536
         qh = torch.randn(b, 128, 576, generator=g, device=dev).to(torch.bfloat16)
-        lat = (torch.randn(b, n, 512, generator=g, device=dev) * 60).clamp(-448, 448).to(torch.float8_e4m3fn)
-        ls = torch.rand(b, n, 8, generator=g, device=dev) * 0.01
-        rope = torch.randn(b, n, 64, generator=g, device=dev).to(torch.bfloat16)
+        # KV caches rotate (over 512 MB in all), as each layer gathers from its own cache
+        kv_bytes = b * n * (512 + 8 * 4 + 64 * 2)
+        nrot = (512 << 20) // kv_bytes + 1
+        kvs = []
+        for _ in range(nrot):
+            lat = (torch.randn(b, n, 512, generator=g, device=dev) * 60).clamp(-448, 448).to(torch.float8_e4m3fn)
+            ls = torch.rand(b, n, 8, generator=g, device=dev) * 0.01
+            rope = torch.randn(b, n, 64, generator=g, device=dev).to(torch.bfloat16)
+            kvs.append((lat, ls, rope))
         idx = torch.stack([torch.randperm(n, generator=g, device=dev)[:2048] for _ in range(b)]).int()
         sink = torch.randn(128, generator=g, device=dev)
-        us = _graph_time(torch, lambda: ops.mla_sparse_decode(qh, lat, ls, rope, idx, 576 ** -0.5, sink,
-                                                              workspace=ws), 10, reps=3)
+        it = iter(range(10 ** 9))
+
+        def mla_fn():
+            lat, ls, rope = kvs[next(it) % nrot]
+            return ops.mla_sparse_decode(qh, lat, ls, rope, idx, 576 ** -0.5, sink, workspace=ws)
+        us = _graph_time(torch, mla_fn, nrot * max(1, 10 // nrot), reps=3)
         fl = 2 * b * 128 * 2048 * (576 + 512)
         out[f"mla_b{b}"] = {"us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 2)}
+        del kvs
     return out
 
 
