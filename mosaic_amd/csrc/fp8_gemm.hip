@@ -723,8 +723,11 @@ static Fp8Plan fp8_plan(int64_t m, int64_t n, int64_t k) {
     const int s = split(tiles);
     if (tiles * s >= 32) return {1, s};
   }
-  // decode shapes with wide N: the ring kernel (>= 128 workgroups of 32 columns, >= 4 blocks per K part)
-  if (m <= 16 && n >= 4096 && nkb >= 8 && (int64_t)n * k < (1ll << 31)) return {4, 1};
+  // decode shapes: the ring kernel for wide N, and for narrower N when K is deep
+  // enough for its 8-wave split to leave each wave >= 4 blocks (M = 1 / 16,
+  // N = 576..2048, K = 7168: 9.2-9.6 -> 7.2-8.1 us and 11.8-12.3 -> 10.6-10.7 us
+  // against the skinny kernel; at K = 1536 the skinny kernel stays faster)
+  if (m <= 16 && nkb >= 8 && (n >= 4096 || nkb >= 32) && (int64_t)n * k < (1ll << 31)) return {4, 1};
   return {0, 1};
 }
 
