@@ -331,20 +331,24 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
 }
 
 // Single A16 linear at one token (y [1, N] = x [1, K] . W^T, W MXT16): a
-// workgroup owns one 16-row group of W; its KS waves split K into equal parts,
+// workgroup owns 16 rows of W (8 when N / 16 < 256); its KS waves split K into equal parts,
 // each streaming its part through a register ring of D super-steps with its x
 // part staged in wave-private LDS; the parts meet in LDS.
 template <int KS, int D, int XV>
 __global__ void __launch_bounds__(KS * 64) mx_dec1_linear_kernel(const uint16_t* __restrict__ x,
                                                                  const uint8_t* __restrict__ packed_t,
                                                                  const uint8_t* __restrict__ scale_t,
-                                                                 uint16_t* __restrict__ y, int N, int K) {
+                                                                 uint16_t* __restrict__ y, int N, int K,
+                                                                 int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t dec_smem[];
   __shared__ float red[KS][16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int g = blockIdx.x;
   const int ns = K / 128, nsp = ns / KS, sbase = w * nsp;
+  // this workgroup's rows (16, or 8 when 16-row groups would leave CUs idle:
+  // lanes past them re-read the window's last row, within the same 128-byte line)
+  const int row = blockIdx.x * rows + min(c, rows - 1);
+  const int g = row >> 4, lr = q * 16 + (row & 15);
   const int nvec = nsp * 16;
   u32x4_t xst[XV];
 #pragma unroll
@@ -354,7 +358,7 @@ __global__ void __launch_bounds__(KS * 64) mx_dec1_linear_kernel(const uint16_t*
   }
   const uint8_t* wt;
   const uint8_t* st;
-  dec_ptrs(packed_t, scale_t, g, ns, lane, wt, st);
+  dec_ptrs(packed_t, scale_t, g, ns, lr, wt, st);
   const int nchunks = (nsp + D - 1) / D;
   u32x4_t r_w[D];
   uint32_t r_s[D];
@@ -389,11 +393,11 @@ __global__ void __launch_bounds__(KS * 64) mx_dec1_linear_kernel(const uint16_t*
   chunk(nchunks - 1, std::false_type{});
   if (q == 0) red[w][c] = acc[0];
   __syncthreads();
-  if (w == 0 && q == 0) {
+  if (w == 0 && q == 0 && c < rows) {
     float v = red[0][c];
 #pragma unroll
     for (int k2 = 1; k2 < KS; ++k2) v += red[k2][c];
-    const int n = 16 * g + c;
+    const int n = blockIdx.x * rows + c;
     if (n < N) y[n] = f32_bf16(v);
   }
 }
@@ -449,10 +453,13 @@ static void launch_dec1_down_z(int DT, dim3 grid, size_t lds, hipStream_t st, co
 template <int KS, int XV>
 static void launch_dec1_linear_x(int D, const uint16_t* x, const uint8_t* pt, const uint8_t* st, uint16_t* y,
                                  int64_t n, int64_t k, hipStream_t s) {
-  const dim3 grid((unsigned)(n / 16));
+  // 8-row workgroups when 16-row groups would leave CUs idle
+  const int rows = n / 16 < 256 ? 8 : 16;
+  const dim3 grid((unsigned)(n / rows));
   const size_t lds = (size_t)k * 2;
-#define DEC_LIN(DV) \
-  hipLaunchKernelGGL((mx_dec1_linear_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, s, x, pt, st, y, (int)n, (int)k)
+#define DEC_LIN(DV)                                                                                              \
+  hipLaunchKernelGGL((mx_dec1_linear_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, s, x, pt, st, y, (int)n, (int)k, \
+                     rows)
   switch (D) {
     case 8: DEC_LIN(8); break;
     case 7: DEC_LIN(7); break;
