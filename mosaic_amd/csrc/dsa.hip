@@ -514,15 +514,18 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
     }
     __builtin_amdgcn_wave_barrier();
   };
-  // ping-pong over this wave's batches (bt = wv + 4 m)
+  // ping-pong over this wave's batches (bt = wv + 4 m).  The loads are
+  // unconditional (a batch past the candidates reads candidate 0's row and
+  // scores nothing): a branch around them would make the compiler wait for
+  // them at its join, before the current batch is scored.
   Batch ba, bb;
   load_batch(wv, ba);
   for (int m = 0; m < my_batches; m += 2) {
     const bool more = m + 1 < my_batches;
-    if (more) load_batch(wv + 4 * (m + 1), bb);
+    load_batch(wv + 4 * (m + 1), bb);
     score_batch(m, ba);
     if (!more) break;
-    if (m + 2 < my_batches) load_batch(wv + 4 * (m + 2), ba);
+    load_batch(wv + 4 * (m + 2), ba);
     score_batch(m + 1, bb);
   }
 }
