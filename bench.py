@@ -41,7 +41,7 @@ HBM_PEAK_GBS = 8000.0
 # scaled by what the same counter reads for --calibration-copy-mib 256:
 # FETCH_SIZE x 2.0, WRITE_SIZE x 1.0.  The profile summary
 # profiles/moe_decode_m1_traffic.md holds the commands and raw figures.
-GATEUP_M1_TRAFFIC_BYTES = (68782 * 2.0 + 36.1) * 1024
+GATEUP_M1_TRAFFIC_BYTES = (68771.5 * 2.0 + 36.1) * 1024
 METRIC = "MXFP4 MoE-layer decode µs & HBM GB/s % peak; FP8/MXFP4 GEMM TFLOPS % peak"
 
 
