@@ -94,7 +94,9 @@ int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_t, const ui
 /* A8 MXFP4 linear ("source semantics"): y [m, n] bf16 = sum over K32 groups of
  * (A_g . W_g^T) * sa[:, g/4] * sw[:, g] with xq e4m3 [m, k] and power-of-two
  * f32 scales sa [m, k/128] (mosaic_act_quant mode 0), W an MXT16-prepacked
- * MXFP4 weight [n, k]; fp32 accumulation on the scaled MFMA.
+ * MXFP4 weight [n, k]; fp32 accumulation on the scaled MFMA.  Checked on the
+ * device, without a host sync: a scale that is not a positive power of two
+ * turns its row of y into NaN.
  * Replaces reference_fp4_linear_source_semantics (kernels/fp4_source.py:132-156)
  * and the A8 GEMVs xsimt_gemm / qpa_mma_gemm / mxint_*_gemm (kernels/xsimt.py:292-325,
  * kernels/qpa_mma.py:498-541, kernels/mxint.py:362-401,1014-1054); upstream fp4_gemm

@@ -22,7 +22,13 @@
 namespace mosaic {
 
 // e8m0 byte of a power-of-two fp32 scale (its biased exponent)
-__device__ __forceinline__ int pow2_e8m0(float s) { return (int)((__float_as_uint(s) >> 23) & 0xFFu); }
+// A power-of-two fp32 activation scale as its e8m0 byte.  Any other value (a
+// mantissa bit or the sign set) maps to 0xFF, the e8m0 NaN, so the scaled MFMA
+// turns the affected outputs into NaN instead of silently using a rounded scale.
+__device__ __forceinline__ int pow2_e8m0(float s) {
+  const uint32_t u = __float_as_uint(s);
+  return (u & 0x807FFFFFu) ? 0xFF : (int)(u >> 23);
+}
 
 template <int SEL>
 __device__ __forceinline__ f32x4_t mfma_a8(const i32x8_t a, int sa, const u32x4_t w, uint32_t sw, f32x4_t acc) {

@@ -16,22 +16,25 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Router score, defined as the fp32 rounding of the exact function value: it
+// is evaluated in fp64 and rounded once, so the device and a CPU restatement
+// (also fp64, rounded once) agree bit for bit, ties included.  sqrtsoftplus
+// keeps torch's softplus threshold (x > 20 -> x).
 __device__ __forceinline__ float score_of(float logit, int func) {
-  if (func == MOSAIC_SCORE_SIGMOID) return 1.0f / (1.0f + expf(-logit));
-  if (func == MOSAIC_SCORE_SQRTSOFTPLUS) {
-    float sp = logit > 20.f ? logit : log1pf(expf(logit));
-    return sqrtf(sp);
-  }
+  const double x = (double)logit;
+  if (func == MOSAIC_SCORE_SIGMOID) return (float)(1.0 / (1.0 + exp(-x)));
+  if (func == MOSAIC_SCORE_SQRTSOFTPLUS) return (float)sqrt(logit > 20.f ? x : log1p(exp(x)));
   return logit;  // softmax handled by the caller
 }
 
 // One wave routes one token; logits stay in registers (PER per lane, E <=
-// 64*PER).  Selection key: the logit when there is no bias (every score
-// function is monotone), else score + bias.  Ties -> lower index.  Each round
-// is two 32-bit DPP max-reductions over (key, ~index).  On return lane r < K
-// holds pick r (rank order) and its weight: score / (fp32 sum of the K scores
-// in rank order) when renormalizing (not softmax), times `scale`; other lanes
-// hold -1 and 0.  Everything stays in registers (readlane broadcasts).
+// 64*PER).  Selection key: the fp32 score (score_of; softmax = exp(x - max) /
+// sum in fp64, rounded once), plus bias when given (one fp32 add).  Ties ->
+// lower index.  Each round is two 32-bit DPP max-reductions over (key,
+// ~index).  On return lane r < K holds pick r (rank order) and its weight:
+// score / max(fp32 sum of the K scores in rank order, 1e-9) when
+// renormalizing (not softmax), times `scale`; other lanes hold -1 and 0.
+// Everything stays in registers (readlane broadcasts).
 template <int PER>
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ lg, int E, int K, int func, int renorm,
                                                  float scale, const float* __restrict__ bias, int& pick,
@@ -46,39 +49,39 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ lg, i
     lv[j] = (e < E) ? lg[e] : -INFINITY;
     mx = fmaxf(mx, lv[j]);
   }
-  float denom = 1.f;
+  float scv[PER];  // the fp32 scores, carried beside the keys
   if (func == MOSAIC_SCORE_SOFTMAX) {
     mx = wave_max_f32(mx);
-    float sum = 0.f;
+    double ex[PER];
+    double sum = 0.0;
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (lane + 64 * j < E) sum += expf(lv[j] - mx);
+    for (int j = 0; j < PER; ++j) {
+      ex[j] = (lane + 64 * j < E) ? exp((double)lv[j] - (double)mx) : 0.0;
+      sum += ex[j];
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    denom = sum;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) scv[j] = (float)(ex[j] / sum);
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) scv[j] = (lane + 64 * j < E) ? score_of(lv[j], func) : 0.f;
   }
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + 64 * j;
-    float k = lv[j];
-    if (bias && e < E) {
-      const float sc = (func == MOSAIC_SCORE_SOFTMAX) ? expf(lv[j] - mx) / denom : score_of(lv[j], func);
-      k = sc + bias[e];
-    }
+    const float k = (bias && e < E) ? scv[j] + bias[e] : scv[j];
     khi[j] = (e < E) ? order_key(k) : 0u;  // absent experts sort below every real one
     klo[j] = (e < E) ? 0xFFFFFFFFu - (uint32_t)e : 0u;
   }
   // sort this lane's PER candidates by (key, lower index) descending once; a
   // round then reduces only the lane heads and the winning lane shifts its list
-  float lgv[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) lgv[j] = lv[j];
   auto cex = [&](int i, int j) {  // order candidates i < j descending
     const bool sw = khi[j] > khi[i] || (khi[j] == khi[i] && klo[j] > klo[i]);
     const uint32_t hi_i = sw ? khi[j] : khi[i], hi_j = sw ? khi[i] : khi[j];
     const uint32_t lo_i = sw ? klo[j] : klo[i], lo_j = sw ? klo[i] : klo[j];
-    const float l_i = sw ? lgv[j] : lgv[i], l_j = sw ? lgv[i] : lgv[j];
-    khi[i] = hi_i; khi[j] = hi_j; klo[i] = lo_i; klo[j] = lo_j; lgv[i] = l_i; lgv[j] = l_j;
+    const float s_i = sw ? scv[j] : scv[i], s_j = sw ? scv[i] : scv[j];
+    khi[i] = hi_i; khi[j] = hi_j; klo[i] = lo_i; klo[j] = lo_j; scv[i] = s_i; scv[j] = s_j;
   };
   if constexpr (PER == 2) {
     cex(0, 1);
@@ -90,7 +93,7 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ lg, i
     cex(0, 4); cex(1, 5); cex(2, 6); cex(3, 7); cex(2, 4); cex(3, 5); cex(1, 2); cex(3, 4); cex(5, 6);
   }
   int my_pick = -1;
-  float my_logit = 0.f;
+  float my_score = 0.f;
   for (int r = 0; r < K; ++r) {
     const uint32_t hi = wave_max_u32(khi[0]);
     // the index reduction is needed only when several lanes hold the winning key
@@ -100,28 +103,26 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ lg, i
                             : wave_max_u32(khi[0] == hi ? klo[0] : 0u);
     const int e = (int)(0xFFFFFFFFu - lo);
     const int src = e & 63;  // expert e lives in lane e % 64
-    const float l = __uint_as_float(wave_bcast_u32(__float_as_uint(lgv[0]), src));
+    const float s = __uint_as_float(wave_bcast_u32(__float_as_uint(scv[0]), src));
     const bool win = lane == src;
 #pragma unroll
     for (int j = 0; j < PER - 1; ++j) {
       khi[j] = win ? khi[j + 1] : khi[j];
       klo[j] = win ? klo[j + 1] : klo[j];
-      lgv[j] = win ? lgv[j + 1] : lgv[j];
+      scv[j] = win ? scv[j + 1] : scv[j];
     }
     khi[PER - 1] = win ? 0u : khi[PER - 1];
     klo[PER - 1] = win ? 0u : klo[PER - 1];
     if (lane == r) {
       my_pick = e;
-      my_logit = l;
+      my_score = s;
     }
   }
-  const float sc = (lane < K) ? ((func == MOSAIC_SCORE_SOFTMAX) ? expf(my_logit - mx) / denom
-                                                               : score_of(my_logit, func))
-                              : 0.f;
+  const float sc = (lane < K) ? my_score : 0.f;
   float sum = 0.f;
   for (int r = 0; r < K; ++r) sum += __uint_as_float(wave_bcast_u32(__float_as_uint(sc), r));  // rank order
   float w = sc;
-  if (renorm && func != MOSAIC_SCORE_SOFTMAX) w = w / sum;
+  if (renorm && func != MOSAIC_SCORE_SOFTMAX) w = w / (sum < 1e-9f ? 1e-9f : sum);  // clamp_min, NaN kept
   w = w * scale;
   pick = lane < K ? my_pick : -1;
   weight = lane < K ? w : 0.f;

@@ -4,6 +4,7 @@ from __future__ import annotations
 import torch
 
 from .. import ops
+from . import _prepack_cache
 
 
 def prequant(x: torch.Tensor | None, prequant) -> tuple[torch.Tensor, torch.Tensor]:
@@ -20,7 +21,7 @@ def weight(packed: torch.Tensor, scale_w: torch.Tensor, prepacked) -> ops.MXT16:
         if not isinstance(prepacked, ops.MXT16):
             raise TypeError("prepacked must be an MXT16 weight (mosaic_amd.ops.mxt16_prepack)")
         return prepacked
-    return ops.mxt16_prepack(packed, scale_w)
+    return _prepack_cache.mxt16(packed, scale_w)
 
 
 def linear(x, packed, scale_w, n_out, prequant_=None, prepacked=None) -> torch.Tensor:

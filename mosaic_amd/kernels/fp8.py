@@ -8,6 +8,7 @@ from __future__ import annotations
 import torch
 
 from .. import ops
+from . import _prepack_cache
 from .fp4_source import e8m0_to_fp32
 
 
@@ -53,13 +54,15 @@ def fp4_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
              scale_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """C = A_fp8[M, K] @ B_fp4[N, K]^T, per-128 act scale, e8m0 per-32 weight scale
     (``inference_kernel.py:518-536``).  The act scales must be powers of two
-    (act_quant with scale_fmt), which the scaled MFMA consumes directly."""
+    (act_quant with scale_fmt; e8m0 scales always are), which the scaled MFMA
+    consumes directly.  The kernel checks them on the device: a row whose
+    scale is not a positive power of two comes out NaN (no host sync here).
+    The weight's MXT16 prepack is cached while ``b``/``b_s`` stay alive and
+    unmodified."""
     k = a.size(-1)
     m = a.numel() // k
     sa = _scales_f32(a_s).reshape(m, -1).contiguous()
-    if bool(((sa.view(torch.int32) & 0x7FFFFF) != 0).any()):
-        raise ValueError("fp4_gemm needs power-of-two activation scales (act_quant(..., scale_fmt=...))")
-    w = ops.mxt16_prepack(b, b_s)
+    w = _prepack_cache.mxt16(b, b_s)
     c = ops.mxt16_linear_a8(None, w, prequant=(a.reshape(m, k), sa))
     return c.reshape(*a.shape[:-1], b.size(0)).to(torch.get_default_dtype())
 

@@ -345,18 +345,32 @@ def emit_tiles(counts: torch.Tensor, block_m: int, tile_cap: int):
 
 # ---------------------------------------------------------- A16 MoE layer ---
 class MoEWorkspace:
-    """Reusable device workspace for ``moe_a16_forward`` (grown on demand)."""
+    """Reusable device workspace for the MoE / DSA / MLA wrappers.
+
+    ``get`` returns a buffer of at least the requested bytes.  When a call needs
+    more than the current buffer, a larger one is allocated and the old one is
+    kept alive for the lifetime of this object, so a HIP graph captured earlier
+    on the old pointer still owns valid memory.  One workspace serves one stream
+    at a time; calls on different streams need different workspaces.  Without a
+    workspace argument the wrappers allocate per call through torch's caching
+    allocator, which is stream- and graph-safe."""
 
     def __init__(self):
         self.buf: torch.Tensor | None = None
+        self._retired: list[torch.Tensor] = []
 
     def get(self, nbytes: int, device) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes or self.buf.device != torch.device(device):
+            if self.buf is not None:
+                self._retired.append(self.buf)
             self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         return self.buf
 
 
-_DEFAULT_WS = MoEWorkspace()
+def _workspace(workspace: "MoEWorkspace | None", nbytes: int, device) -> torch.Tensor:
+    if workspace is not None:
+        return workspace.get(nbytes, device)
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
 def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, **kw):
@@ -422,7 +436,7 @@ def _moe_forward(a8: bool, x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logi
     has_shared = int(shared is not None)
     kind = "a8" if a8 else "a16"
     nbytes = getattr(_lib.lib(), f"mosaic_moe_{kind}_workspace_bytes")(m, h, inter, e, top_k, has_shared)
-    ws = (workspace or _DEFAULT_WS).get(nbytes, x.device)
+    ws = _workspace(workspace, nbytes, x.device)
     y = torch.empty(m, h, dtype=torch.bfloat16, device=x.device)
     args = [_ptr(x), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(gate_up.packed), _ptr(gate_up.scale),
             _ptr(down.packed), _ptr(down.scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(y), m, h,
@@ -493,7 +507,7 @@ def dsa_indexer_topk(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: t
             raise ValueError(f"lengths must be [B], got {tuple(lengths.shape)}")
     idx = torch.empty(b, topk, dtype=torch.int32, device=q.device)
     nbytes = _lib.lib().mosaic_dsa_indexer_workspace_bytes(b, l_)
-    ws = (workspace or _DEFAULT_WS).get(nbytes, q.device)
+    ws = _workspace(workspace, nbytes, q.device)
     _lib.call("mosaic_dsa_indexer_topk", _ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(w), _ptr(lengths), _ptr(idx),
               b, h, d, l_, int(topk), int(offset), _ptr(ws), ws.numel(), _stream())
     return idx
@@ -545,7 +559,7 @@ def mla_sparse_decode(q: torch.Tensor, kv_latent: torch.Tensor, kv_scale: torch.
     topk = idx.shape[1]
     out = torch.empty(b, h, dl, dtype=torch.bfloat16, device=q.device)
     nbytes = _lib.lib().mosaic_mla_decode_workspace_bytes(b, h, topk)
-    ws = (workspace or _DEFAULT_WS).get(nbytes, q.device)
+    ws = _workspace(workspace, nbytes, q.device)
     _lib.call("mosaic_mla_sparse_decode", _ptr(q), _ptr(kv_latent), _ptr(kv_scale), _ptr(kv_rope), _ptr(sink),
               _ptr(idx), _ptr(out), b, h, n, topk, dl, dr, scale_block, float(softmax_scale), _ptr(ws), ws.numel(),
               _stream())
@@ -572,7 +586,7 @@ def mla_sparse_decode_bf16(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor,
     topk = idx.shape[1]
     out = torch.empty(rows, h, 512, dtype=torch.bfloat16, device=q.device)
     nbytes = _lib.lib().mosaic_mla_decode_workspace_bytes(rows, h, topk)
-    ws = (workspace or _DEFAULT_WS).get(nbytes, q.device)
+    ws = _workspace(workspace, nbytes, q.device)
     _lib.call("mosaic_mla_sparse_decode_bf16", _ptr(q), _ptr(kv), _ptr(sink), _ptr(idx), _ptr(out), rows, h, n, topk,
               d, rows // nb, float(softmax_scale), _ptr(ws), ws.numel(), _stream())
     return out

@@ -2,12 +2,15 @@
 
 * ``route_topk`` (A10): ``Gate.forward`` (``.mosaicvm/source/inference_model.py:569-589``)
   and ``Router.forward`` (``model/layers.py:118-150``): scores = f(logits)
-  (sigmoid | softmax | sqrtsoftplus), optional selection bias, top-k, weights =
-  unbiased scores gathered at the picks, renormalized (non-softmax) and scaled.
-  Order and ties (the reference leaves them to ``torch.topk``): picks are listed
-  by descending selection key, equal keys go to the lower expert index.  Without
-  a bias the selection key is the logit itself (each f is monotone, so this is
-  the same ranking wherever f(logit) has no fp32 ties).
+  (sigmoid | softmax | sqrtsoftplus; each the fp32 rounding of the exact value),
+  optional selection bias, top-k, weights = unbiased scores gathered at the
+  picks, renormalized (non-softmax, sum clamped at 1e-9) and scaled.  Order and
+  ties (the reference leaves them to ``torch.topk``): picks are listed by
+  descending selection key (score, or score + bias), equal keys go to the lower
+  expert index.
+* ``router_logits``: the router projection ``F.linear(x.float(), W.float())`` of
+  ``Router.forward`` / ``Gate.forward``, defined as the exact dot product
+  rounded once to fp32.
 * ``layout_assignments`` (A11): ``kernels/moe_layout.py:8-27`` with a STABLE
   order (inside one expert, ascending flat assignment index).
 * ``emit_tiles`` (A12): ``kernels/w4a16_grouped.py:151-169`` without the
@@ -38,20 +41,23 @@ from . import linear as L
 
 
 # --------------------------------------------------------------- routing ----
-def _sigmoid32(x):
-    x = np.asarray(x, dtype=np.float32)
-    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-x).astype(np.float32))).astype(np.float32)
-
-
 def score_fn(logits: np.ndarray, func: str) -> np.ndarray:
+    """Router scores of ``Gate.forward`` (``.mosaicvm/source/inference_model.py:571-577``)
+    and ``_router_scores`` (``model/layers.py:110-115``), each defined as the fp32
+    rounding of the exact value: evaluated in float64 and rounded once.
+    sqrtsoftplus keeps torch's softplus threshold (x > 20 -> x)."""
     lg = np.asarray(logits, dtype=np.float32)
+    x = lg.astype(np.float64)
     if func == "sigmoid":
-        return _sigmoid32(lg)
+        with np.errstate(over="ignore"):
+            return (1.0 / (1.0 + np.exp(-x))).astype(np.float32)
     if func == "softmax":
-        e = np.exp((lg - lg.max(axis=-1, keepdims=True)).astype(np.float64))
+        e = np.exp(x - x.max(axis=-1, keepdims=True))
         return (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
     if func == "sqrtsoftplus":
-        return np.sqrt(np.logaddexp(0.0, lg.astype(np.float64))).astype(np.float32)
+        with np.errstate(over="ignore"):
+            sp = np.where(lg > np.float32(20.0), x, np.log1p(np.exp(x)))
+        return np.sqrt(sp).astype(np.float32)
     raise ValueError(func)
 
 
@@ -72,22 +78,44 @@ def topk_lower_index(keys: np.ndarray, k: int) -> np.ndarray:
 def route_topk(logits: np.ndarray, top_k: int = 8, score_func: str = "sigmoid",
                bias: np.ndarray | None = None, renorm: bool = True,
                route_scale: float = 1.0):
-    """logits [M, E] fp32 -> (ids int64 [M, k], weights fp32 [M, k])."""
+    """logits [M, E] fp32 -> (ids int64 [M, k], weights fp32 [M, k]).
+
+    ``Gate.forward`` (``inference_model.py:569-589``) / ``Router.forward``
+    (``model/layers.py:127-150``): selection key = score (+ bias, one fp32 add),
+    picks listed by descending key with ties to the lower expert index; weight =
+    unbiased score at the pick, divided by the fp32 sum of the k picked scores
+    (in pick order) clamped below at 1e-9 (``layers.py:147``) unless softmax,
+    then times ``route_scale``."""
     logits = np.asarray(logits, dtype=np.float32)
     scores = score_fn(logits, score_func)
-    if bias is None:
-        key = logits
-    else:
-        key = (scores + np.asarray(bias, dtype=np.float32)).astype(np.float32)
+    key = scores if bias is None else (scores + np.asarray(bias, dtype=np.float32)).astype(np.float32)
     ids = topk_lower_index(key, top_k)
     w = np.take_along_axis(scores, ids, axis=1).astype(np.float32)
     if renorm and score_func != "softmax":
         ssum = np.zeros(w.shape[0], dtype=np.float32)
-        for j in range(top_k):  # fp32 sum in slot order
+        for j in range(top_k):  # fp32 sum in pick order
             ssum = (ssum + w[:, j]).astype(np.float32)
+        ssum = np.where(ssum < np.float32(1e-9), np.float32(1e-9), ssum).astype(np.float32)
         w = (w / ssum[:, None]).astype(np.float32)
     w = (w * np.float32(route_scale)).astype(np.float32)
     return ids, w
+
+
+def router_logits(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """logits [M, E] fp32 = x [M, H] . W [E, H]^T, the projection of
+    ``Router.forward`` (``model/layers.py:128``) and ``Gate.forward``
+    (``.mosaicvm/source/inference_model.py:570``), both ``F.linear(x.float(),
+    W.float())``.  Each logit is defined as the exact dot product rounded once
+    to fp32: the products of fp32 (or bf16) values are exact in float64 and
+    ``math.fsum`` returns the correctly rounded float64 of their exact sum."""
+    import math
+    x64 = np.asarray(x, dtype=np.float32).astype(np.float64)
+    w64 = np.asarray(w, dtype=np.float32).astype(np.float64)
+    out = np.empty((x64.shape[0], w64.shape[0]), dtype=np.float32)
+    for t in range(x64.shape[0]):
+        prod = w64 * x64[t][None, :]
+        out[t] = [math.fsum(row) for row in prod]
+    return out
 
 
 # ---------------------------------------------------------------- layout ----
@@ -143,6 +171,29 @@ def expert_a16(xrow: np.ndarray, wgu: np.ndarray, wd: np.ndarray, weight: float,
     return (wd.astype(np.float64) @ zd.astype(np.float64)).astype(np.float32)
 
 
+def _expert_rows(ids: np.ndarray):
+    """{expert id: [(token, slot), ...]} over ids [M, k], in token then slot order."""
+    rows: dict[int, list] = {}
+    for t in range(ids.shape[0]):
+        for s in range(ids.shape[1]):
+            rows.setdefault(int(ids[t, s]), []).append((t, s))
+    return rows
+
+
+def _combine(m: int, h: int, ids: np.ndarray, partial: dict, shared_part):
+    """Per token: fp32 sum of the slot partials in ascending expert id (equal
+    ids in slot order), the shared expert's partial added last."""
+    out = np.zeros((m, h), dtype=np.float32)
+    for t in range(m):
+        acc = np.zeros(h, dtype=np.float32)
+        for s in np.argsort(ids[t], kind="stable"):
+            acc = (acc + partial[(t, int(s))]).astype(np.float32)
+        if shared_part is not None:
+            acc = (acc + shared_part[t]).astype(np.float32)
+        out[t] = acc
+    return out
+
+
 def moe_layer_a16(x, ids, weights, bank_gu, bank_gu_s, bank_d, bank_d_s,
                   shared=None, swiglu_limit: float = 0.0, out_bf16: bool = True):
     """A16 MoE layer over MXFP4 NK banks.
@@ -151,34 +202,36 @@ def moe_layer_a16(x, ids, weights, bank_gu, bank_gu_s, bank_d, bank_d_s,
     bank_gu [E, 2*inter, H/2] u8, bank_gu_s [E, 2*inter, H/32] u8,
     bank_d [E, H, inter/2] u8, bank_d_s [E, H, inter/32] u8 (numpy arrays or
     callables e -> array, so a test can stream experts from the device);
-    shared = (gu, gu_s, d, d_s) or None.  Returns [M, H].
+    shared = (gu, gu_s, d, d_s) or None.  Returns [M, H].  The tokens routed
+    to one expert are multiplied together (each row is computed as
+    ``expert_a16`` computes it, a float64 product rounded once to fp32).
     """
     get = (lambda b, e: b(e)) if callable(bank_gu) else (lambda b, e: b[e])
     x = np.asarray(x, dtype=np.float32)
     ids = np.asarray(ids)
     weights = np.asarray(weights, dtype=np.float32)
     m, h = x.shape
-    out = np.zeros((m, h), dtype=np.float32)
-    cache = {}
 
-    def deq(e):
-        if e not in cache:
-            cache[e] = (C.dequant_mxfp4(get(bank_gu, e), get(bank_gu_s, e)),
-                        C.dequant_mxfp4(get(bank_d, e), get(bank_d_s, e)))
-        return cache[e]
+    def run(wgu, wd, rows_x, rows_w):
+        inter = wgu.shape[0] // 2
+        gu = (rows_x.astype(np.float64) @ wgu.astype(np.float64).T).astype(np.float32)
+        z = swiglu(gu[:, :inter], gu[:, inter:], swiglu_limit)
+        z = C.round_bf16((z * rows_w[:, None]).astype(np.float32))
+        return (z.astype(np.float64) @ wd.astype(np.float64).T).astype(np.float32)
 
-    for t in range(m):
-        order = np.argsort(ids[t], kind="stable")  # ascending expert id
-        acc = np.zeros(h, dtype=np.float32)
-        for s in order:
-            wgu, wd = deq(int(ids[t, s]))
-            acc = (acc + expert_a16(x[t], wgu, wd, float(weights[t, s]), swiglu_limit)).astype(np.float32)
-        if shared is not None:
-            sgu = C.dequant_mxfp4(shared[0], shared[1]) if "sgu" not in cache else cache["sgu"]
-            sd = C.dequant_mxfp4(shared[2], shared[3]) if "sd" not in cache else cache["sd"]
-            cache["sgu"], cache["sd"] = sgu, sd
-            acc = (acc + expert_a16(x[t], sgu, sd, 1.0, swiglu_limit)).astype(np.float32)
-        out[t] = acc
+    partial = {}
+    for e, rows in _expert_rows(ids).items():
+        wgu = C.dequant_mxfp4(get(bank_gu, e), get(bank_gu_s, e))
+        wd = C.dequant_mxfp4(get(bank_d, e), get(bank_d_s, e))
+        ts = [t for t, _ in rows]
+        ys = run(wgu, wd, x[ts], np.array([weights[t, s] for t, s in rows], dtype=np.float32))
+        for i, ts_ in enumerate(rows):
+            partial[ts_] = ys[i]
+    shared_part = None
+    if shared is not None:
+        shared_part = run(C.dequant_mxfp4(shared[0], shared[1]), C.dequant_mxfp4(shared[2], shared[3]), x,
+                          np.ones(m, dtype=np.float32))
+    out = _combine(m, h, ids, partial, shared_part)
     return C.round_bf16(out) if out_bf16 else out
 
 
@@ -188,29 +241,30 @@ def moe_layer_a8(x, ids, weights, bank_gu, bank_gu_s, bank_d, bank_d_s,
     """``fused_moe_mxint`` contract (``kernels/mxint.py:1587-1722``): gate/up A8
     into bf16, SwiGLU fp32, x route weight, bf16, act_quant_ref, A8 down into
     bf16 partials, fp32 sum in ascending expert id, bf16.  ``shared`` (optional)
-    is run through the same A8 expert with weight 1 and added last."""
+    is run through the same A8 expert with weight 1 and added last.  The tokens
+    routed to one expert go through ``mx_linear_a8`` together (its rows are
+    independent: per-row activation scales and accumulators)."""
     get = (lambda b, e: b(e)) if callable(bank_gu) else (lambda b, e: b[e])
     x = np.asarray(x, dtype=np.float32)
     ids = np.asarray(ids)
     weights = np.asarray(weights, dtype=np.float32)
     m, h = x.shape
-    out = np.zeros((m, h), dtype=np.float32)
 
-    def one(xrow, gu, gus, d, ds, w):
+    def run(gu, gus, d, ds, rows_x, rows_w):
         inter = gu.shape[0] // 2
-        g = L.mx_linear_a8(xrow[None, :], gu, gus, out_bf16=True)[0]
-        z = swiglu(g[:inter], g[inter:], swiglu_limit)
-        z = C.round_bf16((z * np.float32(w)).astype(np.float32))
-        return L.mx_linear_a8(z[None, :], d, ds, out_bf16=True)[0]
+        g = L.mx_linear_a8(rows_x, gu, gus, out_bf16=True)
+        z = swiglu(g[:, :inter], g[:, inter:], swiglu_limit)
+        z = C.round_bf16((z * rows_w[:, None]).astype(np.float32))
+        return L.mx_linear_a8(z, d, ds, out_bf16=True)
 
-    for t in range(m):
-        order = np.argsort(ids[t], kind="stable")
-        acc = np.zeros(h, dtype=np.float32)
-        for s in order:
-            e = int(ids[t, s])
-            acc = (acc + one(x[t], get(bank_gu, e), get(bank_gu_s, e), get(bank_d, e),
-                             get(bank_d_s, e), float(weights[t, s]))).astype(np.float32)
-        if shared is not None:
-            acc = (acc + one(x[t], shared[0], shared[1], shared[2], shared[3], 1.0)).astype(np.float32)
-        out[t] = acc
-    return C.round_bf16(out)
+    partial = {}
+    for e, rows in _expert_rows(ids).items():
+        ts = [t for t, _ in rows]
+        ys = run(get(bank_gu, e), get(bank_gu_s, e), get(bank_d, e), get(bank_d_s, e), x[ts],
+                 np.array([weights[t, s] for t, s in rows], dtype=np.float32))
+        for i, ts_ in enumerate(rows):
+            partial[ts_] = ys[i]
+    shared_part = None
+    if shared is not None:
+        shared_part = run(shared[0], shared[1], shared[2], shared[3], x, np.ones(m, dtype=np.float32))
+    return C.round_bf16(_combine(m, h, ids, partial, shared_part))

@@ -180,8 +180,21 @@ def test_upstream_fp8_ops_vs_oracle(dev):
     wp, ws = C.quantize_mxfp4_ceil(w)
     out = fp8.fp4_gemm(qp, sp, T(wp), T(ws))
     _close(out.float().cpu().numpy(), L.mx_linear_a8(xf, wp, ws))
-    with pytest.raises(ValueError, match="power-of-two"):
-        fp8.fp4_gemm(q, s, T(wp), T(ws))
+    # a scale that is not a power of two is caught on the device (no host sync):
+    # exactly the rows that carry one come out NaN
+    sp32 = fp8._scales_f32(sp).clone()
+    sp32[2, 1] *= 1.5
+    sp32[4, 0] = -sp32[4, 0]
+    bad = fp8.fp4_gemm(qp, sp32, T(wp), T(ws)).float().cpu().numpy()
+    assert np.isnan(bad[[2, 4]]).all()
+    np.testing.assert_array_equal(bad[[0, 1, 3]], out.float().cpu().numpy()[[0, 1, 3]])
+    # the MXT16 prepack of (wp, ws) is reused while they live and are unmodified
+    from mosaic_amd.kernels import _prepack_cache
+    wt, wst = T(wp), T(ws)
+    assert _prepack_cache.mxt16(wt, wst) is _prepack_cache.mxt16(wt, wst)
+    w1 = _prepack_cache.mxt16(wt, wst)
+    wt.view(torch.uint8)[0, 0] ^= 0x11
+    assert _prepack_cache.mxt16(wt, wst) is not w1
     # inplace quant-dequant
     xt = T(xf).to(torch.bfloat16)
     x0 = xt.clone()

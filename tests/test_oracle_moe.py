@@ -3,6 +3,8 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
+import torch.nn.functional as F
 
 from oracle import codecs as C
 from oracle import moe as MO
@@ -119,24 +121,194 @@ def test_weight_before_down_is_detectable():
     assert not np.allclose(good, bad, atol=1e-3)
 
 
-def test_moe_a8_equals_mxint_sequence():
-    """fused_moe_mxint contract (kernels/mxint.py:1587-1722): A8 gate/up -> bf16, SwiGLU,
-    x weight, bf16, act_quant, A8 down -> bf16 partials, ascending fp32 sum."""
-    from oracle import linear as L
-    rng = np.random.default_rng(9)
-    e, h, inter = 3, 256, 128
-    bank = _bank(rng, e, h, inter)
-    x = C.round_bf16(rng.standard_normal((2, h)).astype(np.float32))
-    ids = np.array([[2, 0], [1, 2]])
-    w = np.array([[0.6, 0.4], [0.3, 0.7]], dtype=np.float32)
-    got = MO.moe_layer_a8(x, ids, w, *bank, swiglu_limit=10.0)
+# ---- A8 MoE oracle pinned by an independent torch-CPU restatement ----------
+# Written from kernels/mxint.py:1676-1722 (the non-fused epilogue of
+# fused_moe_mxint), kernels/fp4_source.py:110-156 (act_quant_ref and the
+# source-semantics linear) and kernels/mxfp4.py:20-23 (the E2M1 table), with
+# torch's own float8_e4m3fn cast, frexp/ldexp scales, F.silu and explicit
+# bfloat16 casts -- nothing from oracle/ except the test data.
+_E2M1 = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+
+
+def _t_act_quant(x):
+    m, k = x.shape
+    xb = x.float().reshape(m, k // 128, 128)
+    val = xb.abs().amax(-1).clamp_min(1e-4) * (1.0 / 448.0)
+    mant, ex = torch.frexp(val)  # val = mant * 2^ex, mant in [0.5, 1): power-of-two ceil
+    s = torch.ldexp(torch.ones_like(val), torch.where(mant == 0.5, ex - 1, ex))
+    return (xb / s[..., None]).clamp(-448.0, 448.0).reshape(m, k).to(torch.float8_e4m3fn), s
+
+
+def _t_weight(packed, scale):
+    p = torch.from_numpy(packed).long()
+    b = torch.stack([_E2M1[p & 15], _E2M1[p >> 4]], dim=-1).reshape(p.shape[0], -1)  # low nibble = even K
+    return b, torch.ldexp(torch.ones(scale.shape), torch.from_numpy(scale).int() - 127)
+
+
+def _t_linear_a8(x, packed, scale):
+    xq, sa = _t_act_quant(x)
+    a = xq.float()
+    b, sw = _t_weight(packed, scale)
+    acc = torch.zeros(a.shape[0], b.shape[0])
+    for g in range(a.shape[1] // 32):
+        acc = acc + (a[:, 32 * g:32 * g + 32] @ b[:, 32 * g:32 * g + 32].T) * sa[:, g // 4, None] * sw[:, g][None, :]
+    return acc
+
+
+def _t_moe_a8(x, ids, w, bank, limit, mistake=None, shared=None):
+    """mistake: None, "weight_after_down", "no_requant" (down on bf16 z with
+    dequantized weights) or "fp32_gateup" (gate/up kept in fp32)."""
     gp, gs, dp, ds = bank
+    m, h = x.shape
+    k = ids.shape[1]
+
+    def expert(xr, gu_p, gu_s, d_p, d_s, wt):
+        gu = _t_linear_a8(xr, gu_p, gu_s)
+        if mistake != "fp32_gateup":
+            gu = gu.to(torch.bfloat16)
+        inter = gu.shape[1] // 2
+        gate, up = gu[:, :inter].float(), gu[:, inter:].float()
+        if limit > 0:
+            gate, up = gate.clamp(max=limit), up.clamp(-limit, limit)
+        z = F.silu(gate) * up
+        if mistake != "weight_after_down":
+            z = z * wt
+        zd = z.to(torch.bfloat16)
+        if mistake == "no_requant":
+            bd, swd = _t_weight(d_p, d_s)
+            y = zd.float() @ (bd * swd.repeat_interleave(32, dim=1)).T
+        else:
+            y = _t_linear_a8(zd, d_p, d_s)
+        y = y.to(torch.bfloat16).float()
+        return y * wt if mistake == "weight_after_down" else y
+
+    partials = torch.zeros(m, k, h)
+    for t in range(m):
+        for s in range(k):
+            e = int(ids[t, s])
+            partials[t, s] = expert(x[t:t + 1], gp[e], gs[e], dp[e], ds[e], float(w[t, s]))[0]
+    order = torch.from_numpy(ids).long().argsort(dim=1)  # distinct ids per token in these cases
+    out = torch.zeros(m, h)
+    for s in range(k):
+        out = out + partials[torch.arange(m), order[:, s]]
+    if shared is not None:  # upstream MoE.forward: y += shared_experts(x), in fp32
+        out = out + torch.cat([expert(x[t:t + 1], *shared, 1.0) for t in range(m)])
+    return out.to(torch.bfloat16).float().numpy()
+
+
+def _a8_case(seed=9):
+    rng = np.random.default_rng(seed)
+    e, h, inter, m = 4, 512, 256, 3
+    q = lambda n, kk: C.quantize_mxfp4_ceil(C.round_bf16((rng.standard_normal((n, kk)) * 0.05).astype(np.float32)))
+    gu = [q(2 * inter, h) for _ in range(e + 1)]
+    dn = [q(h, inter) for _ in range(e + 1)]
+    bank = tuple(np.stack(v) for v in ([a[0] for a in gu[:e]], [a[1] for a in gu[:e]], [a[0] for a in dn[:e]],
+                                       [a[1] for a in dn[:e]]))
+    shared = (gu[e][0], gu[e][1], dn[e][0], dn[e][1])
+    x = C.round_bf16((rng.standard_normal((m, h)) * 2).astype(np.float32))
+    ids = np.array([[2, 0], [1, 3], [3, 2]])
+    w = np.array([[0.6, 0.4], [0.3, 0.7], [0.55, 0.45]], dtype=np.float32)
+    return x, ids, w, bank, shared
+
+
+@pytest.mark.parametrize("with_shared", [False, True])
+def test_moe_a8_oracle_equals_torch_restatement(with_shared):
+    """The numpy A8 MoE oracle is bit-identical to the torch restatement of
+    kernels/mxint.py:1676-1722 (bf16 gate/up, fp32 SwiGLU, x weight, bf16,
+    act_quant_ref, A8 down, bf16 partials, ascending-id fp32 sum)."""
+    x, ids, w, bank, shared = _a8_case()
+    ref = MO.moe_layer_a8(x, ids, w, *bank, swiglu_limit=10.0, shared=shared if with_shared else None)
+    got = _t_moe_a8(torch.from_numpy(x), ids, w, bank, 10.0, shared=shared if with_shared else None)
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("mistake", ["weight_after_down", "no_requant", "fp32_gateup"])
+def test_moe_a8_planted_mistakes_are_caught(mistake):
+    """Each plausible composition mistake, planted in the restatement, moves
+    most outputs off the oracle (the honest restatement matches bit for bit)."""
+    x, ids, w, bank, _ = _a8_case()
+    ref = MO.moe_layer_a8(x, ids, w, *bank, swiglu_limit=10.0)
+    bad = _t_moe_a8(torch.from_numpy(x), ids, w, bank, 10.0, mistake=mistake)
+    assert np.mean(bad == ref) < 0.5, f"{mistake} not detected"
+
+
+# ---- routing: scores correctly rounded, bias, scale, planted ties ----------
+def _round_f32(v) -> np.float32:
+    """Round an mpmath value to the nearest fp32 (ties to even)."""
+    import mpmath
+    f = np.float32(float(v))
+    best = f
+    for cand in (np.nextafter(f, np.float32(-np.inf)), np.nextafter(f, np.float32(np.inf))):
+        d_c, d_b = abs(mpmath.mpf(float(cand)) - v), abs(mpmath.mpf(float(best)) - v)
+        if d_c < d_b or (d_c == d_b and (int(cand.view(np.uint32)) & 1) == 0):
+            best = cand
+    return best
+
+
+@pytest.mark.parametrize("func", ["sigmoid", "sqrtsoftplus"])
+def test_route_scores_are_correctly_rounded(func):
+    """score_fn = the fp32 rounding of the exact function (50-digit mpmath),
+    across the logit range, torch's softplus threshold 20 included."""
+    import mpmath
+    mpmath.mp.dps = 50
+    rng = np.random.default_rng(3)
+    xs = np.concatenate([rng.standard_normal(200) * 4, [-30.0, -5.0, 0.0, 19.999998, 20.0, 20.000002, 35.0]])
+    xs = xs.astype(np.float32)
+    got = MO.score_fn(xs[None, :], func)[0]
+    for x, g in zip(xs.tolist(), got.tolist()):
+        xm = mpmath.mpf(x)
+        if func == "sigmoid":
+            v = 1 / (1 + mpmath.exp(-xm))
+        else:
+            v = mpmath.sqrt(xm if x > 20.0 else mpmath.log(1 + mpmath.exp(xm)))
+        assert np.float32(g) == _round_f32(v), (func, x)
+
+
+def test_route_bias_scale_ties_brute_force():
+    """sqrtsoftplus + selection bias + renorm (sum clamped at 1e-9) x 1.5, the
+    reference Router (model/layers.py:127-150), against a brute-force stable
+    sort; rows hold planted exact key ties (equal logits and biases) and
+    one-ulp logit neighbours whose scores round together."""
+    rng = np.random.default_rng(4)
+    m, e, k = 32, 256, 8
+    logits = rng.standard_normal((m, e)).astype(np.float32)
+    bias = (rng.standard_normal(e) * 0.1).astype(np.float32)
+    bias[17] = bias[200]
+    for r in range(0, m, 2):
+        logits[r, 200] = logits[r, 17] = logits[r].max() + np.float32(0.5)       # exact tie
+        logits[r, 31] = np.nextafter(logits[r, 200], np.float32(np.inf))          # one ulp above
+        bias[31] = bias[200]
+    ids, w = MO.route_topk(logits, k, "sqrtsoftplus", bias=bias, route_scale=1.5)
+    sc = MO.score_fn(logits, "sqrtsoftplus")
+    key = (sc + bias).astype(np.float32)
+    for r in range(m):
+        order = sorted(range(e), key=lambda j: (-float(key[r, j]), j))[:k]
+        assert ids[r].tolist() == order
+        picked = sc[r, order].astype(np.float32)
+        tot = np.float32(0)
+        for v in picked:
+            tot = np.float32(tot + v)
+        np.testing.assert_array_equal(w[r], (picked / max(tot, np.float32(1e-9)) * np.float32(1.5)).astype(np.float32))
+    # the planted exact tie went to the lower index
+    assert list(ids[0]).index(17) < list(ids[0]).index(200)
+
+
+def test_route_renorm_clamps_tiny_sums():
+    """All picked scores underflow: weights stay finite (clamp_min(1e-9), layers.py:147)."""
+    logits = np.full((1, 16), -200.0, dtype=np.float32)
+    _, w = MO.route_topk(logits, 4, "sigmoid")
+    assert np.all(np.isfinite(w)) and np.all(w == 0)
+
+
+def test_router_logits_are_exact_dot_rounded_once():
+    """router_logits = fp32 rounding of the exact dot (Fraction arithmetic)."""
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    x = C.round_bf16(rng.standard_normal((2, 64)).astype(np.float32))
+    w = (rng.standard_normal((5, 64)) * 0.02).astype(np.float32)
+    w[0] = -w[1]  # a row whose dot cancels against its neighbour's
+    got = MO.router_logits(x, w)
     for t in range(2):
-        acc = np.zeros(h, dtype=np.float32)
-        for s in np.argsort(ids[t], kind="stable"):
-            ex = ids[t, s]
-            g = L.mx_linear_a8(x[t:t + 1], gp[ex], gs[ex])[0]
-            z = MO.swiglu(g[:inter], g[inter:], 10.0)
-            z = C.round_bf16((z * w[t, s]).astype(np.float32))
-            acc = (acc + L.mx_linear_a8(z[None], dp[ex], ds[ex])[0]).astype(np.float32)
-        np.testing.assert_array_equal(got[t], C.round_bf16(acc))
+        for j in range(5):
+            exact = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x[t], w[j]))
+            assert got[t, j] == np.float32(float(exact)), (t, j)
