@@ -200,6 +200,27 @@ int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, int32_t* ids,
                            int renorm, float route_scale, const float* route_bias, float swiglu_limit,
                            void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream);
 
+/* Largest scratch (bytes) mosaic_moe_a16_forward_noalloc can serve. */
+size_t mosaic_moe_a16_noalloc_max_bytes(void);
+
+/* mosaic_moe_a16_forward without a workspace argument and without any device
+ * allocation: the layer's scratch is a static per-GPU device array of
+ * mosaic_moe_a16_noalloc_max_bytes() (8 MiB: M <= 16 tokens at hidden 7168,
+ * inter 2048, 256 experts, top-8, shared expert).  A shape whose workspace
+ * (mosaic_moe_a16_workspace_bytes) is larger is rejected with status < 0.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (several streams or host threads) race.  No stage events.
+ * No counterpart in the reference: it exists for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation). */
+int mosaic_moe_a16_forward_noalloc(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
+                                   const uint8_t* gu_packed, const uint8_t* gu_scale, const uint8_t* d_packed,
+                                   const uint8_t* d_scale, const uint8_t* sh_gu_packed, const uint8_t* sh_gu_scale,
+                                   const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
+                                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
+                                   int renorm, float route_scale, const float* route_bias, float swiglu_limit,
+                                   void* stream);
+
 /* ---------------------------------------------------- A8 routed MoE layer -- */
 size_t mosaic_moe_a8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
                                      int has_shared);

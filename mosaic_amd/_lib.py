@@ -46,6 +46,9 @@ SIGNATURES: dict[str, tuple] = {
                                       P, c_size_t, P]),
     "mosaic_moe_a16_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,
                                        P, c_size_t, P, P]),
+    "mosaic_moe_a16_noalloc_max_bytes": (c_size_t, []),
+    "mosaic_moe_a16_forward_noalloc": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F,
+                                               P, F, P]),
     "mosaic_dsa_indexer_workspace_bytes": (c_size_t, [I64, I64]),
     "mosaic_dsa_indexer_topk": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int32, P, c_size_t,
                                         P]),
