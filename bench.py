@@ -8,16 +8,21 @@ and RNE E2M1, then MXT16-prepacked), tokens bf16 N(0, 1), router logits
 N(0, 1), sigmoid scores, top-8, weights renormalized to 1, SwiGLU.  A step is
 one full layer (routing, stable expert sort, gate/up+SwiGLU, down, combine) on
 one batch of M tokens (default M=1; at M=1 the layer is two launches: routing
-fused into gate/up+SwiGLU, then down fused with the combine).  Inputs are resident in HBM before the
-timed region.  Two independent 6 GB layer banks alternate step by step and the
-routing changes every step, so weights come from HBM, not the 256 MB MALL.
+fused into gate/up+SwiGLU, then down fused with the combine).  Inputs are
+resident in HBM before the timed region.  Three independent 6 GB layer banks
+rotate step by step and the routing changes every step, so a bank's bytes
+(its shared expert included) are read again only after two other layers
+(about 420 MB, more than the 256 MB MALL): weights come from HBM.
 
-``value`` is the algorithmic HBM throughput of the layer (every distinct
-expert's bytes read once + x + y) in GB/s; ``roofline`` reports the gate/up
-kernel (the dominant one) against 8 TB/s, timed with HIP events recorded on
-the kernel's stream inside the timed region; ``cpu_baseline`` times the CPU
-oracle (numpy dequant-then-matmul, the reference's CPU path restated) on one
-token of the same layer.
+The timed region replays a HIP graph of the K steps (one replay = exactly K
+layers); the same K steps run eagerly through the Python wrapper are reported
+beside it.  ``value`` is the algorithmic HBM throughput of the layer (every
+distinct expert's bytes read once + x + y) in GB/s; ``roofline`` reports the
+gate/up kernel (the dominant one) against 8 TB/s, timed with HIP events that
+the kernel's own dispatch records; ``cpu_baseline`` times the reference's own
+CPU kernel (the integer-exact A8 ``vnni_source_gemm`` built from the
+reference's source) on single-token layers of the same weights, beside a
+torch-CPU fp32 dequant-then-matmul of the A16 layer.
 """
 from __future__ import annotations
 
@@ -42,6 +47,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE x 2.0, WRITE_SIZE x 1.0.  The profile summary
 # profiles/moe_decode_m1_traffic.md holds the commands and raw figures.
 GATEUP_M1_TRAFFIC_BYTES = (68771.5 * 2.0 + 36.1) * 1024
+N_BANKS = 3  # independent layers rotated step by step (reuse distance > the 256 MB MALL)
 METRIC = "MXFP4 MoE-layer decode µs & HBM GB/s % peak; FP8/MXFP4 GEMM TFLOPS % peak"
 
 
@@ -94,6 +100,10 @@ def build_banks(torch, ops, n_banks: int, seed: int = 0):
 
 
 def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
+    """K layer steps at M tokens: eager warmup, the K steps eagerly (reported
+    beside the headline), then the K steps captured in one HIP graph and timed
+    by one replay (the headline), then an instrumented eager pass with HIP
+    events at the stage boundaries."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1000 + seed)
@@ -109,15 +119,26 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
 
     for i in range(warmup):
         step(i)
-    ids_all = []
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
     for i in range(steps):
-        _, ids, _ = step(warmup + i)
-        ids_all.append(ids)
+        step(warmup + i)
+    ev1.record()
+    torch.cuda.synchronize()
+    eager_ms = ev0.elapsed_time(ev1)
+    # the same K steps in one graph: one replay = exactly K layers
+    graph = torch.cuda.CUDAGraph()
+    ids_all = []
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            ids_all.append(step(warmup + i)[1])
+    graph.replay()  # untimed: first replay
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    graph.replay()
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -136,12 +157,15 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     layer_bytes = [(u + 1) * EXPERT_BYTES + 2 * m * H * 2 + m * E * 4 for u in distinct]
     gu_bytes = [(u + 1) * GU_BYTES + m * H * 2 + (u + 1) * I * 2 for u in distinct]
     gu_s = sum(t["gu_sec"] for t in times)
+    del graph
     return {
         "m": m,
         "us_per_layer": gpu_ms * 1e3 / steps,
+        "eager_us_per_layer": eager_ms * 1e3 / steps,
         "wall_ms": wall * 1e3,
         "gbs": sum(layer_bytes) / (gpu_ms / 1e3) / 1e9,
         "distinct_experts_avg": sum(distinct) / len(distinct),
+        "layer_bytes_avg": sum(layer_bytes) / steps,
         "stage_us": {k: 1e6 * sum(t[k] for t in times) / steps for k in ops.MOE_STAGES},
         "gateup_us": 1e6 * gu_s / steps,
         "gateup_gbs": sum(gu_bytes) / gu_s / 1e9,
@@ -241,6 +265,15 @@ def config4_prefill(torch, ops, bank, m: int = 4096, seed: int = 13):
                                     workspace=ws)
     _, ids, _ = fn()
     us = _graph_time(torch, fn, 3, reps=3)
+    # per-stage times (eager, HIP events at the stage boundaries), 3 calls
+    reps = [ops.StageEvents(ops.MOE_A8_STAGES) for _ in range(3)]
+    torch.cuda.synchronize()
+    for se in reps:
+        ops.moe_a8_forward(x, bank["gu"], bank["dn"], logits=logits, top_k=K, shared=bank["shared"], workspace=ws,
+                           stage_events=se)
+    torch.cuda.synchronize()
+    st = [se.times() for se in reps]
+    stage_us = {k: round(1e6 * sum(t[k] for t in st) / len(st), 1) for k in ops.MOE_A8_STAGES}
     counts = torch.bincount(ids.flatten().long(), minlength=E)
     used = int((counts > 0).sum().item())
     fl = 2 * m * (K + 1) * 3 * H * I
@@ -248,7 +281,11 @@ def config4_prefill(torch, ops, bank, m: int = 4096, seed: int = 13):
     return {"tokens": m, "us": round(us, 1), "tokens_per_s": round(m / us * 1e6, 1),
             "TFLOPs": round(fl / us / 1e6, 1), "mfma_frac": round(fl / us / 1e6 / 5000.0, 4),
             "hbm_GBs": round(byts / us / 1e3, 1), "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
-            "experts_used": used, "max_expert_rows": int(counts.max().item()), "contract": "A8 (fused_moe_mxint)"}
+            "experts_used": used, "max_expert_rows": int(counts.max().item()), "contract": "A8 (fused_moe_mxint)",
+            "stage_us": stage_us,
+            "stage_note": "eager calls with stage events (the timed line replays a graph); sort/permute = "
+                          "layout_sec, gate/up with the SwiGLU + z requant epilogue fused = gu_sec "
+                          "(down_quant_sec ~ 0), scatter-combine = reduction_sec"}
 
 
 def config5_dsa(torch, ops):
@@ -301,36 +338,171 @@ def config5_dsa(torch, ops):
     return out
 
 
-def cpu_baseline(torch, ops, bank, tokens: int = 8, seed: int = 7):
-    """Oracle (numpy A16 dequant-then-matmul) on ``tokens`` single-token decode
-    steps of the same layer (each token routed on its own, its 8 routed + the
-    shared expert dequantized and multiplied), about 10 s of CPU work."""
+def _cpu_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
+
+
+def _cpu_info() -> dict:
+    model, phys, cores, siblings = "unknown", set(), 0, 0
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name":
+                model = v
+            elif k == "physical id":
+                phys.add(v)
+            elif k == "cpu cores":
+                cores = int(v)
+            elif k == "siblings":
+                siblings = int(v)
+    except OSError:
+        pass
+    return {"model": model, "sockets": max(1, len(phys)), "cores_per_socket": cores,
+            "smt": (siblings // cores) if cores else None, "visible_cpus": os.cpu_count()}
+
+
+def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7):
+    """The reference's CPU path on the host cores, beside the GPU numbers.
+
+    ``value``: the reference's own integer-exact A8 CPU kernel (``vnni_source_gemm``,
+    ``bench/vnni_source_kernel.c:8-47``, built from the reference's source into
+    ``oracle/_ref``) running the A8 MoE layer of ``fused_moe_mxint`` on ``tokens``
+    single-token decode steps (8 routed + the shared expert each; weights tiled
+    outside the timed region, as the reference's bench prepares them).  Also
+    timed: the A16 layer as torch-CPU fp32 dequant-then-matmul (weights
+    dequantized outside the timed region), the config-1 linear both ways, and
+    the config-3 FP8 shapes as torch-CPU fp32 dequant-then-matmul at every M.
+    Without a VNNI-capable build the numpy oracle stands in (kind "port")."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
 
+    from oracle import codecs as C
     from oracle import moe as MO
+    from oracle import ref_c
 
-    cores = len(os.sched_getaffinity(0))
+    cores = _cpu_threads()
+    torch.set_num_threads(cores)
     rng = np.random.default_rng(seed)
     gp, gs, dp, ds = bank["raw"]
-    shared = (gp[E].cpu().numpy(), gs[E].cpu().numpy(), dp[E].cpu().numpy(), ds[E].cpu().numpy())
-    total_s, total_bytes = 0.0, 0
+    lib = ref_c.library()
+    host = {}
+
+    def expert(e):
+        if e not in host:
+            host[e] = (gp[e].cpu().numpy(), gs[e].cpu().numpy(), dp[e].cpu().numpy(), ds[e].cpu().numpy())
+        return host[e]
+
+    steps = []
     for _ in range(tokens):
         x = torch.from_numpy(rng.standard_normal((1, H)).astype(np.float32)).to(torch.bfloat16).float().numpy()
         ids, w = MO.route_topk(rng.standard_normal((1, E)).astype(np.float32), K, "sigmoid")
-        used = sorted(set(ids.flatten().tolist()))
-        host = {e: (gp[e].cpu().numpy(), gs[e].cpu().numpy(), dp[e].cpu().numpy(), ds[e].cpu().numpy())
-                for e in used}
-        with threadpool_limits(limits=cores):
+        steps.append((x, ids, w))
+    used = sorted({int(e) for _, ids, _ in steps for e in ids.flatten()})
+    out = {"cores": cores, "cpu": _cpu_info()}
+
+    # (1) A8 layer on the reference's own CPU kernel
+    if lib is not None:
+        tiles = {e: (ref_c.prepare_weights(*expert(e)[:2]), ref_c.prepare_weights(*expert(e)[2:]))
+                 for e in used + [E]}
+
+        def a8_expert(codes, sa, e, wt):
+            g = C.round_bf16(ref_c.gemm(codes, sa, tiles[e][0], lib))
+            z = C.round_bf16((MO.swiglu(g[:, :I], g[:, I:], 0.0) * np.float32(wt)).astype(np.float32))
+            zc, zs = C.act_quant(z, 128, "pow2")
+            return C.round_bf16(ref_c.gemm(zc, zs, tiles[e][1], lib))
+
+        t_a8, nbytes = 0.0, 0
+        for x, ids, w in steps:
             t0 = time.perf_counter()
-            MO.moe_layer_a16(x, ids, w, lambda e: host[e][0], lambda e: host[e][1], lambda e: host[e][2],
-                             lambda e: host[e][3], shared=shared)
-            total_s += time.perf_counter() - t0
-        total_bytes += (len(used) + 1) * EXPERT_BYTES + 2 * H * 2
-    return {"value": round(total_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "us_per_layer": round(total_s / tokens * 1e6, 1),
-            "sample": f"{tokens} single-token decode steps (8 routed + 1 shared experts each) of the same layer "
-                      f"through the numpy oracle (dequant, then float64 matmul), {total_s:.1f} s total"}
+            codes, sa = C.act_quant(x, 128, "pow2")
+            acc = np.zeros((1, H), dtype=np.float32)
+            for s_ in np.argsort(ids[0], kind="stable"):
+                acc = (acc + a8_expert(codes, sa, int(ids[0, s_]), w[0, s_])).astype(np.float32)
+            acc = (acc + a8_expert(codes, sa, E, 1.0)).astype(np.float32)
+            C.round_bf16(acc)
+            t_a8 += time.perf_counter() - t0
+            nbytes += (len(set(ids.flatten().tolist())) + 1) * EXPERT_BYTES + 2 * H * 2
+        out.update({"value": round(nbytes / t_a8 / 1e9, 3), "unit": "GB/s", "kind": "reference",
+                    "us_per_layer": round(t_a8 / tokens * 1e6, 1),
+                    "sample": f"{tokens} single-token A8 decode layers (8 routed + 1 shared expert, hidden {H}, "
+                              f"inter {I}) through vnni_source_gemm ({cores} OpenMP threads), {t_a8:.2f} s"})
+    # (2) A16 layer, torch-CPU fp32 dequant-then-matmul
+    deq = {e: tuple(torch.from_numpy(C.dequant_mxfp4(*expert(e)[2 * j:2 * j + 2])) for j in range(2))
+           for e in used + [E]}
+    t_a16 = 0.0
+    for x, ids, w in steps:
+        xt = torch.from_numpy(x)
+        t0 = time.perf_counter()
+        acc = torch.zeros(1, H)
+        order = list(np.argsort(ids[0], kind="stable")) + [None]
+        for s_ in order:
+            e, wt = (E, 1.0) if s_ is None else (int(ids[0, s_]), float(w[0, s_]))
+            gu = xt @ deq[e][0].T
+            z = (torch.nn.functional.silu(gu[:, :I]) * gu[:, I:] * wt).to(torch.bfloat16).float()
+            acc = acc + z @ deq[e][1].T
+        acc.to(torch.bfloat16)
+        t_a16 += time.perf_counter() - t0
+    a16_bytes = sum((len(set(ids.flatten().tolist())) + 1) * EXPERT_BYTES + 2 * H * 2 for _, ids, _ in steps)
+    out["a16_torch_fp32"] = {"us_per_layer": round(t_a16 / tokens * 1e6, 1),
+                             "GBs_mxfp4_equiv": round(a16_bytes / t_a16 / 1e9, 3)}
+    if "value" not in out:  # no VNNI build here: the A16 torch path is the baseline
+        out.update({"value": out["a16_torch_fp32"]["GBs_mxfp4_equiv"], "unit": "GB/s", "kind": "port",
+                    "us_per_layer": out["a16_torch_fp32"]["us_per_layer"],
+                    "sample": f"{tokens} single-token A16 decode layers, torch-CPU fp32 dequant-then-matmul"})
+    del deq
+
+    # (3) config 1: MXFP4 linear [2048, 7168] at M = 1 (the first 2048 gate rows of expert 0)
+    p1, s1 = expert(0)[0][:2048], expert(0)[1][:2048]
+    x1 = steps[0][0]
+    c1 = {}
+    if lib is not None:
+        t1 = ref_c.prepare_weights(np.ascontiguousarray(p1), np.ascontiguousarray(s1))
+        codes, sa = C.act_quant(x1, 128, "pow2")
+        t0 = time.perf_counter()
+        for _ in range(20):
+            ref_c.gemm(codes, sa, t1, lib)
+        c1["a8_reference_us"] = round((time.perf_counter() - t0) / 20 * 1e6, 1)
+    w1 = torch.from_numpy(C.dequant_mxfp4(p1, s1))
+    xt = torch.from_numpy(x1)
+    t0 = time.perf_counter()
+    for _ in range(20):
+        xt @ w1.T
+    c1["a16_torch_fp32_us"] = round((time.perf_counter() - t0) / 20 * 1e6, 1)
+    out["config1_linear_m1"] = c1
+
+    # (4) config 3: FP8 block-scaled GEMMs, torch-CPU fp32 dequant-then-matmul
+    c3 = {}
+    g = torch.Generator().manual_seed(12)
+    for n, k in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (18432, 7168)]:
+        wq = (torch.randn(n, k, generator=g) * 0.02 * 448 / 0.08).clamp(-448, 448).to(torch.float8_e4m3fn)
+        bs = torch.rand((n + 127) // 128, k // 128, generator=g) * 1e-4
+        wf = wq.float() * bs.repeat_interleave(128, 0)[:n].repeat_interleave(128, 1)
+        for m in (1, 16, 128, 4096):
+            xa = (torch.randn(m, k, generator=g) * 60).clamp(-448, 448).to(torch.float8_e4m3fn)
+            asc = torch.rand(m, k // 128, generator=g) * 1e-2
+            reps = 5 if m < 4096 else 1
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                (xa.float() * asc.repeat_interleave(128, 1)) @ wf.T
+            us = (time.perf_counter() - t0) / reps * 1e6
+            c3[f"m{m}_n{n}_k{k}"] = {"us": round(us, 1), "TFLOPs": round(2 * m * n * k / us / 1e6, 3)}
+        del wq, wf
+    out["config3_fp8_gemm_torch_fp32"] = c3
+    return out
+
+
+def _stage_view(m: int, st: dict) -> dict:
+    """Per-stage microseconds of the instrumented pass.  At M = 1 the layer is
+    two launches whose dispatches record their own start/end events, so only
+    the two kernels are stages (routing is fused into gate/up, the combine
+    into down); the other event gaps are dispatch latency, not work."""
+    if m != 1:
+        return {k: round(v, 2) for k, v in st.items()}
+    return {"gateup_kernel_with_routing": round(st["gu_sec"], 2),
+            "gap_and_down_kernel_with_combine": round(st["down_sec"], 2),
+            "note": "events recorded by the two dispatches themselves; M=1 has no separate layout or combine stage"}
 
 
 def main():
@@ -346,14 +518,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    banks = build_banks(torch, ops, n_banks=2)
+    banks = build_banks(torch, ops, n_banks=N_BANKS)
     main_r = run_m(torch, ops, banks, args.m, args.steps, args.warmup, seed=0)
     sweep = {}
     for mv in [int(v) for v in args.sweep.split(",") if v.strip()]:
         if mv != args.m:
-            r = run_m(torch, ops, banks, mv, max(5, args.steps // 5), 2, seed=mv)
+            r = run_m(torch, ops, banks, mv, max(6, args.steps // 5), 2, seed=mv)
             sweep[str(mv)] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()
-                              if k in ("us_per_layer", "gbs", "distinct_experts_avg")}
+                              if k in ("us_per_layer", "eager_us_per_layer", "gbs", "distinct_experts_avg")}
             sweep[str(mv)]["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     configs = {}
     if not args.no_configs:
@@ -382,12 +554,15 @@ def main():
         "data": "synthetic (seeded N(0,1) tokens/logits, N(0,0.02) weights quantized to MXFP4)",
         "config": {"workload": "MXFP4 MoE decode layer (BASELINE configs[1])", "tokens": args.m, "hidden": H,
                    "inter": I, "experts": E, "top_k": K, "shared_experts": 1, "score": "sigmoid",
-                   "contract": "A16 dequant-then-matmul", "weight_layout": "MXT16 prepacked", "banks": 2},
+                   "contract": "A16 dequant-then-matmul", "weight_layout": "MXT16 prepacked", "banks": N_BANKS,
+                   "bank_reuse_distance_bytes": round((N_BANKS - 1) * main_r["layer_bytes_avg"]),
+                   "timing": "one HIP-graph replay of the K steps"},
         "us_per_layer": round(main_r["us_per_layer"], 2),
+        "eager_us_per_layer": round(main_r["eager_us_per_layer"], 2),
         "hbm_frac": round(main_r["gbs"] / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(args.m / (main_r["us_per_layer"] / 1e6), 1),
         "distinct_experts_avg": main_r["distinct_experts_avg"],
-        "stage_us": {k: round(v, 2) for k, v in main_r["stage_us"].items()},
+        "stage_us": _stage_view(args.m, main_r["stage_us"]),
         "roofline": {"kernel": "moe_dec1_gateup_kernel" if args.m == 1 else "moe_a16_gateup_kernel", "bound": "hbm",
                      "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),

@@ -145,6 +145,15 @@ int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16_t* out, in
 int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, int64_t top_k, int score_func, int renorm,
                           float route_scale, const float* bias, int32_t* ids, float* weights, void* stream);
 
+/* Router projection: logits [m, e] f32 = x [m, h] . w [e, h]^T with x and w
+ * each f32 or bf16 (x_dtype, w_dtype), every logit the exact dot product
+ * rounded once to fp32 (products exact in fp64, summed in fp64 in a fixed
+ * order, one rounding), so routing keys do not depend on a summation order.
+ * Replaces the F.linear(x.float(), W.float()) of Router.forward
+ * (model/layers.py:128) and Gate.forward (.mosaicvm/source/inference_model.py:570). */
+int mosaic_router_logits(const void* x, int x_dtype, const void* w, int w_dtype, float* logits, int64_t m, int64_t e,
+                         int64_t h, void* stream);
+
 /* Stable expert sort + uncapped tile list for ids [m, top_k] (+ one shared
  * expert row per token when has_shared, virtual expert id e).
  * Replaces layout_assignments (kernels/moe_layout.py:8-27) and emit_tiles
@@ -231,14 +240,18 @@ size_t mosaic_moe_a8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, i
  * the clamps when swiglu_limit > 0, x route weight, bf16, 1x128 pow2 e4m3
  * requant, A8 down into bf16 partials, fp32 sum in ascending expert id (an
  * optional shared expert is added last), bf16.  Arguments as
- * mosaic_moe_a16_forward (MXT16 banks). */
+ * mosaic_moe_a16_forward (MXT16 banks).  stage_events: NULL, or 7 hipEvent_t
+ * recorded on `stream` at start, after routing+layout, after the token
+ * act-quant, after gate/up+SwiGLU, after the z requant (fused into gate/up at
+ * prefill sizes), after down, after combine (fused_moe_mxint's stage_times
+ * boundaries, kernels/mxint.py:1702-1714). */
 int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int32_t* ids, float* weights,
                           const uint8_t* gu_packed, const uint8_t* gu_scale, const uint8_t* d_packed,
                           const uint8_t* d_scale, const uint8_t* sh_gu_packed, const uint8_t* sh_gu_scale,
                           const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
                           int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
                           int renorm, float route_scale, const float* route_bias, float swiglu_limit,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream);
 
 /* ----------------------------------------------------------- DSA decode -- */
 /* Workspace bytes of mosaic_dsa_indexer_topk for b rows of l cached tokens. */

@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_mxt16_linear_a8": (c_int, [P, P, P, P, P, I64, I64, I64, P]),
     "mosaic_fp8_block_dequant": (c_int, [P, P, P, I64, I64, I, I, P]),
     "mosaic_moe_route_topk": (c_int, [P, I64, I64, I64, I, I, F, P, P, P, P]),
+    "mosaic_router_logits": (c_int, [P, I, P, I, P, I64, I64, I64, P]),
     "mosaic_moe_layout_workspace_bytes": (c_size_t, [I64, I64, I64, I]),
     "mosaic_moe_layout": (c_int, [P, P, I64, I64, I64, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I64, P, c_size_t,
                                   P]),
@@ -43,7 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_moe_a16_workspace_bytes": (c_size_t, [I64, I64, I64, I64, I64, I]),
     "mosaic_moe_a8_workspace_bytes": (c_size_t, [I64, I64, I64, I64, I64, I]),
     "mosaic_moe_a8_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,
-                                      P, c_size_t, P]),
+                                      P, c_size_t, P, P]),
     "mosaic_moe_a16_forward": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F, P, F,
                                        P, c_size_t, P, P]),
     "mosaic_moe_a16_noalloc_max_bytes": (c_size_t, []),

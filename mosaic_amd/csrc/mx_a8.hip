@@ -863,7 +863,8 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
                                      const uint8_t* sh_d_packed, const uint8_t* sh_d_scale, uint16_t* y, int64_t m,
                                      int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
                                      int renorm, float route_scale, const float* route_bias, float swiglu_limit,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+                                     void* workspace, size_t workspace_bytes, void* const* stage_events,
+                                     void* stream) {
   MOSAIC_CHECK_ARG(x && ids && weights && gu_packed && gu_scale && d_packed && d_scale && y && workspace,
                    "moe_a8_forward: null pointer");
   const int has_shared = sh_gu_packed != nullptr;
@@ -879,6 +880,10 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
   MOSAIC_CHECK_ARG(workspace_bytes >= w.bytes, "moe_a8_forward: workspace %zu < %zu bytes", workspace_bytes,
                    w.bytes);
   hipStream_t st = (hipStream_t)stream;
+  auto mark = [&](int i) {
+    if (stage_events && stage_events[i]) (void)hipEventRecord((hipEvent_t)stage_events[i], st);
+  };
+  mark(0);
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,
                w.combine_pos, w.tile_expert, w.tile_start, w.tile_rows, w.tile_p0, w.n_tiles, nullptr, 0, 1,
                w.chunk_counts, w.chunk_base};
@@ -892,8 +897,10 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
   int rc = launch_route_layout(logits, route_bias, ids, weights, ids, weights, m, n_experts, top_k, score_func,
                                renorm, route_scale, has_shared, block_m, tcap, lo, st);
   if (rc != 0) return rc;
+  mark(1);
   rc = mosaic_act_quant(x, MOSAIC_DTYPE_BF16, w.xq, w.xs, m, hidden, 128, 0, stream);
   if (rc != 0) return rc;
+  mark(2);
   if (prefill) {
     uint16_t* yb = reinterpret_cast<uint16_t*>(w.yp);  // bf16 partials in the fp32 partial buffer
     const int64_t tcap8 = (tcap + 7) / 8 * 8;
@@ -903,13 +910,18 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
                        w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.zq, w.zs, (int)hidden, (int)inter,
                        (int)n_experts, swiglu_limit);
     MOSAIC_LAUNCH_CHECK("moe_a8_gateup_prefill");
+    mark(3);
+    mark(4);  // the z requant is fused into the gate/up epilogue
     hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows, w.tile_p0,
                        w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts);
     MOSAIC_LAUNCH_CHECK("moe_a8_down_prefill");
+    mark(5);
     hipLaunchKernelGGL(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 8 + 127) / 128), (unsigned)m), dim3(128),
                        0, st, yb, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
-    MOSAIC_RETURN_LAUNCH("moe_a8_combine_bf16");
+    MOSAIC_LAUNCH_CHECK("moe_a8_combine_bf16");
+    mark(6);
+    return kOk;
   }
   constexpr int GT = 2, GKS = 4, DT = 2, DKS = 4;
   hipLaunchKernelGGL((moe_a8_gateup_kernel<GT, GKS>), dim3((unsigned)(inter / (8 * GT)), (unsigned)tcap), dim3(GKS * 64), 0,
@@ -917,14 +929,19 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
                      w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
                      (int)n_experts, swiglu_limit);
   MOSAIC_LAUNCH_CHECK("moe_a8_gateup");
+  mark(3);
   // rows of z past the real assignments are never read by the down kernel
   rc = mosaic_act_quant(w.z, MOSAIC_DTYPE_BF16, w.zq, w.zs, A, inter, 128, 0, stream);
   if (rc != 0) return rc;
+  mark(4);
   hipLaunchKernelGGL((moe_a8_down_kernel<DT, DKS>), dim3((unsigned)(hidden / (16 * DT)), (unsigned)tcap), dim3(DKS * 64), 0,
                      st, w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows,
                      w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
   MOSAIC_LAUNCH_CHECK("moe_a8_down");
+  mark(5);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
                      w.yp, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
-  MOSAIC_RETURN_LAUNCH("moe_a8_combine");
+  MOSAIC_LAUNCH_CHECK("moe_a8_combine");
+  mark(6);
+  return kOk;
 }

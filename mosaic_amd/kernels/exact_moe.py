@@ -3,6 +3,7 @@ from __future__ import annotations
 
 import os
 
+from .mxint import fused_moe_mxint
 from .qpa_mma import fused_moe_qpa
 
 _FALSE = ("0", "false", "False", "no", "")
@@ -18,3 +19,12 @@ def exact_moe(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, pack
     if not exact_target():
         raise RuntimeError("exact_moe requires MOSAICVM_EXACT_TARGET=1")
     return fused_moe_qpa(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down)
+
+
+def exact_moe_mxint(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down, bank=None):
+    """A8 routed MoE through ``fused_moe_mxint``; requires the exact target
+    (``kernels/exact_moe.py:22-31``)."""
+    if not exact_target():
+        raise RuntimeError("exact_moe_mxint requires MOSAICVM_EXACT_TARGET=1")
+    return fused_moe_mxint(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down,
+                           bank=bank)

@@ -12,7 +12,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import ops
-from . import _a8
+from . import _a8, _prepack_cache
 
 
 @dataclass
@@ -65,17 +65,25 @@ def fused_moe_mxint(x, expert_ids, expert_weights, packed_gate_up=None, scale_ga
 
     x [k_tok, H] bf16; expert_ids [k_tok, top_k] (or [k_tok]); expert_weights
     fp32 of the same shape (None = ones).  Weights come from ``bank`` (MXT16Bank)
-    or raw NK tensors (prepacked on every call, as the reference does without a
-    bank).  Sync-free: nothing is read back to the host."""
+    or raw NK tensors (their MXT16 prepack cached while the tensors live).
+    Sync-free unless ``stage_times`` is given: then the stage boundaries are
+    timed with HIP events and the call waits for them, as the reference does."""
     if weight_repr not in ("hot8", "packed4", "hybrid"):
         raise ValueError(f"weight_repr must be hot8|packed4|hybrid, got {weight_repr}")
     if bank is None:
         if packed_gate_up is None or packed_down is None:
             raise TypeError("fused_moe_mxint requires bank= or packed_gate_up/packed_down")
-        bank = prepack_expert_bank_mxint(packed_gate_up, scale_gate_up, packed_d=packed_down, scale_d=scale_down)
+        bank = MXT16Bank(_prepack_cache.mxt16(packed_gate_up, scale_gate_up), _prepack_cache.mxt16(packed_down, scale_down))
     ids = expert_ids if expert_ids.dim() == 2 else expert_ids.reshape(-1, 1)
     k_tok, top_k = ids.shape
     w = (torch.ones(k_tok, top_k, dtype=torch.float32, device=x.device) if expert_weights is None
          else expert_weights.reshape(k_tok, top_k).to(torch.float32))
-    y, _, _ = ops.moe_a8_forward(x, bank.gate_up, bank.down, ids=ids, weights=w, swiglu_limit=swiglu_limit)
+    se = ops.StageEvents(ops.MOE_A8_STAGES) if stage_times is not None else None
+    y, _, _ = ops.moe_a8_forward(x, bank.gate_up, bank.down, ids=ids, weights=w, swiglu_limit=swiglu_limit,
+                                 stage_events=se)
+    if se is not None:  # the reference synchronizes to fill stage_times (kernels/mxint.py:1702-1714)
+        t = se.times()
+        stage_times.update(t)
+        stage_times["decode_int_sec"] = 0.0  # no integer limb split on gfx950
+        stage_times["swiglu_sec"] = 0.0      # fused into the gate/up kernels
     return y

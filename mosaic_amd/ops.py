@@ -289,6 +289,25 @@ def moe_route_topk(logits: torch.Tensor, top_k: int, score_func: str = "sigmoid"
     return ids, w
 
 
+def router_logits(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """logits [M, E] f32 = x [M, H] . w [E, H]^T (x, w each bf16 or f32), each
+    logit the exact dot product rounded once to fp32."""
+    x = _cuda(x, "x")
+    w = _cuda(w, "weight")
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError(f"x {tuple(x.shape)} and weight {tuple(w.shape)} must be [M, H] and [E, H]")
+    dt = {torch.bfloat16: DT_BF16, torch.float32: DT_F32}
+    if x.dtype not in dt:
+        x = x.to(torch.float32)
+    if w.dtype not in dt:
+        w = w.to(torch.float32)
+    m, h = x.shape
+    e = w.shape[0]
+    out = torch.empty(m, e, dtype=torch.float32, device=x.device)
+    _lib.call("mosaic_router_logits", _ptr(x), dt[x.dtype], _ptr(w), dt[w.dtype], _ptr(out), m, e, h, _stream())
+    return out
+
+
 def _tile_cap(a: int, e_ext: int, block_m: int) -> int:
     u = min(a, e_ext)
     return (a + u * (block_m - 1)) // block_m
@@ -384,8 +403,8 @@ def moe_a16_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, **kw):
 
 
 def moe_a8_forward(x: torch.Tensor, gate_up: MXT16, down: MXT16, **kw):
-    """A8 routed MoE layer (fused_moe_mxint contract), same arguments as ``moe_a16_forward``."""
-    kw.pop("stage_events", None)
+    """A8 routed MoE layer (fused_moe_mxint contract), same arguments as
+    ``moe_a16_forward``; ``stage_events`` is a ``StageEvents(MOE_A8_STAGES)``."""
     return _moe_forward(True, x, gate_up, down, **kw)
 
 
@@ -442,33 +461,40 @@ def _moe_forward(a8: bool, x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logi
             _ptr(down.packed), _ptr(down.scale), _ptr(sh[0]), _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(y), m, h,
             inter, e, top_k, SCORE_FUNCS[score_func], int(renorm), float(route_scale), _ptr(route_bias),
             float(swiglu_limit), _ptr(ws), ws.numel()]
-    if not a8:
-        args.append(None if stage_events is None else stage_events.array)
+    want = MOE_A8_STAGES if a8 else MOE_STAGES
+    if stage_events is not None and stage_events.names != want:
+        raise ValueError(f"stage_events must cover {want}")
+    args.append(None if stage_events is None else stage_events.array)
     _lib.call(f"mosaic_moe_{kind}_forward", *args, _stream())
     return y, ids, weights
 
 
 MOE_STAGES = ("layout_sec", "gu_sec", "down_sec", "reduction_sec")
+MOE_A8_STAGES = ("layout_sec", "act_quant_sec", "gu_sec", "down_quant_sec", "down_sec", "reduction_sec")
 
 
 class StageEvents:
-    """Five HIP events recorded by the MoE forward at its stage boundaries
-    (start, after routing+layout, after gate/up+SwiGLU, after down, after
-    combine); ``times()`` returns seconds per stage like the reference's
-    ``stage_times`` dict (``kernels/mxint.py:1702-1714``)."""
+    """HIP events recorded by the MoE forward at its stage boundaries; ``times()``
+    returns seconds per stage like the reference's ``stage_times`` dict
+    (``kernels/mxint.py:1702-1714``).  A16: start, after routing+layout, after
+    gate/up+SwiGLU, after down, after combine (``MOE_STAGES``).  A8
+    (``MOE_A8_STAGES``): start, after routing+layout, after the token
+    act-quant, after gate/up+SwiGLU, after the z requant, after down, after
+    combine."""
 
-    def __init__(self):
-        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    def __init__(self, names: tuple = MOE_STAGES):
+        self.names = tuple(names)
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(len(self.names) + 1)]
         for e in self.events:  # torch creates the underlying hipEvent on first record
             e.record()
         torch.cuda.current_stream().synchronize()
-        self.array = (ctypes.c_void_p * 5)(*[ctypes.c_void_p(e.cuda_event) for e in self.events])
+        self.array = (ctypes.c_void_p * len(self.events))(*[ctypes.c_void_p(e.cuda_event) for e in self.events])
 
     def times(self) -> dict:
         ev = self.events
         ev[-1].synchronize()
-        out = {k: ev[i].elapsed_time(ev[i + 1]) / 1e3 for i, k in enumerate(MOE_STAGES)}
-        out["total_sec"] = sum(out[k] for k in MOE_STAGES)
+        out = {k: ev[i].elapsed_time(ev[i + 1]) / 1e3 for i, k in enumerate(self.names)}
+        out["total_sec"] = sum(out[k] for k in self.names)
         return out
 
 

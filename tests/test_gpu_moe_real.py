@@ -73,6 +73,54 @@ def test_route_kernel_reference_router_bit_exact(dev):
     assert list(ids_ref[0]).index(17) < list(ids_ref[0]).index(200)
 
 
+def _score_tie_case(m: int, func: str, e: int = 256, k: int = 8, seed: int = 8):
+    """Seeded logits where, on every row, two experts whose logits are one ulp
+    apart share one fp32 score and the LARGER logit belongs to the HIGHER
+    index: once inside the picks (experts 40 and 60 near the top) and once at
+    the k-th / (k+1)-th boundary (experts 70 and 90), so ranking by logit
+    would disagree with ranking by score with ties to the lower index."""
+    rng = np.random.default_rng(seed)
+    logits = (rng.standard_normal((m, e)) * 0.5).astype(np.float32)
+    for r in range(m):
+        for lo, hi, base in ((40, 60, 3.0), (70, 90, None)):
+            if base is None:  # 40 and 60 lead, so k - 3 others go before 90 (k-th) and 70
+                rest = np.sort(np.delete(logits[r], [40, 60, 70, 90]))[::-1]
+                base = float(rest[k - 4] + rest[k - 3]) / 2
+            t = np.float32(base)
+            for _ in range(64):  # walk up until t and its lower neighbour share a score
+                tl = np.nextafter(t, np.float32(-np.inf))
+                if MO.score_fn(np.array([[tl, t]], dtype=np.float32), func)[0].tolist() == \
+                        MO.score_fn(np.array([[t, t]], dtype=np.float32), func)[0].tolist():
+                    break
+                t = np.nextafter(t, np.float32(np.inf))
+            logits[r, hi], logits[r, lo] = t, np.nextafter(t, np.float32(-np.inf))
+    return logits
+
+
+@pytest.mark.parametrize("func", ["sigmoid", "sqrtsoftplus"])
+def test_route_score_ties_without_bias(dev, func):
+    """No bias: the kernels select on the logit and must fall back to the
+    scores when two picks, or the last pick and the next candidate, share an
+    fp32 score (ids bit-exact on the router kernel and the decode kernel)."""
+    ops = _ops()
+    logits = _score_tie_case(32, func)
+    ids_ref, w_ref = MO.route_topk(logits, 8, func)
+    assert all(40 in row and 70 in row and 90 not in row for row in ids_ref.tolist())
+    ids, w = ops.moe_route_topk(torch.from_numpy(logits).to(dev), 8, func)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy(), w_ref)
+    e, h, inter = 256, 512, 512
+    g, raw = _device_bank(ops, dev, e - 1, h, inter, seed=5)
+    gp, gs, dp, ds = raw
+    gu_b, d_b = ops.mxt16_prepack(gp, gs), ops.mxt16_prepack(dp, ds)
+    for r in range(4):  # M = 1: routing fused into the decode gate/up kernel
+        x = torch.randn(1, h, generator=g, device=dev).to(torch.bfloat16)
+        _, ids1, w1 = ops.moe_a16_forward(x, gu_b, d_b, logits=torch.from_numpy(logits[r:r + 1]).to(dev), top_k=8,
+                                          score_func=func)
+        np.testing.assert_array_equal(ids1.cpu().numpy(), ids_ref[r:r + 1])
+        np.testing.assert_array_equal(w1.cpu().numpy(), w_ref[r:r + 1])
+
+
 def _device_bank(ops, dev, e, h, inter, seed):
     """e routed experts + 1 shared, N(0, 0.02) quantized on the device (ceil recipe)."""
     g = torch.Generator(device=dev)
