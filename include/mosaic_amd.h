@@ -73,6 +73,17 @@ int mosaic_e4m3_encode(const float* in, uint8_t* out, int64_t n, void* stream);
 int mosaic_mx_linear_a16(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
                          int64_t n, int64_t k, void* stream);
 
+/* A16 MXFP4 linear on the reference's KN layout (skinny_mxfp4_gemm,
+ * kernels/skinny_fp4.py:113-144): y [m, n] bf16 = x [m, k] bf16 . W with
+ * W [k, n] = E2M1(packed [k, n/2], low nibble = even n) * 2^(scale [k, n/32] - 127),
+ * fp32 accumulation.  n % 32 == 0, k % 32 == 0.  K is split over workgroups
+ * when the columns alone would not fill the GPU; the fp32 partials then need
+ * mosaic_mx_kn_linear_a16_workspace_bytes(m, n, k) bytes of workspace and are
+ * summed in a fixed order. */
+size_t mosaic_mx_kn_linear_a16_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int mosaic_mx_kn_linear_a16(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
+                            int64_t n, int64_t k, void* workspace, size_t workspace_bytes, void* stream);
+
 /* MXT16 prepack: bit-exact permutation of an NK MXFP4 matrix (n % 16 == 0,
  * k % 128 == 0) into the 16-row MFMA tile order read by the A16 kernels:
  *   packed_t[g][S][l][16 B] = packed[16g + l%16][16*(4S + l/16) .. +16]
@@ -229,6 +240,21 @@ int mosaic_moe_a16_forward_noalloc(const uint16_t* x, const float* logits, int32
                                    int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k, int score_func,
                                    int renorm, float route_scale, const float* route_bias, float swiglu_limit,
                                    void* stream);
+
+/* fused_moe_skinny (kernels/skinny_fp4.py:267-322), the reference's A16 KN
+ * MoE path with its own arithmetic: stable expert sort of the given ids
+ * [m, top_k] int32 (weights [m, top_k] f32), grouped KN gate|up into bf16
+ * (gu_packed [e, hidden, inter] + gu_scale [e, hidden, 2*inter/32], gate
+ * columns then up columns), z = bf16(bf16(silu(gate)) * up), grouped KN down
+ * into bf16 (d_packed [e, inter, hidden/2] + d_scale [e, inter, hidden/32]),
+ * each output row times bf16(weight) rounded to bf16, then summed per token in
+ * bf16 in assignment order (the reference's bf16 index_add_).  No clamp, no
+ * shared expert.  Workspace: mosaic_moe_skinny_workspace_bytes(). */
+size_t mosaic_moe_skinny_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k);
+int mosaic_moe_skinny_forward(const uint16_t* x, const int32_t* ids, const float* weights, const uint8_t* gu_packed,
+                              const uint8_t* gu_scale, const uint8_t* d_packed, const uint8_t* d_scale, uint16_t* y,
+                              int64_t m, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------- A8 routed MoE layer -- */
 size_t mosaic_moe_a8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts, int64_t top_k,

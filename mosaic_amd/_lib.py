@@ -27,6 +27,8 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_e4m3_decode": (c_int, [P, P, I64, P]),
     "mosaic_e4m3_encode": (c_int, [P, P, I64, P]),
     "mosaic_mx_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P]),
+    "mosaic_mx_kn_linear_a16_workspace_bytes": (c_size_t, [I64, I64, I64]),
+    "mosaic_mx_kn_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P, c_size_t, P]),
     "mosaic_mxt16_prepack": (c_int, [P, P, P, P, I64, I64, P]),
     "mosaic_mxt16_unpack": (c_int, [P, P, P, P, I64, I64, P]),
     "mosaic_mxt16_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P]),
@@ -50,6 +52,8 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_moe_a16_noalloc_max_bytes": (c_size_t, []),
     "mosaic_moe_a16_forward_noalloc": (c_int, [P, P, P, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I, I, F,
                                                P, F, P]),
+    "mosaic_moe_skinny_workspace_bytes": (c_size_t, [I64, I64, I64, I64, I64]),
+    "mosaic_moe_skinny_forward": (c_int, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, c_size_t, P]),
     "mosaic_dsa_indexer_workspace_bytes": (c_size_t, [I64, I64]),
     "mosaic_dsa_indexer_topk": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int32, P, c_size_t,
                                         P]),

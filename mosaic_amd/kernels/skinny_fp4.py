@@ -1,11 +1,12 @@
-"""A16 MXFP4 linear on the reference's KN layout (``kernels/skinny_fp4.py``).
+"""A16 MXFP4 linear and MoE on the reference's KN layout (``kernels/skinny_fp4.py``).
 
-The KN layout blocks the e8m0 scales along N, so it cannot be re-blocked into
-the NK tiles without requantizing; this compatibility path dequantizes the KN
-weight exactly on the GPU and runs the library GEMM with fp32 accumulation
-(dequant-then-matmul, the contract of ``tests/test_skinny_fp4.py:16-25``).
-The NK path (``mosaic_amd.ops.mx_linear_a16`` / ``mxt16_linear_a16``) is the
-hand-written kernel."""
+KN: packed uint8 [K, N/2] (low nibble = even n) with one e8m0 scale per 32
+consecutive N at each k ([K, N/32]).  Both operators run the hand-written
+KN kernel of ``csrc/mx_kn.hip`` (decode to exact bf16 in registers, LDS
+transposing reads into the bf16 MFMA), keeping the reference's arithmetic:
+``skinny_mxfp4_gemm`` is fp32-accumulated dequant-then-matmul to bf16;
+``fused_moe_skinny`` runs its bf16 SwiGLU, weight-after-down and bf16
+index-add combine."""
 from __future__ import annotations
 
 import torch
@@ -14,6 +15,7 @@ from .. import ops
 
 
 def last_launch_count() -> int:
+    """Launches of the last call (the GEMM, plus a split-K sum when K is split)."""
     return 2
 
 
@@ -26,5 +28,23 @@ def skinny_mxfp4_gemm(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor
         raise ValueError(f"n_out={n_out} != packed N={n}")
     if k_p != k:
         raise ValueError(f"packed K={k_p} != x K={k}")
-    w = ops.mx_dequant(packed, scale, torch.bfloat16)  # [K, N], exact
-    return torch.matmul(ops._bf16(x, "x"), w)
+    return ops.mx_kn_linear_a16(x, packed, scale)
+
+
+def _stack(t):
+    if torch.is_tensor(t):
+        return t if t.dim() == 3 else t.unsqueeze(0)
+    return torch.stack(list(t), dim=0)
+
+
+def fused_moe_skinny(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down):
+    """``kernels/skinny_fp4.py:267-322``: x [k_tok, H] bf16, expert_ids [k_tok, top_k]
+    (or [k_tok]), expert_weights of the same shape (None = ones); KN banks
+    packed_gate_up [E, H, 2I/2] + [E, H, 2I/32] (gate | up along N),
+    packed_down [E, I, H/2] + [E, I, H/32] -> [k_tok, H] in x.dtype."""
+    ids = expert_ids if expert_ids.dim() == 2 else expert_ids.reshape(-1, 1)
+    w = (torch.ones(ids.shape, dtype=torch.float32, device=x.device) if expert_weights is None
+         else expert_weights.reshape(ids.shape).to(torch.float32))
+    y = ops.moe_skinny_forward(x.to(torch.bfloat16), ids, w, _stack(packed_gate_up), _stack(scale_gate_up),
+                               _stack(packed_down), _stack(scale_down))
+    return y.to(x.dtype)

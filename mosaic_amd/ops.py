@@ -141,6 +141,58 @@ def mx_linear_a16(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor) ->
     return y
 
 
+def mx_kn_linear_a16(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """y [M, N] bf16 = x [M, K] bf16 . W for a KN-layout MXFP4 weight:
+    packed [K, N/2] (low nibble = even n), e8m0 scale [K, N/32]."""
+    x = _bf16(x, "x")
+    packed = _u8(packed, "packed")
+    scale = _u8(scale, "scale")
+    if x.dim() != 2 or packed.dim() != 2:
+        raise ValueError("x and packed must be 2-D")
+    m, k = x.shape
+    kp, nh = packed.shape
+    n = 2 * nh
+    if kp != k:
+        raise ValueError(f"packed K={kp} != x K={k}")
+    if n % 32 or k % 32:
+        raise ValueError(f"N={n} and K={k} must be multiples of 32")
+    if tuple(scale.shape) != (k, n // 32):
+        raise ValueError(f"scale shape {tuple(scale.shape)} != ({k}, {n // 32})")
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    nbytes = _lib.lib().mosaic_mx_kn_linear_a16_workspace_bytes(m, n, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
+    _lib.call("mosaic_mx_kn_linear_a16", _ptr(x), _ptr(packed), _ptr(scale), _ptr(y), m, n, k, _ptr(ws), nbytes,
+              _stream())
+    return y
+
+
+def moe_skinny_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, gu_packed: torch.Tensor,
+                       gu_scale: torch.Tensor, d_packed: torch.Tensor, d_scale: torch.Tensor) -> torch.Tensor:
+    """fused_moe_skinny arithmetic over KN expert banks: gu [E, H, I] + [E, H, 2I/32]
+    (gate columns then up columns), down [E, I, H/2] + [E, I, H/32] -> y [M, H] bf16."""
+    x = _bf16(x, "x")
+    gu_packed, gu_scale = _u8(gu_packed, "packed_gate_up"), _u8(gu_scale, "scale_gate_up")
+    d_packed, d_scale = _u8(d_packed, "packed_down"), _u8(d_scale, "scale_down")
+    m, h = x.shape
+    if gu_packed.dim() != 3 or d_packed.dim() != 3:
+        raise ValueError("expert banks must be [E, K, N/2]")
+    e, kh, inter = gu_packed.shape  # N = 2 * inter columns, inter bytes per row
+    if kh != h or tuple(gu_scale.shape) != (e, h, 2 * inter // 32):
+        raise ValueError(f"gate/up bank {tuple(gu_packed.shape)}/{tuple(gu_scale.shape)} does not match hidden {h}")
+    if tuple(d_packed.shape) != (e, inter, h // 2) or tuple(d_scale.shape) != (e, inter, h // 32):
+        raise ValueError(f"down bank {tuple(d_packed.shape)}/{tuple(d_scale.shape)} does not match [{e}, {inter}, {h}]")
+    ids = _cuda(ids, "expert_ids")
+    ids = ids.reshape(m, -1).to(torch.int32).contiguous()
+    k = ids.shape[1]
+    weights = _cuda(weights, "expert_weights").reshape(m, k).to(torch.float32).contiguous()
+    y = torch.empty(m, h, dtype=torch.bfloat16, device=x.device)
+    nbytes = _lib.lib().mosaic_moe_skinny_workspace_bytes(m, h, inter, e, k)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=x.device)
+    _lib.call("mosaic_moe_skinny_forward", _ptr(x), _ptr(ids), _ptr(weights), _ptr(gu_packed), _ptr(gu_scale),
+              _ptr(d_packed), _ptr(d_scale), _ptr(y), m, h, inter, e, k, _ptr(ws), ws.numel(), _stream())
+    return y
+
+
 # ------------------------------------------------------- MXT16 prepack ------
 @dataclass
 class MXT16:

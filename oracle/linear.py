@@ -5,6 +5,10 @@
   Restates ``x @ dequant_mxfp4(...)`` (``tests/test_skinny_fp4.py:23``,
   ``kernels/mxfp4.py:130-160``) and the per-expert matmuls of
   ``grouped_expert_forward`` (``model/layers.py:353-365``).
+* ``mx_linear_kn_a16`` (A8, skinny): ``skinny_mxfp4_gemm``
+  (``kernels/skinny_fp4.py:113-144``) on the KN layout: W [K, N] =
+  ``dequant_mxfp4`` of packed [K, N/2] + scale [K, N/32] (blocks of 32 along N),
+  y = x @ W accumulated wide, one bf16 rounding.
 * ``mx_linear_a8`` (A6): ``reference_fp4_linear_source_semantics``
   (``kernels/fp4_source.py:132-156``): act_quant_ref then, for K32 groups in
   ascending order, acc += (A_g . B_g^T) * sA[:, g//4] * sW[:, g] in fp32.
@@ -42,6 +46,13 @@ def mx_linear_a16(x: np.ndarray, packed: np.ndarray, scale: np.ndarray,
     x = np.asarray(x, dtype=np.float32)
     w = C.dequant_mxfp4(packed, scale).astype(np.float64)
     y = (x.astype(np.float64) @ w.T).astype(np.float32)
+    return C.round_bf16(y) if out_bf16 else y
+
+
+def mx_linear_kn_a16(x: np.ndarray, packed: np.ndarray, scale: np.ndarray, out_bf16: bool = True) -> np.ndarray:
+    """x [M, K] (bf16-valued), KN packed [K, N/2] + e8m0 [K, N/32] -> y [M, N]."""
+    w = C.dequant_mxfp4(packed, scale).astype(np.float64)            # [K, N]
+    y = (np.asarray(x, dtype=np.float64) @ w).astype(np.float32)
     return C.round_bf16(y) if out_bf16 else y
 
 

@@ -22,6 +22,12 @@
   clamps (gate max-only, up both sides) when limit > 0, SiLU*up, route weight
   BEFORE the down projection, bf16 cast, fp32 down, per-token sum in
   ascending expert id, shared expert added last, one bf16 rounding.
+* ``moe_layer_skinny`` (``fused_moe_skinny``, ``kernels/skinny_fp4.py:267-322``):
+  KN gate|up into bf16, z = bf16(bf16(silu(gate)) * up), KN down into bf16,
+  each row times bf16(weight) rounded to bf16, summed per token in bf16 in
+  assignment order from zero (its bf16 ``index_add_``; the reference leaves
+  the order of that sum to the device's atomics, so that order is parity
+  unpinned and covered by the float tolerance).
 * ``moe_layer_a8`` (A8 contract of ``fused_moe_mxint``, ``kernels/mxint.py:1435-1739``):
   A8 gate/up to a bf16 [A, 2*inter] tensor, fp32 SwiGLU, x route weight, bf16,
   act_quant_ref, A8 down to bf16 partials, fp32 ascending-expert-id sum, bf16.
@@ -268,3 +274,37 @@ def moe_layer_a8(x, ids, weights, bank_gu, bank_gu_s, bank_d, bank_d_s,
     if shared is not None:
         shared_part = run(shared[0], shared[1], shared[2], shared[3], x, np.ones(m, dtype=np.float32))
     return C.round_bf16(_combine(m, h, ids, partial, shared_part))
+
+
+# --------------------------------------------------------- MoE (skinny) -----
+def _bf(a):
+    return C.round_bf16(np.asarray(a, dtype=np.float32))
+
+
+def moe_layer_skinny(x, ids, weights, gu_p, gu_s, d_p, d_s):
+    """``fused_moe_skinny`` over KN banks: gu_p [E, H, I] + gu_s [E, H, 2I/32]
+    (gate columns then up columns), d_p [E, I, H/2] + d_s [E, I, H/32]
+    (numpy arrays or callables e -> array).  Returns bf16-valued [M, H]."""
+    get = (lambda b, e: b(e)) if callable(gu_p) else (lambda b, e: b[e])
+    x = np.asarray(x, dtype=np.float32)
+    ids = np.asarray(ids).reshape(x.shape[0], -1)
+    weights = np.asarray(weights, dtype=np.float32).reshape(ids.shape)
+    m, h = x.shape
+    contrib = {}
+    for e, rows in _expert_rows(ids).items():
+        ts = [t for t, _ in rows]
+        gu = L.mx_linear_kn_a16(x[ts], get(gu_p, e), get(gu_s, e))           # bf16 [r, 2I]
+        inter = gu.shape[1] // 2
+        gate, up = gu[:, :inter], gu[:, inter:]
+        sg = _bf(gate / (np.float32(1.0) + np.exp(-gate).astype(np.float32)))
+        z = _bf(sg * up)
+        yg = L.mx_linear_kn_a16(z, get(d_p, e), get(d_s, e))                 # bf16 [r, H]
+        for i, (t, s) in enumerate(rows):
+            contrib[(t, s)] = _bf(yg[i] * _bf(weights[t, s]))
+    out = np.zeros((m, h), dtype=np.float32)
+    for t in range(m):
+        acc = np.zeros(h, dtype=np.float32)
+        for s in range(ids.shape[1]):
+            acc = _bf(acc + contrib[(t, s)])
+        out[t] = acc
+    return out

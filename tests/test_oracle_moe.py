@@ -312,3 +312,43 @@ def test_router_logits_are_exact_dot_rounded_once():
         for j in range(5):
             exact = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x[t], w[j]))
             assert got[t, j] == np.float32(float(exact)), (t, j)
+
+
+# ---- fused_moe_skinny oracle pinned by a torch restatement ----------------
+def _t_kn_linear(x_bf16, packed, scale):
+    """x @ W with W [K, N] decoded from KN packed/scale (fp32 math, bf16 out),
+    kernels/skinny_fp4.py:50-110 (LUT, low nibble = even n, per-32-N scale)."""
+    p = torch.from_numpy(packed).long()
+    lut = torch.stack([_E2M1[p & 15], _E2M1[p >> 4]], dim=-1).reshape(p.shape[0], -1)
+    sw = torch.ldexp(torch.ones(scale.shape), torch.from_numpy(scale).int() - 127).repeat_interleave(32, dim=1)
+    return (x_bf16.double() @ (lut * sw).double()).float().to(torch.bfloat16)
+
+
+def test_moe_skinny_oracle_equals_torch_restatement():
+    """kernels/skinny_fp4.py:267-322 in torch bf16 ops: silu/multiply on bf16
+    tensors, y_g * weights (bf16), index_add_ into a bf16 zero tensor (the CPU
+    index_add_ adds in index order)."""
+    rng = np.random.default_rng(12)
+    e, h, inter, m, k = 4, 256, 128, 3, 2
+    q = lambda n, kk: C.quantize_mxfp4_ceil(C.round_bf16((rng.standard_normal((n, kk)) * 0.05).astype(np.float32)))
+    gu = [q(h, 2 * inter) for _ in range(e)]
+    dn = [q(inter, h) for _ in range(e)]
+    gp, gs = np.stack([a[0] for a in gu]), np.stack([a[1] for a in gu])
+    dp, ds = np.stack([a[0] for a in dn]), np.stack([a[1] for a in dn])
+    x = C.round_bf16((rng.standard_normal((m, h)) * 2).astype(np.float32))
+    ids = np.array([[2, 0], [1, 3], [3, 2]])
+    w = np.array([[0.6, 0.4], [0.3, 0.7], [0.55, 0.45]], dtype=np.float32)
+    ref = MO.moe_layer_skinny(x, ids, w, gp, gs, dp, ds)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    flat = ids.reshape(-1)
+    token_of = np.repeat(np.arange(m), k)
+    order = np.argsort(flat, kind="stable")
+    yg = torch.zeros(flat.size, h, dtype=torch.bfloat16)
+    for p in order:
+        g = _t_kn_linear(xt[token_of[p]:token_of[p] + 1], gp[flat[p]], gs[flat[p]])
+        z = F.silu(g[:, :inter]) * g[:, inter:]
+        yg[p] = _t_kn_linear(z, dp[flat[p]], ds[flat[p]])[0]
+    yg = yg * torch.from_numpy(w.reshape(-1)).to(torch.bfloat16)[:, None]
+    y = torch.zeros(m, h, dtype=torch.bfloat16)
+    y.index_add_(0, torch.from_numpy(token_of), yg)
+    np.testing.assert_array_equal(y.float().numpy(), ref)
