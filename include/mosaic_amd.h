@@ -141,6 +141,15 @@ int mosaic_fp8_block_gemm_ws(const uint8_t* a, const float* a_s, const uint8_t* 
                              int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* W8A16 linear with the in-GEMM weight decode of fp8_linear's fused kernel
+ * (bench/fp8_core.py:160-231): y [m, n] bf16 = sum over 128-K blocks of
+ * (x_kb . decode(W_kb)^T) * s[n/128, kb], x bf16 [m, k], W e4m3 [n, k]
+ * row-major, s f32 [ceil(n/128), k/128] (e8m0 scales passed as their fp32
+ * values), fp32 accumulation.  k % 128 == 0, m <= 80 (the reference takes its
+ * dequantize + library GEMM path above 80 rows). */
+int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m, int64_t n,
+                            int64_t k, void* stream);
+
 /* e4m3 [n, k] with one f32 scale per block_n x block_k block -> bf16 [n, k].
  * Replaces dequant_fp8 (runtime/fp8.py:52-64), dsa.dequant_weight
  * (model/dsa.py:72-78) and fp8_core's dequant_kernel (bench/fp8_core.py:60-91). */

@@ -1,0 +1,152 @@
+// W8A16 linear: y [m, n] = x [m, k] bf16 . decode(W)^T with W e4m3 [n, k]
+// (row-major, the checkpoint layout) and one fp32 scale per 128 x 128 block,
+// s [ceil(n/128), k/128]: the fused in-GEMM decode of fp8_linear
+// (bench/fp8_core.py:160-231): per 128-K block the fp32 product of x and the
+// unscaled decoded weight is multiplied by the block scale and added to the
+// fp32 accumulator (acc += dot(x, decode(w)) * s), then one bf16 rounding.
+//
+// Decode-shaped kernel (16 tokens per launch row): MFMA roles transposed, so a
+// lane (c = l%16, q = l/16) holds weight row n0 + 16t + c and token m0 + c of
+// x; of every 128-byte K block it holds weight bytes [16q, 16q + 16) and
+// [64 + 16q, +16), which v_cvt_scalef32_pk_bf16_fp8 turns into exact bf16
+// (unit scale), and the x elements at the same 32 K indices, as four
+// K-steps of v_mfma_f32_16x16x32_bf16 (the sum over K does not care which K
+// a lane holds as long as both operands agree).  A workgroup owns 16 T
+// columns; its KS waves split the K blocks and meet in LDS.  Each wave streams
+// its blocks through a register ring of D entries issued D blocks ahead with
+// buffer loads (rows past n / m read zeros; entries past the wave's range are
+// scaled by 0), as the FP8 x FP8 decode kernel does.
+#include "common.h"
+#include "../../include/mosaic_amd.h"
+
+namespace mosaic {
+namespace {
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w8_rsrc(const void* base, int64_t records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)records, 0x00020000);
+}
+
+// 8 e4m3 bytes (two dwords) -> 8 exact bf16
+__device__ __forceinline__ bf16x8_t e4m3x8_bf16(uint32_t w0, uint32_t w1) {
+  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  return bf16x8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <int T, int KS, int D>
+__global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __restrict__ X,
+                                                             const uint8_t* __restrict__ W,
+                                                             const float* __restrict__ Ws, uint16_t* __restrict__ Y,
+                                                             int M, int N, int K) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16;
+  const int nkb = K / 128;
+  const int kb0 = nkb * ks / KS, nb = nkb * (ks + 1) / KS - kb0;
+  const __amdgpu_buffer_rsrc_t rw = w8_rsrc(W + (int64_t)n0 * K, (int64_t)min(N - n0, 16 * T) * K);
+  const __amdgpu_buffer_rsrc_t rx = w8_rsrc(X + (int64_t)m0 * K, (int64_t)min(M - m0, 16) * K * 2);
+  const uint32_t x_row = (uint32_t)(c * K * 2) + 32u * q;  // byte offset of x[m0 + c][16 q]
+  const float* s_row[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) s_row[t] = Ws + (int64_t)(min(n0 + 16 * t, N - 1) / 128) * nkb;
+  u32x4_t rwv[D][T][2], rxv[D][4];
+  float rs[D][T];
+  auto load = [&](int s, int i) {
+    const int kb = kb0 + (i < nb ? i : nb - 1);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t off = (uint32_t)((16 * t + c) * K + kb * 128 + 16 * q);
+      rwv[s][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, 0);
+      rwv[s][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(off + 64), 0, 0);
+      rs[s][t] = s_row[t][kb];
+    }
+    const int xo = (int)(x_row + kb * 256);
+    rxv[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+    rxv[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16, 0, 0);
+    rxv[s][2] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 128, 0, 0);
+    rxv[s][3] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 144, 0, 0);
+  };
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int s, int i) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t& wv = rwv[s][t][j >> 1];
+        const bf16x8_t wb = e4m3x8_bf16(wv[2 * (j & 1)], wv[2 * (j & 1) + 1]);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, __builtin_bit_cast(bf16x8_t, rxv[s][j]), d, 0, 0, 0);
+      }
+      const float sc = i < nb ? rs[s][t] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(d[r], sc, acc[t][r]);
+    }
+  };
+  const int nchunks = (nb + D - 1) / D;
+  if (nb > 0) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) load(s, s);
+    for (int ch = 0; ch + 1 < nchunks; ++ch) {
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        compute(s, ch * D + s);
+        load(s, ch * D + s + D);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s) compute(s, (nchunks - 1) * D + s);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T && m0 + c < M) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+    // lane (c, q): y[m0 + c][n .. n + 3], n = n0 + 16 t + 4 q
+    const int n = n0 + 16 * t + 4 * q;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) Y[(int64_t)(m0 + c) * N + n + r] = f32_bf16(v[r]);
+  }
+}
+
+template <int KS>
+void launch_w8a16(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m, int64_t n, int64_t k,
+                  hipStream_t st) {
+  const int nb = (int)(k / 128 / KS);
+  const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16));
+  if (nb % 4 == 0 || nb >= 8)
+    hipLaunchKernelGGL((w8a16_gemv_kernel<1, KS, 4>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+  else
+    hipLaunchKernelGGL((w8a16_gemv_kernel<1, KS, 2>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+}
+
+}  // namespace
+}  // namespace mosaic
+
+using namespace mosaic;
+
+extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m,
+                                       int64_t n, int64_t k, void* stream) {
+  MOSAIC_CHECK_ARG(x && w && s && y, "fp8_w8a16_linear: null pointer");
+  MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "fp8_w8a16_linear: K=%lld must be a positive multiple of 128", (long long)k);
+  MOSAIC_CHECK_ARG(n > 0 && m >= 0 && m <= 80, "fp8_w8a16_linear: m=%lld (0..80) n=%lld", (long long)m, (long long)n);
+  MOSAIC_CHECK_ARG(n * k < (1ll << 31) && m * k * 2 < (1ll << 31), "fp8_w8a16_linear: operands beyond 2 GiB");
+  if (m == 0) return kOk;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t tiles = (n + 15) / 16 * ((m + 15) / 16);
+  if (tiles <= 256 && (k / 128) >= 16)
+    launch_w8a16<8>(x, w, s, y, m, n, k, st);
+  else if (tiles <= 1152 && (k / 128) >= 8)
+    launch_w8a16<4>(x, w, s, y, m, n, k, st);
+  else
+    launch_w8a16<2>(x, w, s, y, m, n, k, st);
+  MOSAIC_RETURN_LAUNCH("fp8_w8a16_linear");
+}

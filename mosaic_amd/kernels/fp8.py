@@ -97,11 +97,18 @@ def dequant_fp8(weight: torch.Tensor, scale: torch.Tensor, block: int = 128) -> 
 
 
 def fp8_linear(x: torch.Tensor, w_fp8: torch.Tensor, s: torch.Tensor, out: torch.Tensor | None = None):
-    """W8A16 ``F.linear(x, decode(w, s))`` (``bench/fp8_core.py:198-231``): the
-    weight is decoded once into a bf16 scratch and multiplied by the library
-    GEMM, the reference's own path for M > 80."""
-    w = dequant_fp8(w_fp8, s)
-    y = torch.nn.functional.linear(ops._bf16(x, "x"), w)
+    """W8A16 ``F.linear(x, decode(w, s))`` (``bench/fp8_core.py:198-231``) with the
+    reference's width dispatch: up to 80 rows the e4m3 weight is decoded inside
+    the GEMM (``mosaic_fp8_w8a16_linear``: per 128-K block, x . decode(w)^T
+    times the block scale added to an fp32 accumulator); above 80 rows it is
+    dequantized once by the HIP kernel and multiplied by the library GEMM, as
+    the reference does (dequant + cuBLAS there, hipBLASLt here)."""
+    x = ops._bf16(x, "x")
+    m = x.shape[0]
+    if m <= ops.W8A16_MAX_M:
+        y = ops.fp8_w8a16_linear(x, w_fp8, _scales_f32(s))
+    else:
+        y = torch.nn.functional.linear(x, dequant_fp8(w_fp8, s))
     if out is not None:
         out.copy_(y)
         return out

@@ -307,6 +307,30 @@ def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: tor
     return c
 
 
+W8A16_MAX_M = 80  # rows up to which fp8_linear decodes in the GEMM (bench/fp8_core.py:210-221)
+
+
+def fp8_w8a16_linear(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """y [M, N] bf16 = x [M, K] bf16 . (e4m3 W [N, K] x per-128x128 block scales s)^T,
+    the weight decoded inside the GEMM (M <= 80)."""
+    x = _bf16(x, "x")
+    w = _u8(w, "w_fp8")
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError(f"x {tuple(x.shape)} and w {tuple(w.shape)} must be [M, K] and [N, K]")
+    m, k = x.shape
+    n = w.shape[0]
+    if k % 128:
+        raise ValueError(f"K={k} must be a multiple of 128")
+    if m > W8A16_MAX_M:
+        raise ValueError(f"fp8_w8a16_linear decodes in the GEMM for M <= {W8A16_MAX_M}, got {m}")
+    s = _cuda(s, "s").to(torch.float32).contiguous()
+    if tuple(s.shape) != ((n + 127) // 128, k // 128):
+        raise ValueError(f"scale shape {tuple(s.shape)} != ({(n + 127) // 128}, {k // 128})")
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    _lib.call("mosaic_fp8_w8a16_linear", _ptr(x), _ptr(w), _ptr(s), _ptr(y), m, n, k, _stream())
+    return y
+
+
 def fp8_block_dequant(w: torch.Tensor, s: torch.Tensor, block: tuple[int, int] = (128, 128)) -> torch.Tensor:
     """e4m3 [N, K] + f32 scales [ceil(N/bn), ceil(K/bk)] -> bf16 [N, K]."""
     w = _u8(w, "w")

@@ -18,6 +18,9 @@
   (``.mosaicvm/source/inference_kernel.py:203-273``): per 128-K block the block
   product is scaled by a_s[m, kb] * b_s[n // 128, kb] and added to an fp32
   accumulator.
+* ``fp8_w8a16_linear`` (A18, W8A16): the fused decode kernel of ``fp8_linear``
+  (``bench/fp8_core.py:160-194``): per 128-K block, acc += dot(x, decode(w)) * s
+  in fp32 (x bf16, w e4m3 decoded without its scale), one bf16 rounding.
 * ``quantize_fp8_weight_128`` (config 3 weights): per 128x128 block s =
   amax / 448 (``.mosaicvm/source/hubkernel_act_quant.py:27-35`` restated on
   weight blocks), codes = e4m3(w / s).
@@ -161,3 +164,17 @@ def a8_integer_exact(codes: np.ndarray, sa: np.ndarray, packed: np.ndarray,
         part = (part * sw[None, :, gi]).astype(np.float32)
         acc = (acc + part).astype(np.float32)
     return acc
+
+
+def fp8_w8a16_linear(x: np.ndarray, w_codes: np.ndarray, s: np.ndarray, block: int = 128) -> np.ndarray:
+    """x [M, K] (bf16-valued), e4m3 codes [N, K], fp32 scales [ceil(N/128), K/128] -> bf16 [M, N]."""
+    x = np.asarray(x, dtype=np.float64)
+    wd = C.e4m3_decode(w_codes).astype(np.float64)
+    n, k = wd.shape
+    acc = np.zeros((x.shape[0], n), dtype=np.float32)
+    rows = np.arange(n) // block
+    for kb in range(k // block):
+        sl = slice(kb * block, (kb + 1) * block)
+        d = (x[:, sl] @ wd[:, sl].T).astype(np.float32)
+        acc = (acc + (d * s[rows, kb][None, :]).astype(np.float32)).astype(np.float32)
+    return C.round_bf16(acc)

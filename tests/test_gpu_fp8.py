@@ -53,3 +53,27 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
         bound = 2.0 * (k // 128 + 128) * 2.0 ** -24 * abs_sum + 1e-30
         viol = np.abs(got - ref) - bound
         assert viol.max() <= 0, f"f32 reassociation bound exceeded by {viol.max()} (max scaled err {err.max()})"
+
+
+@pytest.mark.parametrize("m,n,k,e8m0", [(1, 1536, 7168, False), (1, 18432, 7168, True), (16, 576, 7168, False),
+                                        (37, 200, 1024, True), (80, 4096, 512, False), (3, 24576, 1536, True),
+                                        (5, 16, 128, False)])
+def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
+    """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
+    identical codes and scales: bar 2e-2 * max(1, |ref|)."""
+    from mosaic_amd.kernels import fp8
+    rng = np.random.default_rng(m + n + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    bq, bs = L.quantize_fp8_weight_128(w)
+    if e8m0:  # power-of-two block scales, passed as float8_e8m0fnu like the reference's checkpoints
+        e = np.clip(np.ceil(np.log2(bs)), -127, 127).astype(np.int32)
+        bs = np.exp2(e).astype(np.float32)
+        bq = C.e4m3_encode(np.clip(w / np.repeat(np.repeat(bs, 128, 0), 128, 1)[:n, :k], -448, 448))
+        s_dev = torch.from_numpy((e + 127).astype(np.uint8)).to(dev).view(torch.float8_e8m0fnu)
+    else:
+        s_dev = torch.from_numpy(bs).to(dev)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16)
+    y = fp8.fp8_linear(x.to(dev), torch.from_numpy(bq).to(dev).view(torch.float8_e4m3fn), s_dev)
+    ref = L.fp8_w8a16_linear(x.float().numpy(), bq, bs)
+    err = np.abs(y.float().cpu().numpy() - ref) / np.maximum(1.0, np.abs(ref))
+    assert err.max() <= 2e-2, err.max()

@@ -88,3 +88,21 @@ def test_fp8_block_gemm_vs_dequant_matmul():
     deq = C.e4m3_decode(bq) * np.repeat(np.repeat(bs, 128, 0)[:n], 128, 1)
     assert np.max(np.abs(deq - w)) <= np.max(np.abs(w)) * 2 ** -4
     assert np.float32(np.max(np.abs(w[:128, :128])) / 448) == bs[0, 0]
+
+
+def test_fp8_w8a16_oracle_vs_dequant_matmul_and_onehot():
+    """The block-wise W8A16 oracle (acc += dot(x, decode(w)) * s) equals the
+    float64 dequant-then-matmul within fp32 reassociation, and a one-hot x picks
+    the dequantized column exactly."""
+    rng = np.random.default_rng(21)
+    n, k = 192, 384
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    bq, bs = L.quantize_fp8_weight_128(w)
+    wd = C.e4m3_decode(bq).astype(np.float64) * np.repeat(np.repeat(bs, 128, 0), 128, 1)[:n, :k]
+    x = C.round_bf16(rng.standard_normal((3, k)).astype(np.float32))
+    got = L.fp8_w8a16_linear(x, bq, bs)
+    ref = C.round_bf16((x.astype(np.float64) @ wd.T).astype(np.float32))
+    assert np.max(np.abs(got - ref) / np.maximum(1.0, np.abs(ref))) <= 2 ** -7
+    onehot = np.zeros((1, k), dtype=np.float32)
+    onehot[0, 200] = 1.0
+    np.testing.assert_array_equal(L.fp8_w8a16_linear(onehot, bq, bs)[0], C.round_bf16(wd[:, 200].astype(np.float32)))
