@@ -61,8 +61,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1, 3, 4, 5")
     ap.add_argument("--configs", default="",
-                    help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config4_moe_prefill, "
-                         "config5_dsa to run (default: all)")
+                    help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config3_mxfp4_gemm, "
+                         "config4_moe_prefill, config5_dsa to run (default: all)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the line is printed, copy a buffer of this many MiB device to device three times "
                          "(a plain copy of known size that scales FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -244,6 +244,39 @@ def config3_fp8(torch, ops):
                                       "mfma_frac": round(fl / us / 1e6 / 5000.0, 4),
                                       "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
         del bqs, bq0
+    return out
+
+
+def config3_mxfp4(torch, ops):
+    """The config-3 shapes with MXFP4 weights (A8: 1x128 power-of-two e4m3
+    activations, ceil-recipe MXFP4 weights N(0, 0.02)), the dense fp4_gemm of
+    .mosaicvm/source/inference_kernel.py:441-536 at M in {128, 4096}; weight copies
+    rotate past the MALL as in config 3.  Peaks: 5.0 PFLOP/s (the fp8 rate of the
+    f8f6f4 MFMA) and 10.1 (the fp4 rate)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(15)
+    out = {}
+    for n, k in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (18432, 7168)]:
+        w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        p, sc = ops.mx_quantize(w, "ceil")
+        del w
+        wbytes = n * (k // 2 + k // 32)
+        nrot = (512 << 20) // wbytes + 1
+        ws = [ops.mxt16_prepack(p.clone(), sc.clone()) for _ in range(nrot)]
+        for m in (128, 4096):
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            xq, sa = ops.act_quant(x, 128, "pow2")
+            it = iter(range(10 ** 9))
+            us = _graph_time(torch, lambda: ops.mxt16_linear_a8(None, ws[next(it) % nrot], prequant=(xq, sa)), nrot,
+                             reps=3 if m < 4096 else 1)
+            fl = 2 * m * n * k
+            byts = m * k + 4 * m * (k // 128) + wbytes + 2 * m * n
+            out[f"m{m}_n{n}_k{k}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                                      "mfma_frac_fp8_rate": round(fl / us / 1e6 / 5000.0, 4),
+                                      "mfma_frac_fp4_rate": round(fl / us / 1e6 / 10100.0, 4),
+                                      "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del ws, p, sc
     return out
 
 
@@ -531,6 +564,7 @@ def main():
     if not args.no_configs:
         for name, fn in [("config1_linear_m1", lambda: config1_linear(torch, ops)),
                          ("config3_fp8_gemm", lambda: config3_fp8(torch, ops)),
+                         ("config3_mxfp4_gemm", lambda: config3_mxfp4(torch, ops)),
                          ("config4_moe_prefill", lambda: config4_prefill(torch, ops, banks[0])),
                          ("config5_dsa", lambda: config5_dsa(torch, ops))]:
             if args.configs and name not in args.configs.split(","):

@@ -734,13 +734,23 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
     const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
     const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, uint16_t* __restrict__ yb, int H,
-    int I, int E) {
+    int I, int E, int m_dense) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
   __shared__ __attribute__((aligned(16))) uint8_t chunk[2 * kPfChunk];
   int colt, tile;
   pf_coords(blockIdx.x, H / 256, colt, tile);
-  if (tile >= n_tiles[0]) return;
-  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  int e, rows, p0;
+  if (tile_expert) {  // grouped: the MoE tile list
+    if (tile >= n_tiles[0]) return;
+    e = tile_expert[tile];
+    rows = tile_rows[tile];
+    p0 = tile_p0[tile];
+  } else {  // dense A8 GEMM: 256-row tiles of the m_dense rows, one weight matrix (E = 1)
+    p0 = tile * 256;
+    if (p0 >= m_dense) return;
+    rows = min(256, m_dense - p0);
+    e = 0;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 15, q = lane >> 4;
   const int h0 = colt * 256;
   const int ns = I / 128, ns4 = (ns + 3) / 4;
@@ -842,6 +852,15 @@ extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const 
                    "mxt16_linear_a8: shape out of range");
   if (m == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
+  if (m >= 64 && n % 256 == 0 && k % 512 == 0 && m < (1 << 30)) {
+    // prefill-sized: 256-row tiles through the staged scaled-MFMA kernel of the
+    // MoE down projection (one weight matrix, no tile list)
+    const int64_t tiles8 = ((m + 255) / 256 + 7) / 8 * 8;
+    hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(n / 256 * tiles8)), dim3(kPfWaves * 64), 0, st, xq,
+                       sa, packed_t, scale_t, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, y, (int)n, (int)k,
+                       1, (int)m);
+    MOSAIC_RETURN_LAUNCH("mxt16_linear_a8_prefill");
+  }
   const int64_t mt = (m + 15) / 16;
   if (((n + 63) / 64) * mt * 8 >= 4096)
     launch_linear_a8<4, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
@@ -914,7 +933,7 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
     mark(4);  // the z requant is fused into the gate/up epilogue
     hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows, w.tile_p0,
-                       w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts);
+                       w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts, 0);
     MOSAIC_LAUNCH_CHECK("moe_a8_down_prefill");
     mark(5);
     hipLaunchKernelGGL(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 8 + 127) / 128), (unsigned)m), dim3(128),

@@ -427,3 +427,18 @@ def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
     ref = MO.moe_layer_a8(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds, swiglu_limit=limit,
                           shared=None if sh is None else tuple(t[0] for t in sh))
     assert_close(y.float().cpu().numpy(), ref, what="moe a8")
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 256, 512), (257, 512, 1024), (1024, 512, 2048), (300, 7168, 512),
+                                   (64, 1536, 1536), (100, 320, 1024)])
+def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
+    """Dense A8 MXFP4 GEMM at prefill sizes (fp4_gemm, .mosaicvm/source/inference_kernel.py:441-536):
+    256-row tiles through the staged scaled-MFMA kernel when N % 256 == 0 and
+    K % 512 == 0 (the last case falls back to the 16-row kernel)."""
+    ops = _ops()
+    rng = np.random.default_rng(m + n + k + 7)
+    p, s = _quant_weights(rng, n, k)
+    x = C.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    y = ops.mxt16_linear_a8(T(x).to(torch.bfloat16), ops.mxt16_prepack(T(p), T(s)))
+    assert_close(y.float().cpu().numpy(), L.mx_linear_a8(x, p, s), what=f"a8 prefill {m}x{n}x{k}")
