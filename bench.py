@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--configs", default="",
                     help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config3_mxfp4_gemm, "
                          "config4_moe_prefill, config5_dsa to run (default: all)")
+    ap.add_argument("--no-headline", action="store_true",
+                    help="skip the decode layer (one bank is still built for config 4); for profiling the configs")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the line is printed, copy a buffer of this many MiB device to device three times "
                          "(a plain copy of known size that scales FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -538,6 +540,14 @@ def _stage_view(m: int, st: dict) -> dict:
             "note": "events recorded by the two dispatches themselves; M=1 has no separate layout or combine stage"}
 
 
+def _config_fns(torch, ops, banks):
+    return [("config1_linear_m1", lambda: config1_linear(torch, ops)),
+            ("config3_fp8_gemm", lambda: config3_fp8(torch, ops)),
+            ("config3_mxfp4_gemm", lambda: config3_mxfp4(torch, ops)),
+            ("config4_moe_prefill", lambda: config4_prefill(torch, ops, banks[0])),
+            ("config5_dsa", lambda: config5_dsa(torch, ops))]
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -551,7 +561,19 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    banks = build_banks(torch, ops, n_banks=N_BANKS)
+    need_bank = not args.no_headline or (not args.no_configs and (
+        not args.configs or "config4_moe_prefill" in args.configs.split(",")))
+    banks = build_banks(torch, ops, n_banks=1 if args.no_headline else N_BANKS) if need_bank else []
+    if args.no_headline:
+        configs = {}
+        if not args.no_configs:
+            for name, fn in _config_fns(torch, ops, banks):
+                if args.configs and name not in args.configs.split(","):
+                    continue
+                print(f"bench.py: {name}", file=sys.stderr, flush=True)
+                configs[name] = fn()
+        print(json.dumps({"metric": METRIC, "profiling_run": True, "configs": configs}), flush=True)
+        return
     main_r = run_m(torch, ops, banks, args.m, args.steps, args.warmup, seed=0)
     sweep = {}
     for mv in [int(v) for v in args.sweep.split(",") if v.strip()]:
@@ -562,11 +584,7 @@ def main():
             sweep[str(mv)]["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     configs = {}
     if not args.no_configs:
-        for name, fn in [("config1_linear_m1", lambda: config1_linear(torch, ops)),
-                         ("config3_fp8_gemm", lambda: config3_fp8(torch, ops)),
-                         ("config3_mxfp4_gemm", lambda: config3_mxfp4(torch, ops)),
-                         ("config4_moe_prefill", lambda: config4_prefill(torch, ops, banks[0])),
-                         ("config5_dsa", lambda: config5_dsa(torch, ops))]:
+        for name, fn in _config_fns(torch, ops, banks):
             if args.configs and name not in args.configs.split(","):
                 continue
             print(f"bench.py: {name}", file=sys.stderr, flush=True)

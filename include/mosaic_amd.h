@@ -307,6 +307,18 @@ int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const uint8_t* k
                             const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h, int64_t d, int64_t l,
                             int64_t topk, int32_t offset, void* workspace, size_t workspace_bytes, void* stream);
 
+/* mosaic_dsa_indexer_topk for `rows` query rows that share key caches in
+ * groups: query row r scores k [r / rows_per_k] (k [rows / rows_per_k, l, d],
+ * k_s [rows / rows_per_k, l]) with its own length lengths[r] -- the causal
+ * prefill of Indexer.forward (.mosaicvm/source/inference_model.py:430-437;
+ * mosaicvm/model/dsa_layers.py:309-321), where every position of a sequence
+ * scores the same compressed cache up to its own bound.  The workspace is
+ * mosaic_dsa_indexer_workspace_bytes(rows, l). */
+int mosaic_dsa_indexer_topk_shared(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
+                                   const float* w, const int32_t* lengths, int32_t* idx_out, int64_t rows, int64_t h,
+                                   int64_t d, int64_t l, int64_t rows_per_k, int64_t topk, int32_t offset,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* The canonical indexer scores themselves, scores [b, l] f32 (the index_score
  * tensor of Indexer.forward, .mosaicvm/source/inference_model.py:424-425). */
 int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,

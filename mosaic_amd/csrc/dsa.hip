@@ -155,7 +155,7 @@ template <int HT, int U, int D>
 __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ qs, const uint8_t* __restrict__ k,
     const float* __restrict__ ks, const float* __restrict__ w, const int32_t* __restrict__ lengths,
-    float* __restrict__ lo, float* __restrict__ hi, uint32_t* __restrict__ hist1, int64_t L) {
+    float* __restrict__ lo, float* __restrict__ hi, uint32_t* __restrict__ hist1, int64_t L, int kdiv) {
   constexpr int H = HT * 16;
   constexpr int GT = 16 * U;  // tokens per group
   __shared__ uint32_t lh[kHistBins];
@@ -171,8 +171,8 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   const int64_t n_groups = (n + GT - 1) / GT;
   const int64_t nw = (int64_t)gridDim.x * 4, wid = (int64_t)blockIdx.x * 4 + wv;
   const int64_t iters = wid < n_groups ? (n_groups - 1 - wid) / nw + 1 : 0;
-  const uint8_t* kb = k + (int64_t)b * L * kIdxD;
-  const float* ksb = ks + (int64_t)b * L;
+  const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;  // kdiv query rows share one key cache
+  const float* ksb = ks + (int64_t)(b / kdiv) * L;
   float* lob = lo + (int64_t)b * L;
   float* hib = hi + (int64_t)b * L;
   i32x8_t kr[D][U];
@@ -372,7 +372,7 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ qs, const uint8_t* __restrict__ k,
     const float* __restrict__ ks, const float* __restrict__ w, const int32_t* __restrict__ lengths,
     const float* __restrict__ hi, const uint32_t* __restrict__ hist1, uint64_t* __restrict__ keys,
-    uint32_t* __restrict__ wg_counts, float* __restrict__ scores, int64_t L, int topk, int range) {
+    uint32_t* __restrict__ wg_counts, float* __restrict__ scores, int64_t L, int topk, int range, int kdiv) {
   constexpr int H = HT * 16;
   __shared__ uint32_t lh[kHistBins];
   __shared__ uint32_t sh[2];
@@ -452,8 +452,8 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
   const int nb = (C + 15) / 16;
   const int my_batches = nb > wv ? (nb - 1 - wv) / 4 + 1 : 0;
   if (my_batches == 0) return;
-  const uint8_t* kb = k + (int64_t)b * L * kIdxD;
-  const float* ksb = ks + (int64_t)b * L;
+  const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;
+  const float* ksb = ks + (int64_t)(b / kdiv) * L;
   struct Batch {
     u32x4_t x[2];
     float ks;
@@ -1156,23 +1156,23 @@ static void bound_shape(int64_t b, int64_t l, int& gx, int& depth) {
 template <int HT, int D>
 static void launch_bound_d(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t l,
-                           int gx, hipStream_t st) {
+                           int gx, int kdiv, hipStream_t st) {
   hipLaunchKernelGGL((dsa_index_bound_kernel<HT, kBoundU, D>), dim3((unsigned)gx, (unsigned)b), dim3(256), 0, st, q,
-                     qs, k, ks, w, lengths, lo, hi, hist1, l);
+                     qs, k, ks, w, lengths, lo, hi, hist1, l, kdiv);
 }
 
 template <int HT>
 static void launch_bound(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                          const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t l,
-                         hipStream_t st) {
+                         int kdiv, hipStream_t st) {
   int gx, depth;
   bound_shape(b, l, gx, depth);
   if (depth == 4)
-    launch_bound_d<HT, 4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, st);
+    launch_bound_d<HT, 4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, st);
   else if (depth == 2)
-    launch_bound_d<HT, 2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, st);
+    launch_bound_d<HT, 2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, st);
   else
-    launch_bound_d<HT, 1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, st);
+    launch_bound_d<HT, 1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, st);
 }
 
 static int check_indexer(const void* q, const void* qs, const void* k, const void* ks, const void* w, int64_t b,
@@ -1186,12 +1186,12 @@ static int check_indexer(const void* q, const void* qs, const void* k, const voi
 
 static void dispatch_bound(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t h,
-                           int64_t l, hipStream_t st) {
+                           int64_t l, int kdiv, hipStream_t st) {
   switch (h / 16) {
-    case 1: launch_bound<1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, st); break;
-    case 2: launch_bound<2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, st); break;
-    case 3: launch_bound<3>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, st); break;
-    default: launch_bound<4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, st); break;
+    case 1: launch_bound<1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
+    case 2: launch_bound<2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
+    case 3: launch_bound<3>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
+    default: launch_bound<4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
   }
 }
 
@@ -1209,25 +1209,25 @@ static int rescore_range(int64_t b, int64_t l) {
 static void launch_rescore(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, const float* hi, const uint32_t* hist1, uint64_t* keys,
                            uint32_t* wg_counts, float* scores, int64_t b, int64_t h, int64_t l, int topk,
-                           hipStream_t st) {
+                           int kdiv, hipStream_t st) {
   const int range = rescore_range(b, l);
   const dim3 grid((unsigned)((l + range - 1) / range), (unsigned)b);
   switch (h / 16) {
     case 1:
       hipLaunchKernelGGL(dsa_rescore_kernel<1>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range);
+                         wg_counts, scores, l, topk, range, kdiv);
       break;
     case 2:
       hipLaunchKernelGGL(dsa_rescore_kernel<2>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range);
+                         wg_counts, scores, l, topk, range, kdiv);
       break;
     case 3:
       hipLaunchKernelGGL(dsa_rescore_kernel<3>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range);
+                         wg_counts, scores, l, topk, range, kdiv);
       break;
     default:
       hipLaunchKernelGGL(dsa_rescore_kernel<4>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range);
+                         wg_counts, scores, l, topk, range, kdiv);
       break;
   }
 }
@@ -1265,16 +1265,19 @@ extern "C" size_t mosaic_dsa_indexer_workspace_bytes(int64_t b, int64_t l) {
   return indexer_ws(b, l, nullptr, nullptr);
 }
 
-extern "C" int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
-                                       const float* w, const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h,
-                                       int64_t d, int64_t l, int64_t topk, int32_t offset, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
+namespace mosaic {
+static int indexer_topk_impl(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
+                             const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h, int64_t d, int64_t l,
+                             int64_t topk, int32_t offset, int64_t kdiv, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   int rc = check_indexer(q, q_s, k, k_s, w, b, h, d, l);
   if (rc) return rc;
   MOSAIC_CHECK_ARG(idx_out, "dsa_indexer_topk: null output");
   MOSAIC_CHECK_ARG(topk >= 1 && topk <= kMaxTopk, "dsa_indexer_topk: topk %lld (1..%d)", (long long)topk, kMaxTopk);
   MOSAIC_CHECK_ARG(l <= (int64_t)kRsMaxWgs * kRsMaxRange, "dsa_indexer_topk: l %lld (at most %lld)", (long long)l,
                    (long long)kRsMaxWgs * kRsMaxRange);
+  MOSAIC_CHECK_ARG(kdiv >= 1 && b % kdiv == 0, "dsa_indexer_topk: %lld query rows do not split into groups of %lld",
+                   (long long)b, (long long)kdiv);
   const size_t need = indexer_ws(b, l, nullptr, nullptr);
   MOSAIC_CHECK_ARG(workspace && workspace_bytes >= need, "dsa_indexer_topk: workspace %zu bytes < %zu",
                    workspace_bytes, need);
@@ -1285,13 +1288,30 @@ extern "C" int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const
   hipLaunchKernelGGL(dsa_zero_kernel, dim3((unsigned)((ws.zero_words + 255) / 256)), dim3(256), 0, st, ws.hist1,
                      (int64_t)ws.zero_words);
   if (l > 0) {
-    dispatch_bound(q, q_s, k, k_s, w, lengths, ws.lo, ws.hi, ws.hist1, b, h, l, st);
+    dispatch_bound(q, q_s, k, k_s, w, lengths, ws.lo, ws.hi, ws.hist1, b, h, l, (int)kdiv, st);
     launch_rescore(q, q_s, k, k_s, w, lengths, ws.hi, ws.hist1, ws.keys, ws.wg_counts, nullptr, b, h, l, (int)topk,
-                   st);
+                   (int)kdiv, st);
   }
   hipLaunchKernelGGL(dsa_finish_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.wg_counts, lengths, l,
                      rescore_range(b, l), (int)topk, (int)offset, idx_out);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_topk");
+}
+}  // namespace mosaic
+
+extern "C" int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
+                                       const float* w, const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h,
+                                       int64_t d, int64_t l, int64_t topk, int32_t offset, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  return indexer_topk_impl(q, q_s, k, k_s, w, lengths, idx_out, b, h, d, l, topk, offset, 1, workspace,
+                           workspace_bytes, stream);
+}
+
+extern "C" int mosaic_dsa_indexer_topk_shared(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
+                                              const float* w, const int32_t* lengths, int32_t* idx_out, int64_t rows,
+                                              int64_t h, int64_t d, int64_t l, int64_t rows_per_k, int64_t topk,
+                                              int32_t offset, void* workspace, size_t workspace_bytes, void* stream) {
+  return indexer_topk_impl(q, q_s, k, k_s, w, lengths, idx_out, rows, h, d, l, topk, offset, rows_per_k, workspace,
+                           workspace_bytes, stream);
 }
 
 extern "C" int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
@@ -1301,7 +1321,7 @@ extern "C" int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, con
   if (rc) return rc;
   MOSAIC_CHECK_ARG(scores, "dsa_indexer_scores: null output");
   if (b == 0 || l == 0) return kOk;
-  launch_rescore(q, q_s, k, k_s, w, nullptr, nullptr, nullptr, nullptr, nullptr, scores, b, h, l, 0,
+  launch_rescore(q, q_s, k, k_s, w, nullptr, nullptr, nullptr, nullptr, nullptr, scores, b, h, l, 0, 1,
                  (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_scores");
 }
@@ -1313,7 +1333,7 @@ extern "C" int mosaic_dsa_indexer_bounds(const uint8_t* q, const float* q_s, con
   if (rc) return rc;
   MOSAIC_CHECK_ARG(lo && hi, "dsa_indexer_bounds: null output");
   if (b == 0 || l == 0) return kOk;
-  dispatch_bound(q, q_s, k, k_s, w, nullptr, lo, hi, nullptr, b, h, l, (hipStream_t)stream);
+  dispatch_bound(q, q_s, k, k_s, w, nullptr, lo, hi, nullptr, b, h, l, 1, (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_bounds");
 }
 

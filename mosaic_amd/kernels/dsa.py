@@ -11,6 +11,11 @@
 * ``indexer_topk`` / ``indexer_scores`` -- the FP8 indexer of ``Indexer.forward``
   (``.mosaicvm/source/inference_model.py:408-439``) from quantized q/k.
 * ``mla_decode_fp8`` -- MLA decode over an FP8 latent cache (BASELINE format).
+* ``Indexer`` -- the scoring and top-k of ``Indexer.forward``
+  (``.mosaicvm/source/inference_model.py:408-439``, ``mosaicvm/model/dsa_layers.py:281-321``)
+  from already projected FP8 q and the FP8 compressed key cache: the causal
+  prefill mask at ``start_pos == 0``, ``min(index_topk, end_pos // ratio)``
+  picks, ``-1`` for masked picks, ``+ offset`` otherwise.
 """
 from __future__ import annotations
 
@@ -73,3 +78,40 @@ def indexer_scores(q_fp8, q_scale, k_fp8, k_scale, weights):
 
 def mla_decode_fp8(q, kv_latent, kv_scale, kv_rope, topk_idxs, softmax_scale, attn_sink=None):
     return ops.mla_sparse_decode(q, kv_latent, kv_scale, kv_rope, topk_idxs, softmax_scale, attn_sink)
+
+
+class Indexer(torch.nn.Module):
+    """Scoring + top-k stage of ``Indexer.forward`` on FP8 operands.
+
+    ``forward(q_fp8, q_scale, weights, k_cache, k_scale, start_pos, offset)``:
+    q_fp8 [bsz, seqlen, H, 128] e4m3 with q_scale [bsz, seqlen, H] f32 (the
+    rotated, projected queries), weights [bsz, seqlen, H] f32 (weights_proj(x)
+    * softmax_scale * H^-0.5), k_cache [bsz, >= end_pos // ratio, 128] e4m3 with
+    k_scale [bsz, ...] f32 -> topk_idxs [bsz, seqlen, min(index_topk, end_pos //
+    ratio)] int32.  Score = sum over heads of w_h ReLU(q_h . k_t * q_s * k_s) in
+    the canonical order; ties go to the lower index (the reference leaves them
+    to torch.topk)."""
+
+    def __init__(self, index_topk: int = 2048, compress_ratio: int = 4):
+        super().__init__()
+        self.index_topk = index_topk
+        self.compress_ratio = compress_ratio
+
+    def forward(self, q_fp8, q_scale, weights, k_cache, k_scale, start_pos: int, offset: int):
+        bsz, seqlen, h, d = q_fp8.shape
+        ratio = self.compress_ratio
+        end_pos = start_pos + seqlen
+        n_c = end_pos // ratio
+        k = min(self.index_topk, n_c)
+        if k == 0:
+            return torch.empty(bsz, seqlen, 0, dtype=torch.int32, device=q_fp8.device)
+        kc, ks = k_cache[:, :n_c], k_scale[:, :n_c]
+        q2 = q_fp8.reshape(bsz * seqlen, h, d)
+        qs2, w2 = q_scale.reshape(bsz * seqlen, h).float(), weights.reshape(bsz * seqlen, h).float()
+        if start_pos == 0:  # causal: position i scores the first (i + 1) // ratio compressed entries
+            bounds = (torch.arange(1, seqlen + 1, device=q_fp8.device) // ratio).to(torch.int32)
+            lengths = bounds.repeat(bsz)
+        else:
+            lengths = torch.full((bsz * seqlen,), n_c, dtype=torch.int32, device=q_fp8.device)
+        idx = ops.dsa_indexer_topk_shared(q2, qs2, kc.contiguous(), ks.float().contiguous(), w2, k, lengths, offset)
+        return idx.reshape(bsz, seqlen, k)

@@ -615,6 +615,32 @@ def dsa_indexer_topk(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: t
     return idx
 
 
+def dsa_indexer_topk_shared(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: torch.Tensor,
+                            w: torch.Tensor, topk: int, lengths: torch.Tensor, offset: int = 0,
+                            workspace: MoEWorkspace | None = None) -> torch.Tensor:
+    """Indexer top-k for R query rows q [R, H, D] sharing key caches k [G, L, D]
+    in groups of R / G consecutive rows, each row with its own length."""
+    q, k = _u8(q, "q"), _u8(k, "k")
+    q_s, k_s, w = _f32(q_s, "q_s"), _f32(k_s, "k_s"), _f32(w, "weights")
+    if q.dim() != 3 or k.dim() != 3 or q.shape[2] != k.shape[2]:
+        raise ValueError(f"q must be [R, H, D] and k [G, L, D], got {tuple(q.shape)} and {tuple(k.shape)}")
+    r, h, d = q.shape
+    g, l_, _ = k.shape
+    if g == 0 or r % g:
+        raise ValueError(f"{r} query rows do not split into {g} key caches")
+    if tuple(q_s.shape) != (r, h) or tuple(w.shape) != (r, h) or tuple(k_s.shape) != (g, l_):
+        raise ValueError("q_s and weights must be [R, H], k_s [G, L]")
+    lengths = _cuda(lengths, "lengths").to(torch.int32).contiguous()
+    if tuple(lengths.shape) != (r,):
+        raise ValueError(f"lengths must be [R], got {tuple(lengths.shape)}")
+    idx = torch.empty(r, topk, dtype=torch.int32, device=q.device)
+    nbytes = _lib.lib().mosaic_dsa_indexer_workspace_bytes(r, l_)
+    ws = _workspace(workspace, nbytes, q.device)
+    _lib.call("mosaic_dsa_indexer_topk_shared", _ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(w), _ptr(lengths),
+              _ptr(idx), r, h, d, l_, r // g, int(topk), int(offset), _ptr(ws), ws.numel(), _stream())
+    return idx
+
+
 def dsa_indexer_scores(q, q_s, k, k_s, w) -> torch.Tensor:
     """The canonical indexer scores [B, L] f32."""
     q, q_s, k, k_s, w, b, h, d, l_ = _indexer_args(q, q_s, k, k_s, w)

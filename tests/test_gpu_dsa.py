@@ -247,3 +247,48 @@ def test_upstream_sparse_attn_signature(dev):
     with pytest.raises(ValueError, match="512"):
         sparse_attn_fused(T(q[0, :, :, :256]).to(torch.bfloat16).contiguous(),
                           T(kv[0, :, :256]).to(torch.bfloat16).contiguous(), T(sink), T(idx[0]), 0.1)
+
+
+def _indexer_drop_in_case(rng, bsz, seqlen, h, n_cache):
+    q, qs = D.quantize_rows_e4m3(rng.standard_normal((bsz * seqlen, h, 128)))
+    k, ks = D.quantize_rows_e4m3(rng.standard_normal((bsz, n_cache, 128)))
+    w = (rng.standard_normal((bsz * seqlen, h)) * (128 ** -0.5) * (h ** -0.5)).astype(np.float32)
+    return q, qs, k, ks, w
+
+
+def test_indexer_drop_in_decode(dev):
+    """Indexer.forward at decode (start_pos > 0, seqlen 1): min(index_topk, end_pos // 4)
+    picks over the compressed cache, + offset (.mosaicvm/source/inference_model.py:430-439)."""
+    from mosaic_amd.kernels.dsa import Indexer
+    rng = np.random.default_rng(31)
+    bsz, h, start = 2, 64, 4000
+    n_c = (start + 1) // 4
+    q, qs, k, ks, w = _indexer_drop_in_case(rng, bsz, 1, h, n_c + 50)
+    ix = Indexer(index_topk=512)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    got = ix(T(q).view(torch.float8_e4m3fn).reshape(bsz, 1, h, 128), T(qs).reshape(bsz, 1, h),
+             T(w).reshape(bsz, 1, h), T(k).view(torch.float8_e4m3fn), T(ks), start, 128).cpu().numpy()
+    ref = D.indexer_topk(q, qs, k[:, :n_c], ks[:, :n_c], w, 512, None, 128)
+    np.testing.assert_array_equal(got.reshape(bsz, 512), ref)
+
+
+def test_indexer_drop_in_prefill_causal(dev):
+    """Indexer.forward at start_pos 0: position i sees the first (i + 1) // 4
+    compressed entries, masked picks are -1, valid ones + offset (the query
+    rows of one sequence share its cache)."""
+    from mosaic_amd.kernels.dsa import Indexer
+    rng = np.random.default_rng(32)
+    bsz, seqlen, h = 2, 96, 32
+    n_c = seqlen // 4
+    q, qs, k, ks, w = _indexer_drop_in_case(rng, bsz, seqlen, h, n_c)
+    ix = Indexer(index_topk=2048)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    got = ix(T(q).view(torch.float8_e4m3fn).reshape(bsz, seqlen, h, 128), T(qs).reshape(bsz, seqlen, h),
+             T(w).reshape(bsz, seqlen, h), T(k).view(torch.float8_e4m3fn), T(ks), 0, 7).cpu().numpy()
+    assert got.shape == (bsz, seqlen, n_c)
+    kk = np.repeat(k, seqlen, axis=0)
+    kss = np.repeat(ks, seqlen, axis=0)
+    lengths = np.tile((np.arange(1, seqlen + 1) // 4).astype(np.int32), bsz)
+    ref = D.indexer_topk(q, qs, kk, kss, w, n_c, lengths, 7)
+    np.testing.assert_array_equal(got.reshape(bsz * seqlen, n_c), ref)
+    assert (got[:, 2, :] == -1).all() and (got[:, 3, 1:] == -1).all() and got[0, 3, 0] == 7
