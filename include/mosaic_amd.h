@@ -330,6 +330,19 @@ int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, const uint8_t*
 int mosaic_dsa_indexer_bounds(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
                               float* lo, float* hi, int64_t b, int64_t h, int64_t d, int64_t l, void* stream);
 
+/* Per-head top-k sparse attention of one decoding token, replacing
+ * dsa_decode_attention (mosaicvm/kernels/dsa_attention.py:113-154): q [h, d]
+ * bf16, k [ctx, h, d] bf16, v [ctx, h, dv] bf16; per head s[t] = fp32(exact
+ * q_h . k[t, h]) * scale, idx [h, topk] int32 = the top-k positions by
+ * descending score (ties to the lower position), out [h, dv] bf16 =
+ * softmax(s[idx]) . v[idx, h] in fp32.  d % 8 == 0, d <= 512, topk <= 2048,
+ * topk <= ctx.  Workspace: mosaic_dsa_head_attention_workspace_bytes(ctx, h)
+ * (the [h, ctx] fp32 scores). */
+size_t mosaic_dsa_head_attention_workspace_bytes(int64_t ctx, int64_t h);
+int mosaic_dsa_head_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, int32_t* idx,
+                              int64_t h, int64_t ctx, int64_t d, int64_t dv, int64_t topk, float scale,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes of mosaic_mla_sparse_decode. */
 size_t mosaic_mla_decode_workspace_bytes(int64_t b, int64_t h, int64_t topk);
 

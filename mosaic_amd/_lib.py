@@ -62,6 +62,8 @@ SIGNATURES: dict[str, tuple] = {
                                                P, c_size_t, P]),
     "mosaic_dsa_indexer_scores": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, P]),
     "mosaic_dsa_indexer_bounds": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
+    "mosaic_dsa_head_attention_workspace_bytes": (c_size_t, [I64, I64]),
+    "mosaic_dsa_head_attention": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F, P, c_size_t, P]),
     "mosaic_mla_decode_workspace_bytes": (c_size_t, [I64, I64, I64]),
     "mosaic_mla_sparse_decode": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, F, P, c_size_t,
                                          P]),

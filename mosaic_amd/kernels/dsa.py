@@ -11,6 +11,11 @@
 * ``indexer_topk`` / ``indexer_scores`` -- the FP8 indexer of ``Indexer.forward``
   (``.mosaicvm/source/inference_model.py:408-439``) from quantized q/k.
 * ``mla_decode_fp8`` -- MLA decode over an FP8 latent cache (BASELINE format).
+* ``dsa_decode_attention(q, k_index, v_full, topk, scale)`` --
+  ``mosaicvm/kernels/dsa_attention.py:113-154``: per-head top-k positions and
+  softmax attention over them for one token (q [H, d], k_index [ctx, H, d],
+  v_full [ctx, H, dv] bf16) -> (out [H, dv], idx [H, topk]); picks listed by
+  descending score, ties to the lower position.
 * ``Indexer`` -- the scoring and top-k of ``Indexer.forward``
   (``.mosaicvm/source/inference_model.py:408-439``, ``mosaicvm/model/dsa_layers.py:281-321``)
   from already projected FP8 q and the FP8 compressed key cache: the causal
@@ -115,3 +120,22 @@ class Indexer(torch.nn.Module):
             lengths = torch.full((bsz * seqlen,), n_c, dtype=torch.int32, device=q_fp8.device)
         idx = ops.dsa_indexer_topk_shared(q2, qs2, kc.contiguous(), ks.float().contiguous(), w2, k, lengths, offset)
         return idx.reshape(bsz, seqlen, k)
+
+
+HEAD_GROUP = 8
+CANDIDATES = 512
+
+
+def dsa_decode_attention(q, k_index, v_full, topk: int = CANDIDATES, scale: float | None = None):
+    """``mosaicvm/kernels/dsa_attention.py:113-154`` on the HIP per-head kernels."""
+    if q.dim() != 2:
+        raise ValueError("batch=1 decode path: q must be [H, index_dim]")
+    h, index_dim = q.shape
+    ctx = k_index.shape[0]
+    if h % HEAD_GROUP:
+        raise ValueError(f"heads {h} must be a multiple of {HEAD_GROUP}")
+    if ctx < topk:
+        raise ValueError("context must cover candidate set")
+    if scale is None:
+        scale = 1.0 / (index_dim ** 0.5)
+    return ops.dsa_head_attention(q.contiguous(), k_index.contiguous(), v_full.contiguous(), topk, scale)

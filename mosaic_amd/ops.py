@@ -660,6 +660,27 @@ def dsa_indexer_bounds(q, q_s, k, k_s, w) -> tuple[torch.Tensor, torch.Tensor]:
     return lo, hi
 
 
+def dsa_head_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, topk: int,
+                       scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-head top-k attention of one token: q [H, d], k [ctx, H, d], v [ctx, H, dv]
+    (bf16) -> (out [H, dv] bf16, idx [H, topk] int32)."""
+    q, k, v = _bf16(q, "q"), _bf16(k, "k_index"), _bf16(v, "v_full")
+    if q.dim() != 2 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q must be [H, d], k_index [ctx, H, d], v_full [ctx, H, dv]")
+    h, d = q.shape
+    ctx = k.shape[0]
+    if tuple(k.shape) != (ctx, h, d) or v.shape[0] != ctx or v.shape[1] != h:
+        raise ValueError(f"shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not agree")
+    dv = v.shape[2]
+    out = torch.empty(h, dv, dtype=torch.bfloat16, device=q.device)
+    idx = torch.empty(h, topk, dtype=torch.int32, device=q.device)
+    nbytes = _lib.lib().mosaic_dsa_head_attention_workspace_bytes(ctx, h)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    _lib.call("mosaic_dsa_head_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(idx), h, ctx, d, dv, int(topk),
+              float(scale), _ptr(ws), ws.numel(), _stream())
+    return out, idx
+
+
 def mla_sparse_decode(q: torch.Tensor, kv_latent: torch.Tensor, kv_scale: torch.Tensor, kv_rope: torch.Tensor,
                       idx: torch.Tensor, softmax_scale: float, sink: torch.Tensor | None = None,
                       workspace: MoEWorkspace | None = None) -> torch.Tensor:

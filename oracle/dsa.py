@@ -139,3 +139,26 @@ def mla_sparse_decode(q, lat_codes, lat_scale, rope, sink, idx, softmax_scale: f
     lat = dequant_kv_latent(lat_codes, lat_scale, scale_block)
     kv = np.concatenate([lat, np.asarray(rope, dtype=np.float32)], axis=-1)
     return sparse_attn(q, kv, sink, idx, softmax_scale, dv=lat_codes.shape[-1])
+
+
+def head_topk_attention(q, k, v, topk: int, scale: float):
+    """``dsa_decode_attention`` (``mosaicvm/kernels/dsa_attention.py:113-154``):
+    q [H, d], k [ctx, H, d], v [ctx, H, dv] (bf16-valued) -> (out [H, dv],
+    idx [H, topk]).  s[h, t] = fp32(exact q_h . k[t, h]) * fp32(scale); per head
+    the top-k by (score desc, position asc); out = softmax(s[idx]) . v[idx]."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    dots = np.einsum("hd,thd->ht", q, k).astype(np.float32)     # exact products, float64 sums
+    s = (dots * np.float32(scale)).astype(np.float32)
+    h, ctx = s.shape
+    idx = np.empty((h, topk), dtype=np.int64)
+    out = np.empty((h, v.shape[2]), dtype=np.float32)
+    pos = np.arange(ctx)
+    for i in range(h):
+        order = np.lexsort((pos, -s[i].astype(np.float64)))[:topk]
+        idx[i] = order
+        sc = s[i, order].astype(np.float64)
+        p = np.exp(sc - sc.max())
+        out[i] = (p[:, None] * v[order, i, :]).sum(0) / p.sum()
+    return out, idx

@@ -292,3 +292,19 @@ def test_indexer_drop_in_prefill_causal(dev):
     ref = D.indexer_topk(q, qs, kk, kss, w, n_c, lengths, 7)
     np.testing.assert_array_equal(got.reshape(bsz * seqlen, n_c), ref)
     assert (got[:, 2, :] == -1).all() and (got[:, 3, 1:] == -1).all() and got[0, 3, 0] == 7
+
+
+@pytest.mark.parametrize("h,d,ctx,topk,dv", [(64, 128, 4096, 256, 128), (8, 64, 1000, 512, 512), (16, 128, 700, 700, 64)])
+def test_dsa_decode_attention_vs_oracle(dev, h, d, ctx, topk, dv):
+    """dsa_decode_attention (mosaicvm/kernels/dsa_attention.py:113-154; the
+    reference's tests/test_dsa_parity.py shape first): per-head picks
+    bit-exact in (score desc, position asc) order, output within 2e-2."""
+    from mosaic_amd.kernels.dsa import dsa_decode_attention
+    rng = np.random.default_rng(h + ctx)
+    bf = lambda *sh: torch.from_numpy(rng.standard_normal(sh).astype(np.float32)).to(torch.bfloat16)
+    q, k, v = bf(h, d), bf(ctx, h, d), bf(ctx, h, dv)
+    k[10:20] = k[5]  # exact score ties within every head
+    out, idx = dsa_decode_attention(q.to(dev), k.to(dev), v.to(dev), topk)
+    out_ref, idx_ref = D.head_topk_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), topk, d ** -0.5)
+    np.testing.assert_array_equal(idx.cpu().numpy(), idx_ref)
+    _close(out.float().cpu().numpy(), out_ref)
