@@ -736,10 +736,72 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
 // ===================================================================== MLA
 constexpr int kMlaBT = 32;        // tokens per online-softmax block
 constexpr int kMlaDl = 512;       // latent (value) width
-constexpr int kVtStride = 40;     // bf16 per V^T row (32 tokens + 8)
+constexpr int kMlaDt = kMlaDl / 16;  // 16-wide latent column tiles
+constexpr int kPsStride = 40;     // bf16 per row of the P exchange (32 tokens + 8)
+constexpr int kMlaMaxSplits = 64;
+// A head's running maximum moves only when a block's maximum exceeds it by
+// more than this (natural log units): probabilities stay below e^8, which
+// bf16 P and the fp32 sums hold with their usual relative precision, and the
+// O rescale is skipped for almost every block after the first.
+constexpr float kMlaLazyMax = 8.f;
+
+constexpr int kMlaMaxChunk = 1024;  // token ids of one split (staged in LDS)
+// FP8 gather stages: raw latent rows, scale rows (up to 32 floats), rope rows
+constexpr int kMlaStages = 3;
+constexpr int kMlaStgLat = kMlaBT * kMlaDl;
+constexpr int kMlaStgSc = kMlaBT * 32 * 4;
+constexpr int kMlaStgRope = kMlaBT * 64 * 2;
+constexpr int kMlaStage = kMlaStgLat + kMlaStgSc + kMlaStgRope;
+constexpr int kMlaCopies = 9;  // copies per wave per block: 4 latent, 4 scale, 1 rope
+
+typedef short mla_v4s __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t mla_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// one 16-byte (resp. 4-byte) global -> LDS copy per lane; the LDS address of
+// lane i is base + 16 i (resp. 4 i).  Issued from inline asm so the compiler
+// neither waits for them before LDS reads nor stages them in registers; the
+// kernel waits with explicit vmcnt counts.
+__device__ __forceinline__ void mla_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void mla_copy4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
 
 __device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t a, const bf16x8_t b, const f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Token order inside a block: MFMA K index / P slot p = 8 g + 4 r + i holds
+// block token 8 g + 2 i + r.  With it the four 4-token LDS transpose reads of
+// two 16-lane groups touch 8 rows whose bank offsets (36 dwords apart) are
+// 8 dwords apart, and a QK A-operand read still takes 16 rows distinct mod 16.
+__device__ __forceinline__ int mla_slot_token(int p) { return (p & ~7) | ((p & 3) << 1) | ((p >> 2) & 1); }
+
+// 4 bf16 of V column c' (of a 16-column tile) for 4 tokens, from row-major
+// K rows in LDS: with lane 4 i + j of a 16-lane group pointing at row token_i,
+// columns 4 j .. 4 j + 3, lane c' receives row token_i, column c' as element i.
+__device__ __forceinline__ mla_v4s lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) mla_v4s*)(p));
+}
+
+// max / sum over the 16 lanes of each row (pair, quad, half-row and row
+// mirrors); every lane of the row gets the result
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0xB1, 0xF)));
+  v = fmaxf(v, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x4E, 0xF)));
+  v = fmaxf(v, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x141, 0xF)));
+  return fmaxf(v, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x140, 0xF)));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0xB1, 0xF));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x4E, 0xF));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x141, 0xF));
+  return v + __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x140, 0xF));
 }
 
 // Where the KV of a row lives.  FP8: latent e4m3 [rows, 512] + f32 scales
@@ -756,44 +818,70 @@ struct MlaKv {
 };
 
 // One split (a contiguous slice of the selected tokens) of one query row and
-// one group of 16*NW heads: partial (m, l, O) per head.  Waves own 16 heads;
-// with at most 4 waves a workgroup runs one wave per SIMD, which leaves room
-// for each wave's 16x512 fp32 O tile in accumulation registers.  Blocks of
-// kMlaBT tokens go through two LDS buffers: while block i is multiplied out of
-// one, block i + 1's raw KV rows are already in registers (loaded before the
-// math) and are converted into the other after it; the token ids are read two
-// blocks ahead.  A thread gathers one (token, 64-wide latent segment) item and
-// one 16-byte rope chunk per block.
-template <int NW, bool FP8, int DR>
-__global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
+// one group of 16*HT heads (HT head tiles): partial (m, l, O) per head.  The
+// split's token ids are staged in LDS first (masked or out-of-range ids as -1).
+// Blocks of kMlaBT tokens then go through two LDS buffers of bf16 K rows
+// (latent then rope).  FP8 caches: raw rows, their scales and rope rows are
+// copied global -> LDS directly (global_load_lds) into a ring of kMlaStages
+// stages, issued three blocks ahead of their conversion to bf16, so the gather
+// latency hides behind three blocks of math; every wave issues kMlaCopies
+// copies per block, so `s_waitcnt vmcnt` + a barrier hands a stage over.  BF16
+// caches: each thread gathers its item of block i + 1 into registers while
+// block i is multiplied out, and stores it after.
+//
+// Four waves.  Wave w < HT scores and soft-maxes head tile w (S = Q K^T:
+// its heads' q kept in registers as the A operand, K rows from LDS as B), then
+// the workgroup swaps roles for O += P V: P (bf16) and the per-head rescale
+// factors go through LDS, and each wave multiplies every head of the group
+// into its own quarter of the 512 latent columns, reading V straight out of
+// the K rows with LDS transpose reads.  So V is read once per workgroup rather
+// than once per 16 heads, and no transposed copy of it is written.  A
+// workgroup runs one wave per SIMD, which leaves room for the O tiles (16 HT
+// heads x 128 columns per wave) in accumulation registers.
+template <int HT, bool FP8, int DR>
+__global__ void __launch_bounds__(256) mla_decode_split_kernel(
     const uint16_t* __restrict__ q, const MlaKv kv, const int32_t* __restrict__ idx, float* __restrict__ part_o,
     float* __restrict__ part_ml, int topk, float scale, int chunk) {
   constexpr int DQK = kMlaDl + DR;
   constexpr int KS = DQK + 8;  // bf16 per K row in LDS: 16-byte reads of 16 rows hit distinct banks
-  constexpr int NT = NW * 64;
-  constexpr int ITEMS = kMlaBT * 8;               // (token, segment) items per block
-  constexpr int IPT = (ITEMS + NT - 1) / NT;      // items per thread
-  constexpr int RCH = kMlaBT * (DR / 8);          // 16-byte rope chunks per block
-  constexpr int RPT = DR > 0 ? (RCH + NT - 1) / NT : 0;
-  constexpr int RAWV = FP8 ? 4 : 8;               // 16-byte vectors per item
+  constexpr int NW = 4, NT = NW * 64;
+  constexpr int RAWV = FP8 ? 4 : 8;               // 16-byte vectors per (token, 64-wide segment) item
+  constexpr int DTW = kMlaDt / NW;                // latent column tiles per wave in O += P V
+  static_assert(kMlaBT * 8 == NT && (DR == 0 || kMlaBT * (DR / 8) == NT), "one item and one rope chunk a thread");
+  static_assert(!FP8 || DR == 64, "FP8 caches carry a 64-wide bf16 rope");
   __shared__ __attribute__((aligned(16))) uint16_t Kt[2][kMlaBT * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kMlaDl * kVtStride];
-  __shared__ int tok_id[2][kMlaBT];
-  const int H = NW * 16 * gridDim.z;
+  __shared__ __attribute__((aligned(16))) uint8_t Stg[FP8 ? kMlaStages * kMlaStage : 16];
+  __shared__ __attribute__((aligned(16))) uint16_t Ps[16 * HT * kPsStride];
+  __shared__ __attribute__((aligned(16))) float As[16 * HT];
+  __shared__ int Fl[HT];
+  __shared__ int Ids[kMlaMaxChunk];
+  const int H = HT * 16 * gridDim.z;
   const int split = blockIdx.x, b = blockIdx.y, S = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = tid >> 6, hw = (int)blockIdx.z * NW + wv;  // wave's 16-head group in the row
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool scorer = wv < HT;             // this wave scores head tile wv
+  const int hw = (int)blockIdx.z * HT + (scorer ? wv : 0);  // its 16-head group in the row
   const int c = lane & 15, qd = lane >> 4;
   const int head = 16 * hw + c;
+  const int dt0 = wv * DTW;  // this wave's first latent column tile
   const int64_t n = kv.n;
   const int64_t kvb = b / kv.rows_per_kv;
   const int t_begin = split * chunk;
   const int t_end = min(topk, t_begin + chunk);
-  const int nblk = t_end > t_begin ? (t_end - t_begin + kMlaBT - 1) / kMlaBT : 0;
-  // q as the B operand of S^T = K Q^T: lane (c, qd) holds q[head][32 s + 8 qd .. +8]
+  // (an empty cache masks every token: nothing is read)
+  const int nblk = t_end > t_begin && n > 0 ? (t_end - t_begin + kMlaBT - 1) / kMlaBT : 0;
+  const int nsc = kMlaDl >> kv.sb_shift;  // scales per FP8 row
+  // the split's ids (loaded first, so that they fly together with q)
+  constexpr int IDS_PT = kMlaMaxChunk / NT;
+  int idv[IDS_PT];
+#pragma unroll
+  for (int k = 0; k < IDS_PT; ++k) {
+    const int s = tid + NT * k, ti = t_begin + s;
+    idv[k] = s < nblk * kMlaBT && ti < t_end ? idx[(int64_t)b * topk + ti] : -1;
+  }
+  // q as the A operand of S = Q K^T: lane (c, qd) holds q[head][32 s + 8 qd .. +8]
   // (kept in registers: the empty asm stops the compiler from re-loading q in
-  // every block, where those loads would queue behind the next block's gather
-  // and the QK products would wait for the whole gather)
+  // every block, where those loads would queue behind the gather)
   bf16x8_t qb[DQK / 32];
   {
     const uint16_t* qrow = q + ((int64_t)b * H + head) * DQK;
@@ -802,308 +890,330 @@ __global__ void __launch_bounds__(NW * 64) mla_decode_split_kernel(
 #pragma unroll
     for (int s = 0; s < DQK / 32; ++s) asm volatile("" : "+v"(qb[s]));
   }
-  // Token ids of a block's slots in two steps: token_raw loads the index
-  // unconditionally (clamped to the row), token_fix turns it into the id or -1
-  // (masked or past the split).  The ids of block i + 2 are loaded behind block
-  // i + 1's gather and fixed only in the next iteration: a branch around the
-  // load, or math on it right away, would make the compiler wait for every
-  // load in flight, the gather included.
-  auto token_raw = [&](int blk, int slot) -> int {
-    const int ti = t_begin + blk * kMlaBT + slot;
-    return idx[(int64_t)b * topk + min(ti, topk - 1)];
-  };
-  auto token_fix = [&](int blk, int slot, int raw) -> int {
-    const int ti = t_begin + blk * kMlaBT + slot;
-    const bool live = blk < nblk && ti < t_end && raw >= 0 && (int64_t)raw < n;
-    return live ? raw : -1;
-  };
-  // this thread's items: latent (token it % kMlaBT, segment it / kMlaBT) and rope chunk
-  int iid[IPT], rid[RPT > 0 ? RPT : 1];
-  u32x4_t raw[IPT][RAWV];
-  float rsc[IPT][4];
-  u32x4_t rrope[RPT > 0 ? RPT : 1];
-  auto load_ids = [&](int blk, int (&ii)[IPT], int (&ri)[RPT > 0 ? RPT : 1]) {
 #pragma unroll
-    for (int k = 0; k < IPT; ++k) ii[k] = token_raw(blk, (tid + NT * k) % kMlaBT);
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) ri[k] = token_raw(blk, ((tid + NT * k) / (DR / 8)) % kMlaBT);
-  };
-  auto fix_ids = [&](int blk, int (&ii)[IPT], int (&ri)[RPT > 0 ? RPT : 1]) {
-#pragma unroll
-    for (int k = 0; k < IPT; ++k) {
-      const int it = tid + NT * k;
-      ii[k] = it < ITEMS ? token_fix(blk, it % kMlaBT, ii[k]) : -1;
-    }
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int it = tid + NT * k;
-      ri[k] = it < RCH ? token_fix(blk, it / (DR / 8), ri[k]) : -1;
-    }
-  };
-  auto issue = [&](const int (&ii)[IPT], const int (&ri)[RPT > 0 ? RPT : 1]) {
-#pragma unroll
-    for (int k = 0; k < IPT; ++k) {
-      const int it = tid + NT * k, seg = it / kMlaBT;
-      const int64_t row = kvb * n + (ii[k] >= 0 ? ii[k] : 0);
-      if constexpr (FP8) {
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(kv.lat) + row * kMlaDl + seg * 64;
-        const float* ssrc = kv.lat_s + row * (kMlaDl >> kv.sb_shift);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          raw[k][v] = *reinterpret_cast<const u32x4_t*>(src + 16 * v);
-          rsc[k][v] = ssrc[(seg * 64 + 16 * v) >> kv.sb_shift];
-        }
-      } else {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(kv.lat) + row * DQK + seg * 64;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) raw[k][v] = *reinterpret_cast<const u32x4_t*>(src + 8 * v);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int it = tid + NT * k, pc = it % (DR / 8);
-      const int64_t row = kvb * n + (ri[k] >= 0 ? ri[k] : 0);
-      const uint16_t* src = FP8 ? kv.rope + row * DR : reinterpret_cast<const uint16_t*>(kv.lat) + row * DQK + kMlaDl;
-      rrope[k] = *reinterpret_cast<const u32x4_t*>(src + 8 * pc);
-    }
-  };
-  // raw registers -> bf16 rows of Kt and columns of Vt of buffer bf
-  auto fill = [&](int bf, const int (&ii)[IPT], const int (&ri)[RPT > 0 ? RPT : 1]) {
-#pragma unroll
-    for (int k = 0; k < IPT; ++k) {
-      const int it = tid + NT * k;
-      if (it >= ITEMS) continue;
-      const int tk = it % kMlaBT, seg = it / kMlaBT;
-      const bool ok = ii[k] >= 0;
-      uint32_t outw[32];
-      if constexpr (FP8) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float sc = rsc[k][v];
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            // exact e4m3 -> fp32, fp32 product with the scale, one RNE rounding to bf16
-            f32x2_t a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw[k][v][e2], false);
-            f32x2_t b2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw[k][v][e2], true);
-            a2[0] *= sc;
-            a2[1] *= sc;
-            b2[0] *= sc;
-            b2[1] *= sc;
-            outw[8 * v + 2 * e2] = __builtin_bit_cast(uint32_t, __builtin_convertvector(a2, bf16x2_t));
-            outw[8 * v + 2 * e2 + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(b2, bf16x2_t));
-          }
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 8; ++v)
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) outw[4 * v + e2] = raw[k][v][e2];
-      }
-#pragma unroll
-      for (int i = 0; i < 32; ++i) outw[i] = ok ? outw[i] : 0u;
-      u32x4_t* kdst = reinterpret_cast<u32x4_t*>(&Kt[bf][tk * KS + seg * 64]);
-#pragma unroll
-      for (int v = 0; v < 8; ++v) kdst[v] = u32x4_t{outw[4 * v], outw[4 * v + 1], outw[4 * v + 2], outw[4 * v + 3]};
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        Vt[bf][(seg * 64 + 2 * i) * kVtStride + tk] = (uint16_t)(outw[i] & 0xFFFFu);
-        Vt[bf][(seg * 64 + 2 * i + 1) * kVtStride + tk] = (uint16_t)(outw[i] >> 16);
-      }
-      if (seg == 0) tok_id[bf][tk] = ii[k];
-    }
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-      const int it = tid + NT * k;
-      if (it >= RCH) continue;
-      const int tk = it / (DR / 8), pc = it % (DR / 8);
-      const u32x4_t v = ri[k] >= 0 ? rrope[k] : u32x4_t{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4_t*>(&Kt[bf][tk * KS + kMlaDl + 8 * pc]) = v;
-    }
-  };
-  f32x4_t o[kMlaDl / 16];
-#pragma unroll
-  for (int i = 0; i < kMlaDl / 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  int nid[IPT], nrid[RPT > 0 ? RPT : 1];  // ids of the block after the next
-  if (nblk > 0) {
-    int ii0[IPT], ri0[RPT > 0 ? RPT : 1];
-    load_ids(0, ii0, ri0);
-    fix_ids(0, ii0, ri0);
-    issue(ii0, ri0);
-    load_ids(1, nid, nrid);
-    fill(0, ii0, ri0);
+  for (int k = 0; k < IDS_PT; ++k) {
+    const int s = tid + NT * k;
+    if (s < nblk * kMlaBT) Ids[s] = idv[k] >= 0 && (int64_t)idv[k] < n ? idv[k] : -1;
   }
+  __syncthreads();
+  // row of the cache that token t of block j reads (masked tokens read row 0
+  // of their batch and are zeroed when converted)
+  auto row_of = [&](int j, int t) -> int64_t {
+    const int id = Ids[j * kMlaBT + t];
+    return kvb * n + (id >= 0 ? id : 0);
+  };
+  // ---- FP8: global -> LDS copies of block j into stage j % kMlaStages.  Latent
+  // rows keep their 16-byte chunks XOR-swizzled by (token & 15) and scale rows
+  // their floats by (token & 31), so the conversion's reads of 16 tokens hit
+  // distinct banks.
+  auto issue_fp8 = [&](int j) {
+    uint8_t* st = &Stg[(j % kMlaStages) * kMlaStage];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // latent: tokens 8 wv + 2 k (lanes 0-31) and + 1 (lanes 32-63)
+      const int t = 8 * wv + 2 * k + (lane >> 5), p = lane & 31;
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(kv.lat) + row_of(j, t) * kMlaDl + 16 * (p ^ (t & 15));
+      mla_copy16(src, mla_lds_addr(st + (8 * wv + 2 * k) * kMlaDl));
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // scales: floats 64 (wv + 4 k) + lane = (token f / 32, slot f % 32)
+      const int f = 64 * (wv + 4 * k) + lane, t = f >> 5, p = f & 31;
+      const int e = min(p ^ (t & 31), nsc - 1);
+      mla_copy4(kv.lat_s + row_of(j, t) * nsc + e, mla_lds_addr(st + kMlaStgLat + 256 * (wv + 4 * k)));
+    }
+    {  // rope: tokens 8 wv .. 8 wv + 7
+      const int t = 8 * wv + (lane >> 3), pc = lane & 7;
+      mla_copy16(kv.rope + row_of(j, t) * DR + 8 * pc, mla_lds_addr(st + kMlaStgLat + kMlaStgSc + 1024 * wv));
+    }
+  };
+  // wait until at most `after` blocks' copies of this wave are in flight, then barrier
+  auto wait_stage = [&](int after) {
+    if (after >= 2)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * kMlaCopies) : "memory");
+    else if (after == 1)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kMlaCopies) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  // item of thread tid: token tid % 32, latent segment tid / 32 (64 values);
+  // rope chunk: token tid / 8, 8 values at 8 (tid % 8)
+  const int tk = tid % kMlaBT, seg = tid / kMlaBT;
+  const int rtk = tid / 8, rpc = tid % 8;
+  // stage of block j -> bf16 K rows of buffer j & 1
+  auto convert_fp8 = [&](int j) {
+    const uint8_t* st = &Stg[(j % kMlaStages) * kMlaStage];
+    const bool ok = Ids[j * kMlaBT + tk] >= 0;
+    const float* srow = reinterpret_cast<const float*>(st + kMlaStgLat) + tk * 32;
+    uint32_t outw[32];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(st + tk * kMlaDl + 16 * ((4 * seg + v) ^ (tk & 15)));
+      const float sc = srow[((seg * 64 + 16 * v) >> kv.sb_shift) ^ (tk & 31)];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        // exact e4m3 -> fp32, fp32 product with the scale, one RNE rounding to bf16
+        f32x2_t a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[e2], false);
+        f32x2_t b2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[e2], true);
+        a2[0] *= sc;
+        a2[1] *= sc;
+        b2[0] *= sc;
+        b2[1] *= sc;
+        outw[8 * v + 2 * e2] = __builtin_bit_cast(uint32_t, __builtin_convertvector(a2, bf16x2_t));
+        outw[8 * v + 2 * e2 + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(b2, bf16x2_t));
+      }
+    }
+    u32x4_t* kdst = reinterpret_cast<u32x4_t*>(&Kt[j & 1][tk * KS + seg * 64]);
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      kdst[v] = ok ? u32x4_t{outw[4 * v], outw[4 * v + 1], outw[4 * v + 2], outw[4 * v + 3]} : u32x4_t{0u, 0u, 0u, 0u};
+    const u32x4_t r = *reinterpret_cast<const u32x4_t*>(st + kMlaStgLat + kMlaStgSc + rtk * 128 + 16 * rpc);
+    *reinterpret_cast<u32x4_t*>(&Kt[j & 1][rtk * KS + kMlaDl + 8 * rpc]) =
+        Ids[j * kMlaBT + rtk] >= 0 ? r : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  // ---- BF16: register-staged gather of block j, stored by fill_bf16
+  u32x4_t raw[RAWV];
+  u32x4_t rrope;
+  auto issue_bf16 = [&](int j) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(kv.lat) + row_of(j, tk) * DQK + seg * 64;
+#pragma unroll
+    for (int v = 0; v < RAWV; ++v) raw[v] = *reinterpret_cast<const u32x4_t*>(src + 8 * v);
+    if constexpr (DR > 0)
+      rrope = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(kv.lat) + row_of(j, rtk) * DQK +
+                                                 kMlaDl + 8 * rpc);
+  };
+  auto fill_bf16 = [&](int j) {
+    const bool ok = Ids[j * kMlaBT + tk] >= 0;
+    u32x4_t* kdst = reinterpret_cast<u32x4_t*>(&Kt[j & 1][tk * KS + seg * 64]);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) kdst[v] = ok ? raw[v] : u32x4_t{0u, 0u, 0u, 0u};
+    if constexpr (DR > 0)
+      *reinterpret_cast<u32x4_t*>(&Kt[j & 1][rtk * KS + kMlaDl + 8 * rpc]) =
+          Ids[j * kMlaBT + rtk] >= 0 ? rrope : u32x4_t{0u, 0u, 0u, 0u};
+  };
+  // O tiles: rows = heads 16 ht + 4 qd + r of the group, columns 16 (dt0 + dl) + c
+  f32x4_t o[HT][DTW];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+    for (int dl = 0; dl < DTW; ++dl) o[ht][dl] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // running maximum and sum of heads 16 hw + 4 qd + r (all 16 lanes of a row agree)
+  float m_run[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, l_run[4] = {0.f, 0.f, 0.f, 0.f};
+  if (nblk > 0) {
+    if constexpr (FP8) {
+      issue_fp8(0);
+      if (nblk > 1) issue_fp8(1);
+      wait_stage(nblk > 1 ? 1 : 0);
+      convert_fp8(0);
+      if (nblk > 2) issue_fp8(2);
+    } else {
+      issue_bf16(0);
+      fill_bf16(0);
+    }
+  }
+  // V transpose reads: lane 4 vi + vj of group qd points at block token
+  // 8 qd + 2 vi (+ 1 for the second read), columns 4 vj .. 4 vj + 3 of a tile
+  const int vi = c >> 2, vj = c & 3;
   for (int blk = 0; blk < nblk; ++blk) {
     const int bf = blk & 1;
-    __syncthreads();  // buffer bf is filled; buffer bf ^ 1 is no longer read
-    int cid[IPT], crid[RPT > 0 ? RPT : 1];
-#pragma unroll
-    for (int k = 0; k < IPT; ++k) cid[k] = nid[k];
-#pragma unroll
-    for (int k = 0; k < RPT; ++k) crid[k] = nrid[k];
+    const int* bid = &Ids[blk * kMlaBT];
+    __syncthreads();  // buffer bf is filled; buffer bf ^ 1, its stage, P and the rescale flags are no longer read
     const bool more = blk + 1 < nblk;
-    if (more) {
-      fix_ids(blk + 1, cid, crid);
-      issue(cid, crid);             // block blk + 1 flies while block blk is multiplied out
-      load_ids(blk + 2, nid, nrid);
+    if constexpr (FP8) {
+      if (blk + 3 < nblk) issue_fp8(blk + 3);  // into the stage block blk came from
+    } else {
+      if (more) issue_bf16(blk + 1);  // block blk + 1 flies while block blk is multiplied out
     }
-    // S^T tiles (rows = tokens 16 j + 4 qd + r, column = head c); two
-    // accumulators per tile (even and odd K steps) halve the dependent MFMA chain
-    f32x4_t st[kMlaBT / 16], st2[kMlaBT / 16];
+    if (scorer) {  // QK and the online softmax of head tile wv
+      // S tiles (rows = heads 4 qd + r of the tile, column = slot 16 j + c): A = q
+      // (registers), B = K rows; two accumulators per tile (even and odd K steps)
+      // halve the dependent MFMA chain.  The ids of this lane's two tokens are
+      // read first so that their LDS latency hides behind the products.
+      bool live[kMlaBT / 16];
 #pragma unroll
-    for (int j = 0; j < kMlaBT / 16; ++j) st[j] = st2[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // K fragments in batches of KB steps, double-buffered: batch i + 1's LDS
-    // reads are issued before batch i's products (the scheduling barriers keep
-    // the compiler from interleaving them into a read-wait-multiply chain)
-    constexpr int KB = 3, NSQ = DQK / 32, NKB = (NSQ + KB - 1) / KB;
-    bf16x8_t kop[2][KB][kMlaBT / 16];
-    auto read_k = [&](int kb2, bf16x8_t (&dst)[KB][kMlaBT / 16]) {
+      for (int j = 0; j < kMlaBT / 16; ++j) live[j] = bid[mla_slot_token(16 * j + c)] >= 0;
+      f32x4_t st[kMlaBT / 16], st2[kMlaBT / 16];
 #pragma unroll
-      for (int ss = 0; ss < KB; ++ss)
+      for (int j = 0; j < kMlaBT / 16; ++j) st[j] = st2[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      // K fragments in batches of KB steps, double-buffered: batch i + 1's LDS
+      // reads are issued before batch i's products (the scheduling barriers keep
+      // the compiler from interleaving them into a read-wait-multiply chain)
+      constexpr int KB = 3, NSQ = DQK / 32, NKB = (NSQ + KB - 1) / KB;
+      bf16x8_t kop[2][KB][kMlaBT / 16];
+      int krow[kMlaBT / 16];
 #pragma unroll
-        for (int j = 0; j < kMlaBT / 16; ++j)
-          if (kb2 * KB + ss < NSQ)
-            dst[ss][j] = *reinterpret_cast<const bf16x8_t*>(&Kt[bf][(16 * j + c) * KS + 8 * qd + 32 * (kb2 * KB + ss)]);
-    };
-    read_k(0, kop[0]);
+      for (int j = 0; j < kMlaBT / 16; ++j) krow[j] = mla_slot_token(16 * j + c) * KS + 8 * qd;
+      auto read_k = [&](int kb2, bf16x8_t (&dst)[KB][kMlaBT / 16]) {
 #pragma unroll
-    for (int kb2 = 0; kb2 < NKB; ++kb2) {
-      if (kb2 + 1 < NKB) read_k(kb2 + 1, kop[(kb2 + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int ss = 0; ss < KB; ++ss)
 #pragma unroll
-      for (int ss = 0; ss < KB; ++ss)
+          for (int j = 0; j < kMlaBT / 16; ++j)
+            if (kb2 * KB + ss < NSQ)
+              dst[ss][j] = *reinterpret_cast<const bf16x8_t*>(&Kt[bf][krow[j] + 32 * (kb2 * KB + ss)]);
+      };
+      read_k(0, kop[0]);
+#pragma unroll
+      for (int kb2 = 0; kb2 < NKB; ++kb2) {
+        if (kb2 + 1 < NKB) read_k(kb2 + 1, kop[(kb2 + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ss = 0; ss < KB; ++ss)
+#pragma unroll
+          for (int j = 0; j < kMlaBT / 16; ++j) {
+            const int s = kb2 * KB + ss;
+            if (s >= NSQ) continue;
+            if (s & 1)
+              st2[j] = mfma_bf16(qb[s], kop[kb2 & 1][ss][j], st2[j]);
+            else
+              st[j] = mfma_bf16(qb[s], kop[kb2 & 1][ss][j], st[j]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int j = 0; j < kMlaBT / 16; ++j) st[j] += st2[j];
+      // online softmax of heads 4 qd + r: reductions over the 16 lanes of a row
+      float sc[kMlaBT / 16][4], p[kMlaBT / 16][4], alpha[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float bm = -INFINITY;
 #pragma unroll
         for (int j = 0; j < kMlaBT / 16; ++j) {
-          const int s = kb2 * KB + ss;
-          if (s >= NSQ) continue;
-          if (s & 1)
-            st2[j] = mfma_bf16(kop[kb2 & 1][ss][j], qb[s], st2[j]);
-          else
-            st[j] = mfma_bf16(kop[kb2 & 1][ss][j], qb[s], st[j]);
+          sc[j][r] = live[j] ? st[j][r] * scale : -INFINITY;
+          bm = fmaxf(bm, sc[j][r]);
         }
+        bm = row16_max(bm);
+        // the running maximum moves only past the lazy margin (or from -inf)
+        const bool move = bm > m_run[r] + kMlaLazyMax;
+        const float m_new = move ? bm : m_run[r];
+        alpha[r] = (move && m_run[r] != -INFINITY) ? __expf(m_run[r] - m_new) : 1.f;
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMlaBT / 16; ++j) {
+          p[j][r] = m_new == -INFINITY ? 0.f : __expf(sc[j][r] - m_new);
+          psum += p[j][r];
+        }
+        l_run[r] = l_run[r] * alpha[r] + row16_sum(psum);
+        m_run[r] = m_new;
+      }
+      // P (bf16, rows = the tile's heads, columns = slots) and the heads' O
+      // rescale factors into LDS; a flag per wave says whether any is not 1
+#pragma unroll
+      for (int j = 0; j < kMlaBT / 16; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          const uint32_t pw =
+              __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{p[j][r], p[j][r + 1]}, bf16x2_t));
+          Ps[(16 * wv + 4 * qd + r) * kPsStride + 16 * j + c] = (uint16_t)(pw & 0xFFFFu);
+          Ps[(16 * wv + 4 * qd + r + 1) * kPsStride + 16 * j + c] = (uint16_t)(pw >> 16);
+        }
+      if (c == 0) *reinterpret_cast<f32x4_t*>(&As[16 * wv + 4 * qd]) = f32x4_t{alpha[0], alpha[1], alpha[2], alpha[3]};
+      const bool rescale = __ballot(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f) != 0;
+      if (lane == 0) Fl[wv] = rescale ? 1 : 0;
+    }
+    __syncthreads();  // P, the factors and the flags of every wave are in
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      if (__builtin_amdgcn_readfirstlane(Fl[ht])) {  // the same word for every lane
+        const f32x4_t al = *reinterpret_cast<const f32x4_t*>(&As[16 * ht + 4 * qd]);
+#pragma unroll
+        for (int dl = 0; dl < DTW; ++dl) o[ht][dl] *= al;
+      }
+    }
+    // O += P V over this wave's column tiles: A = P rows of every head tile
+    // (k = slots 8 qd .. 8 qd + 7), B = V by two transpose reads per tile
+    bf16x8_t pa[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) pa[ht] = *reinterpret_cast<const bf16x8_t*>(&Ps[(16 * ht + c) * kPsStride + 8 * qd]);
+    const uint16_t* vbase = &Kt[bf][(8 * qd + 2 * vi) * KS + 4 * vj];
+    constexpr int VB = 4, NVB = DTW / VB;
+    bf16x8_t vv[2][VB];
+    auto read_v = [&](int vb2, bf16x8_t (&dst)[VB]) {
+#pragma unroll
+      for (int dd = 0; dd < VB; ++dd) {
+        const uint16_t* vp = vbase + 16 * (dt0 + vb2 * VB + dd);
+        const mla_v4s a = lds_read_tr16(vp), e = lds_read_tr16(vp + KS);
+        dst[dd] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(a, e, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    read_v(0, vv[0]);
+#pragma unroll
+    for (int vb2 = 0; vb2 < NVB; ++vb2) {
+      if (vb2 + 1 < NVB) read_v(vb2 + 1, vv[(vb2 + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int dd = 0; dd < VB; ++dd)
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht)
+          o[ht][vb2 * VB + dd] = mfma_bf16(pa[ht], vv[vb2 & 1][dd], o[ht][vb2 * VB + dd]);
       __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int j = 0; j < kMlaBT / 16; ++j) st[j] += st2[j];
-    float sc[kMlaBT / 16][4];
-    float bm = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMlaBT / 16; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sc[j][r] = tok_id[bf][16 * j + 4 * qd + r] >= 0 ? st[j][r] * scale : -INFINITY;
-        bm = fmaxf(bm, sc[j][r]);
-      }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float m_new = fmaxf(m_run, bm);
-    const bool none = m_new == -INFINITY;
-    const float alpha = none ? 1.f : __expf(m_run - m_new);
-    float psum = 0.f;
-    float p[kMlaBT / 16][4];
-#pragma unroll
-    for (int j = 0; j < kMlaBT / 16; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[j][r] = none ? 0.f : __expf(sc[j][r] - m_new);
-        psum += p[j][r];
-      }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    // rescale O rows (heads 4 qd + r of this wave) by their alpha, unless no
-    // head's running maximum moved (then every alpha is 1) or O is still zero
-    // (the first block)
-    if (blk > 0 && __ballot(alpha != 1.f)) {
-      float al[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) al[r] = __shfl(alpha, 4 * qd + r, 64);
-#pragma unroll
-      for (int dt = 0; dt < kMlaDl / 16; ++dt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[dt][r] *= al[r];
-    }
-    // O += P V: k index 8 qd + j <-> token 32 s2 + 4 qd + j (j < 4), 32 s2 + 16 + 4 qd + j - 4 (j >= 4)
-#pragma unroll
-    for (int s2 = 0; s2 < kMlaBT / 32; ++s2) {
-      bf16x8_t pa;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pa[r] = __builtin_bit_cast(__bf16, f32_bf16(p[2 * s2][r]));
-        pa[4 + r] = __builtin_bit_cast(__bf16, f32_bf16(p[2 * s2 + 1][r]));
-      }
-      // V fragments in batches of VB column tiles, double-buffered like K
-      constexpr int VB = 8, NVB = kMlaDl / 16 / VB;
-      u32x4_t vv[2][VB];
-      auto read_v = [&](int vb2, u32x4_t (&dst)[VB]) {
-#pragma unroll
-        for (int dd = 0; dd < VB; ++dd) {
-          const uint16_t* vrow = &Vt[bf][(16 * (vb2 * VB + dd) + c) * kVtStride + 32 * s2 + 4 * qd];
-          const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
-          const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
-          dst[dd] = u32x4_t{v0.x, v0.y, v1.x, v1.y};
-        }
-      };
-      read_v(0, vv[0]);
-#pragma unroll
-      for (int vb2 = 0; vb2 < NVB; ++vb2) {
-        if (vb2 + 1 < NVB) read_v(vb2 + 1, vv[(vb2 + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int dd = 0; dd < VB; ++dd)
-          o[vb2 * VB + dd] = mfma_bf16(pa, __builtin_bit_cast(bf16x8_t, vv[vb2 & 1][dd]), o[vb2 * VB + dd]);
-        __builtin_amdgcn_sched_barrier(0);
+    if (more) {
+      if constexpr (FP8) {
+        wait_stage(min(2, nblk - blk - 2));  // block blk + 1's copies (of every wave) have landed
+        convert_fp8(blk + 1);
+      } else {
+        fill_bf16(blk + 1);
       }
     }
-    if (more) fill(bf ^ 1, cid, crid);
   }
-  // partials: O rows are heads 16 hw + 4 qd + r, columns 16 dt + c
-  float* po = part_o + (((int64_t)b * S + split) * H) * kMlaDl;
+  // partial O in MFMA tile order: part_o[b][split][head tile][column tile][lane][4]
+  // (rows = heads 16 tile + 4 qd + r, column 16 tile + c)
+  float* po = part_o + ((int64_t)b * S + split) * (H / 16) * (kMlaDt * 256);
 #pragma unroll
-  for (int dt = 0; dt < kMlaDl / 16; ++dt)
+  for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) po[(int64_t)(16 * hw + 4 * qd + r) * kMlaDl + 16 * dt + c] = o[dt][r];
-  if (qd == 0) {
-    float* pml = part_ml + (((int64_t)b * S + split) * H + head) * 2;
-    pml[0] = m_run;
-    pml[1] = l_run;
+    for (int dl = 0; dl < DTW; ++dl)
+      *reinterpret_cast<f32x4_t*>(po + (((int64_t)(blockIdx.z * HT + ht) * kMlaDt + dt0 + dl) * 64 + lane) * 4) =
+          o[ht][dl];
+  if (scorer && c == 0) {
+    float* pml = part_ml + (((int64_t)b * S + split) * H + 16 * hw + 4 * qd) * 2;
+    *reinterpret_cast<f32x4_t*>(pml) = f32x4_t{m_run[0], l_run[0], m_run[1], l_run[1]};
+    *reinterpret_cast<f32x4_t*>(pml + 4) = f32x4_t{m_run[2], l_run[2], m_run[3], l_run[3]};
   }
 }
 
-// Merge the splits of one (row, head) with the sink term and normalize: one
-// wave turns the split maxima/sums into weights, then each thread blends
-// four consecutive output columns over the splits.
-__global__ void __launch_bounds__(128) mla_combine_kernel(const float* __restrict__ part_o,
+// Merge the splits of one (row, 16-head tile, 16-column tile) with the sink
+// term and normalize.  Each wave turns the split maxima/sums of four heads
+// into weights (lane = split); then wave w blends splits w, w + 4, ... of the
+// tile's 64 x 4 partial values, and wave 0 sums the four and writes bf16.
+__global__ void __launch_bounds__(256) mla_combine_kernel(const float* __restrict__ part_o,
                                                           const float* __restrict__ part_ml,
                                                           const float* __restrict__ sink, uint16_t* __restrict__ out,
                                                           int H, int S) {
-  __shared__ float wgt[64];
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  if (tid < 64) {
-    const bool ok = tid < S;
-    const float m = ok ? part_ml[(((int64_t)b * S + tid) * H + h) * 2] : -INFINITY;
-    const float l = ok ? part_ml[(((int64_t)b * S + tid) * H + h) * 2 + 1] : 0.f;
+  __shared__ float wgt[kMlaMaxSplits][16];
+  __shared__ f32x4_t red[4][64];
+  const int dt = blockIdx.x, ht = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int hh = 4 * wv + k, h = 16 * ht + hh;
+    const bool ok = lane < S;
+    const float m = ok ? part_ml[(((int64_t)b * S + lane) * H + h) * 2] : -INFINITY;
+    const float l = ok ? part_ml[(((int64_t)b * S + lane) * H + h) * 2 + 1] : 0.f;
     float M = m;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     const float e = (m == -INFINITY) ? 0.f : __expf(m - M);
     const float lsum = wave_sum_f32(l * e) + ((sink && M != -INFINITY) ? __expf(sink[h] - M) : 0.f);
-    wgt[tid] = (M == -INFINITY) ? 0.f : e / lsum;
+    if (ok) wgt[lane][hh] = (M == -INFINITY) ? 0.f : e / lsum;
   }
   __syncthreads();
-  const int d = 4 * tid;
+  const int hq = lane >> 4;  // rows 4 hq + r of the tile
+  const int64_t sstride = (int64_t)(H / 16) * kMlaDt * 256;
+  const float* po = part_o + (int64_t)b * S * sstride + ((int64_t)ht * kMlaDt + dt) * 256 + lane * 4;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  const float* po = part_o + ((int64_t)b * S * H + h) * kMlaDl + d;
-#pragma unroll 8
-  for (int s = 0; s < S; ++s) {
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(po + (int64_t)s * H * kMlaDl);
-    acc += wgt[s] * v;
+#pragma unroll 4
+  for (int s = wv; s < S; s += 4) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(po + s * sstride);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += wgt[s][4 * hq + r] * v[r];
   }
-  uint16_t* dst = out + ((int64_t)b * H + h) * kMlaDl + d;
-  const uint32_t w0 = (uint32_t)f32_bf16(acc[0]) | ((uint32_t)f32_bf16(acc[1]) << 16);
-  const uint32_t w1 = (uint32_t)f32_bf16(acc[2]) | ((uint32_t)f32_bf16(acc[3]) << 16);
-  *reinterpret_cast<uint2*>(dst) = uint2{w0, w1};
+  red[wv][lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+    const f32x4_t v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      out[((int64_t)b * H + 16 * ht + 4 * hq + r) * kMlaDl + 16 * dt + (lane & 15)] = f32_bf16(v[r]);
+  }
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1243,7 +1353,18 @@ static int mla_splits(int64_t b, int64_t topk) {
   int64_t s = (128 + b - 1) / b;
   s = std::min<int64_t>(s, blocks);
   s = std::min<int64_t>(s, 32);
+  // a split's ids must fit the LDS id buffer
+  s = std::max<int64_t>(s, (blocks + kMlaMaxChunk / kMlaBT - 1) / (kMlaMaxChunk / kMlaBT));
+  static_assert(32 <= kMlaMaxSplits, "the combine kernel weighs at most kMlaMaxSplits splits");
   return (int)std::max<int64_t>(s, 1);
+}
+// head tiles per workgroup: as many as divide the heads (at most 4), fewer
+// while the grid would leave most CUs idle
+static int mla_head_tiles(int64_t b, int64_t h, int S) {
+  int ht = 4;
+  while (ht > 1 && (h / 16) % ht != 0) --ht;
+  while (ht > 1 && (h / 16) % (ht / 2) == 0 && (int64_t)S * b * (h / (16 * ht)) < 128) ht /= 2;
+  return ht;
 }
 static size_t mla_ws(int64_t b, int64_t h, int64_t topk, char* base, MlaWs* w) {
   const int64_t S = mla_splits(b, topk);
@@ -1352,20 +1473,20 @@ static int launch_mla(const uint16_t* q, const MlaKv& kv, const float* sink, con
   const int S = mla_splits(rows, topk);
   const int blocks = (int)((topk + kMlaBT - 1) / kMlaBT);
   const int chunk = ((blocks + S - 1) / S) * kMlaBT;
-  const int nw = h >= 64 ? 4 : (int)(h / 16);
-  dim3 grid((unsigned)S, (unsigned)rows, (unsigned)(h / (16 * nw)));
-  switch (nw) {
-#define MLA_CASE(NWV)                                                                                                  \
-  case NWV:                                                                                                            \
-    hipLaunchKernelGGL((mla_decode_split_kernel<NWV, FP8, DR>), grid, dim3(NWV * 64), 0, st, q, kv, idx, ws.part_o,  \
+  const int ht = mla_head_tiles(rows, h, S);
+  dim3 grid((unsigned)S, (unsigned)rows, (unsigned)(h / (16 * ht)));
+  switch (ht) {
+#define MLA_CASE(HTV)                                                                                                  \
+  case HTV:                                                                                                            \
+    hipLaunchKernelGGL((mla_decode_split_kernel<HTV, FP8, DR>), grid, dim3(256), 0, st, q, kv, idx, ws.part_o,       \
                        ws.part_ml, (int)topk, softmax_scale, chunk);                                                   \
     break;
     MLA_CASE(1) MLA_CASE(2) MLA_CASE(3) MLA_CASE(4)
 #undef MLA_CASE
   }
   MOSAIC_LAUNCH_CHECK("mla_decode_split");
-  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)h, (unsigned)rows), dim3(128), 0, st, ws.part_o, ws.part_ml,
-                     sink, out, (int)h, S);
+  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)kMlaDt, (unsigned)(h / 16), (unsigned)rows), dim3(256), 0, st,
+                     ws.part_o, ws.part_ml, sink, out, (int)h, S);
   MOSAIC_RETURN_LAUNCH("mla_sparse_decode");
 }
 
@@ -1373,8 +1494,9 @@ static int check_mla_common(int64_t rows, int64_t h, int64_t n, int64_t topk, in
                             size_t workspace_bytes) {
   MOSAIC_CHECK_ARG(h >= 16 && h <= 256 && h % 16 == 0 && (h <= 64 || h % 64 == 0),
                    "mla_sparse_decode: heads %lld (16, 32, 48, 64 or a multiple of 64 up to 256)", (long long)h);
-  MOSAIC_CHECK_ARG(rows >= 0 && rows <= 65535 && n >= 0 && n < (1ll << 31) && topk >= 0 && topk < (1ll << 24),
-                   "mla_sparse_decode: shape out of range");
+  MOSAIC_CHECK_ARG(rows >= 0 && rows <= 65535 && n >= 0 && n < (1ll << 31) && topk >= 0 &&
+                       topk <= (int64_t)kMlaMaxSplits * kMlaMaxChunk,
+                   "mla_sparse_decode: shape out of range (topk at most %d)", kMlaMaxSplits * kMlaMaxChunk);
   MOSAIC_CHECK_ARG(rows_per_kv >= 1 && rows % rows_per_kv == 0, "mla_sparse_decode: rows %lld, rows_per_kv %lld",
                    (long long)rows, (long long)rows_per_kv);
   const size_t need = mla_ws(rows, h, topk, nullptr, nullptr);

@@ -188,7 +188,9 @@ def _mla(rng, b, h, n, t, sb, masked=0.0):
                                                      (2, 128, 3000, 2048, 512, False, 0.1),
                                                      (3, 64, 500, 300, 64, True, 0.3),
                                                      (1, 16, 100, 64, 128, True, 0.0),
-                                                     (2, 32, 80, 20, 64, True, 0.2)])
+                                                     (2, 32, 80, 20, 64, True, 0.2),
+                                                     (2, 48, 300, 100, 64, True, 0.1),
+                                                     (1, 128, 5000, 300, 64, False, 0.0)])
 def test_mla_fp8_vs_oracle(dev, b, h, n, t, sb, sink, masked):
     from mosaic_amd import ops
     rng = np.random.default_rng(b * 1000 + t)
@@ -199,6 +201,24 @@ def test_mla_fp8_vs_oracle(dev, b, h, n, t, sb, sink, masked):
     out = ops.mla_sparse_decode(qd.to(torch.bfloat16), latd, lsd, rd.to(torch.bfloat16), idxd, scale,
                                 None if snk is None else torch.from_numpy(snk).to(dev))
     _close(out.float().cpu().numpy(), D.mla_sparse_decode(q, lat, ls, rope, snk, idx, scale, sb))
+
+
+def test_mla_wide_score_range(dev):
+    """Scores rising by over a hundred nats along the token order (the rope part
+    grows 300-fold): every head's running maximum moves past the lazy margin
+    about six times, within a split and across splits."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(33)
+    b, h, n, t = 2, 64, 3000, 1024
+    q, lat, ls, rope, idx = _mla(rng, b, h, n, t, 64)
+    ramp = np.linspace(0.2, 60.0, n).astype(np.float32)
+    rope = C.round_bf16(rope * ramp[None, :, None])
+    idx = np.sort(idx, axis=1).astype(np.int32)
+    snk = rng.standard_normal(h).astype(np.float32)
+    qd, latd, lsd, rd, idxd = _t(dev, q, lat, ls, rope, idx)
+    out = ops.mla_sparse_decode(qd.to(torch.bfloat16), latd, lsd, rd.to(torch.bfloat16), idxd, 0.1,
+                                torch.from_numpy(snk).to(dev))
+    _close(out.float().cpu().numpy(), D.mla_sparse_decode(q, lat, ls, rope, snk, idx, 0.1, 64))
 
 
 def test_mla_all_masked_row_is_zero(dev):
