@@ -39,9 +39,8 @@
 // sparse_attn_ref, mosaicvm/model/dsa.py:214-242): per (row, head)
 //   o = sum_t bf16(p_t) * v_t / (sum_t p_t + exp(sink - m)),  p_t = exp(s_t - m),
 //   s_t = q . kv_t * scale over the selected t (index -1 masked), kv_t = [latent
-//   e4m3 * scale -> bf16, rope bf16], v_t = latent.  Online softmax over 64-token
-//   blocks (the reference's block size) in each of several token splits, then a
-//   combine over splits.
+//   e4m3 * scale -> bf16, rope bf16], v_t = latent.  Online softmax over 32-token
+//   blocks in each of several token splits, then a combine over splits.
 #include <algorithm>
 
 #include "common.h"

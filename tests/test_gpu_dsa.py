@@ -108,7 +108,8 @@ def test_indexer_bounds_enclose_wide_product_spans(dev):
     np.testing.assert_array_equal(idx, D.indexer_topk(q, qs, k, ks, w, 512))
 
 
-@pytest.mark.parametrize("b,l,topk", [(2, 32768, 2048), (1, 5000, 512), (3, 1000, 2048), (1, 64, 16)])
+@pytest.mark.parametrize("b,l,topk", [(2, 32768, 2048), (1, 5000, 512), (3, 1000, 2048), (1, 64, 16),
+                                        (2, 70000, 2048)])
 def test_indexer_topk_bit_exact(dev, b, l, topk):
     from mosaic_amd import ops
     rng = np.random.default_rng(l + topk)
