@@ -357,7 +357,7 @@ size_t mosaic_mla_decode_workspace_bytes(int64_t b, int64_t h, int64_t topk);
  *   out [b, h, d_latent] bf16 = sum_t bf16(exp(s_t - m)) v_t / (sum_t exp(s_t - m)
  *   + exp(sink - m)), v_t = the latent part.  A row with no valid entry gives 0.
  *   d_latent = 512, d_rope = 64, h in {16, 32, 48, 64} or a multiple of 64 up
- *   to 256, scale_block a power of two in 16..512. */
+ *   to 256, scale_block a power of two in 16..512, topk <= 65536. */
 int mosaic_mla_sparse_decode(const uint16_t* q, const uint8_t* kv_latent, const float* kv_scale,
                              const uint16_t* kv_rope, const float* sink, const int32_t* idx, uint16_t* out, int64_t b,
                              int64_t h, int64_t n, int64_t topk, int64_t d_latent, int64_t d_rope,
@@ -376,6 +376,32 @@ int mosaic_mla_sparse_decode_bf16(const uint16_t* q, const uint16_t* kv, const f
                                   uint16_t* out, int64_t rows, int64_t h, int64_t n, int64_t topk, int64_t d,
                                   int64_t rows_per_kv, float softmax_scale, void* workspace, size_t workspace_bytes,
                                   void* stream);
+
+/* KV-cache writer of the DSA attention step (the kv rows of ExactAttention.forward
+ * and attention_core, mosaicvm/model/dsa_layers.py:550-553 and 579-582, stored
+ * as _core_body stores them, :510-534): kv [rows, d] bf16 = [d - rope
+ * non-rope dims | rope dims]; row r goes to cache row slots[r] (slots NULL:
+ * row r; a slot outside [0, n) skips the row).  The non-rope dims get
+ * act_quant_sim (mosaicvm/model/dsa.py:81-93): per 64 values
+ * s = 2^ceil(log2(max(amax, 1e-4) / 448)), codes = e4m3(clamp(x / s, +-448)).
+ * Either cache_bf16 [n, d] receives bf16(codes * s) | rope (the reference's
+ * bf16 cache), or codes [n, d - rope] e4m3, scales [n, (d - rope) / 64] fp32
+ * and rope_cache [n, rope] bf16 receive them (the FP8 cache
+ * mosaic_mla_sparse_decode reads).  d - rope a multiple of 64, at most 512;
+ * rope a multiple of 8. */
+int mosaic_dsa_kv_write(const uint16_t* kv, const int32_t* slots, int64_t rows, int64_t d, int64_t rope, int64_t n,
+                        uint16_t* cache_bf16, uint8_t* codes, float* scales, uint16_t* rope_cache, void* stream);
+
+/* Gather indices of one decode step per query row, replacing window_topk_idxs
+ * + compress_topk_idxs_static (mosaicvm/model/dsa.py:185-212) concatenated as
+ * in _core_body (mosaicvm/model/dsa_layers.py:479-481): pos [rows] int32
+ * absolute positions; out [rows, window + nc] int32 = the ring slots (position
+ * % window) of positions max(0, p - window + 1) .. p, oldest first, -1 padded
+ * while p < window - 1, then either cidx [rows, nc] (the indexer's picks,
+ * already offset) or, with cidx NULL, offset + 0 .. offset + (p + 1) / ratio - 1,
+ * -1 padded to nc. */
+int mosaic_dsa_decode_indices(const int32_t* pos, int64_t rows, int64_t window, const int32_t* cidx, int64_t nc,
+                              int64_t ratio, int64_t offset, int32_t* out, void* stream);
 
 #ifdef __cplusplus
 }

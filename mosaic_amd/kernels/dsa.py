@@ -21,6 +21,12 @@
   from already projected FP8 q and the FP8 compressed key cache: the causal
   prefill mask at ``start_pos == 0``, ``min(index_topk, end_pos // ratio)``
   picks, ``-1`` for masked picks, ``+ offset`` otherwise.
+* ``DecodeKVCache`` -- the decode-step state of one DSA attention layer
+  (``kv_cache`` of ``ExactAttention``, ``mosaicvm/model/dsa_layers.py:393-400``,
+  and the ``s == 1`` branch of ``_core_body``, ``:469-481,517-521``): a ring of
+  ``window`` kv rows followed by the compressed rows; ``step`` writes the new
+  kv row (act_quant_sim of the non-rope dims) into its ring slot, builds the
+  window + compressed gather indices and attends with the sink.
 """
 from __future__ import annotations
 
@@ -139,3 +145,66 @@ def dsa_decode_attention(q, k_index, v_full, topk: int = CANDIDATES, scale: floa
     if scale is None:
         scale = 1.0 / (index_dim ** 0.5)
     return ops.dsa_head_attention(q.contiguous(), k_index.contiguous(), v_full.contiguous(), topk, scale)
+
+
+class DecodeKVCache:
+    """One sequence's DSA decode cache: rows 0 .. window-1 are the kv ring (slot
+    = position % window), rows window .. window + n_compressed - 1 the
+    compressed entries (the compressor writes them; ``write_compressed``).
+
+    ``fp8=False``: a bf16 [window + n_compressed, head_dim] cache, the
+    reference's own (V4 geometry: head_dim 512 with the rope in the last 64,
+    V = the whole row).  ``fp8=True``: e4m3 codes + fp32 scales per 64 + bf16
+    rope for the 512 + 64 MLA layout (head_dim 576, V = the 512 latent dims),
+    the cache ``ops.mla_sparse_decode`` reads; the attended values are the same
+    bf16 numbers either way."""
+
+    def __init__(self, head_dim: int = 512, window: int = 128, n_compressed: int = 0, rope: int = 64,
+                 fp8: bool = False, device="cuda"):
+        if fp8 and (head_dim - rope != 512 or rope != 64):
+            raise ValueError("the FP8 cache holds the 512 + 64 MLA layout")
+        self.head_dim, self.window, self.n_compressed, self.rope, self.fp8 = head_dim, window, n_compressed, rope, fp8
+        n = window + n_compressed
+        dev = torch.device(device)
+        if fp8:
+            self.cache = (torch.zeros(n, head_dim - rope, dtype=torch.uint8, device=dev),
+                          torch.zeros(n, (head_dim - rope) // 64, dtype=torch.float32, device=dev),
+                          torch.zeros(n, rope, dtype=torch.bfloat16, device=dev))
+        else:
+            self.cache = torch.zeros(n, head_dim, dtype=torch.bfloat16, device=dev)
+
+    def write_window(self, kv: torch.Tensor, start_pos: int) -> None:
+        """kv [1, head_dim] bf16 of position ``start_pos`` -> ring slot start_pos % window."""
+        slots = torch.full((kv.shape[0],), start_pos % self.window, dtype=torch.int32, device=kv.device)
+        ops.dsa_kv_write(kv, self.cache, slots, self.rope)
+
+    def write_compressed(self, ckv: torch.Tensor, first: int = 0) -> None:
+        """Compressed kv rows [c, head_dim] -> compressed entries first .. first + c - 1."""
+        if first < 0 or first + ckv.shape[0] > self.n_compressed:
+            raise ValueError(f"compressed rows {first}..{first + ckv.shape[0]} beyond {self.n_compressed}")
+        slots = torch.arange(self.window + first, self.window + first + ckv.shape[0], dtype=torch.int32,
+                             device=ckv.device)
+        ops.dsa_kv_write(ckv, self.cache, slots, self.rope)
+
+    def attend(self, q: torch.Tensor, start_pos: int, softmax_scale: float, sink: torch.Tensor | None = None,
+               cidx: torch.Tensor | None = None, ratio: int = 4) -> torch.Tensor:
+        """q [1, H, head_dim] bf16 at position start_pos over the window and the
+        compressed entries: the indexer picks ``cidx`` [1, t] (already offset by
+        window) or, without them, every compressed entry up to (p + 1) // ratio."""
+        pos = torch.full((q.shape[0],), start_pos, dtype=torch.int32, device=q.device)
+        idx = ops.dsa_decode_indices(pos, self.window, cidx, nc=None if cidx is not None else self.n_compressed,
+                                     ratio=ratio, offset=self.window)
+        n = self.window + self.n_compressed
+        if self.fp8:
+            codes, scales, rope = self.cache
+            return ops.mla_sparse_decode(q, codes.view(1, n, -1), scales.view(1, n, -1), rope.view(1, n, -1), idx,
+                                         softmax_scale, sink)
+        return _attend(q, self.cache.view(1, n, -1), sink, idx, softmax_scale)
+
+    def step(self, q: torch.Tensor, kv: torch.Tensor, start_pos: int, softmax_scale: float,
+             sink: torch.Tensor | None = None, cidx: torch.Tensor | None = None, ratio: int = 4) -> torch.Tensor:
+        """One decode step: write kv into the ring, then attend (the order of
+        ``_core_body``'s ``s == 1`` branch)."""
+        self.write_window(kv, start_pos)
+        return self.attend(q, start_pos, softmax_scale, sink, cidx, ratio)
+

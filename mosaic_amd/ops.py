@@ -739,3 +739,63 @@ def mla_sparse_decode_bf16(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor,
     _lib.call("mosaic_mla_sparse_decode_bf16", _ptr(q), _ptr(kv), _ptr(sink), _ptr(idx), _ptr(out), rows, h, n, topk,
               d, rows // nb, float(softmax_scale), _ptr(ws), ws.numel(), _stream())
     return out
+
+
+def dsa_kv_write(kv: torch.Tensor, cache, slots: torch.Tensor | None = None, rope: int = 64) -> None:
+    """Write kv rows [R, D] bf16 into a DSA cache with act_quant_sim on the
+    first D - rope dims: ``cache`` is either a bf16 tensor [N, D] (the
+    reference's cache) or (codes [N, D - rope] e4m3/uint8, scales [N, (D -
+    rope) / 64] fp32, rope [N, rope] bf16), the FP8 cache ``mla_sparse_decode``
+    reads.  Row r goes to cache row ``slots[r]`` (default r); slots outside
+    [0, N) skip the row."""
+    kv = _bf16(kv, "kv").contiguous()
+    if kv.dim() != 2:
+        raise ValueError(f"kv must be [R, D], got {tuple(kv.shape)}")
+    rows, d = kv.shape
+    if slots is not None:
+        slots = _cuda(slots, "slots").to(torch.int32).contiguous()
+        if tuple(slots.shape) != (rows,):
+            raise ValueError(f"slots must be [{rows}], got {tuple(slots.shape)}")
+    if isinstance(cache, torch.Tensor):
+        cache = _bf16(cache, "cache")
+        if cache.dim() != 2 or cache.shape[1] != d or not cache.is_contiguous():
+            raise ValueError(f"bf16 cache must be a contiguous [N, {d}], got {tuple(cache.shape)}")
+        n = cache.shape[0]
+        _lib.call("mosaic_dsa_kv_write", _ptr(kv), _ptr(slots), rows, d, rope, n, _ptr(cache), None, None, None,
+                  _stream())
+        return
+    codes, scales, rope_c = cache
+    codes = _u8(codes, "codes")
+    scales = _f32(scales, "scales")
+    rope_c = _bf16(rope_c, "rope")
+    n = codes.shape[0]
+    dn = d - rope
+    if tuple(codes.shape) != (n, dn) or tuple(scales.shape) != (n, dn // 64) or tuple(rope_c.shape) != (n, rope) \
+            or not (codes.is_contiguous() and scales.is_contiguous() and rope_c.is_contiguous()):
+        raise ValueError(f"fp8 cache must be contiguous [N, {dn}] codes, [N, {dn // 64}] scales, [N, {rope}] rope")
+    _lib.call("mosaic_dsa_kv_write", _ptr(kv), _ptr(slots), rows, d, rope, n, None, _ptr(codes), _ptr(scales),
+              _ptr(rope_c), _stream())
+
+
+def dsa_decode_indices(pos: torch.Tensor, window: int, cidx: torch.Tensor | None = None, nc: int | None = None,
+                       ratio: int = 4, offset: int | None = None) -> torch.Tensor:
+    """Gather indices of one decode step: pos [R] int32 absolute positions ->
+    [R, window + nc] int32 = the window ring slots of the last ``window``
+    positions (oldest first, -1 padded), then the indexer picks ``cidx`` [R, nc]
+    (already offset) or, without them, the static compressed list ``offset`` ..
+    ``offset + (p + 1) // ratio - 1`` padded with -1 to ``nc`` entries
+    (``offset`` defaults to ``window``)."""
+    pos = _cuda(pos, "pos").to(torch.int32).contiguous()
+    rows = pos.shape[0]
+    if cidx is not None:
+        cidx = _cuda(cidx, "cidx").to(torch.int32).contiguous()
+        if cidx.dim() != 2 or cidx.shape[0] != rows:
+            raise ValueError(f"cidx must be [{rows}, nc], got {tuple(cidx.shape)}")
+        nc = cidx.shape[1]
+    nc = 0 if nc is None else int(nc)
+    offset = window if offset is None else int(offset)
+    out = torch.empty(rows, window + nc, dtype=torch.int32, device=pos.device)
+    _lib.call("mosaic_dsa_decode_indices", _ptr(pos), rows, window, _ptr(cidx), nc, ratio, offset, _ptr(out),
+              _stream())
+    return out
+

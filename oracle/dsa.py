@@ -30,6 +30,16 @@
   (``act_quant_sim``, ``mosaicvm/model/dsa.py:81-90``); the rope part stays
   bf16 (``mosaicvm/model/dsa_layers.py:553``).  The value is the latent part.
 
+* ``kv_act_quant`` / ``kv_cache_row``: the kv-row act_quant_sim of the DSA
+  step (``mosaicvm/model/dsa.py:81-93``, applied at
+  ``mosaicvm/model/dsa_layers.py:553``): per 64 non-rope values
+  s = 2^ceil(log2(max(amax, 1e-4) / 448)) (quotient rounded to fp32, ceiling
+  from its IEEE bits), codes = e4m3(clamp(x / s, +-448)), stored e4m3 * s;
+  rope dims unchanged.
+* ``decode_indices``: window_topk_idxs + compress_topk_idxs_static for one
+  decoding row (``mosaicvm/model/dsa.py:185-212``), concatenated as
+  ``_core_body`` does (``mosaicvm/model/dsa_layers.py:479-481``).
+
 Pinned by ``tests/test_oracle_dsa.py``: the exact dot against an integer
 (int64) restatement; the scores against an independent float64 formula; the
 top-k against a brute-force full sort with ties; closed forms for the
@@ -162,3 +172,53 @@ def head_topk_attention(q, k, v, topk: int, scale: float):
         p = np.exp(sc - sc.max())
         out[i] = (p[:, None] * v[order, i, :]).sum(0) / p.sum()
     return out, idx
+
+
+def kv_act_quant(x: np.ndarray, block: int = 64):
+    """act_quant_sim of [..., Dn] bf16-valued rows -> (codes u8 [..., Dn],
+    scales fp32 [..., Dn/block], values fp32 [..., Dn] = decode(codes) * s)."""
+    x = np.asarray(x, dtype=np.float32)
+    lead, dn = x.shape[:-1], x.shape[-1]
+    xb = x.reshape(lead + (dn // block, block))
+    amax = np.max(np.abs(xb), axis=-1).astype(np.float32)
+    v = (np.maximum(amax, np.float32(1e-4)) / np.float32(448.0)).astype(np.float32)
+    bits = v.view(np.uint32)
+    e = ((bits >> 23) & 0xFF).astype(np.int64) - 127 + ((bits & 0x7FFFFF) != 0).astype(np.int64)
+    s = ((e + 127).astype(np.uint32) << 23).view(np.float32)
+    y = np.clip(xb / s[..., None], -448.0, 448.0).astype(np.float32)
+    codes = C.e4m3_encode(y).reshape(lead + (dn,))
+    vals = (C.e4m3_decode(codes).reshape(xb.shape) * s[..., None]).astype(np.float32).reshape(lead + (dn,))
+    return codes, s.astype(np.float32), vals
+
+
+def kv_cache_row(kv: np.ndarray, rope: int = 64) -> np.ndarray:
+    """The bf16 cache row of a kv row [..., D]: act_quant_sim of the first D - rope
+    dims, the rope dims unchanged (fp32 holding bf16 values)."""
+    kv = np.asarray(kv, dtype=np.float32)
+    _, _, vals = kv_act_quant(kv[..., :kv.shape[-1] - rope])
+    return np.concatenate([vals, kv[..., kv.shape[-1] - rope:]], axis=-1)
+
+
+def window_indices(p: int, window: int) -> np.ndarray:
+    """Ring slots (position % window) of positions max(0, p - window + 1) .. p,
+    oldest first; while the ring is not full (p < window - 1) the positions
+    0 .. p sit at the front and -1 pads the rest."""
+    if p < window - 1:
+        return np.array([i if i <= p else -1 for i in range(window)], dtype=np.int32)
+    return np.array([(p - window + 1 + i) % window for i in range(window)], dtype=np.int32)
+
+
+def decode_indices(pos, window: int, cidx=None, nc: int = 0, ratio: int = 1, offset: int = 0) -> np.ndarray:
+    """[rows, window + nc]: window_indices, then the row's cidx or the static
+    compressed list offset .. offset + (p + 1) // ratio - 1 padded with -1."""
+    pos = np.asarray(pos, dtype=np.int64)
+    out = np.full((len(pos), window + nc), -1, dtype=np.int32)
+    for r, p in enumerate(pos):
+        out[r, :window] = window_indices(int(p), window)
+        if cidx is not None:
+            out[r, window:] = np.asarray(cidx)[r]
+        else:
+            n = min(nc, (int(p) + 1) // ratio)
+            out[r, window:window + n] = offset + np.arange(n)
+    return out
+

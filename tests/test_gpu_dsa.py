@@ -329,3 +329,95 @@ def test_dsa_decode_attention_vs_oracle(dev, h, d, ctx, topk, dv):
     out_ref, idx_ref = D.head_topk_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), topk, d ** -0.5)
     np.testing.assert_array_equal(idx.cpu().numpy(), idx_ref)
     _close(out.float().cpu().numpy(), out_ref)
+
+
+def _kv_bf16_rows(rng, rows, d, rope=64):
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    mags = np.float32(2.0) ** rng.integers(-20, 12, size=(rows, d // 64)).astype(np.float32)
+    x = x * np.repeat(mags, 64, axis=1)[:, :d]
+    x[0, :64] = 0.0
+    x[1, 5] = 448.0 * 2.0 ** -3
+    return C.round_bf16(x)
+
+
+@pytest.mark.parametrize("d", [512, 576])
+def test_kv_write_bf16_cache_bit_exact(dev, d):
+    from mosaic_amd import ops
+    rng = np.random.default_rng(d + 1)
+    rows, n = 37, 50
+    kv = _kv_bf16_rows(rng, rows, d)
+    slots = rng.permutation(n)[:rows].astype(np.int32)
+    slots[3] = -1      # skipped
+    slots[4] = n + 7   # out of range: skipped
+    cache = torch.full((n, d), 7.0, dtype=torch.bfloat16, device=dev)
+    ops.dsa_kv_write(torch.from_numpy(kv).to(dev).to(torch.bfloat16), cache, torch.from_numpy(slots).to(dev))
+    got = cache.float().cpu().numpy()
+    want = np.full((n, d), 7.0, np.float32)
+    rows_ok = [(r, s) for r, s in enumerate(slots) if 0 <= s < n]
+    for r, s in rows_ok:
+        want[s] = D.kv_cache_row(kv[r:r + 1])[0]
+    np.testing.assert_array_equal(got, want)
+
+
+def test_kv_write_fp8_cache_bit_exact(dev):
+    from mosaic_amd import ops
+    rng = np.random.default_rng(3)
+    rows, n = 20, 24
+    kv = _kv_bf16_rows(rng, rows, 576)
+    slots = np.arange(rows, dtype=np.int32)[::-1].copy()
+    codes = torch.zeros(n, 512, dtype=torch.uint8, device=dev)
+    scales = torch.zeros(n, 8, dtype=torch.float32, device=dev)
+    rope = torch.zeros(n, 64, dtype=torch.bfloat16, device=dev)
+    ops.dsa_kv_write(torch.from_numpy(kv).to(dev).to(torch.bfloat16), (codes, scales, rope),
+                     torch.from_numpy(slots).to(dev))
+    wc, ws, _ = D.kv_act_quant(kv[:, :512])
+    np.testing.assert_array_equal(codes.cpu().numpy()[slots], wc)
+    np.testing.assert_array_equal(scales.cpu().numpy()[slots], ws)
+    np.testing.assert_array_equal(rope.float().cpu().numpy()[slots], kv[:, 512:])
+
+
+def test_decode_indices_match_oracle(dev):
+    from mosaic_amd import ops
+    pos = np.array([0, 1, 5, 126, 127, 128, 129, 1000, 65535], dtype=np.int32)
+    got = ops.dsa_decode_indices(torch.from_numpy(pos).to(dev), 128, nc=300, ratio=4).cpu().numpy()
+    np.testing.assert_array_equal(got, D.decode_indices(pos, 128, nc=300, ratio=4, offset=128))
+    rng = np.random.default_rng(4)
+    cidx = rng.integers(-1, 900, size=(len(pos), 512)).astype(np.int32)
+    got2 = ops.dsa_decode_indices(torch.from_numpy(pos).to(dev), 128, torch.from_numpy(cidx).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got2, D.decode_indices(pos, 128, cidx=cidx, nc=512))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_step_against_oracle(dev, fp8):
+    """A decode step of the DSA layer (V4: 64 heads, head_dim 512, window 128,
+    top-512 compressed picks; FP8: the 512 + 64 MLA cache): write the position's
+    kv into the ring, gather window + picks, attend with the sink."""
+    from mosaic_amd.kernels.dsa import DecodeKVCache
+    rng = np.random.default_rng(40 + fp8)
+    d = 576 if fp8 else 512
+    h, win, ncomp, t, p = 64, 128, 1024, 512, 700
+    cache = DecodeKVCache(head_dim=d, window=win, n_compressed=ncomp, fp8=fp8, device=dev)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    hist = C.round_bf16(rng.standard_normal((win, d)).astype(np.float32))
+    ring_pos = np.arange(p - win + 1, p)                      # positions already in the ring
+    cache.write_window(T(hist[:1]).to(torch.bfloat16), 0)      # exercised once, then overwritten
+    for j, q_ in enumerate(ring_pos):
+        cache.write_window(T(hist[j:j + 1]).to(torch.bfloat16), int(q_))
+    comp = C.round_bf16(rng.standard_normal((ncomp, d)).astype(np.float32))
+    cache.write_compressed(T(comp).to(torch.bfloat16))
+    kv_new = C.round_bf16(rng.standard_normal((1, d)).astype(np.float32))
+    q = C.round_bf16(rng.standard_normal((1, h, d)).astype(np.float32))
+    sink = rng.standard_normal(h).astype(np.float32)
+    picks = rng.choice(ncomp, t, replace=False).astype(np.int32) + win
+    picks[::7] = -1
+    scale = d ** -0.5
+    o = cache.step(T(q).to(torch.bfloat16), T(kv_new).to(torch.bfloat16), p, scale, T(sink), T(picks[None]))
+    # oracle cache: ring rows by slot, compressed rows after them
+    ref_cache = np.zeros((win + ncomp, d), np.float32)
+    for j, q_ in enumerate(ring_pos):
+        ref_cache[q_ % win] = D.kv_cache_row(hist[j:j + 1])[0]
+    ref_cache[p % win] = D.kv_cache_row(kv_new)[0]
+    ref_cache[win:] = D.kv_cache_row(comp)
+    idx = D.decode_indices([p], win, cidx=picks[None], nc=t)
+    ref = D.sparse_attn(q, ref_cache[None], sink, idx, scale, dv=512)
+    _close(o.float().cpu().numpy(), ref)

@@ -135,3 +135,63 @@ def test_mla_matches_naive_softmax():
         p = np.exp(s - m)
         ref = (p @ kv[:, :512]) / (p.sum(1) + np.exp(sink - m[:, 0]))[:, None]
         assert np.all(np.abs(o[b] - ref) <= 2e-2 * np.maximum(1, np.abs(ref)))
+
+
+def _kv_rows(rng, rows, dn):
+    """bf16 kv rows whose 64-blocks span tiny, zero, ordinary and large
+    magnitudes, with blocks whose max is exactly 448 * 2^k."""
+    x = rng.standard_normal((rows, dn)).astype(np.float32)
+    mags = np.float32(2.0) ** rng.integers(-20, 12, size=(rows, dn // 64)).astype(np.float32)
+    x = x * np.repeat(mags, 64, axis=1)
+    x[0, :64] = 0.0                 # all-zero block: the 1e-4 floor
+    x[0, 64:128] *= 1e-7            # below the floor
+    x[1, :64] = np.clip(x[1, :64], -1, 1)
+    x[1, 7] = 448.0 * 2.0 ** -3     # max exactly 448 * 2^k
+    x[1, 64:128] = np.clip(x[1, 64:128], -1, 1)
+    x[1, 70] = -448.0 * 2.0 ** 5
+    return C.round_bf16(x)
+
+
+def test_kv_act_quant_matches_torch_restatement():
+    """act_quant_sim as torch writes it (log2 / ceil / pow on fp32 tensors and
+    torch's e4m3 cast), an independent restatement of the bit-level oracle."""
+    import torch
+    rng = np.random.default_rng(12)
+    x = _kv_rows(rng, 40, 448)
+    codes, s, vals = D.kv_act_quant(x)
+    xt = torch.from_numpy(x).view(40, 7, 64)
+    amax = xt.abs().amax(-1, keepdim=True).clamp_min(1e-4)
+    st = torch.pow(2.0, torch.ceil(torch.log2(amax / 448.0)))
+    qt = (xt / st).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    np.testing.assert_array_equal(s, st[..., 0].numpy())
+    np.testing.assert_array_equal(codes, qt.view(torch.uint8).reshape(40, 448).numpy())
+    np.testing.assert_array_equal(vals, (qt.float() * st).to(torch.bfloat16).float().reshape(40, 448).numpy())
+    # the bf16 cache row keeps the rope dims and stores exactly the bf16 values
+    kv = np.concatenate([x[:3], C.round_bf16(rng.standard_normal((3, 64)).astype(np.float32))], 1)
+    row = D.kv_cache_row(kv)
+    np.testing.assert_array_equal(row[:, 448:], kv[:, 448:])
+    np.testing.assert_array_equal(row[:, :448], C.round_bf16(row[:, :448]))
+
+
+def test_window_indices_follow_a_ring_buffer():
+    """Simulate the ring (slot = position % window) and read back the slots of
+    the last `window` positions, oldest first."""
+    w = 8
+    for p in range(0, 40):
+        ring = {}
+        for pos in range(p + 1):
+            ring[pos % w] = pos
+        got = D.window_indices(p, w)
+        listed = [ring[s] for s in got if s >= 0]
+        assert listed == list(range(max(0, p - w + 1), p + 1)), (p, got)
+        assert (got[len(listed):] == -1).all()
+
+
+def test_decode_indices_static_and_given():
+    out = D.decode_indices([3, 40], 8, nc=12, ratio=4, offset=8)
+    np.testing.assert_array_equal(out[0, 8:], [8] + [-1] * 11)           # (3 + 1) // 4 = 1 entry
+    np.testing.assert_array_equal(out[1, 8:], list(range(8, 18)) + [-1, -1])  # 41 // 4 = 10
+    cidx = np.array([[9, 11, -1], [8, 8, 13]], dtype=np.int32)
+    out2 = D.decode_indices([3, 40], 8, cidx=cidx, nc=3)
+    np.testing.assert_array_equal(out2[:, 8:], cidx)
+    np.testing.assert_array_equal(out2[:, :8], out[:, :8])
