@@ -377,6 +377,18 @@ int mosaic_mla_sparse_decode_bf16(const uint16_t* q, const uint16_t* kv, const f
                                   int64_t rows_per_kv, float softmax_scale, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* RMSNorm with the 1x128 activation quantizer fused into its epilogue: the
+ * input side of an A8 linear (linear(), .mosaicvm/source/inference_model.py:
+ * 114-124, act_quant on an RMSNorm.forward output, :197-202) in one pass.
+ * x [m, h] bf16, w [h] fp32: var = fp32(fp64 sum of x^2 / h), r = fp32(1 /
+ * sqrt(var + eps)), y = bf16(w * (x * r)); y [m, h] bf16 is written when
+ * non-NULL; q [m, h] e4m3 and s [m, h/128] f32 are mosaic_act_quant's output
+ * for y with the same mode (0 power of two, 1 max(amax,1e-4)/448, 2 amax/448),
+ * ready for mosaic_mxt16_linear_a8 / mosaic_fp8_gemm.  h % 128 == 0,
+ * h <= 16384. */
+int mosaic_rmsnorm_act_quant(const uint16_t* x, const float* w, float eps, int64_t m, int64_t h, uint16_t* y,
+                             uint8_t* q, float* s, int mode, void* stream);
+
 /* KV-cache writer of the DSA attention step (the kv rows of ExactAttention.forward
  * and attention_core, mosaicvm/model/dsa_layers.py:550-553 and 579-582, stored
  * as _core_body stores them, :510-534): kv [rows, d] bf16 = [d - rope

@@ -106,6 +106,28 @@ def act_quant(x: torch.Tensor, block: int = 128, mode: str = "pow2") -> tuple[to
     return q.view(torch.float8_e4m3fn), s
 
 
+def rmsnorm_act_quant(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6, mode: str = "pow2",
+                      return_y: bool = False):
+    """RMSNorm of x [M, H] bf16 (weight [H]) with the 1x128 act_quant fused into
+    its epilogue -> (e4m3fn codes [M, H], f32 scales [M, H/128]) [, y bf16
+    [M, H]]: the input of ``mxt16_linear_a8(..., prequant=...)`` /
+    ``fp8_block_gemm`` without a bf16 round trip through HBM."""
+    x = _bf16(x, "x").contiguous()
+    if x.dim() != 2:
+        raise ValueError(f"rmsnorm_act_quant expects [M, H], got {tuple(x.shape)}")
+    m, h = x.shape
+    w = _cuda(weight, "weight").to(torch.float32).contiguous()
+    if tuple(w.shape) != (h,):
+        raise ValueError(f"weight must be [{h}], got {tuple(w.shape)}")
+    q = torch.empty(m, h, dtype=torch.uint8, device=x.device)
+    s = torch.empty(m, h // 128, dtype=torch.float32, device=x.device)
+    y = torch.empty(m, h, dtype=torch.bfloat16, device=x.device) if return_y else None
+    _lib.call("mosaic_rmsnorm_act_quant", _ptr(x), _ptr(w), float(eps), m, h, _ptr(y), _ptr(q), _ptr(s),
+              ACT_MODES[mode], _stream())
+    out = (q.view(torch.float8_e4m3fn), s)
+    return out + (y,) if return_y else out
+
+
 def e4m3_decode(codes: torch.Tensor) -> torch.Tensor:
     codes = _u8(codes, "codes")
     out = torch.empty(codes.shape, dtype=torch.float32, device=codes.device)

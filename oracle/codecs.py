@@ -266,3 +266,18 @@ def act_quant(x: np.ndarray, block: int = ACT_BLOCK, mode: str = "pow2"):
         y = (xb / s[..., None]).astype(np.float32)
     y = np.clip(y, -FP8_MAX, FP8_MAX)
     return e4m3_encode(y.reshape(m, k)), s.astype(np.float32)
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """``RMSNorm.forward`` (``.mosaicvm/source/inference_model.py:197-202``) with
+    its reductions pinned: ss = fp64 sum of squares (bf16 inputs square exactly),
+    var = fp32(ss / H), r = fp32(1 / sqrt(fp64(var) + fp64(eps))),
+    y = bf16(fp32(w * fp32(x * r))).  x [M, H] bf16 values; returns bf16 values."""
+    x = np.asarray(x, dtype=np.float32)
+    w = np.asarray(w, dtype=np.float32)
+    ss = np.sum(x.astype(np.float64) ** 2, axis=-1)
+    var = (ss / np.float64(x.shape[-1])).astype(np.float32)
+    r = (1.0 / np.sqrt(var.astype(np.float64) + np.float64(np.float32(eps)))).astype(np.float32)
+    y = (w[None, :] * (x * r[:, None]).astype(np.float32)).astype(np.float32)
+    return round_bf16(y)
+

@@ -188,3 +188,21 @@ def test_act_quant_matches_torch_cast_path():
     xs = (x.view(8, 4, 128) / torch.from_numpy(s)[..., None]).clamp(-448, 448).reshape(8, 512)
     want = xs.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     np.testing.assert_array_equal(q, want)
+
+
+def test_rmsnorm_pins():
+    """Against torch's RMSNorm.forward (fp32 mean, rsqrt) within one bf16 ulp,
+    exactly invariant to power-of-two scaling of x, and the constant-row closed
+    form y = sign(a) * w."""
+    import torch
+    rng = np.random.default_rng(17)
+    x = C.round_bf16(rng.standard_normal((9, 1024)).astype(np.float32) * 3)
+    w = rng.uniform(0.5, 1.5, 1024).astype(np.float32)
+    y = C.rmsnorm(x, w, 1e-6)
+    xt = torch.from_numpy(x)
+    ref = (torch.from_numpy(w) * (xt * torch.rsqrt(xt.square().mean(-1, keepdim=True) + 1e-6))).to(torch.bfloat16)
+    diff = np.abs(y - ref.float().numpy())
+    assert (diff <= np.abs(ref.float().numpy()) * 2.0 ** -7).all()
+    np.testing.assert_array_equal(C.rmsnorm(x * 4.0, w, 0.0), C.rmsnorm(x, w, 0.0))
+    a = np.full((2, 256), -0.375, np.float32)
+    np.testing.assert_array_equal(C.rmsnorm(a, w[:256], 0.0), C.round_bf16(-w[:256])[None].repeat(2, 0))
