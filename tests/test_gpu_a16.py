@@ -433,8 +433,8 @@ def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
                                    (64, 1536, 1536), (100, 320, 1024)])
 def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
     """Dense A8 MXFP4 GEMM at prefill sizes (fp4_gemm, .mosaicvm/source/inference_kernel.py:441-536):
-    256-row tiles through the staged scaled-MFMA kernel when N % 256 == 0 and
-    K % 512 == 0 (the last case falls back to the 16-row kernel)."""
+    256-row tiles through the staged scaled-MFMA kernel when M > 256, N % 256 == 0 and
+    K % 512 == 0 (the 128-, 64- and 100-row cases run the 16-row kernel)."""
     ops = _ops()
     rng = np.random.default_rng(m + n + k + 7)
     p, s = _quant_weights(rng, n, k)
