@@ -69,6 +69,12 @@ __device__ __forceinline__ uint16_t f32_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// LDS written by some lanes of a wave and read back by other lanes of the same
+// wave, with no workgroup barrier between: wait for the wave's LDS operations
+// and keep the compiler from moving the reads above the writes (without the
+// fence it may, since another lane's write is invisible to the C++ model).
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // 128-bit streaming load that bypasses cache allocation (read-once data)
 __device__ __forceinline__ u32x4_t load_nt_u32x4(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));

@@ -496,8 +496,7 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
         terms[wv][c][16 * j + 4 * qd + r] = rr * wvv[j][r];
       }
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the terms are in LDS
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();  // the terms are in LDS
     if (qd == 0 && in.t >= 0) {
       float tv[H];
 #pragma unroll

@@ -174,6 +174,7 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_gateup_kernel(
     const int i = lane + 64 * v;
     if (i < nvec) reinterpret_cast<u32x4_t*>(xs)[i] = xst[v];
   }
+  wave_lds_fence();
   f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
   auto chunk = [&](int ch, auto more) {
 #pragma unroll
@@ -330,6 +331,163 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
   }
 }
 
+// Small-batch down + combine (2 <= M <= kSmallDnRows tokens, after the layout
+// and the grouped gate/up kernels).  The same walk as moe_dec1_down_kernel: a
+// workgroup owns cpw hidden columns, its KS waves take one K part each, and
+// every tile of the list streams through a register ring of DT entries, the
+// shared expert first (its weights need no tile list), then the routed tiles
+// in list order (ascending expert id).  A tile's rows are up to MR tokens: its
+// z rows (this wave's part, 16 bytes a lane a row) ride in the ring with the
+// weights and are written to a wave-private LDS buffer just before use, where
+// the MFMA operand reads them (lane (c, q) reads row min(c, MR - 1); rows past
+// the tile's count repeat its last row and are not used).  Each tile's fresh
+// partial rows 0..MR-1 (the q == 0 lanes) are added to their tokens' running
+// fp32 sums in tile order and the shared partial after them, so the combine
+// order of the reference (ascending expert id, shared last) is kept and y is
+// written directly: no partial buffer, no combine launch.
+constexpr int kSmallDnRows = 4;    // tokens of the small-batch down kernel
+constexpr int kSmallDnTiles = 68;  // tile list entries it stages (M * top_k + M at M = 4, top_k <= 16)
+
+template <int KS, int NSP, int DT, int MR>
+__global__ void __launch_bounds__(KS * 64) moe_small_down_kernel(
+    const uint16_t* __restrict__ z, const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
+    const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, const int32_t* __restrict__ perm_token,
+    const uint8_t* __restrict__ d_p, const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p,
+    const uint8_t* __restrict__ sh_s, uint16_t* __restrict__ y, int M, int H, int I, int E, int has_shared,
+    int cpw) {
+  constexpr int ZW = NSP * 16;  // 16-byte vectors of one z row in a K part
+  __shared__ int s_e[kSmallDnTiles], s_rows[kSmallDnTiles], s_p0[kSmallDnTiles];
+  __shared__ int s_tok[kSmallDnTiles * MR];
+  __shared__ __attribute__((aligned(16))) u32x4_t zs[KS][MR][ZW + 1];  // +1: rows start on different banks
+  __shared__ float red[KS][MR][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int col0 = blockIdx.x * cpw;
+  const int ns = I / 128, sbase = w * NSP, ns4 = (ns + 3) / 4;
+  const bool row_ok = c < cpw;
+  const int row = col0 + (row_ok ? c : cpw - 1);
+  const int gr = row >> 4, l = q * 16 + (row & 15);
+  const uint32_t woff = (uint32_t)gr * ns * 1024u + (uint32_t)sbase * 1024u + (uint32_t)l * 16u;
+  const uint32_t soff = (uint32_t)gr * ns4 * 256u + (uint32_t)(sbase >> 2) * 256u + (uint32_t)l * 4u;
+  const int64_t ebytes = (int64_t)H * (I / 2), sbytes = (int64_t)(H / 16) * ns4 * 256;
+  const int zl = min(lane, ZW - 1);
+  u32x4_t r_w[DT][NSP];
+  uint32_t r_s[DT];
+  u32x4_t r_z[DT][MR];
+  // ring entry t: the shared expert (t == 0 with has_shared, the list's last
+  // tile) or routed list tile t - has_shared; padded entries (t >= nt) get
+  // scale 0 and are not accumulated
+  auto list_index = [&](int t, int nt) { return t >= nt ? 0 : (has_shared ? (t == 0 ? nt - 1 : t - 1) : t); };
+  // a padded entry reads one fixed 1 KB block (cache hits, no HBM bytes)
+  auto load_w = [&](int li, bool shared_t, bool pad, u32x4_t (&wt)[NSP], uint32_t& sv) {
+    const int e = shared_t ? E : s_e[li];
+    const uint8_t* wp = pad ? d_p : (e == E ? sh_p : d_p + (int64_t)e * ebytes);
+    const uint8_t* sp = pad ? d_s : (e == E ? sh_s : d_s + (int64_t)e * sbytes);
+    const uint32_t wo = pad ? (uint32_t)lane * 16u : woff, so = pad ? (uint32_t)lane * 4u : soff;
+    const uint32_t step = pad ? 0u : 1024u;
+#pragma unroll
+    for (int u = 0; u < NSP; ++u) wt[u] = load_nt_u32x4(wp + wo + u * step);
+    sv = *reinterpret_cast<const uint32_t*>(sp + so);
+  };
+  auto load_z = [&](int li, u32x4_t (&zt)[MR]) {
+    const int rows = s_rows[li], p0 = s_p0[li];
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const int pos = p0 + max(min(i, rows - 1), 0);
+      zt[i] = reinterpret_cast<const u32x4_t*>(z + (int64_t)pos * I + (int64_t)sbase * 128)[zl];
+    }
+  };
+  // 1. the shared expert's weights need no tile list: issued first
+  if (has_shared) load_w(0, true, false, r_w[0], r_s[0]);
+  // 2. the tile list (rows, first position and the tokens of its rows) -> LDS
+  const int nt = n_tiles[0];
+  for (int i = threadIdx.x; i < nt; i += KS * 64) {
+    const int rows = tile_rows[i], p0 = tile_p0[i];
+    s_e[i] = tile_expert[i];
+    s_rows[i] = rows;
+    s_p0[i] = p0;
+#pragma unroll
+    for (int mm = 0; mm < MR; ++mm) s_tok[i * MR + mm] = perm_token[p0 + max(min(mm, rows - 1), 0)];
+  }
+  __syncthreads();
+  // 3. ring prologue
+  if (nt > 0) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const int li = list_index(d, nt);
+      if (!(has_shared && d == 0)) load_w(li, false, d >= nt, r_w[d], r_s[d]);
+      load_z(li, r_z[d]);
+    }
+  }
+  float ysum[MR], ysh[MR];
+#pragma unroll
+  for (int mm = 0; mm < MR; ++mm) ysum[mm] = ysh[mm] = 0.f;
+  const int nchunks = (nt + DT - 1) / DT;
+  auto chunk = [&](int ch, auto more) {
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const int t = ch * DT + d;
+      const bool real = t < nt;
+      const bool shared_t = has_shared && t == 0;
+      const int li = list_index(t, nt);
+      // this tile's z rows -> the wave's LDS rows (the previous tile's reads
+      // were issued before these writes; the fence orders the reads after them)
+      if (lane < ZW) {
+#pragma unroll
+        for (int i = 0; i < MR; ++i) zs[w][i][lane] = r_z[d][i];
+      }
+      wave_lds_fence();
+      const u32x4_t* zr = zs[w][min(c, MR - 1)];
+      f32x4_t part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < NSP; ++u) {
+        u32x4_t xv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xv[k] = zr[16 * u + 4 * q + k];
+        const uint32_t sb = real ? (r_s[d] >> (8 * ((sbase + u) & 3))) & 0xFFu : 0u;
+        dec_mfma(r_w[d][u], sb, xv, part);
+      }
+      // fold the tile's rows into their tokens' sums (selects; the token and
+      // row count are the same in every lane)
+      const int rows = real ? s_rows[li] : 0;
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        const int tok = s_tok[li * MR + i];
+#pragma unroll
+        for (int mm = 0; mm < MR; ++mm) {
+          // both arrays updated by selects: a branch between them would make
+          // the compiler pick an array by pointer and move both to scratch
+          const bool hit = i < rows && tok == mm;
+          ysh[mm] = (hit && shared_t) ? part[i] : ysh[mm];
+          ysum[mm] = (hit && !shared_t) ? ysum[mm] + part[i] : ysum[mm];
+        }
+      }
+      if constexpr (decltype(more)::value) {
+        const int ln = list_index(t + DT, nt);
+        load_w(ln, false, t + DT >= nt, r_w[d], r_s[d]);
+        load_z(ln, r_z[d]);
+      }
+    }
+  };
+  if (nt > 0) {
+    for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
+    chunk(nchunks - 1, std::false_type{});
+  }
+  if (q == 0) {
+#pragma unroll
+    for (int mm = 0; mm < MR; ++mm) red[w][mm][c] = ysum[mm] + ysh[mm];
+  }
+  __syncthreads();
+  if (w == 0 && q == 0 && row_ok) {
+    for (int mm = 0; mm < M; ++mm) {
+      float v = red[0][mm][c];
+#pragma unroll
+      for (int k2 = 1; k2 < KS; ++k2) v += red[k2][mm][c];
+      y[(int64_t)mm * H + row] = f32_bf16(v);
+    }
+  }
+}
+
 // Single A16 linear at one token (y [1, N] = x [1, K] . W^T, W MXT16): a
 // workgroup owns 16 rows of W (8 when N / 16 < 256); its KS waves split K into equal parts,
 // each streaming its part through a register ring of D super-steps with its x
@@ -375,6 +533,7 @@ __global__ void __launch_bounds__(KS * 64) mx_dec1_linear_kernel(const uint16_t*
     const int i = lane + 64 * v;
     if (i < nvec) reinterpret_cast<u32x4_t*>(xs)[i] = xst[v];
   }
+  wave_lds_fence();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   auto chunk = [&](int ch, auto more) {
 #pragma unroll
@@ -570,6 +729,47 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
   MOSAIC_LAUNCH_CHECK("moe_decode1_down");
   mark(4);  // mark 3 is the down kernel's end; the combine is fused into it
   return kOk;
+}
+
+bool moe_small_down_supported(int64_t m, int64_t hidden, int64_t inter, int64_t tile_cap) {
+  return m >= 2 && m <= kSmallDnRows && hidden % 128 == 0 && inter % 128 == 0 && dec_dn_ks(inter / 128) != 0 &&
+         tile_cap <= kSmallDnTiles;
+}
+
+template <int KS, int NSP, int DT>
+static void launch_small_down_k(dim3 grid, int mr, hipStream_t st, const uint16_t* z, const int32_t* te,
+                                const int32_t* tr, const int32_t* tp, const int32_t* nt, const int32_t* ptok,
+                                const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_p, const uint8_t* sh_s,
+                                uint16_t* y, int M, int H, int I, int E, int has_shared, int cpw) {
+  if (mr == 2)
+    hipLaunchKernelGGL((moe_small_down_kernel<KS, NSP, DT, 2>), grid, dim3(KS * 64), 0, st, z, te, tr, tp, nt, ptok,
+                       d_p, d_s, sh_p, sh_s, y, M, H, I, E, has_shared, cpw);
+  else
+    hipLaunchKernelGGL((moe_small_down_kernel<KS, NSP, DT, 4>), grid, dim3(KS * 64), 0, st, z, te, tr, tp, nt, ptok,
+                       d_p, d_s, sh_p, sh_s, y, M, H, I, E, has_shared, cpw);
+}
+
+void launch_moe_small_down(const uint16_t* z, const int32_t* tile_expert, const int32_t* tile_rows,
+                           const int32_t* tile_p0, const int32_t* n_tiles, const int32_t* perm_token,
+                           const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_d_p, const uint8_t* sh_d_s,
+                           uint16_t* y, int64_t M, int64_t H, int64_t I, int64_t E, int has_shared, hipStream_t st) {
+  // K parts as the batch-1 down kernel; 8 columns per workgroup when 16 would
+  // give fewer workgroups than CUs
+  const int dn_ks = dec_dn_ks(I / 128), dn_part = (int)(I / 128 / dn_ks);
+  const int cpw = H / 16 >= 256 ? 16 : 8;
+  const dim3 grid((unsigned)(H / cpw));
+  const int mr = M <= 2 ? 2 : 4;
+#define SD_ARGS grid, mr, st, z, tile_expert, tile_rows, tile_p0, n_tiles, perm_token, d_p, d_s, sh_d_p, sh_d_s, y, \
+                (int)M, (int)H, (int)I, (int)E, has_shared, cpw
+  if (dn_ks == 8)
+    launch_small_down_k<8, 4, 3>(SD_ARGS);
+  else if (dn_part == 4)
+    launch_small_down_k<4, 4, 3>(SD_ARGS);
+  else if (dn_part == 2)
+    launch_small_down_k<4, 2, 3>(SD_ARGS);
+  else
+    launch_small_down_k<4, 1, 4>(SD_ARGS);
+#undef SD_ARGS
 }
 
 }  // namespace mosaic

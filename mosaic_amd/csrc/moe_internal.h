@@ -119,6 +119,14 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
                        int64_t K, int has_shared, int func, int renorm, float route_scale, float limit, uint16_t* z,
                        int32_t* tile_expert, int32_t* n_tiles, void* const* marks, hipStream_t st);
 
+// Down + combine for 2..4 tokens after the layout and grouped gate/up kernels
+// (moe_decode.hip): every workgroup walks the whole tile list and writes y.
+bool moe_small_down_supported(int64_t m, int64_t hidden, int64_t inter, int64_t tile_cap);
+void launch_moe_small_down(const uint16_t* z, const int32_t* tile_expert, const int32_t* tile_rows,
+                           const int32_t* tile_p0, const int32_t* n_tiles, const int32_t* perm_token,
+                           const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_d_p, const uint8_t* sh_d_s,
+                           uint16_t* y, int64_t M, int64_t H, int64_t I, int64_t E, int has_shared, hipStream_t st);
+
 // Single MXT16 A16 linear at one token (moe_decode.hip).
 bool linear_decode1_supported(int64_t m, int64_t n, int64_t k);
 void launch_linear_decode1(const uint16_t* x, const uint8_t* pt, const uint8_t* st, uint16_t* y, int64_t n, int64_t k,

@@ -15,8 +15,11 @@
 //  * MXT16 (prepacked, codec.hip): the 64 lanes' blocks of one super-step are
 //    one contiguous 1 KB, scales one contiguous 256 B per 4 super-steps, so
 //    every weight load is a fully coalesced streaming read.
+#include <algorithm>
+
 #include "common.h"
 #include "moe_internal.h"
+#include "route_token.h"
 #include "../../include/mosaic_amd.h"
 
 namespace mosaic {
@@ -146,27 +149,19 @@ __device__ __forceinline__ void t16_ptrs(const uint8_t* pt, const uint8_t* st, i
 }
 
 // ---------------------------------------------------- MoE gate/up + SwiGLU --
-// grid (inter/(8T), tile_cap), KS waves.  Column tiles 0..T/2-1 are gate row
-// groups (j0/16 + t), tiles T/2.. the matching up row groups, so after the K
-// reduction gate and up of one z element sit in the same lane.
+// One workgroup's share of a tile: Column tiles 0..T/2-1 are gate row groups
+// (j0/16 + t), tiles T/2.. the matching up row groups, so after the K
+// reduction gate and up of one z element sit in the same lane.  Row c of the
+// tile is token toks[c] (c < rows) with route weight rw[c]; z row p0 + c.
 template <int T, int KS>
-__global__ void __launch_bounds__(KS * 64) moe_a16_gateup_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ gu_p, const uint8_t* __restrict__ gu_s,
-    const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s, const int32_t* __restrict__ tile_expert,
-    const int32_t* __restrict__ tile_rows, const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles,
-    const int32_t* __restrict__ perm_token, const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H,
-    int I, int E, float limit) {
-  __shared__ f32x4_t red[KS][T][64];
-  const int tile = blockIdx.y;
-  if (tile >= n_tiles[0]) return;
-  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+__device__ __forceinline__ void gateup_tile(const uint16_t* __restrict__ x, const uint8_t* bp, const uint8_t* bs,
+                                            const int32_t* toks, const float* rw, int rows, int p0,
+                                            uint16_t* __restrict__ z, int H, int I, float limit,
+                                            f32x4_t (&red)[KS][T][64]) {
   const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
   const int j0 = blockIdx.x * 8 * T;
-  const int ns = H / 128, ns4 = (ns + 3) / 4;
-  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
-  const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * ebytes;
-  const uint8_t* bs = (e == E) ? sh_s : gu_s + (int64_t)e * sbytes;
+  const int ns = H / 128;
   const uint8_t* wt[T];
   const uint8_t* st[T];
 #pragma unroll
@@ -175,7 +170,7 @@ __global__ void __launch_bounds__(KS * 64) moe_a16_gateup_kernel(
     t16_ptrs(bp, bs, g, ns, lane, wt[t], st[t]);
   }
   const bool xvalid = c < rows;
-  const uint16_t* xrow = x + (int64_t)(xvalid ? perm_token[p0 + c] : 0) * H;
+  const uint16_t* xrow = x + (int64_t)(xvalid ? toks[c] : 0) * H;
   int s0, s1;
   k_slice(ns, ks, KS, s0, s1);
   f32x4_t acc[T];
@@ -195,10 +190,152 @@ __global__ void __launch_bounds__(KS * 64) moe_a16_gateup_kernel(
     for (int r = 0; r < 4; ++r) {
       const int ti = 4 * q + r;
       if (ti < rows) {
-        const float zv = swiglu_f32(g[r], u[r], limit) * perm_weight[p0 + ti];
+        const float zv = swiglu_f32(g[r], u[r], limit) * rw[ti];
         z[(int64_t)(p0 + ti) * I + j0 + 16 * t + c] = f32_bf16(zv);
       }
     }
+  }
+}
+
+// grid (inter/(8T), tile_cap), KS waves: tile blockIdx.y of the layout's list
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) moe_a16_gateup_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ gu_p, const uint8_t* __restrict__ gu_s,
+    const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s, const int32_t* __restrict__ tile_expert,
+    const int32_t* __restrict__ tile_rows, const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles,
+    const int32_t* __restrict__ perm_token, const float* __restrict__ perm_weight, uint16_t* __restrict__ z, int H,
+    int I, int E, float limit) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int tile = blockIdx.y;
+  if (tile >= n_tiles[0]) return;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
+  const int ns4 = (H / 128 + 3) / 4;
+  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
+  const uint8_t* bp = (e == E) ? sh_p : gu_p + (int64_t)e * ebytes;
+  const uint8_t* bs = (e == E) ? sh_s : gu_s + (int64_t)e * sbytes;
+  gateup_tile<T, KS>(x, bp, bs, perm_token + p0, perm_weight + p0, rows, p0, z, H, I, limit, red);
+}
+
+// 2..kSmallGuTokens tokens routed on the device, without a layout launch:
+// grid (inter/(8T), R), KS >= M waves, R rows of workgroups small enough for
+// the whole grid to be resident, so every workgroup routes once.  Wave t
+// routes token t (the arithmetic of the layout kernels, so ids and weights are
+// identical); wave 0 then sorts the M*K picks by (expert id, flat index) as
+// the layout does (positions = ranks; one tile per distinct expert in
+// ascending id, at most one row per token; the shared expert's tile last, its
+// rows at positions M*K.., every pick being valid) into an LDS tile table, and
+// the workgroup takes tiles blockIdx.y, blockIdx.y + R, ...  Workgroup (0, 0)
+// also writes the ids / weights and what the down kernel reads: the tile
+// list, perm_token and perm_weight.
+constexpr int kSmallGuTokens = 4;
+constexpr int kSmallGuTiles = kSmallGuTokens * kRouteMaxTopK + 1;
+constexpr int kSmallGuResidentWgs = 768;  // 3 four-wave workgroups per CU at <= 168 VGPRs
+
+template <int T, int KS>
+__global__ void __launch_bounds__(KS * 64) moe_small_gateup_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ logits, const float* __restrict__ bias,
+    int32_t* __restrict__ ids_out, float* __restrict__ w_out, const uint8_t* __restrict__ gu_p,
+    const uint8_t* __restrict__ gu_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
+    int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_rows, int32_t* __restrict__ tile_p0,
+    int32_t* __restrict__ n_tiles, int32_t* __restrict__ perm_token, float* __restrict__ perm_weight,
+    uint16_t* __restrict__ z, int M, int H, int I, int E, int K, int has_shared, int func, int renorm,
+    float route_scale, float limit) {
+  static_assert(KS >= kSmallGuTokens, "one routing wave per token");
+  __shared__ f32x4_t red[KS][T][64];
+  __shared__ int16_t s_ids[kSmallGuTokens * kRouteMaxTopK];
+  __shared__ float s_w[kSmallGuTokens * kRouteMaxTopK];
+  __shared__ int s_te[kSmallGuTiles], s_rows[kSmallGuTiles], s_p0[kSmallGuTiles];
+  __shared__ int32_t s_tok[kSmallGuTiles][kSmallGuTokens];
+  __shared__ float s_rw[kSmallGuTiles][kSmallGuTokens];
+  __shared__ int s_nt;
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int A = M * K;
+  // 1. routing: wave t routes token t
+  if (ks < M)
+    route_one_token(logits + (int64_t)ks * E, E, K, func, renorm, route_scale, bias, s_ids + ks * K, s_w + ks * K,
+                    nullptr, nullptr);
+  __syncthreads();
+  // 2. wave 0: lane a < A holds pick a; its stable rank by (expert, a), the
+  //    count of its expert, first occurrence, and the rank of its expert among
+  //    the distinct experts -> the tile table
+  if (ks == 0) {
+    const bool va = lane < A;
+    const int ea = va ? s_ids[lane] : 0x7FFF;
+    const float wa = va ? s_w[lane] : 0.f;
+    int rank = 0, cnt = 0, dup = 0;  // dup: earlier picks of the same expert = row in its tile
+    for (int b = 0; b < A; ++b) {
+      const int eb = __builtin_amdgcn_readlane(ea, b);
+      rank += (eb < ea || (eb == ea && b < lane)) ? 1 : 0;
+      cnt += eb == ea ? 1 : 0;
+      dup += (eb == ea && b < lane) ? 1 : 0;
+    }
+    const bool first = dup == 0;
+    const uint64_t fm = __ballot(va && first);
+    int dr = 0;
+    for (int b = 0; b < A; ++b) {
+      const int eb = __builtin_amdgcn_readlane(ea, b);
+      dr += (((fm >> b) & 1ull) && eb < ea) ? 1 : 0;
+    }
+    const int n_routed = __builtin_popcountll(fm);
+    if (va && first) {
+      s_te[dr] = ea;
+      s_rows[dr] = cnt;
+      s_p0[dr] = rank;
+    }
+    // row dup of tile dr: the pick's token and route weight (the picks of one
+    // token are distinct experts, so dup < M)
+    if (va) {
+      s_tok[dr][dup] = lane / K;
+      s_rw[dr][dup] = wa;
+    }
+    if (has_shared && lane < kSmallGuTokens) {
+      s_tok[n_routed][lane] = min(lane, M - 1);
+      s_rw[n_routed][lane] = 1.0f;
+    }
+    if (lane == 0) {
+      if (has_shared) {
+        s_te[n_routed] = E;
+        s_rows[n_routed] = M;
+        s_p0[n_routed] = A;
+      }
+      s_nt = n_routed + has_shared;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      if (va) {
+        ids_out[lane] = ea;
+        w_out[lane] = wa;
+        perm_token[rank] = lane / K;
+        perm_weight[rank] = wa;
+        if (first) {
+          tile_expert[dr] = ea;
+          tile_rows[dr] = cnt;
+          tile_p0[dr] = rank;
+        }
+      }
+      if (has_shared && lane < M) {
+        perm_token[A + lane] = lane;
+        perm_weight[A + lane] = 1.0f;
+      }
+      if (lane == 0) {
+        if (has_shared) {
+          tile_expert[n_routed] = E;
+          tile_rows[n_routed] = M;
+          tile_p0[n_routed] = A;
+        }
+        n_tiles[0] = n_routed + has_shared;
+      }
+    }
+  }
+  __syncthreads();
+  const int ns4 = (H / 128 + 3) / 4;
+  const int64_t ebytes = (int64_t)2 * I * (H / 2), sbytes = (int64_t)(2 * I / 16) * ns4 * 256;
+  const int nt = s_nt;
+  for (int u = blockIdx.y; u < nt; u += gridDim.y) {
+    const int e = s_te[u];
+    const uint8_t* bp = e == E ? sh_p : gu_p + (int64_t)e * ebytes;
+    const uint8_t* bs = e == E ? sh_s : gu_s + (int64_t)e * sbytes;
+    gateup_tile<T, KS>(x, bp, bs, s_tok[u], s_rw[u], s_rows[u], s_p0[u], z, H, I, limit, red);
+    __syncthreads();  // red is rewritten by the next tile
   }
 }
 
@@ -418,6 +555,34 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
                               d_scale, sh_gu_packed, sh_gu_scale, sh_d_packed, sh_d_scale, y, hidden, inter, n_experts,
                               top_k, has_shared, score_func, renorm, route_scale, swiglu_limit, w.z, w.tile_expert,
                               w.n_tiles, stage_events, st);
+  if (logits && m <= kSmallGuTokens && moe_small_down_supported(m, hidden, inter, w.tile_cap)) {
+    // 2..4 tokens routed here: routing and the layout run inside the gate/up
+    // launch, the combine inside the down launch (two launches in all).  The
+    // picks of one token are distinct experts, so a tile has at most one row
+    // per token, as the down kernel assumes.
+    MOSAIC_CHECK_ARG(n_experts >= 1 && n_experts <= kRouteMaxExperts, "moe_a16_forward: E=%lld (1..%d)",
+                     (long long)n_experts, kRouteMaxExperts);
+    MOSAIC_CHECK_ARG(top_k >= 1 && top_k <= kRouteMaxTopK && top_k <= n_experts,
+                     "moe_a16_forward: top_k=%lld (max %d, <= E)", (long long)top_k, kRouteMaxTopK);
+    MOSAIC_CHECK_ARG(score_func >= 0 && score_func <= 2, "moe_a16_forward: score func %d", score_func);
+    mark(1);  // no layout stage: routing is part of gate/up
+    // rows of workgroups: at most one per tile, and few enough for the grid to be resident
+    const int64_t cols = inter / (8 * kGuT);
+    const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(m * top_k + has_shared, kSmallGuResidentWgs / cols));
+    hipLaunchKernelGGL((moe_small_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)cols, (unsigned)rows), dim3(kGuKS * 64), 0,
+                       st, x, logits, route_bias, ids, weights, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale,
+                       w.tile_expert, w.tile_rows, w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)m,
+                       (int)hidden, (int)inter, (int)n_experts, (int)top_k, has_shared, score_func, renorm,
+                       route_scale, swiglu_limit);
+    MOSAIC_LAUNCH_CHECK("moe_small_gateup");
+    mark(2);
+    launch_moe_small_down(w.z, w.tile_expert, w.tile_rows, w.tile_p0, w.n_tiles, w.perm_token, d_packed, d_scale,
+                          sh_d_packed, sh_d_scale, y, m, hidden, inter, n_experts, has_shared, st);
+    MOSAIC_LAUNCH_CHECK("moe_small_down");
+    mark(3);
+    mark(4);  // the combine is fused into the down kernel
+    return kOk;
+  }
   // counts/offsets are not read by the MoE kernels, so small decode batches may
   // take the single-wave layout path
   LayoutOut lo{w.counts, w.offsets, w.perm, w.perm_token, w.perm_weight, w.sorted_ids, w.inv_pos,

@@ -106,8 +106,7 @@ __global__ void __launch_bounds__(256) mx_kn_a16_kernel(const uint16_t* __restri
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<bf16x8_t*>(buf + rr * kKnPitch + (32 * half + 8 * j) * 2) = d[j];
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slice is in LDS before any lane reads it
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();  // the slice is in LDS before any lane reads it
     // A: row c16 of the tile, K 8g .. 8g + 8 of this step
     const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&s_x[c16][32 * s + 8 * g]);
 #pragma unroll

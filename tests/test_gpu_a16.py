@@ -322,6 +322,38 @@ def test_moe_a16_decode1_given_ids_drop_and_duplicate(dev):
     assert_close(y.float().cpu().numpy(), ref, what="moe decode1 given ids")
 
 
+# ---- 2..4 tokens with routing on the device: layout, grouped gate/up, then
+# one down kernel that walks every tile and combines in registers ----
+@pytest.mark.parametrize("m,e,h,inter,k,shared,limit,func", [
+    (2, 16, 512, 512, 4, True, 0.0, "sigmoid"),          # 1 super-step per K part, 2-row buffers
+    (3, 32, 1024, 1024, 8, False, 10.0, "softmax"),      # 2 super-steps per part, no shared expert
+    (4, 64, 2048, 2048, 8, True, 10.0, "sqrtsoftplus"),  # 4 super-steps per part
+    (4, 8, 512, 4096, 2, True, 0.0, "sigmoid"),          # 8 K parts
+    (2, 8, 4096, 512, 8, True, 0.0, "sigmoid"),          # 16-column workgroups; every token picks every expert
+    (4, 8, 1024, 512, 8, True, 10.0, "sigmoid"),         # every tile holds all 4 tokens
+    (4, 256, 512, 512, 16, True, 0.0, "sigmoid")])       # the longest tile list (68 tiles)
+def test_moe_a16_small_batch_down_vs_oracle(dev, m, e, h, inter, k, shared, limit, func):
+    ops = _ops()
+    rng = np.random.default_rng(m * 11 + e + h + inter + k)
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    sh = _make_bank(rng, 1, h, inter) if shared else None
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    gu_b, d_b = ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds))
+    shb = None if sh is None else (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])),
+                                   ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    ws = ops.MoEWorkspace()
+    for rep in range(2):  # two calls in a row with different tokens and routing share the workspace
+        x = _bf16(rng.standard_normal((m, h)))
+        logits = rng.standard_normal((m, e)).astype(np.float32)
+        y, ids, w = ops.moe_a16_forward(x.to(dev), gu_b, d_b, logits=T(logits), top_k=k, shared=shb,
+                                        swiglu_limit=limit, score_func=func, workspace=ws)
+        ids_ref, w_ref = MO.route_topk(logits, k, func)
+        np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+        ref = MO.moe_layer_a16(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds,
+                               shared=None if sh is None else tuple(t[0] for t in sh), swiglu_limit=limit)
+        assert_close(y.float().cpu().numpy(), ref, what=f"moe a16 m={m} small-batch down, call {rep}")
+
+
 @pytest.mark.parametrize("a8", [False, True])
 def test_moe_given_ids_repeated_and_dropped_multi_token(dev, a8):
     """Layout path (M > 1): a repeated expert id in one token counts once per
