@@ -7,8 +7,8 @@ routed experts + 1 shared expert, each gate+up [2*2048, 7168] and down
 and RNE E2M1, then MXT16-prepacked), tokens bf16 N(0, 1), router logits
 N(0, 1), sigmoid scores, top-8, weights renormalized to 1, SwiGLU.  A step is
 one full layer (routing, stable expert sort, gate/up+SwiGLU, down, combine) on
-one batch of M tokens (default M=1; at M=1 the layer is two launches: routing
-fused into gate/up+SwiGLU, then down fused with the combine).  Inputs are
+one batch of M tokens (default M=1; at M=1..4 the layer is two launches:
+routing fused into gate/up+SwiGLU, then down fused with the combine).  Inputs are
 resident in HBM before the timed region.  Three independent 6 GB layer banks
 rotate step by step and the routing changes every step, so a bank's bytes
 (its shared expert included) are read again only after two other layers
@@ -62,7 +62,8 @@ def parse():
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1, 3, 4, 5")
     ap.add_argument("--configs", default="",
                     help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config3_mxfp4_gemm, "
-                         "config4_moe_prefill, config5_dsa to run (default: all)")
+                         "config4_moe_prefill, config5_dsa to run (default: all); config3_vendor_fp8 (the "
+                         "vendor library's FP8 GEMM at the config-3 shapes, a calibration) runs only when named")
     ap.add_argument("--no-headline", action="store_true",
                     help="skip the decode layer (one bank is still built for config 4); for profiling the configs")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -246,6 +247,31 @@ def config3_fp8(torch, ops):
                                       "mfma_frac": round(fl / us / 1e6 / 5000.0, 4),
                                       "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
         del bqs, bq0
+    return out
+
+
+def config3_vendor_fp8(torch, ops):
+    """Calibration, not a path of this build: AMD's hipBLASLt FP8 GEMM (through
+    torch._scaled_mm, one scale per tensor, so no per-128-block rescale; bf16 out)
+    at the config-3 M = 4096 shapes, weights rotating past the MALL as in config 3.
+    It shows what the vendor library reaches on this box for the simpler problem."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(16)
+    one = torch.ones((), device=dev)
+    out = {}
+    for n, k in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (18432, 7168)]:
+        b0 = (torch.randn(n, k, generator=g, device=dev) * 8.0).clamp(-448, 448).to(torch.float8_e4m3fn)
+        nrot = (512 << 20) // (n * k) + 1
+        bs = [b0] + [b0.clone() for _ in range(nrot - 1)]
+        a = (torch.randn(4096, k, generator=g, device=dev) * 8.0).clamp(-448, 448).to(torch.float8_e4m3fn)
+        it = iter(range(10 ** 9))
+        us = _graph_time(torch, lambda: torch._scaled_mm(a, bs[next(it) % nrot].t(), scale_a=one, scale_b=one,
+                                                         out_dtype=torch.bfloat16), nrot, reps=1)
+        fl = 2 * 4096 * n * k
+        out[f"m4096_n{n}_k{k}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                                   "mfma_frac": round(fl / us / 1e6 / 5000.0, 4)}
+        del bs, b0
     return out
 
 
@@ -528,11 +554,21 @@ def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7):
     return out
 
 
+def _gateup_kernel_name(m: int) -> str:
+    """The gate/up kernel the A16 forward launches for M tokens (routing on the device)."""
+    return "moe_dec1_gateup_kernel" if m == 1 else ("moe_small_gateup_kernel" if m <= 4 else "moe_a16_gateup_kernel")
+
+
 def _stage_view(m: int, st: dict) -> dict:
     """Per-stage microseconds of the instrumented pass.  At M = 1 the layer is
     two launches whose dispatches record their own start/end events, so only
     the two kernels are stages (routing is fused into gate/up, the combine
     into down); the other event gaps are dispatch latency, not work."""
+    if 2 <= m <= 4:
+        return {"gateup_kernel_with_routing": round(st["gu_sec"], 2),
+                "down_kernel_with_combine": round(st["down_sec"], 2),
+                "note": "2..4 tokens: two launches (routing in gate/up, the combine in down); "
+                        "the other event gaps are dispatch latency"}
     if m != 1:
         return {k: round(v, 2) for k, v in st.items()}
     return {"gateup_kernel_with_routing": round(st["gu_sec"], 2),
@@ -546,6 +582,18 @@ def _config_fns(torch, ops, banks):
             ("config3_mxfp4_gemm", lambda: config3_mxfp4(torch, ops)),
             ("config4_moe_prefill", lambda: config4_prefill(torch, ops, banks[0])),
             ("config5_dsa", lambda: config5_dsa(torch, ops))]
+
+
+# run only when named in --configs (calibration lines, not BASELINE configs)
+def _optional_config_fns(torch, ops):
+    return [("config3_vendor_fp8", lambda: config3_vendor_fp8(torch, ops))]
+
+
+def _selected_configs(args, torch, ops, banks):
+    names = [v for v in args.configs.split(",") if v]
+    fns = [(n, f) for n, f in _config_fns(torch, ops, banks) if not names or n in names]
+    fns += [(n, f) for n, f in _optional_config_fns(torch, ops) if n in names]
+    return fns
 
 
 def main():
@@ -567,9 +615,7 @@ def main():
     if args.no_headline:
         configs = {}
         if not args.no_configs:
-            for name, fn in _config_fns(torch, ops, banks):
-                if args.configs and name not in args.configs.split(","):
-                    continue
+            for name, fn in _selected_configs(args, torch, ops, banks):
                 print(f"bench.py: {name}", file=sys.stderr, flush=True)
                 configs[name] = fn()
         print(json.dumps({"metric": METRIC, "profiling_run": True, "configs": configs}), flush=True)
@@ -584,9 +630,7 @@ def main():
             sweep[str(mv)]["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     configs = {}
     if not args.no_configs:
-        for name, fn in _config_fns(torch, ops, banks):
-            if args.configs and name not in args.configs.split(","):
-                continue
+        for name, fn in _selected_configs(args, torch, ops, banks):
             print(f"bench.py: {name}", file=sys.stderr, flush=True)
             configs[name] = fn()
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch, ops, banks[0])
@@ -615,7 +659,7 @@ def main():
         "tokens_per_s": round(args.m / (main_r["us_per_layer"] / 1e6), 1),
         "distinct_experts_avg": main_r["distinct_experts_avg"],
         "stage_us": _stage_view(args.m, main_r["stage_us"]),
-        "roofline": {"kernel": "moe_dec1_gateup_kernel" if args.m == 1 else "moe_a16_gateup_kernel", "bound": "hbm",
+        "roofline": {"kernel": _gateup_kernel_name(args.m), "bound": "hbm",
                      "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": round(GATEUP_M1_TRAFFIC_BYTES) if args.m == 1 else None,
