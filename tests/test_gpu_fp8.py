@@ -28,6 +28,10 @@ def _case(rng, m, n, k):
                                    (256, 128, 128), (300, 576, 1024), (1024, 1536, 2048), (513, 700, 384),
                                    (129, 8200, 512), (200, 640, 1536), (96, 1536, 7168), (2304, 7200, 384),
                                    (1024, 16384, 384), (1024, 16384, 2304),
+                                   # persistent big-tile grid with more tiles than CUs: a tile's last scale
+                                   # chunk of 1 / 3 blocks, ragged N, ragged M (the next tile's first stage
+                                   # and scale chunk go out during the current tile's last blocks)
+                                   (4096, 4608, 1152), (2560, 7000, 1408), (4000, 4352, 640),
                                    # split K (tiles under half the GPU): tiled<128> x 8 / x 4, tiled<256> x 3
                                    (128, 576, 7168), (128, 7168, 4096), (4096, 576, 7168),
                                    # decode ring kernel (M <= 16, N >= 4096): full rows, ragged N, uneven K parts;
