@@ -700,7 +700,8 @@ extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16
 }
 
 // Kernel choice of the block GEMM.  kind 0: skinny, 1: tiled<128>, 2: tiled<256>,
-// 3: big tiles, 4: decode ring (M <= 16, wide N).  The tiled kernels split K into S slices (S > 1 needs the
+// 3: big tiles, 4: decode ring (M <= 16 with N >= 4096, or narrower N when K has
+// at least 32 blocks).  The tiled kernels split K into S slices (S > 1 needs the
 // S * M * N * 4-byte partials workspace) when their tiles cover fewer than
 // half of the 256 CUs: S = min(8, 256 / tiles, K-blocks / 4).
 struct Fp8Plan {
