@@ -15,8 +15,8 @@ rotate step by step and the routing changes every step, so a bank's bytes
 (about 420 MB, more than the 256 MB MALL): weights come from HBM.
 
 The timed region replays a HIP graph of the K steps (one replay = exactly K
-layers); the same K steps run eagerly through the Python wrapper are reported
-beside it.  ``value`` is the algorithmic HBM throughput of the layer (every
+layers), three times between synchronizations, and reports the median replay;
+the same K steps run eagerly through the Python wrapper are reported beside it.  ``value`` is the algorithmic HBM throughput of the layer (every
 distinct expert's bytes read once + x + y) in GB/s; ``roofline`` reports the
 gate/up kernel (the dominant one) against 8 TB/s, timed with HIP events that
 the kernel's own dispatch records; ``cpu_baseline`` times the reference's own
@@ -105,8 +105,8 @@ def build_banks(torch, ops, n_banks: int, seed: int = 0):
 def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     """K layer steps at M tokens: eager warmup, the K steps eagerly (reported
     beside the headline), then the K steps captured in one HIP graph and timed
-    by one replay (the headline), then an instrumented eager pass with HIP
-    events at the stage boundaries."""
+    by three replays (the median is the headline), then an instrumented eager
+    pass with HIP events at the stage boundaries."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1000 + seed)
@@ -139,13 +139,18 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
             ids_all.append(step(warmup + i)[1])
     graph.replay()  # untimed: first replay
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record()
-    graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = ev0.elapsed_time(ev1)
+    # three timed replays, each exactly the K steps between synchronizations;
+    # the median is reported (one replay moved by +-3 us per layer run to run)
+    samples = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ev0.record()
+        graph.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        samples.append((ev0.elapsed_time(ev1), time.perf_counter() - t0))
+    samples.sort()
+    gpu_ms, wall = samples[1]
     # instrumented pass over the same steps: HIP events at the stage boundaries,
     # on the kernels' stream (at M = 1 the gate/up and down dispatches record
     # them, so they bracket those kernels' execution); the headline above is
@@ -652,7 +657,7 @@ def main():
                    "inter": I, "experts": E, "top_k": K, "shared_experts": 1, "score": "sigmoid",
                    "contract": "A16 dequant-then-matmul", "weight_layout": "MXT16 prepacked", "banks": N_BANKS,
                    "bank_reuse_distance_bytes": round((N_BANKS - 1) * main_r["layer_bytes_avg"]),
-                   "timing": "one HIP-graph replay of the K steps"},
+                   "timing": "median of three HIP-graph replays, each of exactly the K steps"},
         "us_per_layer": round(main_r["us_per_layer"], 2),
         "eager_us_per_layer": round(main_r["eager_us_per_layer"], 2),
         "hbm_frac": round(main_r["gbs"] / HBM_PEAK_GBS, 4),

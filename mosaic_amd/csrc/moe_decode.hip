@@ -261,8 +261,8 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
   u32x4_t r_w[DT][NSP];
   uint32_t r_s[DT];
   // ring entry t >= has_shared is routed tile t - has_shared; padded entries
-  // (t >= nt) reload routed tile 0 and get scale 0 (selects only: the ring
-  // issues its loads without branches)
+  // (t >= nt) read one fixed 1 KB block (cache hits, no HBM bytes) and get
+  // scale 0 (selects only: the ring issues its loads without branches)
   auto load_tile = [&](int t, u32x4_t (&wt)[NSP], uint32_t& sv) {
     const uint8_t* wp;
     const uint8_t* sp;
@@ -275,9 +275,16 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_down_kernel(
       wp = d_p + (int64_t)e * ebytes;
       sp = d_s + (int64_t)e * sbytes;
     }
+    const bool pad = t >= nt;
+    const uint32_t wo = pad ? (uint32_t)lane * 16u : woff, so = pad ? (uint32_t)lane * 4u : soff;
+    const uint32_t step = pad ? 0u : 1024u;
+    if (pad) {
+      wp = d_p;
+      sp = d_s;
+    }
 #pragma unroll
-    for (int u = 0; u < NSP; ++u) wt[u] = load_nt_u32x4(wp + woff + u * 1024);
-    sv = *reinterpret_cast<const uint32_t*>(sp + soff);
+    for (int u = 0; u < NSP; ++u) wt[u] = load_nt_u32x4(wp + wo + u * step);
+    sv = *reinterpret_cast<const uint32_t*>(sp + so);
   };
   const int nchunks = (nt + DT - 1) / DT;
   if (nt > 0) {
@@ -656,12 +663,16 @@ static int dec_dn_ks(int64_t nsi) {
   if (nsi == 4 || nsi == 8 || nsi == 16) return 4;
   return 0;
 }
+// the batch-1 down kernel: 8 parts of 2 steps at inter 2048 as well (3584 waves
+// instead of 1792 keep more bytes in flight; measured 13.5-13.7 against
+// 13.8-14.2 us at the BASELINE shape)
+static int dec1_dn_ks(int64_t nsi) { return nsi == 16 ? 8 : dec_dn_ks(nsi); }
 
 bool moe_decode1_supported(int64_t m, int64_t hidden, int64_t inter, int64_t top_k, int has_shared) {
   if (m != 1 || top_k < 1 || top_k > kRouteMaxTopK) return false;
   const int64_t nsh = hidden / 128, nsi = inter / 128;
-  if (hidden % 128 || inter % 128 || nsh % kDecGuKS || dec_dn_ks(nsi) == 0) return false;
-  const int64_t gu_part = nsh / kDecGuKS, dn_part = nsi / dec_dn_ks(nsi);
+  if (hidden % 128 || inter % 128 || nsh % kDecGuKS || dec1_dn_ks(nsi) == 0) return false;
+  const int64_t gu_part = nsh / kDecGuKS, dn_part = nsi / dec1_dn_ks(nsi);
   if (gu_part * 16 > 64 * kDecXVMax) return false;                        // x staging registers
   if ((top_k + has_shared) * dn_part * 16 > 64 * kDecZVMax) return false;  // z staging registers (one wave's share or less)
   if ((size_t)(top_k + has_shared) * inter * 2 > 64 * 1024) return false;
@@ -683,7 +694,7 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
   auto ev = [&](int i) { return marks ? (hipEvent_t)marks[i] : (hipEvent_t) nullptr; };
   // routing runs inside the gate/up launch (the layout stage is the dispatch
   // latency); marks 1 and 2 are the gate/up kernel's own start and end
-  const int dn_ks = dec_dn_ks(I / 128);
+  const int dn_ks = dec1_dn_ks(I / 128);
   const int gu_part = (int)(H / 128 / kDecGuKS), dn_part = (int)(I / 128 / dn_ks);
   const int nz = (int)K + has_shared;
   const int gd = dec_depth(gu_part);
@@ -715,7 +726,9 @@ int launch_moe_decode1(const uint16_t* x, const float* logits, const float* bias
     launch_dec1_down_z<KSV, NSPV, 10>(DN_ARGS);          \
   else                                                   \
     launch_dec1_down_z<KSV, NSPV, kDecZVMax>(DN_ARGS);
-  if (dn_ks == 8) {
+  if (dn_ks == 8 && dn_part == 2) {
+    DN_Z(8, 2)
+  } else if (dn_ks == 8) {
     DN_Z(8, 4)
   } else if (dn_part == 4) {
     DN_Z(4, 4)
