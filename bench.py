@@ -66,6 +66,9 @@ def parse():
                          "vendor library's FP8 GEMM at the config-3 shapes, a calibration) runs only when named")
     ap.add_argument("--no-headline", action="store_true",
                     help="skip the decode layer (one bank is still built for config 4); for profiling the configs")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time the K steps eagerly instead of replaying a HIP graph (for counter-collecting "
+                         "profiler passes; the headline line is graph-timed)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the line is printed, copy a buffer of this many MiB device to device three times "
                          "(a plain copy of known size that scales FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -98,11 +101,13 @@ def build_banks(torch, ops, n_banks: int, seed: int = 0):
         sdn = ops.mxt16_prepack(dp[E], ds[E])
         raw = (gp, gs, dp, ds)
         banks.append({"gu": gu, "dn": dn, "shared": (sgu, sdn), "raw": raw})
+        # progress (a counter-collecting profiler makes each set-up launch slow)
+        print(f"bench.py: weight bank {len(banks)}/{n_banks} built", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     return banks
 
 
-def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
+def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int, graph: bool = True):
     """K layer steps at M tokens: eager warmup, the K steps eagerly (reported
     beside the headline), then the K steps captured in one HIP graph and timed
     by three replays (the median is the headline), then an instrumented eager
@@ -123,6 +128,7 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
+    print(f"bench.py: M={m} warmup done", file=sys.stderr, flush=True)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
@@ -131,26 +137,34 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     ev1.record()
     torch.cuda.synchronize()
     eager_ms = ev0.elapsed_time(ev1)
-    # the same K steps in one graph: one replay = exactly K layers
-    graph = torch.cuda.CUDAGraph()
     ids_all = []
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            ids_all.append(step(warmup + i)[1])
-    graph.replay()  # untimed: first replay
-    torch.cuda.synchronize()
-    # three timed replays, each exactly the K steps between synchronizations;
-    # the median is reported (one replay moved by +-3 us per layer run to run)
-    samples = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        ev0.record()
-        graph.replay()
-        ev1.record()
+    if graph:
+        # the same K steps in one graph: one replay = exactly K layers
+        g_k = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_k):
+            for i in range(steps):
+                ids_all.append(step(warmup + i)[1])
+        g_k.replay()  # untimed: first replay
         torch.cuda.synchronize()
-        samples.append((ev0.elapsed_time(ev1), time.perf_counter() - t0))
-    samples.sort()
-    gpu_ms, wall = samples[1]
+        # three timed replays, each exactly the K steps between synchronizations;
+        # the median is reported (one replay moved by +-3 us per layer run to run)
+        samples = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ev0.record()
+            g_k.replay()
+            ev1.record()
+            torch.cuda.synchronize()
+            samples.append((ev0.elapsed_time(ev1), time.perf_counter() - t0))
+        samples.sort()
+        gpu_ms, wall = samples[1]
+        del g_k
+    else:
+        # counter passes: the eager K steps are the timed ones
+        ids_all = [step(warmup + i)[1] for i in range(steps)]
+        torch.cuda.synchronize()
+        gpu_ms, wall = eager_ms, eager_ms / 1e3
+    print(f"bench.py: M={m} timed steps done", file=sys.stderr, flush=True)
     # instrumented pass over the same steps: HIP events at the stage boundaries,
     # on the kernels' stream (at M = 1 the gate/up and down dispatches record
     # them, so they bracket those kernels' execution); the headline above is
@@ -165,7 +179,6 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int):
     layer_bytes = [(u + 1) * EXPERT_BYTES + 2 * m * H * 2 + m * E * 4 for u in distinct]
     gu_bytes = [(u + 1) * GU_BYTES + m * H * 2 + (u + 1) * I * 2 for u in distinct]
     gu_s = sum(t["gu_sec"] for t in times)
-    del graph
     return {
         "m": m,
         "us_per_layer": gpu_ms * 1e3 / steps,
@@ -625,11 +638,11 @@ def main():
                 configs[name] = fn()
         print(json.dumps({"metric": METRIC, "profiling_run": True, "configs": configs}), flush=True)
         return
-    main_r = run_m(torch, ops, banks, args.m, args.steps, args.warmup, seed=0)
+    main_r = run_m(torch, ops, banks, args.m, args.steps, args.warmup, seed=0, graph=not args.no_graph)
     sweep = {}
     for mv in [int(v) for v in args.sweep.split(",") if v.strip()]:
         if mv != args.m:
-            r = run_m(torch, ops, banks, mv, max(6, args.steps // 5), 2, seed=mv)
+            r = run_m(torch, ops, banks, mv, max(6, args.steps // 5), 2, seed=mv, graph=not args.no_graph)
             sweep[str(mv)] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r.items()
                               if k in ("us_per_layer", "eager_us_per_layer", "gbs", "distinct_experts_avg")}
             sweep[str(mv)]["hbm_frac"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
@@ -657,7 +670,8 @@ def main():
                    "inter": I, "experts": E, "top_k": K, "shared_experts": 1, "score": "sigmoid",
                    "contract": "A16 dequant-then-matmul", "weight_layout": "MXT16 prepacked", "banks": N_BANKS,
                    "bank_reuse_distance_bytes": round((N_BANKS - 1) * main_r["layer_bytes_avg"]),
-                   "timing": "median of three HIP-graph replays, each of exactly the K steps"},
+                   "timing": ("the K steps run eagerly (--no-graph)" if args.no_graph
+                              else "median of three HIP-graph replays, each of exactly the K steps")},
         "us_per_layer": round(main_r["us_per_layer"], 2),
         "eager_us_per_layer": round(main_r["eager_us_per_layer"], 2),
         "hbm_frac": round(main_r["gbs"] / HBM_PEAK_GBS, 4),
