@@ -379,12 +379,13 @@ def test_moe_given_ids_repeated_and_dropped_multi_token(dev, a8):
 
 def test_moe_a8_prefill_tile_boundaries(dev):
     """Prefill kernels (A8) at the tile-shape boundaries, with given ids: experts
-    with 1, 64 (last light tile), 65 (first full-tile path), 256 (one full tile)
-    and 257 rows (a full tile plus a one-row light tile), plus the shared expert."""
+    with 1, 64 (last light tile), 65 (first full-tile path), 128 and 129 (the
+    second and third row quarters of a partial tile), 256 (one full tile) and 257
+    rows (a full tile plus a one-row light tile), plus the shared expert."""
     ops = _ops()
     rng = np.random.default_rng(61)
-    e, h, inter = 5, 512, 512
-    rows = [1, 64, 65, 256, 257]
+    e, h, inter = 7, 512, 512
+    rows = [1, 64, 65, 128, 129, 256, 257]
     ids = np.concatenate([np.full(r, i) for i, r in enumerate(rows)])
     rng.shuffle(ids)
     m = ids.size
@@ -462,11 +463,12 @@ def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
 
 
 @pytest.mark.parametrize("m,n,k", [(128, 256, 512), (257, 512, 1024), (1024, 512, 2048), (300, 7168, 512),
-                                   (64, 1536, 1536), (100, 320, 1024)])
+                                   (64, 1536, 1536), (100, 320, 1024), (384, 512, 1536), (400, 256, 512)])
 def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
     """Dense A8 MXFP4 GEMM at prefill sizes (fp4_gemm, .mosaicvm/source/inference_kernel.py:441-536):
     256-row tiles through the staged scaled-MFMA kernel when M > 256, N % 256 == 0 and
-    K % 512 == 0 (the 128-, 64- and 100-row cases run the 16-row kernel)."""
+    K % 512 == 0 (the 128-, 64- and 100-row cases run the 16-row kernel); the last
+    tile is light (257, 300) or a partial full-path tile (384: 128 rows, 400: 144)."""
     ops = _ops()
     rng = np.random.default_rng(m + n + k + 7)
     p, s = _quant_weights(rng, n, k)
