@@ -838,7 +838,7 @@ struct MlaKv {
 // heads x 128 columns per wave) in accumulation registers.
 template <int HT, bool FP8, int DR>
 __global__ void __launch_bounds__(256) mla_decode_split_kernel(
-    const uint16_t* __restrict__ q, const MlaKv kv, const int32_t* __restrict__ idx, float* __restrict__ part_o,
+    const uint16_t* __restrict__ q, const MlaKv kv, const int32_t* __restrict__ idx, uint16_t* __restrict__ part_o,
     float* __restrict__ part_ml, int topk, float scale, int chunk) {
   constexpr int DQK = kMlaDl + DR;
   constexpr int KS = DQK + 8;  // bf16 per K row in LDS: 16-byte reads of 16 rows hit distinct banks
@@ -1152,15 +1152,19 @@ __global__ void __launch_bounds__(256) mla_decode_split_kernel(
       }
     }
   }
-  // partial O in MFMA tile order: part_o[b][split][head tile][column tile][lane][4]
-  // (rows = heads 16 tile + 4 qd + r, column 16 tile + c)
-  float* po = part_o + ((int64_t)b * S + split) * (H / 16) * (kMlaDt * 256);
+  // partial O (bf16, un-normalized) in MFMA tile order:
+  // part_o[b][split][head tile][column tile][lane][4] (rows = heads 16 tile + 4 qd + r,
+  // column 16 tile + c); bf16 halves the partials' store and the combine's read
+  uint16_t* po = part_o + ((int64_t)b * S + split) * (H / 16) * (kMlaDt * 256);
 #pragma unroll
   for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-    for (int dl = 0; dl < DTW; ++dl)
-      *reinterpret_cast<f32x4_t*>(po + (((int64_t)(blockIdx.z * HT + ht) * kMlaDt + dt0 + dl) * 64 + lane) * 4) =
-          o[ht][dl];
+    for (int dl = 0; dl < DTW; ++dl) {
+      const f32x4_t v = o[ht][dl];
+      *reinterpret_cast<uint2*>(po + (((int64_t)(blockIdx.z * HT + ht) * kMlaDt + dt0 + dl) * 64 + lane) * 4) =
+          uint2{(uint32_t)f32_bf16(v[0]) | ((uint32_t)f32_bf16(v[1]) << 16),
+                (uint32_t)f32_bf16(v[2]) | ((uint32_t)f32_bf16(v[3]) << 16)};
+    }
   if (scorer && c == 0) {
     float* pml = part_ml + (((int64_t)b * S + split) * H + 16 * hw + 4 * qd) * 2;
     *reinterpret_cast<f32x4_t*>(pml) = f32x4_t{m_run[0], l_run[0], m_run[1], l_run[1]};
@@ -1172,7 +1176,7 @@ __global__ void __launch_bounds__(256) mla_decode_split_kernel(
 // term and normalize.  Each wave turns the split maxima/sums of four heads
 // into weights (lane = split); then wave w blends splits w, w + 4, ... of the
 // tile's 64 x 4 partial values, and wave 0 sums the four and writes bf16.
-__global__ void __launch_bounds__(256) mla_combine_kernel(const float* __restrict__ part_o,
+__global__ void __launch_bounds__(256) mla_combine_kernel(const uint16_t* __restrict__ part_o,
                                                           const float* __restrict__ part_ml,
                                                           const float* __restrict__ sink, uint16_t* __restrict__ out,
                                                           int H, int S) {
@@ -1196,11 +1200,13 @@ __global__ void __launch_bounds__(256) mla_combine_kernel(const float* __restric
   __syncthreads();
   const int hq = lane >> 4;  // rows 4 hq + r of the tile
   const int64_t sstride = (int64_t)(H / 16) * kMlaDt * 256;
-  const float* po = part_o + (int64_t)b * S * sstride + ((int64_t)ht * kMlaDt + dt) * 256 + lane * 4;
+  const uint16_t* po = part_o + (int64_t)b * S * sstride + ((int64_t)ht * kMlaDt + dt) * 256 + lane * 4;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
   for (int s = wv; s < S; s += 4) {
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(po + s * sstride);
+    const uint2 raw = *reinterpret_cast<const uint2*>(po + s * sstride);
+    const float v[4] = {__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xFFFF0000u),
+                        __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xFFFF0000u)};
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] += wgt[s][4 * hq + r] * v[r];
   }
@@ -1341,7 +1347,8 @@ static void launch_rescore(const uint8_t* q, const float* qs, const uint8_t* k, 
 }
 
 struct MlaWs {
-  float *part_o, *part_ml;
+  uint16_t* part_o;
+  float* part_ml;
 };
 
 // splits per row: about 256 workgroups over the batch (two head groups per
@@ -1366,10 +1373,10 @@ static int mla_head_tiles(int64_t b, int64_t h, int S) {
 }
 static size_t mla_ws(int64_t b, int64_t h, int64_t topk, char* base, MlaWs* w) {
   const int64_t S = mla_splits(b, topk);
-  const size_t ob = align256((size_t)b * S * h * kMlaDl * 4);
+  const size_t ob = align256((size_t)b * S * h * kMlaDl * 2);
   const size_t mb = align256((size_t)b * S * h * 2 * 4);
   if (w) {
-    w->part_o = (float*)base;
+    w->part_o = (uint16_t*)base;
     w->part_ml = (float*)(base + ob);
   }
   return ob + mb;
