@@ -66,6 +66,13 @@ int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s, int64_t m
 int mosaic_e4m3_decode(const uint8_t* in, float* out, int64_t n, void* stream);
 int mosaic_e4m3_encode(const float* in, uint8_t* out, int64_t n, void* stream);
 
+/* Self-check with no counterpart in the reference: compares gfx950's bf16 and
+ * e4m3 converters, which the fused prefill epilogues use, with the library's
+ * software roundings over every fp32 input.  counts (2 x uint64, zeroed by the
+ * caller) receives the mismatches: [0] bf16 over all non-NaN inputs, [1] e4m3
+ * over all inputs after the clamp to [-448, 448].  Both must stay 0. */
+int mosaic_selfcheck_converters(unsigned long long* counts, void* stream);
+
 /* ------------------------------------------------------ A16 MXFP4 linear -- */
 /* y [m, n] bf16 = x [m, k] bf16 . dequant(W)^T, fp32 accumulation, NK layout.
  * Replaces the A16 "dequant-then-matmul" linear: skinny_mxfp4_gemm semantics

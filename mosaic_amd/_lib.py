@@ -26,6 +26,7 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_act_quant": (c_int, [P, I, P, P, I64, I64, I, I, P]),
     "mosaic_e4m3_decode": (c_int, [P, P, I64, P]),
     "mosaic_e4m3_encode": (c_int, [P, P, I64, P]),
+    "mosaic_selfcheck_converters": (c_int, [P, P]),
     "mosaic_mx_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P]),
     "mosaic_mx_kn_linear_a16_workspace_bytes": (c_size_t, [I64, I64, I64]),
     "mosaic_mx_kn_linear_a16": (c_int, [P, P, P, P, I64, I64, I64, P, c_size_t, P]),

@@ -212,6 +212,24 @@ __global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__
   if ((threadIdx.x & 15) == 0) s_out[ch / 16] = s;
 }
 
+// Every fp32 bit pattern once (grid-stride over 2^32): counts[0] = non-NaN
+// inputs where bf16_round_hw differs from f32_bf16, counts[1] = inputs whose
+// clamp to [-448, 448] encodes differently under e4m3_hw and e4m3_rne.
+__global__ void __launch_bounds__(256) selfcheck_converters_kernel(unsigned long long* __restrict__ counts) {
+  const uint64_t nt = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t bad_b = 0, bad_e = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (1ull << 32); i += nt) {
+    const float f = __uint_as_float((uint32_t)i);
+    if (f == f) {
+      bad_b += __float_as_uint(bf16_round_hw(f)) != ((uint32_t)f32_bf16(f) << 16);
+      const float y = fminf(fmaxf(f, -448.0f), 448.0f);
+      bad_e += e4m3_hw(y) != e4m3_rne(y);
+    }
+  }
+  if (bad_b) atomicAdd(&counts[0], (unsigned long long)bad_b);
+  if (bad_e) atomicAdd(&counts[1], (unsigned long long)bad_e);
+}
+
 __global__ void __launch_bounds__(256) e4m3_decode_kernel(const uint8_t* __restrict__ in, float* __restrict__ out,
                                                           int64_t n) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -333,6 +351,12 @@ extern "C" int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s
     hipLaunchKernelGGL(act_quant_kernel<uint16_t>, dim3(grid), dim3(256), 0, st, (const uint16_t*)x, q, s, m, k,
                        block, mode);
   MOSAIC_RETURN_LAUNCH("act_quant");
+}
+
+extern "C" int mosaic_selfcheck_converters(unsigned long long* counts, void* stream) {
+  MOSAIC_CHECK_ARG(counts, "selfcheck_converters: null pointer");
+  hipLaunchKernelGGL(selfcheck_converters_kernel, dim3(4096), dim3(256), 0, (hipStream_t)stream, counts);
+  MOSAIC_RETURN_LAUNCH("selfcheck_converters");
 }
 
 extern "C" int mosaic_e4m3_decode(const uint8_t* in, float* out, int64_t n, void* stream) {

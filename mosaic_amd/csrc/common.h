@@ -142,6 +142,20 @@ __device__ __forceinline__ uint32_t e4m3_rne(float v) {
   return sign | code;
 }
 
+// The same roundings on gfx950's converters (one instruction each).  Both
+// round to nearest even; mosaic_selfcheck_converters compares them with the
+// software versions above over every fp32 input (bf16: every non-NaN input;
+// e4m3: every input after the clamp to [-448, 448] these callers apply).
+__device__ __forceinline__ float bf16_round_hw(float f) {  // f finite or inf
+  return (float)(__bf16)f;
+}
+__device__ __forceinline__ uint16_t f32_bf16_hw(float f) {  // f not NaN
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t e4m3_hw(float v) {  // v in [-448, 448]
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xFFu;
+}
+
 // power-of-two 1x128 activation scale: 2^ceil(log2(max(amax, 1e-4) * fp32(1/448)))
 // by IEEE bits (act_quant_ref, kernels/fp4_source.py:110-129)
 __device__ __forceinline__ float act_scale_pow2(float amax) {

@@ -605,6 +605,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
     PfLSrc lsrc;
     pfl_sources(lsrc, xq + (int64_t)perm_token[p0 + (arow < rows ? arow : 0)] * H, bp, bsc, groups, ns,
                 xs + (int64_t)perm_token[p0 + (lane < rows ? lane : 0)] * ns);
+    const float wl = perm_weight[p0 + (lane < rows ? lane : 0)];  // row lane's route weight
     f32x4_t lacc[4][2];
     uint8_t* lring = &ring[0][0];
     pfl_kloop(lsrc, ns, rows, wv, 8 + wv, lacc, lring);
@@ -614,9 +615,9 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mt + 4 * q + r;
-        const float wgt = perm_weight[p0 + (row < rows ? row : 0)];
-        const float gb = bf16_f32(f32_bf16(lacc[mt][0][r])), ub = bf16_f32(f32_bf16(lacc[mt][1][r]));
-        const float zb = bf16_f32(f32_bf16(swiglu_f32(gb, ub, limit) * wgt));
+        const float wgt = __shfl(wl, row, 64);
+        const float gb = bf16_round_hw(lacc[mt][0][r]), ub = bf16_round_hw(lacc[mt][1][r]);
+        const float zb = bf16_round_hw(swiglu_f32(gb, ub, limit) * wgt);
         lacc[mt][0][r] = zb;
         uint32_t u = __float_as_uint(fabsf(zb));
         u = max(u, MOSAIC_DPP(0u, u, 0xB1, 0xF));
@@ -647,7 +648,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
         if (row < rows) {
           const int64_t pp = p0 + row;
           const float y = fminf(fmaxf(lacc[mt][0][r] * (1.0f / sc), -448.0f), 448.0f);  // sc = 2^e: exact
-          zq[pp * I + j0 + 16 * wv + c] = (uint8_t)e4m3_rne(y);
+          zq[pp * I + j0 + 16 * wv + c] = (uint8_t)e4m3_hw(y);
           if (wv == 0 && c == 0) zs[pp * nbk + j0 / 128] = sc;
         }
       }
@@ -670,23 +671,30 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
     wg[n] = 4 * hc + n;
     wg[n + 4] = 8 + 4 * hc + n;
   }
+  // route weight of the wave's row 64 (wv >> 1) + lane: one load, read back by
+  // lane shuffles (the epilogue's per-row loads each waited out a full memory
+  // round trip)
+  const int wrow = 64 * (wv >> 1) + lane;
+  const float wl = perm_weight[p0 + (wrow < rows ? wrow : 0)];
   f32x4_t acc[4][8];
   pf_kloop(src, ns, rows, wg, acc, ring, chunk);
   // z = bf16(SwiGLU(bf16 gate, bf16 up) * route weight) in acc[mt][n][r], and
   // the amax of each row over this wave's 64 columns (DPP max over the 16
-  // lanes of the row, on the bits of non-negative floats)
+  // lanes of the row, on the bits of non-negative floats).  The roundings use
+  // the hardware converters: 64 values a lane made the software ones (with
+  // their divergent branches) a quarter of the workgroup's time.
   uint32_t rmax[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
-      const float wgt = perm_weight[p0 + (row < rows ? row : 0)];
+      const float wgt = __shfl(wl, 16 * mt + 4 * q + r, 64);
       float m = 0.f;
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const float gb = bf16_f32(f32_bf16(acc[mt][n][r])), ub = bf16_f32(f32_bf16(acc[mt][n + 4][r]));
-        const float zb = bf16_f32(f32_bf16(swiglu_f32(gb, ub, limit) * wgt));
+        const float gb = bf16_round_hw(acc[mt][n][r]), ub = bf16_round_hw(acc[mt][n + 4][r]);
+        const float zb = bf16_round_hw(swiglu_f32(gb, ub, limit) * wgt);
         acc[mt][n][r] = zb;
         m = fmaxf(m, fabsf(zb));
       }
@@ -720,7 +728,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           const float y = fminf(fmaxf(acc[mt][n][r] * (1.0f / sc), -448.0f), 448.0f);  // sc = 2^e: exact
-          zq[pp * I + j0 + 64 * hc + 16 * n + c] = (uint8_t)e4m3_rne(y);
+          zq[pp * I + j0 + 64 * hc + 16 * n + c] = (uint8_t)e4m3_hw(y);
         }
         if (hc == 0 && c == 0) zs[pp * nbk + j0 / 128] = sc;
       }
@@ -773,7 +781,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = 16 * mt + 4 * q + r;
-          if (row < rows) yb[(int64_t)(p0 + row) * H + h0 + 32 * wv + 16 * gi + c] = f32_bf16(lacc[mt][gi][r]);
+          if (row < rows) yb[(int64_t)(p0 + row) * H + h0 + 32 * wv + 16 * gi + c] = f32_bf16_hw(lacc[mt][gi][r]);
         }
     return;
   }
@@ -800,7 +808,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
-        if (row < rows) yb[(int64_t)(p0 + row) * H + h0 + 128 * hc + 16 * n + c] = f32_bf16(acc[mt][n][r]);
+        if (row < rows) yb[(int64_t)(p0 + row) * H + h0 + 128 * hc + 16 * n + c] = f32_bf16_hw(acc[mt][n][r]);
       }
 }
 

@@ -142,6 +142,14 @@ def e4m3_encode(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def selfcheck_converters(device=None) -> list[int]:
+    """Mismatch counts [bf16, e4m3] of gfx950's hardware converters against the
+    library's software roundings over every fp32 input (see the C header)."""
+    counts = torch.zeros(2, dtype=torch.int64, device=device or torch.device("cuda", torch.cuda.current_device()))
+    _lib.call("mosaic_selfcheck_converters", _ptr(counts), _stream())
+    return counts.cpu().tolist()
+
+
 # ------------------------------------------------------------- A16 linear ---
 def mx_linear_a16(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """y [M, N] bf16 = x [M, K] bf16 . dequant(packed [N, K/2], scale [N, K/32])^T."""

@@ -111,6 +111,14 @@ def test_e4m3_decode_all_bytes(dev):
     assert np.isnan(got[nan]).all()
 
 
+def test_hardware_converters_equal_software_roundings(dev):
+    """The fused prefill epilogues round to bf16 and encode e4m3 with gfx950's
+    converters; over every fp32 bit pattern they equal the software roundings
+    (f32_bf16 on every non-NaN input; e4m3_rne, pinned to torch's cast by the
+    test below, on every input after the epilogue's clamp to [-448, 448])."""
+    assert _ops().selfcheck_converters(dev) == [0, 0]
+
+
 def test_e4m3_encode_dense(dev):
     ops = _ops()
     fin = C.E4M3_TABLE[np.isfinite(C.E4M3_TABLE)]
