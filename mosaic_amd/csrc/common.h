@@ -216,4 +216,17 @@ __device__ __forceinline__ float swiglu_f32(float gate, float up, float limit) {
   return (gate / (1.0f + expf(-gate))) * up;
 }
 
+// The same SwiGLU on the hardware exp2 and reciprocal (a few ulp of fp32
+// instead of correctly rounded expf and division; about 5 VALU instead of 25),
+// for the prefill epilogues that evaluate 64 values a lane.  gate -> -inf gives
+// gate * rcp(inf) = -0, as the accurate form does.
+__device__ __forceinline__ float swiglu_fast_f32(float gate, float up, float limit) {
+  if (limit > 0.f) {
+    gate = fminf(gate, limit);
+    up = fmaxf(fminf(up, limit), -limit);
+  }
+  const float e = __builtin_amdgcn_exp2f(-gate * 1.4426950408889634f);
+  return gate * __builtin_amdgcn_rcpf(1.0f + e) * up;
+}
+
 }  // namespace mosaic

@@ -617,7 +617,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
         const int row = 16 * mt + 4 * q + r;
         const float wgt = __shfl(wl, row, 64);
         const float gb = bf16_round_hw(lacc[mt][0][r]), ub = bf16_round_hw(lacc[mt][1][r]);
-        const float zb = bf16_round_hw(swiglu_f32(gb, ub, limit) * wgt);
+        const float zb = bf16_round_hw(swiglu_fast_f32(gb, ub, limit) * wgt);
         lacc[mt][0][r] = zb;
         uint32_t u = __float_as_uint(fabsf(zb));
         u = max(u, MOSAIC_DPP(0u, u, 0xB1, 0xF));
@@ -694,7 +694,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const float gb = bf16_round_hw(acc[mt][n][r]), ub = bf16_round_hw(acc[mt][n + 4][r]);
-        const float zb = bf16_round_hw(swiglu_f32(gb, ub, limit) * wgt);
+        const float zb = bf16_round_hw(swiglu_fast_f32(gb, ub, limit) * wgt);
         acc[mt][n][r] = zb;
         m = fmaxf(m, fabsf(zb));
       }
