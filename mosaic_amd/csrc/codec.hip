@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const T* __restrict__ x,
     const float xv = load_as_f32<T>(x, base + i);
     float y = mode == 0 ? xv * inv : xv / s;
     y = fminf(fmaxf(y, -448.0f), 448.0f);
-    q[base + i] = (uint8_t)e4m3_rne(y);
+    q[base + i] = (uint8_t)e4m3_hw(y);
   }
   if (lane == 0) s_out[row * nb + kb] = s;
 }
@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__
   for (int i = 0; i < 8; ++i) {
     float y = mode == 0 ? v[i] * inv : v[i] / s;
     y = fminf(fmaxf(y, -448.0f), 448.0f);
-    const uint32_t b = e4m3_rne(y);
+    const uint32_t b = e4m3_hw(y);  // y clamped to [-448, 448] above
     if (i < 4) lo |= b << (8 * i);
     else hi |= b << (8 * (i - 4));
   }

@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(256) dsa_kv_write_kernel(const uint16_t* __res
   const float inv = 1.0f / s;  // exact: s is a power of two
   uint32_t c[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) c[i] = e4m3_rne(fminf(fmaxf(x[i] * inv, -448.f), 448.f));
+  for (int i = 0; i < 8; ++i) c[i] = e4m3_hw(fminf(fmaxf(x[i] * inv, -448.f), 448.f));
   if (act) {
     if (cache_bf16) {
       // codes * s in bf16: the e4m3 value scaled by a power of two is exact

@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(256) rmsnorm_act_quant_kernel(const uint16_t* 
     for (int e = 0; e < 8; ++e) {
       float t = mode == 0 ? yv[e] * inv : yv[e] / s;
       t = fminf(fmaxf(t, -448.0f), 448.0f);
-      cw[e >> 2] |= e4m3_rne(t) << (8 * (e & 3));
+      cw[e >> 2] |= e4m3_hw(t) << (8 * (e & 3));
     }
     *reinterpret_cast<uint2*>(q + (int64_t)row * H + 8 * c) = uint2{cw[0], cw[1]};
     if ((lane & 15) == 0) s_out[(int64_t)row * nb + c / 16] = s;
