@@ -218,8 +218,8 @@ __device__ __forceinline__ float swiglu_f32(float gate, float up, float limit) {
 
 // The same SwiGLU on the hardware exp2 and reciprocal (a few ulp of fp32
 // instead of correctly rounded expf and division; about 5 VALU instead of 25),
-// for the prefill epilogues that evaluate 64 values a lane.  gate -> -inf gives
-// gate * rcp(inf) = -0, as the accurate form does.
+// for the prefill epilogues that evaluate 64 values a lane.  A large negative
+// gate gives gate * rcp(inf) = -0, as the accurate form does.
 __device__ __forceinline__ float swiglu_fast_f32(float gate, float up, float limit) {
   if (limit > 0.f) {
     gate = fminf(gate, limit);

@@ -688,8 +688,7 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_gateup_prefill_kernel
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
-      const float wgt = __shfl(wl, 16 * mt + 4 * q + r, 64);
+      const float wgt = __shfl(wl, 16 * mt + 4 * q + r, 64);  // row 64 (wv >> 1) + 16 mt + 4 q + r
       float m = 0.f;
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
