@@ -368,17 +368,34 @@ __global__ void __launch_bounds__(kLayoutChunk) layout_count_kernel(const int32_
   for (int x = tid; x < E_ext; x += kLayoutChunk) chunk_counts[(int64_t)ch * E_ext + x] = cnt[x];
 }
 
+constexpr int kScanTile = 32768;  // chunk counts (ints) the scan stages in LDS at a time: 128 KB
+
 __global__ void __launch_bounds__(1024) layout_scan_kernel(const int32_t* __restrict__ chunk_counts, int n_chunks,
                                                            int E_ext, int block_m, int tile_cap, LayoutOut out) {
+  // The [chunk][expert] counts are staged through LDS in tiles of whole chunks with coalesced loads;
+  // each expert's walk over the chunks then runs on LDS. A table that fits one tile stays resident
+  // between the totals pass and the bases pass.
+  __shared__ int32_t s_tile[kScanTile];
   __shared__ int32_t s_cnt[kRouteMaxExperts + 2];
   __shared__ int32_t s_off[kRouteMaxExperts + 2];
   __shared__ int32_t s_toff[kRouteMaxExperts + 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E_ext; e += 1024) {
-    int c = 0;
-    for (int ch = 0; ch < n_chunks; ++ch) c += chunk_counts[(int64_t)ch * E_ext + e];
-    s_cnt[e] = c;
+  const int cb = kScanTile / E_ext;  // whole chunks per tile (>= 63)
+  const bool resident = n_chunks <= cb;
+  int tot = 0;
+  for (int c0 = 0; c0 < n_chunks; c0 += cb) {
+    const int nc = min(cb, n_chunks - c0), n = nc * E_ext;
+    const int32_t* src = chunk_counts + (int64_t)c0 * E_ext;
+#pragma unroll 8
+    for (int i = tid; i < n; i += 1024) s_tile[i] = src[i];
+    __syncthreads();
+    if (tid < E_ext) {
+#pragma unroll 8
+      for (int c = 0; c < nc; ++c) tot += s_tile[c * E_ext + tid];
+    }
+    __syncthreads();
   }
+  if (tid < E_ext) s_cnt[tid] = tot;
   __syncthreads();
   if (wave == 0) {
     uint32_t carry = 0, tcarry = 0;
@@ -400,12 +417,32 @@ __global__ void __launch_bounds__(1024) layout_scan_kernel(const int32_t* __rest
     }
   }
   __syncthreads();
-  for (int e = tid; e < E_ext; e += 1024) {
-    int run = s_off[e];
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      out.chunk_base[(int64_t)ch * E_ext + e] = run;
-      run += chunk_counts[(int64_t)ch * E_ext + e];
+  // Bases: each expert's running offset replaces its counts in the staged tile, which is then
+  // stored whole.
+  int run = tid < E_ext ? s_off[tid] : 0;
+  for (int c0 = 0; c0 < n_chunks; c0 += cb) {
+    const int nc = min(cb, n_chunks - c0), n = nc * E_ext;
+    if (!resident) {
+      const int32_t* src = chunk_counts + (int64_t)c0 * E_ext;
+#pragma unroll 8
+      for (int i = tid; i < n; i += 1024) s_tile[i] = src[i];
+      __syncthreads();
     }
+    if (tid < E_ext) {
+#pragma unroll 8
+      for (int c = 0; c < nc; ++c) {
+        const int v = s_tile[c * E_ext + tid];
+        s_tile[c * E_ext + tid] = run;
+        run += v;
+      }
+    }
+    __syncthreads();
+    int32_t* dst = out.chunk_base + (int64_t)c0 * E_ext;
+#pragma unroll 8
+    for (int i = tid; i < n; i += 1024) dst[i] = s_tile[i];
+    __syncthreads();
+  }
+  for (int e = tid; e < E_ext; e += 1024) {
     out.counts[e] = s_cnt[e];
     out.offsets[e] = s_off[e];
     const int nt = (s_cnt[e] + block_m - 1) / block_m;

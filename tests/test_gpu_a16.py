@@ -158,7 +158,7 @@ def test_route_topk_vs_oracle(dev, m, e, k, func):
 
 @pytest.mark.parametrize("m,k,e,shared", [(1, 8, 256, True), (4, 8, 256, False), (64, 8, 256, True),
                                           (300, 8, 16, True), (2, 1, 4, False), (4096, 8, 256, True),
-                                          (700, 8, 16, False), (5000, 1, 4, True)])
+                                          (700, 8, 16, False), (5000, 1, 4, True), (8000, 8, 512, True)])
 def test_layout_vs_oracle(dev, m, k, e, shared):
     ops = _ops()
     rng = np.random.default_rng(m * 7 + e)
