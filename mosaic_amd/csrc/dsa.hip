@@ -132,11 +132,6 @@ __device__ __forceinline__ void lds_hist_add(uint32_t* lh, uint32_t bin, bool ac
   }
 }
 
-__global__ void dsa_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
 // Buffer resource over `records` bytes from `base` (raw addressing): loads past
 // the range read zero and stores past it are dropped.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int records) {
@@ -149,7 +144,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int
 // nw, ... of U 16-token tiles and streams them through a register ring of D
 // groups.  Each group's loads and stores go through buffer resources that end
 // at the row's length, so tokens past it read as zero and are not written: the
-// ring issues every load unconditionally and its waits stay exact.
+// ring issues every load unconditionally and its waits stay exact.  `lo` may
+// be null (the top-k path reads only the upper bounds and the histogram).
 template <int HT, int U, int D>
 __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ qs, const uint8_t* __restrict__ k,
@@ -172,8 +168,8 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   const int64_t iters = wid < n_groups ? (n_groups - 1 - wid) / nw + 1 : 0;
   const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;  // kdiv query rows share one key cache
   const float* ksb = ks + (int64_t)(b / kdiv) * L;
-  float* lob = lo + (int64_t)b * L;
   float* hib = hi + (int64_t)b * L;
+  float* lob = lo ? lo + (int64_t)b * L : hib;  // without lo: a zero-length range, the stores drop
   i32x8_t kr[D][U];
   float sr[D][U];
   // tokens of group g inside the row (wave-uniform)
@@ -236,7 +232,7 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   auto compute = [&](int s, int64_t i) {
     const int64_t g = wid + i * nw;
     const int nt = group_tokens(g);
-    const __amdgpu_buffer_rsrc_t rl = buf_rsrc(lob + g * GT, nt * 4);
+    const __amdgpu_buffer_rsrc_t rl = buf_rsrc(lob + g * GT, lo ? nt * 4 : 0);
     const __amdgpu_buffer_rsrc_t rh = buf_rsrc(hib + g * GT, nt * 4);
     f32x4_t d[U][HT];
 #pragma unroll
@@ -304,50 +300,50 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   }
 }
 
-// Within a histogram of kHistBins digits (in `h`, LDS), find the digit that
-// holds the rem-th largest element: the largest d with count(> d) < rem.
-// Block of NT threads; returns the digit to every thread.
-template <int NT>
-__device__ uint32_t find_digit(const uint32_t* h, uint32_t rem, uint32_t* sh_out) {
-  constexpr int PER = kHistBins / NT;
-  constexpr int NW = NT / 64;
-  __shared__ uint32_t wtot[NW];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  // thread tid owns digits (top down) kHistBins-1-PER*tid ... kHistBins-PER*(tid+1)
-  uint32_t cnt[PER], local = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    cnt[i] = h[kHistBins - 1 - (PER * tid + i)];
-    local += cnt[i];
-  }
-  const uint32_t incl = wave_incl_scan_u32(local);
-  if (lane == 63) wtot[wv] = incl;
-  __syncthreads();
-  uint32_t acc = incl - local;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) acc += i < wv ? wtot[i] : 0u;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    if (acc < rem && rem <= acc + cnt[i]) sh_out[0] = kHistBins - 1 - (PER * tid + i);
-    acc += cnt[i];
-  }
-  __syncthreads();
-  return sh_out[0];
-}
-
 typedef __attribute__((ext_vector_type(4))) int i32x4_v;
 
-// 16 e4m3 codes -> three int8 limb vectors: 512 v = L2 2^14 + L1 2^7 + L0
+// 4 e4m3 codes -> three int8 limb words: 512 v = L2 2^14 + L1 2^7 + L0
+__device__ __forceinline__ void e4m3_limbs_word(uint32_t x, int (&o)[3]) {
+  const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, false);
+  const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, true);
+  const int v0 = (int)(a[0] * 512.f), v1 = (int)(a[1] * 512.f);
+  const int v2 = (int)(c[0] * 512.f), v3 = (int)(c[1] * 512.f);
+  o[0] = (v0 & 127) | ((v1 & 127) << 8) | ((v2 & 127) << 16) | ((v3 & 127) << 24);
+  o[1] = ((v0 >> 7) & 127) | (((v1 >> 7) & 127) << 8) | (((v2 >> 7) & 127) << 16) | (((v3 >> 7) & 127) << 24);
+  o[2] = ((v0 >> 14) & 255) | (((v1 >> 14) & 255) << 8) | (((v2 >> 14) & 255) << 16) | ((v3 >> 14) << 24);
+}
+// 16 e4m3 codes -> three int8 limb vectors
 __device__ __forceinline__ void e4m3_limbs(const u32x4_t x, i32x4_v (&o)[3]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[i], false);
-    const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[i], true);
-    const int v0 = (int)(a[0] * 512.f), v1 = (int)(a[1] * 512.f);
-    const int v2 = (int)(c[0] * 512.f), v3 = (int)(c[1] * 512.f);
-    o[0][i] = (v0 & 127) | ((v1 & 127) << 8) | ((v2 & 127) << 16) | ((v3 & 127) << 24);
-    o[1][i] = ((v0 >> 7) & 127) | (((v1 >> 7) & 127) << 8) | (((v2 >> 7) & 127) << 16) | (((v3 >> 7) & 127) << 24);
-    o[2][i] = ((v0 >> 14) & 255) | (((v1 >> 14) & 255) << 8) | (((v2 >> 14) & 255) << 16) | ((v3 >> 14) << 24);
+    int t[3];
+    e4m3_limbs_word(x[i], t);
+    o[0][i] = t[0];
+    o[1][i] = t[1];
+    o[2][i] = t[2];
+  }
+}
+
+// First kernel of a top-k call: clears the row histograms and writes q's int8
+// limbs in the rescoring kernel's operand order, so that its workgroups load
+// them (one coalesced 6 KB block per 16 heads) instead of converting q each:
+// row r, heads 16 j + c, dims 64 ch + 16 qd + 4 i .. +3, limb la is word
+// ((((r * HT + j) * 2 + ch) * 3 + la) * 64 + c + 16 qd) * 4 + i, HT = heads / 16.
+__global__ void dsa_prep_kernel(uint32_t* __restrict__ hist, int64_t n_hist, const uint32_t* __restrict__ q,
+                                uint32_t* __restrict__ qlimbs, int64_t n_qwords, int heads) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n_hist) hist[i] = 0u;
+  if (i < n_qwords) {
+    constexpr int W = kIdxD / 4;  // code words per head row
+    const int64_t hrow = i / W;    // row * heads + head
+    const int wd = (int)(i - hrow * W), head = (int)(hrow % heads);
+    const int64_t r = hrow / heads;
+    const int j = head >> 4, c = head & 15, ch = wd >> 4, qd = (wd >> 2) & 3, e = wd & 3;
+    const int64_t base = (r * (heads >> 4) + j) * 2 + ch;
+    int t[3];
+    e4m3_limbs_word(q[i], t);
+#pragma unroll
+    for (int la = 0; la < 3; ++la) qlimbs[((base * 3 + la) * 64 + c + 16 * qd) * 4 + e] = (uint32_t)t[la];
   }
 }
 
@@ -362,22 +358,36 @@ __device__ __forceinline__ i32x4_v mfma_i8(const i32x4_v a, const i32x4_v b, con
 // topk others), scores them 16 at a time on the MFMA (lanes = 16 candidates x
 // 4 head groups) and appends 64-bit keys (score key << 32 | ~index) to the
 // row's key list; without `hi` it scores every token into `scores`.  The
-// histogram, the range's upper bounds and q are loaded together up front.
+// histogram, the range's upper bounds and q are loaded together up front, and
+// a range of at most kRsPfRange tokens loads its k rows and scales with them
+// into LDS (PF), so the candidates' rows are there once tau is known.  The
+// histogram is scanned from registers.
 constexpr int kRsMaxRange = 4096;
 constexpr int kRsPer = kRsMaxRange / 256;
 constexpr int kRsMaxWgs = 4096;  // rescoring workgroups per row (rows up to 2^24 tokens)
-template <int HT>
+constexpr int kRsPfRange = 256;  // ranges up to this many tokens stage their k rows in LDS up front
+static_assert(kHistBins == 8 * 4 * 256, "the threshold scan gives each of 256 threads 8 vectors of 4 digits");
+template <int HT, bool PF, bool QL>
 __global__ void __launch_bounds__(256) dsa_rescore_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ qs, const uint8_t* __restrict__ k,
     const float* __restrict__ ks, const float* __restrict__ w, const int32_t* __restrict__ lengths,
-    const float* __restrict__ hi, const uint32_t* __restrict__ hist1, uint64_t* __restrict__ keys,
-    uint32_t* __restrict__ wg_counts, float* __restrict__ scores, int64_t L, int topk, int range, int kdiv) {
+    const float* __restrict__ hi, const uint32_t* __restrict__ hist1, const uint32_t* __restrict__ qlimbs,
+    uint64_t* __restrict__ keys, uint32_t* __restrict__ wg_counts, float* __restrict__ scores, int64_t L, int topk,
+    int range, int kdiv) {
   constexpr int H = HT * 16;
-  __shared__ uint32_t lh[kHistBins];
-  __shared__ uint32_t sh[2];
+  constexpr int kCand = PF ? kRsPfRange : kRsMaxRange;
+  constexpr int kPfVec = PF ? kRsPfRange * kIdxD / 16 : 1;  // 16-byte pieces of the staged k rows
+  constexpr int kPfPer = PF ? kPfVec / 256 : 1;
+  __shared__ uint32_t sh[1];
+  __shared__ uint32_t hsum[8][4];
   __shared__ uint32_t wsum[4];
-  __shared__ int cand[kRsMaxRange];
+  __shared__ int cand[kCand];
   __shared__ float terms[4][16][H + 1];
+  __shared__ u32x4_t kpf[kPfVec];
+  __shared__ float kspf[PF ? kRsPfRange : 1];
+  constexpr int kQlVec = HT * 2 * 3 * 64;  // 16-byte vectors of this row's q limbs
+  constexpr int kQlPer = (kQlVec + 255) / 256;
+  __shared__ i32x4_v qls[QL ? kQlVec : 1];
   const int b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
@@ -387,48 +397,115 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
   if (t_begin >= n) return;
   const int nr = (int)min((int64_t)range, n - t_begin);  // tokens of this workgroup
   const bool select = hi != nullptr && n > topk;
-  // in flight together: the row's histogram, this range's upper bounds, q
-  constexpr int kHistLoads = kHistBins / 4 / 256;
-  u32x4_t hbuf[kHistLoads];
+  const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;
+  const float* ksb = ks + (int64_t)(b / kdiv) * L;
+  // in flight together: the row's histogram (thread tid holds digit vectors
+  // v = tid + 256 i, digits 4 v .. 4 v + 3, coalesced), this range's upper
+  // bounds, q, and the range's k rows and scales when they are staged
+  u32x4_t hbuf[8];
   if (select) {
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(hist1 + (int64_t)b * kHistBins);
 #pragma unroll
-    for (int i = 0; i < kHistLoads; ++i) hbuf[i] = src[tid + 256 * i];
+    for (int i = 0; i < 8; ++i) hbuf[i] = src[tid + 256 * i];
   }
-  float hv[kRsPer];
+  constexpr int kPer = PF ? kRsPfRange / 256 : kRsPer;  // tokens per thread
+  float hv[kPer];
   if (hi) {
     const __amdgpu_buffer_rsrc_t rh = buf_rsrc(hi + (int64_t)b * L + t_begin, nr * 4);
 #pragma unroll
-    for (int i = 0; i < kRsPer; ++i)
+    for (int i = 0; i < kPer; ++i)
       hv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rh, (tid + 256 * i) * 4, 0, 0));
   }
-  // A operands (rows = heads 16 j + c) as int8 limbs of dims 64 ch + 16 qd ..+16;
+  // A operands (rows = heads 16 j + c) as int8 limbs of dims 64 ch + 16 qd ..+16:
+  // with QL the row's limbs (written by the prep kernel) are staged in LDS once
+  // per workgroup and read after the compaction, otherwise converted here;
   // per-lane constants of the D layout (heads 16 j + 4 qd + r)
   i32x4_v ql[HT][2][3];
+  i32x4_v qlb[kQlPer];
+  if constexpr (QL) {
+    const i32x4_v* src = reinterpret_cast<const i32x4_v*>(qlimbs) + (int64_t)b * kQlVec;
+#pragma unroll
+    for (int i = 0; i < kQlPer; ++i)
+      if (kQlVec % 256 == 0 || tid + 256 * i < kQlVec) qlb[i] = src[tid + 256 * i];
+  }
   float qsv[HT][4], wvv[HT][4];
 #pragma unroll
   for (int j = 0; j < HT; ++j) {
-    const uint8_t* qrow = q + ((int64_t)b * H + 16 * j + c) * kIdxD + 16 * qd;
+    if constexpr (!QL) {
+      const uint8_t* qrow = q + ((int64_t)b * H + 16 * j + c) * kIdxD + 16 * qd;
 #pragma unroll
-    for (int ch = 0; ch < 2; ++ch) e4m3_limbs(*reinterpret_cast<const u32x4_t*>(qrow + 64 * ch), ql[j][ch]);
+      for (int ch = 0; ch < 2; ++ch) e4m3_limbs(*reinterpret_cast<const u32x4_t*>(qrow + 64 * ch), ql[j][ch]);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       qsv[j][r] = qs[(int64_t)b * H + 16 * j + 4 * qd + r];
       wvv[j][r] = w[(int64_t)b * H + 16 * j + 4 * qd + r];
     }
   }
+  // the staged k rows go out last: tau and the compaction wait only for the
+  // loads issued before them
+  u32x4_t kbuf[kPfPer];
+  float ksv = 0.f;
+  if constexpr (PF) {
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kb + t_begin * kIdxD, nr * kIdxD);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(ksb + t_begin, nr * 4);
+#pragma unroll
+    for (int i = 0; i < kPfPer; ++i) kbuf[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, (tid + 256 * i) * 16, 0, 0);
+    ksv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4, 0, 0));
+  }
+  // tau: the digit holding the topk-th largest lower bound.  Chunk i (digits
+  // 1024 i .. 1024 i + 1023) is one vector per thread: a block scan per chunk
+  // gives each vector the count of digits above it (the chunks above, plus the
+  // higher vectors of its chunk), and the thread whose digits cross topk names it.
   uint32_t tau = 0u;
   if (select) {
+    uint32_t vs[8], incl[8];
 #pragma unroll
-    for (int i = 0; i < kHistLoads; ++i) reinterpret_cast<u32x4_t*>(lh)[tid + 256 * i] = hbuf[i];
+    for (int i = 0; i < 8; ++i) {
+      vs[i] = (hbuf[i][0] + hbuf[i][1]) + (hbuf[i][2] + hbuf[i][3]);
+      incl[i] = wave_incl_scan_u32(vs[i]);
+    }
+    if (lane == 63)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hsum[i][wv] = incl[i];
     __syncthreads();
-    tau = find_digit<256>(lh, (uint32_t)topk, sh) << kHistShift;
+    const uint32_t rem = (uint32_t)topk;
+    uint32_t above = 0;  // digits in the chunks above chunk i
+#pragma unroll
+    for (int i = 7; i >= 0; --i) {
+      uint32_t tot = 0, before = 0;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        tot += hsum[i][w2];
+        before += w2 < wv ? hsum[i][w2] : 0u;
+      }
+      uint32_t acc = above + (tot - (before + incl[i]));  // digits above this thread's top digit
+#pragma unroll
+      for (int r = 3; r >= 0; --r) {
+        const uint32_t cnt = hbuf[i][r];
+        if (acc < rem && rem <= acc + cnt) sh[0] = (uint32_t)(4 * (tid + 256 * i) + r);
+        acc += cnt;
+      }
+      above += tot;
+    }
+    __syncthreads();
+    tau = sh[0] << kHistShift;
+  }
+  if constexpr (QL) {  // visible after the compaction's barriers
+#pragma unroll
+    for (int i = 0; i < kQlPer; ++i)
+      if (kQlVec % 256 == 0 || tid + 256 * i < kQlVec) qls[tid + 256 * i] = qlb[i];
+  }
+  if constexpr (PF) {
+#pragma unroll
+    for (int i = 0; i < kPfPer; ++i) kpf[tid + 256 * i] = kbuf[i];
+    kspf[tid] = ksv;
   }
   // compaction: thread tid's tokens are tid + 256 i; a block scan of the
   // per-thread counts places them
   uint32_t keep = 0u, nk = 0u;
 #pragma unroll
-  for (int i = 0; i < kRsPer; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const bool ok = tid + 256 * i < nr && (!hi || key_high_nan(hv[i]) >= tau);
     keep |= ok ? 1u << i : 0u;
     nk += ok ? 1u : 0u;
@@ -441,18 +518,22 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
   for (int i = 0; i < 4; ++i) pos += i < wv ? wsum[i] : 0u;
   const int C = (int)(wsum[0] + wsum[1] + wsum[2] + wsum[3]);
 #pragma unroll
-  for (int i = 0; i < kRsPer; ++i)
+  for (int i = 0; i < kPer; ++i)
     if (keep & (1u << i)) cand[pos++] = (int)(t_begin + tid + 256 * i);
   __syncthreads();
   // the keys go to this workgroup's own token range, keys[b][t_begin + i] for
   // candidate i, and the count to wg_counts[b][blockIdx.x] (no atomics)
   if (hi && tid == 0) wg_counts[(int64_t)b * kRsMaxWgs + blockIdx.x] = (uint32_t)C;
-  // this wave's batches: bt = wv, wv + 4, ...
-  const int nb = (C + 15) / 16;
-  const int my_batches = nb > wv ? (nb - 1 - wv) / 4 + 1 : 0;
-  if (my_batches == 0) return;
-  const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;
-  const float* ksb = ks + (int64_t)(b / kdiv) * L;
+  const int nb = __builtin_amdgcn_readfirstlane((C + 15) / 16);  // batches of 16 candidates (block-uniform)
+  if (nb == 0) return;
+  if constexpr (QL) {
+#pragma unroll
+    for (int j = 0; j < HT; ++j)
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int la = 0; la < 3; ++la) ql[j][ch][la] = qls[((j * 2 + ch) * 3 + la) * 64 + lane];
+  }
   struct Batch {
     u32x4_t x[2];
     float ks;
@@ -463,53 +544,84 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
     const bool ok = i < C;
     o.t = ok ? cand[i] : -1;
     const int64_t tt = ok ? o.t : cand[0];
-    o.ks = ksb[tt];
+    if constexpr (PF) {
+      const int r = (int)(tt - t_begin);
+      o.ks = kspf[r];
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) o.x[ch] = kpf[r * (kIdxD / 16) + 4 * ch + qd];
+    } else {
+      o.ks = ksb[tt];
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+        o.x[ch] = *reinterpret_cast<const u32x4_t*>(kb + tt * kIdxD + 64 * ch + 16 * qd);
+    }
+  };
+  // head tile j of a batch (18 MFMAs): the terms of heads 16 j .. 16 j + 15 into tm[candidate][head]
+  auto head_tile = [&](int j, const i32x4_v (&kl)[2][3], float kscale, float (*tm)[H + 1]) {
+    i32x4_v g[5];
+#pragma unroll
+    for (int mm = 0; mm < 5; ++mm) g[mm] = i32x4_v{0, 0, 0, 0};
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch)
-      o.x[ch] = *reinterpret_cast<const u32x4_t*>(kb + tt * kIdxD + 64 * ch + 16 * qd);
+#pragma unroll
+      for (int la = 0; la < 3; ++la)
+#pragma unroll
+        for (int lb = 0; lb < 3; ++lb) g[la + lb] = mfma_i8(ql[j][ch][la], kl[ch][lb], g[la + lb]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      double x = (double)g[4][r];
+      x = fma(x, 128.0, (double)g[3][r]);
+      x = fma(x, 128.0, (double)g[2][r]);
+      x = fma(x, 128.0, (double)g[1][r]);
+      x = fma(x, 128.0, (double)g[0][r]);
+      const float d = (float)(x * 0x1p-18);
+      const float a = (d * qsv[j][r]) * kscale;
+      const float rr = a > 0.f ? a : 0.f;
+      tm[c][16 * j + 4 * qd + r] = rr * wvv[j][r];
+    }
   };
+  // candidate i (token t): its terms summed in head order, then its key (or score)
+  auto emit = [&](int i, int t, const float* row) {
+    float tv[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) tv[h] = row[h];
+    float sc = 0.f;
+#pragma unroll
+    for (int h = 0; h < H; ++h) sc = sc + tv[h];
+    if (hi)
+      keys[(int64_t)b * L + t_begin + i] = ((uint64_t)key_low_nan(sc) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)t);
+    else
+      scores[(int64_t)b * L + t] = sc;
+  };
+  if (HT == 4 && nb <= 4) {
+    // At most 64 candidates: the four waves share the batches' head tiles,
+    // each wave one batch (4 / nbw waves per batch, nbw tiles each), and the
+    // terms meet in LDS.
+    const int nbw = nb == 3 ? 4 : nb;
+    const int bt = wv * nbw / 4, j0 = (wv % (4 / nbw)) * nbw;
+    Batch in;
+    load_batch(bt, in);  // a batch past the candidates reads candidate 0's row and writes unused terms
+    i32x4_v kl[2][3];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) e4m3_limbs(in.x[ch], kl[ch]);
+#pragma unroll
+    for (int j = 0; j < HT; ++j)
+      if (j >= j0 && j < j0 + nbw) head_tile(j, kl, in.ks, terms[bt]);
+    __syncthreads();
+    if (tid < C) emit(tid, cand[tid], terms[tid >> 4][tid & 15]);
+    return;
+  }
+  // More candidates: wave wv scores batches bt = wv, wv + 4, ... whole.
+  const int my_batches = nb > wv ? (nb - 1 - wv) / 4 + 1 : 0;
+  if (my_batches == 0) return;
   auto score_batch = [&](int m, const Batch& in) {
     i32x4_v kl[2][3];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) e4m3_limbs(in.x[ch], kl[ch]);
 #pragma unroll
-    for (int j = 0; j < HT; ++j) {
-      i32x4_v g[5];
-#pragma unroll
-      for (int mm = 0; mm < 5; ++mm) g[mm] = i32x4_v{0, 0, 0, 0};
-#pragma unroll
-      for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-        for (int la = 0; la < 3; ++la)
-#pragma unroll
-          for (int lb = 0; lb < 3; ++lb) g[la + lb] = mfma_i8(ql[j][ch][la], kl[ch][lb], g[la + lb]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        double x = (double)g[4][r];
-        x = fma(x, 128.0, (double)g[3][r]);
-        x = fma(x, 128.0, (double)g[2][r]);
-        x = fma(x, 128.0, (double)g[1][r]);
-        x = fma(x, 128.0, (double)g[0][r]);
-        const float d = (float)(x * 0x1p-18);
-        const float a = (d * qsv[j][r]) * in.ks;
-        const float rr = a > 0.f ? a : 0.f;
-        terms[wv][c][16 * j + 4 * qd + r] = rr * wvv[j][r];
-      }
-    }
+    for (int j = 0; j < HT; ++j) head_tile(j, kl, in.ks, terms[wv]);
     wave_lds_fence();  // the terms are in LDS
-    if (qd == 0 && in.t >= 0) {
-      float tv[H];
-#pragma unroll
-      for (int h = 0; h < H; ++h) tv[h] = terms[wv][c][h];
-      float sc = 0.f;
-#pragma unroll
-      for (int h = 0; h < H; ++h) sc = sc + tv[h];
-      if (hi)
-        keys[(int64_t)b * L + t_begin + 16 * (wv + 4 * m) + c] =
-            ((uint64_t)key_low_nan(sc) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)in.t);
-      else
-        scores[(int64_t)b * L + in.t] = sc;
-    }
+    if (qd == 0 && in.t >= 0) emit(16 * (wv + 4 * m) + c, in.t, terms[wv][c]);
     __builtin_amdgcn_wave_barrier();
   };
   // ping-pong over this wave's batches (bt = wv + 4 m).  The loads are
@@ -1223,10 +1335,11 @@ __global__ void __launch_bounds__(256) mla_combine_kernel(const uint16_t* __rest
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct IndexerWs {
-  float *lo, *hi;
+  float* hi;
   uint64_t* keys;
   uint32_t *wg_counts, *hist1;
   size_t zero_words;  // hist1
+  uint32_t* qlimbs;   // q's int8 limbs, written by the prep kernel
 };
 
 static size_t indexer_ws(int64_t b, int64_t l, char* base, IndexerWs* w) {
@@ -1236,19 +1349,19 @@ static size_t indexer_ws(int64_t b, int64_t l, char* base, IndexerWs* w) {
     off += align256(bytes);
     return p;
   };
-  float* lo = (float*)take((size_t)b * l * 4);
   float* hi = (float*)take((size_t)b * l * 4);
   uint64_t* keys = (uint64_t*)take((size_t)b * l * 8);
   uint32_t* wgc = (uint32_t*)take((size_t)b * kRsMaxWgs * 4);
   const size_t zbytes = (size_t)b * kHistBins * 4;
   uint32_t* z = (uint32_t*)take(zbytes);
+  uint32_t* qlimbs = (uint32_t*)take((size_t)b * 64 * 3 * kIdxD);  // q's int8 limbs, up to 64 heads
   if (w) {
-    w->lo = lo;
     w->hi = hi;
     w->keys = keys;
     w->wg_counts = wgc;
     w->hist1 = z;
     w->zero_words = zbytes / 4;
+    w->qlimbs = qlimbs;
   }
   return off;
 }
@@ -1321,29 +1434,28 @@ static int rescore_range(int64_t b, int64_t l) {
 }
 
 static void launch_rescore(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
-                           const int32_t* lengths, const float* hi, const uint32_t* hist1, uint64_t* keys,
-                           uint32_t* wg_counts, float* scores, int64_t b, int64_t h, int64_t l, int topk,
-                           int kdiv, hipStream_t st) {
+                           const int32_t* lengths, const float* hi, const uint32_t* hist1, const uint32_t* qlimbs,
+                           uint64_t* keys, uint32_t* wg_counts, float* scores, int64_t b, int64_t h, int64_t l,
+                           int topk, int kdiv, hipStream_t st) {
   const int range = rescore_range(b, l);
   const dim3 grid((unsigned)((l + range - 1) / range), (unsigned)b);
+#define MOSAIC_RESCORE(HT)                                                                                          \
+  if (!qlimbs)                                                                                                      \
+    hipLaunchKernelGGL((dsa_rescore_kernel<HT, false, false>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,   \
+                       hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);                           \
+  else if (range <= kRsPfRange)                                                                                     \
+    hipLaunchKernelGGL((dsa_rescore_kernel<HT, true, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, \
+                       hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);                               \
+  else                                                                                                              \
+    hipLaunchKernelGGL((dsa_rescore_kernel<HT, false, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,    \
+                       hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);
   switch (h / 16) {
-    case 1:
-      hipLaunchKernelGGL(dsa_rescore_kernel<1>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range, kdiv);
-      break;
-    case 2:
-      hipLaunchKernelGGL(dsa_rescore_kernel<2>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range, kdiv);
-      break;
-    case 3:
-      hipLaunchKernelGGL(dsa_rescore_kernel<3>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range, kdiv);
-      break;
-    default:
-      hipLaunchKernelGGL(dsa_rescore_kernel<4>, grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, hist1, keys,
-                         wg_counts, scores, l, topk, range, kdiv);
-      break;
+    case 1: MOSAIC_RESCORE(1) break;
+    case 2: MOSAIC_RESCORE(2) break;
+    case 3: MOSAIC_RESCORE(3) break;
+    default: MOSAIC_RESCORE(4) break;
   }
+#undef MOSAIC_RESCORE
 }
 
 struct MlaWs {
@@ -1411,12 +1523,14 @@ static int indexer_topk_impl(const uint8_t* q, const float* q_s, const uint8_t* 
   hipStream_t st = (hipStream_t)stream;
   IndexerWs ws;
   indexer_ws(b, l, (char*)workspace, &ws);
-  hipLaunchKernelGGL(dsa_zero_kernel, dim3((unsigned)((ws.zero_words + 255) / 256)), dim3(256), 0, st, ws.hist1,
-                     (int64_t)ws.zero_words);
+  const int64_t qwords = b * h * (kIdxD / 4);
+  const int64_t prep_n = std::max<int64_t>((int64_t)ws.zero_words, qwords);
+  hipLaunchKernelGGL(dsa_prep_kernel, dim3((unsigned)((prep_n + 255) / 256)), dim3(256), 0, st, ws.hist1,
+                     (int64_t)ws.zero_words, reinterpret_cast<const uint32_t*>(q), ws.qlimbs, qwords, (int)h);
   if (l > 0) {
-    dispatch_bound(q, q_s, k, k_s, w, lengths, ws.lo, ws.hi, ws.hist1, b, h, l, (int)kdiv, st);
-    launch_rescore(q, q_s, k, k_s, w, lengths, ws.hi, ws.hist1, ws.keys, ws.wg_counts, nullptr, b, h, l, (int)topk,
-                   (int)kdiv, st);
+    dispatch_bound(q, q_s, k, k_s, w, lengths, nullptr, ws.hi, ws.hist1, b, h, l, (int)kdiv, st);
+    launch_rescore(q, q_s, k, k_s, w, lengths, ws.hi, ws.hist1, ws.qlimbs, ws.keys, ws.wg_counts, nullptr, b, h, l,
+                   (int)topk, (int)kdiv, st);
   }
   hipLaunchKernelGGL(dsa_finish_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.wg_counts, lengths, l,
                      rescore_range(b, l), (int)topk, (int)offset, idx_out);
@@ -1447,7 +1561,7 @@ extern "C" int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, con
   if (rc) return rc;
   MOSAIC_CHECK_ARG(scores, "dsa_indexer_scores: null output");
   if (b == 0 || l == 0) return kOk;
-  launch_rescore(q, q_s, k, k_s, w, nullptr, nullptr, nullptr, nullptr, nullptr, scores, b, h, l, 0, 1,
+  launch_rescore(q, q_s, k, k_s, w, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, scores, b, h, l, 0, 1,
                  (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_scores");
 }
