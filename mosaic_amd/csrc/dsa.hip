@@ -662,7 +662,8 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // threads per row.  Rescoring workgroup w left wg_counts[b][w] keys at
 // keys[b][w * range ..].
 //  - At most kSortCap candidates: every key goes to registers (4 per thread),
-//    found through the prefix of the per-workgroup counts.  Otherwise a radix
+//    placed through the prefix of the per-workgroup counts (the first key
+//    slots of every workgroup are read together with the counts).  Otherwise a radix
 //    select over the keys in global memory finds the kk-th largest key and
 //    only the kk keys at or above it are kept.
 //  - Keys are bucketed by (key - smallest key) >> shift into kBuckets buckets,
@@ -683,6 +684,23 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t n = row_length(lengths, b, L);
   const int nwg = (int)((n + range - 1) / range);
+  const uint64_t* kb = keys + (int64_t)b * L;
+  // In flight with the counts: the first 4 S key slots of every rescoring
+  // workgroup (S = 1024 / nwg threads each), read before their counts are
+  // known and kept where the count covers them.
+  const int S = nwg <= 1024 ? 1024 / nwg : 0;
+  const bool spec = S > 0 && tid < S * nwg;
+  const int sw = spec ? tid / S : 0, ss = spec ? tid - sw * S : 0;
+  uint32_t sc = 0u;
+  uint64_t sk[4];
+  if (spec) {
+    sc = wg_counts[(int64_t)b * kRsMaxWgs + sw];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t slot = (int64_t)sw * range + ss + S * r;
+      sk[r] = slot < L ? kb[slot] : 0ull;
+    }
+  }
   // edge[w] = first slot of rescoring workgroup w (exclusive prefix)
   {
     uint32_t cw[4], local = 0;
@@ -711,7 +729,6 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
   int32_t* dst = idx_out + (int64_t)b * topk;
   for (int i = kk + tid; i < topk; i += 1024) dst[i] = -1;
   if (kk == 0) return;
-  const uint64_t* kb = keys + (int64_t)b * L;
   // slot i -> its key: the last workgroup w with edge[w] <= i owns it
   auto key_at = [&](int i) -> uint64_t {
     int lo = 0, hi = nwg - 1;
@@ -723,7 +740,20 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
   };
   int m;
   uint64_t x[4];
-  if (cnt <= kSortCap) {
+  if (cnt <= kSortCap && S > 0) {
+    // the keys into LDS at their workgroup's edge (the slots past 4 S one at a time), then 4 per thread
+    m = (int)cnt;
+    if (spec) {
+      const uint32_t e0 = edge[sw];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if ((uint32_t)(ss + S * r) < sc) bk[e0 + ss + S * r] = sk[r];
+      for (uint32_t j = (uint32_t)(ss + 4 * S); j < sc; j += (uint32_t)S) bk[e0 + j] = kb[(int64_t)sw * range + j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = tid + 1024 * r < m ? bk[tid + 1024 * r] : 0ull;
+  } else if (cnt <= kSortCap) {
     m = (int)cnt;
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = tid + 1024 * r < m ? key_at(tid + 1024 * r) : 0ull;
