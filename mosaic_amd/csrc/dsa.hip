@@ -293,9 +293,11 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   }
   if (hist1) {
     __syncthreads();
-    for (int i = threadIdx.x; i < kHistBins; i += 256) {
-      const uint32_t v = lh[i];
-      if (v) atomicAdd(&hist1[(int64_t)b * kHistBins + i], v);
+    // adjacent digits share one 64-bit add (each count < 2^32: no carry between them)
+    unsigned long long* h2 = reinterpret_cast<unsigned long long*>(hist1 + (int64_t)b * kHistBins);
+    for (int i = threadIdx.x; i < kHistBins / 2; i += 256) {
+      const unsigned long long v = (unsigned long long)lh[2 * i] | ((unsigned long long)lh[2 * i + 1] << 32);
+      if (v) atomicAdd(&h2[i], v);
     }
   }
 }
