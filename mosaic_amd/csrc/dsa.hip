@@ -153,16 +153,26 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     float* __restrict__ lo, float* __restrict__ hi, uint32_t* __restrict__ hist1, int64_t L, int kdiv) {
   constexpr int H = HT * 16;
   constexpr int GT = 16 * U;  // tokens per group
+  constexpr int kQv = H * kIdxD / 16;  // 16-byte pieces of the q row
   __shared__ uint32_t lh[kHistBins];
+  __shared__ u32x4_t qsh[kQv];
+  __shared__ float qssh[H], wsh[H];
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int c = lane & 15, qq = lane >> 4;
   const int64_t n = row_length(lengths, b, L);
-  if (hist1) {
-    for (int i = threadIdx.x; i < kHistBins; i += 256) lh[i] = 0u;
-    __syncthreads();
+  // the q row, its scales and weights are loaded once per workgroup (first,
+  // so that staging them waits for nothing else) and read from LDS below
+  u32x4_t qv[(kQv + 255) / 256];
+  {
+    const u32x4_t* q4 = reinterpret_cast<const u32x4_t*>(q + (int64_t)b * H * kIdxD);
+#pragma unroll
+    for (int i = 0; i < (kQv + 255) / 256; ++i)
+      if (kQv % 256 == 0 || threadIdx.x + 256 * i < kQv) qv[i] = q4[threadIdx.x + 256 * i];
   }
+  const float qsl = threadIdx.x < H ? qs[(int64_t)b * H + threadIdx.x] : 0.f;
+  const float wl = threadIdx.x < H ? w[(int64_t)b * H + threadIdx.x] : 0.f;
   const int64_t n_groups = (n + GT - 1) / GT;
   const int64_t nw = (int64_t)gridDim.x * 4, wid = (int64_t)blockIdx.x * 4 + wv;
   const int64_t iters = wid < n_groups ? (n_groups - 1 - wid) / nw + 1 : 0;
@@ -196,27 +206,34 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
 #pragma unroll
     for (int s = 0; s < D; ++s) load(s, s);
   }
-  const uint8_t* qb = q + (int64_t)b * H * kIdxD;
-  const float* qsb = qs + (int64_t)b * H;
-  const float* wb = w + (int64_t)b * H;
+  if (hist1)
+    for (int i = threadIdx.x; i < kHistBins; i += 256) lh[i] = 0u;
+#pragma unroll
+  for (int i = 0; i < (kQv + 255) / 256; ++i)
+    if (kQv % 256 == 0 || threadIdx.x + 256 * i < kQv) qsh[threadIdx.x + 256 * i] = qv[i];
+  if (threadIdx.x < H) {
+    qssh[threadIdx.x] = qsl;
+    wsh[threadIdx.x] = wl;
+  }
+  __syncthreads();
   // A operands: head rows 16 j + c as bf16, in 4 chunks of 8 of this lane's 32
   // code bytes (the same byte order as the k operand, so every K pairs once),
   // negated where q_scale < 0; per-lane weights c = w |q_scale| of the D rows
   // (heads 16 j + 4 qq + r)
-  // every load first (one round trip for the whole setup), then the math
   bf16x8_t qa[HT][4];
   float cw[HT][4];
   i32x8_t raw[HT];
   float qsr[HT], wr[HT], cq[HT][4], cwr[HT][4];
 #pragma unroll
   for (int j = 0; j < HT; ++j) {
-    raw[j] = load_fp8_operand(qb + (int64_t)(16 * j + c) * kIdxD, 0, qq);
-    qsr[j] = qsb[16 * j + c];
-    wr[j] = wb[16 * j + c];
+    const u32x4_t a0 = qsh[(16 * j + c) * (kIdxD / 16) + qq], a1 = qsh[(16 * j + c) * (kIdxD / 16) + 4 + qq];
+    raw[j] = i32x8_t{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+    qsr[j] = qssh[16 * j + c];
+    wr[j] = wsh[16 * j + c];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      cq[j][r] = qsb[16 * j + 4 * qq + r];
-      cwr[j][r] = wb[16 * j + 4 * qq + r];
+      cq[j][r] = qssh[16 * j + 4 * qq + r];
+      cwr[j][r] = wsh[16 * j + 4 * qq + r];
     }
   }
   float bound = 0.f;
