@@ -391,6 +391,7 @@ def config5_dsa(torch, ops):
         out[f"indexer_b{b}_l{l}"] = {"us": round(us, 1), "GBs": round(byts / us / 1e3, 1),
                                      "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)}
         del ks, kss
+    ws = ops.MoEWorkspace()  # the MLA calls' own workspace (its placement does not follow the indexer's size)
     for b in (1, 8):
         n = 65536
         qh = torch.randn(b, 128, 576, generator=g, device=dev).to(torch.bfloat16)
