@@ -1525,11 +1525,12 @@ static int mla_splits(int64_t b, int64_t topk) {
   return (int)std::max<int64_t>(s, 1);
 }
 // head tiles per workgroup: as many as divide the heads (at most 4), fewer
-// while the grid would leave most CUs idle
+// while the grid has fewer workgroups than CUs (B = 1, 128 heads: 32 splits x
+// 8 groups of 16 heads, 18.3 against 19.6 us for 4 groups of 32 heads)
 static int mla_head_tiles(int64_t b, int64_t h, int S) {
   int ht = 4;
   while (ht > 1 && (h / 16) % ht != 0) --ht;
-  while (ht > 1 && (h / 16) % (ht / 2) == 0 && (int64_t)S * b * (h / (16 * ht)) < 128) ht /= 2;
+  while (ht > 1 && (h / 16) % (ht / 2) == 0 && (int64_t)S * b * (h / (16 * ht)) < 256) ht /= 2;
   return ht;
 }
 static size_t mla_ws(int64_t b, int64_t h, int64_t topk, char* base, MlaWs* w) {
