@@ -659,21 +659,50 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
   }
 }
 
+// 64-bit min / max over the 64 lanes (all lanes active) on DPP moves of both
+// halves (the wave_max_u32 steps; lanes without a source get the identity),
+// broadcast from lane 63
+#define MOSAIC_DPP64(ident, v, ctrl, rmask)                                                       \
+  (((uint64_t)MOSAIC_DPP((uint32_t)((ident) >> 32), (uint32_t)((v) >> 32), ctrl, rmask) << 32) | \
+   (uint64_t)MOSAIC_DPP((uint32_t)(ident), (uint32_t)(v), ctrl, rmask))
+__device__ __forceinline__ uint64_t wave_bcast63_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off, 64);
-    v = o < v ? o : v;
-  }
-  return v;
+  constexpr uint64_t I = ~0ull;
+  uint64_t o;
+  o = MOSAIC_DPP64(I, v, 0xB1, 0xF);
+  v = o < v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x4E, 0xF);
+  v = o < v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x141, 0xF);
+  v = o < v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x140, 0xF);
+  v = o < v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x142, 0xA);
+  v = o < v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x143, 0xC);
+  v = o < v ? o : v;
+  return wave_bcast63_u64(v);
 }
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
+  constexpr uint64_t I = 0ull;
+  uint64_t o;
+  o = MOSAIC_DPP64(I, v, 0xB1, 0xF);
+  v = o > v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x4E, 0xF);
+  v = o > v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x141, 0xF);
+  v = o > v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x140, 0xF);
+  v = o > v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x142, 0xA);
+  v = o > v ? o : v;
+  o = MOSAIC_DPP64(I, v, 0x143, 0xC);
+  v = o > v ? o : v;
+  return wave_bcast63_u64(v);
 }
 
 // Stage 3: the kk best of the row's candidate keys (unique: exact score key <<
@@ -695,12 +724,14 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
                                                           const int32_t* __restrict__ lengths, int64_t L, int range,
                                                           int topk, int offset, int32_t* __restrict__ idx_out) {
   __shared__ uint64_t bk[kSortCap];
-  __shared__ uint32_t edge[kBuckets + 1];  // workgroup prefix, then bucket edges
+  __shared__ uint32_t edge[kBuckets + 1];  // workgroup prefix
+  __shared__ uint32_t bcnt[kBuckets];      // bucket counts, then bucket edges
   __shared__ uint32_t lh[256];
   __shared__ uint32_t sh[4];
   __shared__ uint64_t red[2][16];
   __shared__ uint32_t wtot[16];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  for (int i = tid; i < kBuckets; i += 1024) bcnt[i] = 0u;  // visible after the prefix's barriers
   const int64_t n = row_length(lengths, b, L);
   const int nwg = (int)((n + range - 1) / range);
   const uint64_t* kb = keys + (int64_t)b * L;
@@ -824,7 +855,6 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = tid + 1024 * r < m ? bk[tid + 1024 * r] : 0ull;
   }
-  __syncthreads();  // edge is reused for the buckets below
   // smallest and largest key
   uint64_t mn = ~0ull, mx = 0ull;
 #pragma unroll
@@ -839,7 +869,6 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
     red[0][wv] = mn;
     red[1][wv] = mx;
   }
-  for (int i = tid; i < kBuckets; i += 1024) edge[i] = 0u;
   __syncthreads();
   mn = red[0][0];
   mx = red[1][0];
@@ -855,15 +884,15 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     bx[r] = (uint32_t)((x[r] - mn) >> shift);
-    if (tid + 1024 * r < m) atomicAdd(&edge[bx[r]], 1u);
+    if (tid + 1024 * r < m) atomicAdd(&bcnt[bx[r]], 1u);
   }
   __syncthreads();
-  // descending exclusive scan: edge[d] = number of keys in buckets above d
+  // descending exclusive scan: bcnt[d] = number of keys in buckets above d
   // (thread tid owns buckets kBuckets-1-4 tid .. kBuckets-4-4 tid)
   uint32_t cb[4], local = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    cb[i] = edge[kBuckets - 1 - (4 * tid + i)];
+    cb[i] = bcnt[kBuckets - 1 - (4 * tid + i)];
     local += cb[i];
   }
   const uint32_t incl = wave_incl_scan_u32(local);
@@ -873,19 +902,19 @@ __global__ void __launch_bounds__(1024) dsa_finish_kernel(const uint64_t* __rest
   for (int i = 0; i < wv; ++i) acc += wtot[i];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    edge[kBuckets - 1 - (4 * tid + i)] = acc;
+    bcnt[kBuckets - 1 - (4 * tid + i)] = acc;
     acc += cb[i];
   }
   __syncthreads();
-  // scatter into bucket order; afterwards edge[d] = the end of bucket d
+  // scatter into bucket order; afterwards bcnt[d] = the end of bucket d
 #pragma unroll
   for (int r = 0; r < 4; ++r)
-    if (tid + 1024 * r < m) bk[atomicAdd(&edge[bx[r]], 1u)] = x[r];
+    if (tid + 1024 * r < m) bk[atomicAdd(&bcnt[bx[r]], 1u)] = x[r];
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     if (tid + 1024 * r >= m) continue;
-    const uint32_t s = bx[r] + 1 < kBuckets ? edge[bx[r] + 1] : 0u, e = edge[bx[r]];
+    const uint32_t s = bx[r] + 1 < kBuckets ? bcnt[bx[r] + 1] : 0u, e = bcnt[bx[r]];
     uint32_t rank = s;
     for (uint32_t j = s; j < e; ++j) rank += bk[j] > x[r] ? 1u : 0u;
     if (rank < (uint32_t)kk) dst[rank] = (int32_t)(0xFFFFFFFFu - (uint32_t)x[r]) + offset;
