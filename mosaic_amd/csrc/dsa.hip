@@ -77,6 +77,17 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
+// The same sum on DPP moves (the wave_max_u32 steps, another fp32 addition
+// order), broadcast from lane 63
+__device__ __forceinline__ float wave_sum_dpp_f32(float v) {
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0xB1, 0xF));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x4E, 0xF));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x141, 0xF));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x140, 0xF));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x142, 0xA));
+  v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x143, 0xC));
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
+}
 
 // Sum of |decoded e4m3| over the 32 code bytes of one MFMA operand lane.
 __device__ __forceinline__ float abs_sum_fp8(const i32x8_t v) {
@@ -1380,11 +1391,10 @@ __global__ void __launch_bounds__(256) mla_combine_kernel(const uint16_t* __rest
     const bool ok = lane < S;
     const float m = ok ? part_ml[(((int64_t)b * S + lane) * H + h) * 2] : -INFINITY;
     const float l = ok ? part_ml[(((int64_t)b * S + lane) * H + h) * 2 + 1] : 0.f;
-    float M = m;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    // DPP max (exact in any order); a NaN lane is left out, as fmaxf would
+    const float M = wave_max_f32(m == m ? m : -INFINITY);
     const float e = (m == -INFINITY) ? 0.f : __expf(m - M);
-    const float lsum = wave_sum_f32(l * e) + ((sink && M != -INFINITY) ? __expf(sink[h] - M) : 0.f);
+    const float lsum = wave_sum_dpp_f32(l * e) + ((sink && M != -INFINITY) ? __expf(sink[h] - M) : 0.f);
     if (ok) wgt[lane][hh] = (M == -INFINITY) ? 0.f : e / lsum;
   }
   __syncthreads();
