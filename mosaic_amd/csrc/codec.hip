@@ -187,8 +187,11 @@ __global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  // max over the chunk's 16-lane row on DPP moves (amax is never NaN: fmaxf drops NaN inputs)
+  amax = fmaxf(amax, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(amax), 0xB1, 0xF)));
+  amax = fmaxf(amax, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(amax), 0x4E, 0xF)));
+  amax = fmaxf(amax, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(amax), 0x141, 0xF)));
+  amax = fmaxf(amax, __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(amax), 0x140, 0xF)));
   float s;
   if (mode == 0) {
     s = act_scale_pow2(amax);
