@@ -72,14 +72,9 @@ __device__ __forceinline__ int64_t row_length(const int32_t* lengths, int b, int
   return n < 0 ? 0 : (n > L ? L : n);
 }
 
+// Sum over the 64 lanes (all lanes active) on DPP moves (the wave_max_u32
+// steps), broadcast from lane 63
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-// The same sum on DPP moves (the wave_max_u32 steps, another fp32 addition
-// order), broadcast from lane 63
-__device__ __forceinline__ float wave_sum_dpp_f32(float v) {
   v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0xB1, 0xF));
   v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x4E, 0xF));
   v += __uint_as_float(MOSAIC_DPP(0u, __float_as_uint(v), 0x141, 0xF));
@@ -256,7 +251,7 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) cw[j][r] = cwr[j][r] * fabsf(cq[j][r]);
   }
-  const float qbound = wave_sum_f32(bound) * kBoundFactor;
+  const float qbound = wave_sum_f32(bound) * kBoundFactor;  // any fp32 summation order is within the slack
   auto compute = [&](int s, int64_t i) {
     const int64_t g = wid + i * nw;
     const int nt = group_tokens(g);
@@ -1394,7 +1389,7 @@ __global__ void __launch_bounds__(256) mla_combine_kernel(const uint16_t* __rest
     // DPP max (exact in any order); a NaN lane is left out, as fmaxf would
     const float M = wave_max_f32(m == m ? m : -INFINITY);
     const float e = (m == -INFINITY) ? 0.f : __expf(m - M);
-    const float lsum = wave_sum_dpp_f32(l * e) + ((sink && M != -INFINITY) ? __expf(sink[h] - M) : 0.f);
+    const float lsum = wave_sum_f32(l * e) + ((sink && M != -INFINITY) ? __expf(sink[h] - M) : 0.f);
     if (ok) wgt[lane][hh] = (M == -INFINITY) ? 0.f : e / lsum;
   }
   __syncthreads();
