@@ -332,8 +332,9 @@ int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, const uint8_t*
                               float* scores, int64_t b, int64_t h, int64_t d, int64_t l, void* stream);
 
 /* First stage of mosaic_dsa_indexer_topk on its own: per token an interval
- * [lo, hi] (each [b, l] f32) that contains the canonical score, from the fp8
- * MFMA pass.  Diagnostic; same arguments as the scoring above. */
+ * [lo, hi] (each [b, l] f32) that contains the canonical score, from the
+ * bf16-MFMA pass over the exactly decoded fp8 codes.  Diagnostic; same
+ * arguments as the scoring above. */
 int mosaic_dsa_indexer_bounds(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
                               float* lo, float* hi, int64_t b, int64_t h, int64_t d, int64_t l, void* stream);
 
