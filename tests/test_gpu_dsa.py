@@ -118,6 +118,17 @@ def test_indexer_topk_bit_exact(dev, b, l, topk):
     np.testing.assert_array_equal(got, D.indexer_topk(q, qs, k, ks, w, topk))
 
 
+@pytest.mark.parametrize("h,b,l,topk", [(16, 2, 5000, 512), (32, 1, 70000, 2048), (48, 3, 1000, 256)])
+def test_indexer_topk_bit_exact_fewer_heads(dev, h, b, l, topk):
+    """16/32/48 heads: the rescoring's staged q limbs for fewer head tiles, with the range's k rows
+    staged in LDS (short ranges) and read from global memory (l = 70000)."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(h * 1000 + l)
+    q, qs, k, ks, w = _indexer_inputs(rng, b, h, l)
+    got = ops.dsa_indexer_topk(*_t(dev, q, qs, k, ks, w), topk).cpu().numpy()
+    np.testing.assert_array_equal(got, D.indexer_topk(q, qs, k, ks, w, topk))
+
+
 def test_indexer_lengths_offset_and_ties(dev):
     from mosaic_amd import ops
     rng = np.random.default_rng(11)
