@@ -39,6 +39,13 @@ extern "C" {
 int mosaic_version(void);
 /* Thread-local text of the last non-zero status. */
 const char* mosaic_last_error(void);
+/* Kernel launches this library has made on the calling thread since the
+ * process started.  Backs the reference's per-module last_launch_count()
+ * (kernels/skinny_fp4.py:17-22, kernels/mxint.py:33-34,
+ * kernels/qpa_mma.py:58-59, kernels/xsimt.py:31-32,
+ * kernels/w4a16_grouped.py:15-16), which count the launches of a module's
+ * operators since its MoE entry point last reset them. */
+uint64_t mosaic_launch_count(void);
 
 /* ------------------------------------------------------------- codecs ---- */
 /* MXFP4 quantizer, NK layout: w [n, k] (f32 or bf16) -> packed [n, k/2] + e8m0 [n, k/32].
@@ -202,6 +209,9 @@ int mosaic_moe_layout(const int32_t* ids, const float* weights, int64_t m, int64
 
 /* Tile list from per-expert counts [e] int32: one (expert, m_start, rows)
  * entry per block_m rows, ascending expert order, no per-expert cap.
+ * n_tiles[0] is the true tile total, as the reference returns
+ * tile_offsets[-1:]; entries past tile_cap are not written, so a caller
+ * sizes tile_cap >= the total (A / block_m + e bounds it).
  * Replaces emit_tiles (kernels/w4a16_grouped.py:151-169; the reference caps
  * each expert at MAX_TILES=32, :55-60).  e <= 4096. */
 int mosaic_emit_tiles(const int32_t* counts, int64_t e, int block_m, int32_t* tile_expert, int32_t* tile_start,

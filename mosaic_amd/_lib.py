@@ -21,6 +21,7 @@ F = c_float
 SIGNATURES: dict[str, tuple] = {
     "mosaic_version": (c_int, []),
     "mosaic_last_error": (ctypes.c_char_p, []),
+    "mosaic_launch_count": (ctypes.c_uint64, []),
     "mosaic_mx_quantize": (c_int, [P, I, P, P, I64, I64, I, P]),
     "mosaic_mx_dequant": (c_int, [P, P, P, I, I64, I64, P]),
     "mosaic_act_quant": (c_int, [P, I, P, P, I64, I64, I, I, P]),

@@ -301,10 +301,10 @@ extern "C" int mosaic_mx_quantize(const void* w, int w_dtype, uint8_t* packed, u
   if (nb == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
   if (w_dtype == MOSAIC_DTYPE_F32)
-    hipLaunchKernelGGL(mx_quantize_kernel<float>, dim3(grid1d(nb, 256)), dim3(256), 0, st, (const float*)w, packed,
+    MOSAIC_LAUNCH(mx_quantize_kernel<float>, dim3(grid1d(nb, 256)), dim3(256), 0, st, (const float*)w, packed,
                        scale, nb, k / 32, recipe);
   else
-    hipLaunchKernelGGL(mx_quantize_kernel<uint16_t>, dim3(grid1d(nb, 256)), dim3(256), 0, st, (const uint16_t*)w,
+    MOSAIC_LAUNCH(mx_quantize_kernel<uint16_t>, dim3(grid1d(nb, 256)), dim3(256), 0, st, (const uint16_t*)w,
                        packed, scale, nb, k / 32, recipe);
   MOSAIC_RETURN_LAUNCH("mx_quantize");
 }
@@ -317,9 +317,9 @@ extern "C" int mosaic_mx_dequant(const uint8_t* packed, const uint8_t* scale, vo
   if (nb == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
   if (out_dtype == MOSAIC_DTYPE_F32)
-    hipLaunchKernelGGL(mx_dequant_f32_kernel, dim3(grid1d(nb, 256)), dim3(256), 0, st, packed, scale, (float*)out, nb);
+    MOSAIC_LAUNCH(mx_dequant_f32_kernel, dim3(grid1d(nb, 256)), dim3(256), 0, st, packed, scale, (float*)out, nb);
   else if (out_dtype == MOSAIC_DTYPE_BF16)
-    hipLaunchKernelGGL(mx_dequant_bf16_kernel, dim3(grid1d(nb, 256)), dim3(256), 0, st, packed, scale,
+    MOSAIC_LAUNCH(mx_dequant_bf16_kernel, dim3(grid1d(nb, 256)), dim3(256), 0, st, packed, scale,
                        (uint16_t*)out, nb);
   else
     MOSAIC_CHECK_ARG(false, "mx_dequant: out dtype %d", out_dtype);
@@ -340,39 +340,39 @@ extern "C" int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s
     const int64_t chunks = m * k / 8;
     const unsigned g = grid1d(chunks, 256);
     if (x_dtype == MOSAIC_DTYPE_F32)
-      hipLaunchKernelGGL(act_quant128_kernel<float>, dim3(g), dim3(256), 0, st, (const float*)x, q, s, chunks, mode);
+      MOSAIC_LAUNCH(act_quant128_kernel<float>, dim3(g), dim3(256), 0, st, (const float*)x, q, s, chunks, mode);
     else
-      hipLaunchKernelGGL(act_quant128_kernel<uint16_t>, dim3(g), dim3(256), 0, st, (const uint16_t*)x, q, s, chunks,
+      MOSAIC_LAUNCH(act_quant128_kernel<uint16_t>, dim3(g), dim3(256), 0, st, (const uint16_t*)x, q, s, chunks,
                          mode);
     MOSAIC_RETURN_LAUNCH("act_quant");
   }
   unsigned grid = grid1d(waves * 64, 256);
   if (x_dtype == MOSAIC_DTYPE_F32)
-    hipLaunchKernelGGL(act_quant_kernel<float>, dim3(grid), dim3(256), 0, st, (const float*)x, q, s, m, k, block,
+    MOSAIC_LAUNCH(act_quant_kernel<float>, dim3(grid), dim3(256), 0, st, (const float*)x, q, s, m, k, block,
                        mode);
   else
-    hipLaunchKernelGGL(act_quant_kernel<uint16_t>, dim3(grid), dim3(256), 0, st, (const uint16_t*)x, q, s, m, k,
+    MOSAIC_LAUNCH(act_quant_kernel<uint16_t>, dim3(grid), dim3(256), 0, st, (const uint16_t*)x, q, s, m, k,
                        block, mode);
   MOSAIC_RETURN_LAUNCH("act_quant");
 }
 
 extern "C" int mosaic_selfcheck_converters(unsigned long long* counts, void* stream) {
   MOSAIC_CHECK_ARG(counts, "selfcheck_converters: null pointer");
-  hipLaunchKernelGGL(selfcheck_converters_kernel, dim3(4096), dim3(256), 0, (hipStream_t)stream, counts);
+  MOSAIC_LAUNCH(selfcheck_converters_kernel, dim3(4096), dim3(256), 0, (hipStream_t)stream, counts);
   MOSAIC_RETURN_LAUNCH("selfcheck_converters");
 }
 
 extern "C" int mosaic_e4m3_decode(const uint8_t* in, float* out, int64_t n, void* stream) {
   MOSAIC_CHECK_ARG(in && out, "e4m3_decode: null pointer");
   if (n == 0) return kOk;
-  hipLaunchKernelGGL(e4m3_decode_kernel, dim3(grid1d(n, 256)), dim3(256), 0, (hipStream_t)stream, in, out, n);
+  MOSAIC_LAUNCH(e4m3_decode_kernel, dim3(grid1d(n, 256)), dim3(256), 0, (hipStream_t)stream, in, out, n);
   MOSAIC_RETURN_LAUNCH("e4m3_decode");
 }
 
 extern "C" int mosaic_e4m3_encode(const float* in, uint8_t* out, int64_t n, void* stream) {
   MOSAIC_CHECK_ARG(in && out, "e4m3_encode: null pointer");
   if (n == 0) return kOk;
-  hipLaunchKernelGGL(e4m3_encode_kernel, dim3(grid1d(n, 256)), dim3(256), 0, (hipStream_t)stream, in, out, n);
+  MOSAIC_LAUNCH(e4m3_encode_kernel, dim3(grid1d(n, 256)), dim3(256), 0, (hipStream_t)stream, in, out, n);
   MOSAIC_RETURN_LAUNCH("e4m3_encode");
 }
 
@@ -383,7 +383,7 @@ extern "C" int mosaic_mxt16_prepack(const uint8_t* packed, const uint8_t* scale,
   MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_prepack: K=%lld must be a positive multiple of 128", (long long)k);
   const int ns = (int)(k / 128), ns4 = (ns + 3) / 4;
   const int64_t total = (n / 16) * (int64_t)ns4 * 4 * 64;
-  hipLaunchKernelGGL(mxt16_pack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, packed, scale,
+  MOSAIC_LAUNCH(mxt16_pack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, packed, scale,
                      packed_t, scale_t, n / 16, ns, ns4, k / 32, 0);
   MOSAIC_RETURN_LAUNCH("mxt16_prepack");
 }
@@ -395,7 +395,7 @@ extern "C" int mosaic_mxt16_unpack(const uint8_t* packed_t, const uint8_t* scale
   MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_unpack: K=%lld must be a positive multiple of 128", (long long)k);
   const int ns = (int)(k / 128), ns4 = (ns + 3) / 4;
   const int64_t total = (n / 16) * (int64_t)ns4 * 4 * 64;
-  hipLaunchKernelGGL(mxt16_pack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, packed, scale,
+  MOSAIC_LAUNCH(mxt16_pack_kernel, dim3(grid1d(total, 256)), dim3(256), 0, (hipStream_t)stream, packed, scale,
                      const_cast<uint8_t*>(packed_t), const_cast<uint8_t*>(scale_t), n / 16, ns, ns4, k / 32, 1);
   MOSAIC_RETURN_LAUNCH("mxt16_unpack");
 }

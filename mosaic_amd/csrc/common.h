@@ -23,6 +23,16 @@ enum : int { kOk = 0, kInvalid = -1, kUnsupported = -2, kTooLarge = -3 };
 
 void set_last_error(const char* fmt, ...);
 
+// Counts kernel launches made by this library on the calling thread
+// (mosaic_launch_count); every launch site goes through MOSAIC_LAUNCH.
+void note_launch();
+
+#define MOSAIC_LAUNCH(...)         \
+  do {                             \
+    ::mosaic::note_launch();       \
+    hipLaunchKernelGGL(__VA_ARGS__); \
+  } while (0)
+
 #define MOSAIC_CHECK_ARG(cond, ...)                     \
   do {                                                  \
     if (!(cond)) {                                      \

@@ -1467,7 +1467,7 @@ template <int HT, int D>
 static void launch_bound_d(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t l,
                            int gx, int kdiv, hipStream_t st) {
-  hipLaunchKernelGGL((dsa_index_bound_kernel<HT, kBoundU, D>), dim3((unsigned)gx, (unsigned)b), dim3(256), 0, st, q,
+  MOSAIC_LAUNCH((dsa_index_bound_kernel<HT, kBoundU, D>), dim3((unsigned)gx, (unsigned)b), dim3(256), 0, st, q,
                      qs, k, ks, w, lengths, lo, hi, hist1, l, kdiv);
 }
 
@@ -1524,13 +1524,13 @@ static void launch_rescore(const uint8_t* q, const float* qs, const uint8_t* k, 
   const dim3 grid((unsigned)((l + range - 1) / range), (unsigned)b);
 #define MOSAIC_RESCORE(HT)                                                                                          \
   if (!qlimbs)                                                                                                      \
-    hipLaunchKernelGGL((dsa_rescore_kernel<HT, false, false>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,   \
+    MOSAIC_LAUNCH((dsa_rescore_kernel<HT, false, false>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,   \
                        hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);                           \
   else if (range <= kRsPfRange)                                                                                     \
-    hipLaunchKernelGGL((dsa_rescore_kernel<HT, true, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, \
+    MOSAIC_LAUNCH((dsa_rescore_kernel<HT, true, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, \
                        hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);                               \
   else                                                                                                              \
-    hipLaunchKernelGGL((dsa_rescore_kernel<HT, false, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,    \
+    MOSAIC_LAUNCH((dsa_rescore_kernel<HT, false, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,    \
                        hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);
   switch (h / 16) {
     case 1: MOSAIC_RESCORE(1) break;
@@ -1609,14 +1609,14 @@ static int indexer_topk_impl(const uint8_t* q, const float* q_s, const uint8_t* 
   indexer_ws(b, l, (char*)workspace, &ws);
   const int64_t qwords = b * h * (kIdxD / 4);
   const int64_t prep_n = std::max<int64_t>((int64_t)ws.zero_words, qwords);
-  hipLaunchKernelGGL(dsa_prep_kernel, dim3((unsigned)((prep_n + 255) / 256)), dim3(256), 0, st, ws.hist1,
+  MOSAIC_LAUNCH(dsa_prep_kernel, dim3((unsigned)((prep_n + 255) / 256)), dim3(256), 0, st, ws.hist1,
                      (int64_t)ws.zero_words, reinterpret_cast<const uint32_t*>(q), ws.qlimbs, qwords, (int)h);
   if (l > 0) {
     dispatch_bound(q, q_s, k, k_s, w, lengths, nullptr, ws.hi, ws.hist1, b, h, l, (int)kdiv, st);
     launch_rescore(q, q_s, k, k_s, w, lengths, ws.hi, ws.hist1, ws.qlimbs, ws.keys, ws.wg_counts, nullptr, b, h, l,
                    (int)topk, (int)kdiv, st);
   }
-  hipLaunchKernelGGL(dsa_finish_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.wg_counts, lengths, l,
+  MOSAIC_LAUNCH(dsa_finish_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.wg_counts, lengths, l,
                      rescore_range(b, l), (int)topk, (int)offset, idx_out);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_topk");
 }
@@ -1681,14 +1681,14 @@ static int launch_mla(const uint16_t* q, const MlaKv& kv, const float* sink, con
   switch (ht) {
 #define MLA_CASE(HTV)                                                                                                  \
   case HTV:                                                                                                            \
-    hipLaunchKernelGGL((mla_decode_split_kernel<HTV, FP8, DR>), grid, dim3(256), 0, st, q, kv, idx, ws.part_o,       \
+    MOSAIC_LAUNCH((mla_decode_split_kernel<HTV, FP8, DR>), grid, dim3(256), 0, st, q, kv, idx, ws.part_o,       \
                        ws.part_ml, (int)topk, softmax_scale, chunk);                                                   \
     break;
     MLA_CASE(1) MLA_CASE(2) MLA_CASE(3) MLA_CASE(4)
 #undef MLA_CASE
   }
   MOSAIC_LAUNCH_CHECK("mla_decode_split");
-  hipLaunchKernelGGL(mla_combine_kernel, dim3((unsigned)kMlaDt, (unsigned)(h / 16), (unsigned)rows), dim3(256), 0, st,
+  MOSAIC_LAUNCH(mla_combine_kernel, dim3((unsigned)kMlaDt, (unsigned)(h / 16), (unsigned)rows), dim3(256), 0, st,
                      ws.part_o, ws.part_ml, sink, out, (int)h, S);
   MOSAIC_RETURN_LAUNCH("mla_sparse_decode");
 }

@@ -146,7 +146,7 @@ extern "C" int mosaic_dsa_kv_write(const uint16_t* kv, const int32_t* slots, int
                    "dsa_kv_write: give either the bf16 cache or the fp8 codes");
   MOSAIC_CHECK_ARG(cache_bf16 || (scales && (rope == 0 || rope_cache)), "dsa_kv_write: fp8 cache needs scales/rope");
   if (rows == 0) return kOk;
-  hipLaunchKernelGGL(dsa_kv_write_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, kv,
+  MOSAIC_LAUNCH(dsa_kv_write_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, kv,
                      slots, (int)rows, (int)d, (int)rope, (int)n, cache_bf16, codes, scales, rope_cache);
   MOSAIC_RETURN_LAUNCH("dsa_kv_write");
 }
@@ -160,7 +160,7 @@ extern "C" int mosaic_dsa_decode_indices(const int32_t* pos, int64_t rows, int64
   MOSAIC_CHECK_ARG(offset >= 0 && offset < (1ll << 31), "dsa_decode_indices: offset out of range");
   if (rows == 0) return kOk;
   const int64_t width = window + nc;
-  hipLaunchKernelGGL(dsa_decode_indices_kernel, dim3((unsigned)((width + 255) / 256), (unsigned)rows), dim3(256), 0,
+  MOSAIC_LAUNCH(dsa_decode_indices_kernel, dim3((unsigned)((width + 255) / 256), (unsigned)rows), dim3(256), 0,
                      (hipStream_t)stream, pos, (int)window, cidx, (int)nc, (int)(ratio > 0 ? ratio : 1), (int)offset,
                      out);
   MOSAIC_RETURN_LAUNCH("dsa_decode_indices");

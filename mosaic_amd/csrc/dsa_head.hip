@@ -204,14 +204,14 @@ extern "C" int mosaic_dsa_head_attention(const uint16_t* q, const uint16_t* k, c
                    workspace_bytes, (size_t)ctx * h * 4);
   hipStream_t st = (hipStream_t)stream;
   float* scores = (float*)workspace;
-  hipLaunchKernelGGL(head_scores_kernel, dim3((unsigned)((ctx + 255) / 256), (unsigned)h), dim3(256), 0, st, q, k,
+  MOSAIC_LAUNCH(head_scores_kernel, dim3((unsigned)((ctx + 255) / 256), (unsigned)h), dim3(256), 0, st, q, k,
                      scores, (int)ctx, (int)h, (int)d, scale);
   MOSAIC_LAUNCH_CHECK("dsa_head_scores");
   int sort_n = 1;
   while (sort_n < topk) sort_n <<= 1;
-  hipLaunchKernelGGL(head_topk_kernel, dim3((unsigned)h), dim3(1024), 0, st, scores, idx, (int)ctx, (int)topk, sort_n);
+  MOSAIC_LAUNCH(head_topk_kernel, dim3((unsigned)h), dim3(1024), 0, st, scores, idx, (int)ctx, (int)topk, sort_n);
   MOSAIC_LAUNCH_CHECK("dsa_head_topk");
-  hipLaunchKernelGGL(head_attend_kernel, dim3((unsigned)h), dim3(256), 0, st, scores, idx, v, out, (int)ctx, (int)h,
+  MOSAIC_LAUNCH(head_attend_kernel, dim3((unsigned)h), dim3(256), 0, st, scores, idx, v, out, (int)ctx, (int)h,
                      (int)dv, (int)topk);
   MOSAIC_RETURN_LAUNCH("dsa_head_attend");
 }

@@ -202,7 +202,7 @@ static void launch_fp8_gemv(const uint8_t* a, const float* as, const uint8_t* b,
   const int nb = (int)(k / 128 / KS);
   const dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)));
 #define FP8_GEMV(DV) \
-  hipLaunchKernelGGL((fp8_gemv_kernel<T, KS, DV>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, out_f32)
+  MOSAIC_LAUNCH((fp8_gemv_kernel<T, KS, DV>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, out_f32)
   if (nb % 8 == 0)
     FP8_GEMV(8);
   else if (nb % 7 == 0)
@@ -218,7 +218,7 @@ template <int T, int KS>
 static void launch_fp8_skinny(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c,
                               int64_t m, int64_t n, int64_t k, int out_f32, hipStream_t st) {
   dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)), (unsigned)((m + 15) / 16));
-  hipLaunchKernelGGL((fp8_gemm_skinny_kernel<T, KS>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n,
+  MOSAIC_LAUNCH((fp8_gemm_skinny_kernel<T, KS>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n,
                      (int)k, out_f32);
 }
 
@@ -447,11 +447,11 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
                              float* part = nullptr) {
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + kTileN - 1) / kTileN);
   const int nkb = (int)(k / 128), kps = (nkb + S - 1) / S;
-  hipLaunchKernelGGL((fp8_gemm_tiled_kernel<BM>), dim3((unsigned)tiles, (unsigned)S), dim3(BM * 2), 0, st, a, as, b,
+  MOSAIC_LAUNCH((fp8_gemm_tiled_kernel<BM>), dim3((unsigned)tiles, (unsigned)S), dim3(BM * 2), 0, st, a, as, b,
                      bs, c, (int)m, (int)n, (int)k, out_f32, kps, S > 1 ? part : nullptr);
   if (S > 1) {
     const int64_t mn = m * n;
-    hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, part, S, mn,
+    MOSAIC_LAUNCH(fp8_splitk_reduce_kernel, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, part, S, mn,
                        c, out_f32);
   }
 }
@@ -694,7 +694,7 @@ extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16
                    "fp8_block_dequant: K=%lld, block %dx%d", (long long)k, block_n, block_k);
   if (n == 0) return kOk;
   const int64_t total = n * k / 4;
-  hipLaunchKernelGGL(fp8_block_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+  MOSAIC_LAUNCH(fp8_block_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, w, s, out, n, k, block_n, block_k, (k + block_k - 1) / block_k);
   MOSAIC_RETURN_LAUNCH("fp8_block_dequant");
 }
@@ -759,7 +759,7 @@ static int fp8_block_gemm_impl(const uint8_t* a, const float* a_s, const uint8_t
   switch (plan.kind) {
     case 3: {
       const int64_t big_tiles = ((m + 255) / 256) * ((n + 255) / 256);
-      hipLaunchKernelGGL(fp8_gemm_big_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a, a_s, b, b_s, c, (int)m,
+      MOSAIC_LAUNCH(fp8_gemm_big_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a, a_s, b, b_s, c, (int)m,
                          (int)n, (int)k, f32);
       break;
     }

@@ -123,9 +123,9 @@ void launch_w8a16(const uint16_t* x, const uint8_t* w, const float* s, uint16_t*
   const int nb = (int)(k / 128 / KS);
   const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((m + 15) / 16));
   if (nb % 4 == 0 || nb >= 8)
-    hipLaunchKernelGGL((w8a16_gemv_kernel<1, KS, 4>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+    MOSAIC_LAUNCH((w8a16_gemv_kernel<1, KS, 4>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
   else
-    hipLaunchKernelGGL((w8a16_gemv_kernel<1, KS, 2>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+    MOSAIC_LAUNCH((w8a16_gemv_kernel<1, KS, 2>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
 }
 
 }  // namespace

@@ -586,6 +586,7 @@ static void launch_dec1_gateup_x(int D, dim3 grid, size_t lds, hipStream_t st, c
   // the events (stage timing, may be null) are recorded by the dispatch itself:
   // they bracket the kernel's execution, not the launch around it
 #define DEC_GU(DV)                                                                                              \
+  note_launch();                                                                                                \
   hipExtLaunchKernelGGL((moe_dec1_gateup_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, st, ev_start, ev_stop, \
                         0u, x, logits, bias, ids_in, w_in, ids_out, w_out, gu_p, gu_s, sh_p, sh_s, z, te, nt, H,  \
                         I, E, K, func, renorm, scale, limit)
@@ -605,6 +606,7 @@ static void launch_dec1_down_z(int DT, dim3 grid, size_t lds, hipStream_t st, co
                                const uint8_t* sh_s, uint16_t* y, int H, int I, int E, int K, int has_shared, int cpw,
                                hipEvent_t ev_stop) {
 #define DEC_DN(DV)                                                                                              \
+  note_launch();                                                                                                \
   hipExtLaunchKernelGGL((moe_dec1_down_kernel<KS, NSP, DV, ZV>), grid, dim3(KS * 64), lds, st, nullptr, ev_stop, \
                         0u, z, te, nt, d_p, d_s, sh_p, sh_s, y, H, I, E, K, has_shared, cpw)
   switch (DT) {
@@ -624,7 +626,7 @@ static void launch_dec1_linear_x(int D, const uint16_t* x, const uint8_t* pt, co
   const dim3 grid((unsigned)(n / rows));
   const size_t lds = (size_t)k * 2;
 #define DEC_LIN(DV)                                                                                              \
-  hipLaunchKernelGGL((mx_dec1_linear_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, s, x, pt, st, y, (int)n, (int)k, \
+  MOSAIC_LAUNCH((mx_dec1_linear_kernel<KS, DV, XV>), grid, dim3(KS * 64), lds, s, x, pt, st, y, (int)n, (int)k, \
                      rows)
   switch (D) {
     case 8: DEC_LIN(8); break;
@@ -755,10 +757,10 @@ static void launch_small_down_k(dim3 grid, int mr, hipStream_t st, const uint16_
                                 const uint8_t* d_p, const uint8_t* d_s, const uint8_t* sh_p, const uint8_t* sh_s,
                                 uint16_t* y, int M, int H, int I, int E, int has_shared, int cpw) {
   if (mr == 2)
-    hipLaunchKernelGGL((moe_small_down_kernel<KS, NSP, DT, 2>), grid, dim3(KS * 64), 0, st, z, te, tr, tp, nt, ptok,
+    MOSAIC_LAUNCH((moe_small_down_kernel<KS, NSP, DT, 2>), grid, dim3(KS * 64), 0, st, z, te, tr, tp, nt, ptok,
                        d_p, d_s, sh_p, sh_s, y, M, H, I, E, has_shared, cpw);
   else
-    hipLaunchKernelGGL((moe_small_down_kernel<KS, NSP, DT, 4>), grid, dim3(KS * 64), 0, st, z, te, tr, tp, nt, ptok,
+    MOSAIC_LAUNCH((moe_small_down_kernel<KS, NSP, DT, 4>), grid, dim3(KS * 64), 0, st, z, te, tr, tp, nt, ptok,
                        d_p, d_s, sh_p, sh_s, y, M, H, I, E, has_shared, cpw);
 }
 

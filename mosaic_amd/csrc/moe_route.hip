@@ -203,7 +203,8 @@ __global__ void __launch_bounds__(1024) emit_tiles_kernel(const int32_t* __restr
       }
     }
   }
-  if (tid == 0) n_tiles[0] = min(s_toff[E], tile_cap);
+  // the true total, as the reference returns tile_offsets[-1:]; entries past tile_cap are not written
+  if (tid == 0) n_tiles[0] = s_toff[E];
 }
 
 // Small-batch fast path for the MoE forward (A_ext <= 256, M <= 16): one
@@ -534,7 +535,7 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
   MOSAIC_CHECK_ARG(logits ? (ids_out && weights_out) : (ids_in && weights_in), "moe layout: missing ids/weights");
   if (out.small_ok && A_ext <= kSmallAssign && M <= kSmallTokens) {
     const unsigned threads = logits ? 1024u : 256u;
-    hipLaunchKernelGGL(route_layout_small_kernel, dim3(1), dim3(threads), 0, st, logits, bias, ids_in, weights_in,
+    MOSAIC_LAUNCH(route_layout_small_kernel, dim3(1), dim3(threads), 0, st, logits, bias, ids_in, weights_in,
                        ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
                        out);
     MOSAIC_RETURN_LAUNCH("moe_route_layout_small");
@@ -549,20 +550,20 @@ int launch_route_layout(const float* logits, const float* bias, const int32_t* i
     const int32_t* ids = ids_in;
     const float* wts = weights_in;
     if (logits) {
-      hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, logits, bias, ids_out,
+      MOSAIC_LAUNCH(route_topk_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, logits, bias, ids_out,
                          weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale);
       ids = ids_out;
       wts = weights_out;
     }
-    hipLaunchKernelGGL(layout_count_kernel, dim3((unsigned)nch), dim3(kLayoutChunk), 0, st, ids, A, (int)A_ext,
+    MOSAIC_LAUNCH(layout_count_kernel, dim3((unsigned)nch), dim3(kLayoutChunk), 0, st, ids, A, (int)A_ext,
                        (int)E, E_ext, out.chunk_counts, out.counters, out.n_counters);
-    hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(1024), 0, st, out.chunk_counts, nch, E_ext, block_m,
+    MOSAIC_LAUNCH(layout_scan_kernel, dim3(1), dim3(1024), 0, st, out.chunk_counts, nch, E_ext, block_m,
                        (int)tile_cap, out);
-    hipLaunchKernelGGL(layout_scatter_kernel, dim3((unsigned)nch), dim3(kLayoutChunk), 0, st, ids, wts, A,
+    MOSAIC_LAUNCH(layout_scatter_kernel, dim3((unsigned)nch), dim3(kLayoutChunk), 0, st, ids, wts, A,
                        (int)A_ext, (int)E, E_ext, (int)K, (int)K + (has_shared ? 1 : 0), out);
     MOSAIC_RETURN_LAUNCH("moe_route_layout_multi");
   }
-  hipLaunchKernelGGL(route_layout_kernel, dim3(1), dim3(kRouteThreads), 0, st, logits, bias, ids_in, weights_in,
+  MOSAIC_LAUNCH(route_layout_kernel, dim3(1), dim3(kRouteThreads), 0, st, logits, bias, ids_in, weights_in,
                      ids_out, weights_out, (int)M, (int)E, (int)K, func, renorm, route_scale, has_shared, block_m,
                      (int)tile_cap, out);
   MOSAIC_RETURN_LAUNCH("moe_route_layout");
@@ -583,7 +584,7 @@ extern "C" int mosaic_moe_route_topk(const float* logits, int64_t m, int64_t e, 
   MOSAIC_CHECK_ARG(score_func >= 0 && score_func <= 2, "moe_route_topk: score func %d", score_func);
   if (m <= 0) return kOk;
   unsigned grid = (unsigned)((m * 64 + 255) / 256);
-  hipLaunchKernelGGL(route_topk_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, logits, bias, ids, weights,
+  MOSAIC_LAUNCH(route_topk_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, logits, bias, ids, weights,
                      (int)m, (int)e, (int)top_k, score_func, renorm, route_scale);
   MOSAIC_RETURN_LAUNCH("moe_route_topk");
 }
@@ -620,7 +621,7 @@ extern "C" int mosaic_emit_tiles(const int32_t* counts, int64_t e, int block_m, 
   MOSAIC_CHECK_ARG(e >= 1 && e <= 4096, "emit_tiles: E=%lld (1..4096)", (long long)e);
   MOSAIC_CHECK_ARG(block_m >= 1, "emit_tiles: block_m=%d", block_m);
   MOSAIC_CHECK_ARG(tile_cap >= 0 && tile_cap < (1ll << 31), "emit_tiles: tile_cap=%lld", (long long)tile_cap);
-  hipLaunchKernelGGL(emit_tiles_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, counts, (int)e, block_m,
+  MOSAIC_LAUNCH(emit_tiles_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, counts, (int)e, block_m,
                      tile_expert, tile_start, tile_rows, n_tiles, (int)tile_cap);
   MOSAIC_RETURN_LAUNCH("emit_tiles");
 }

@@ -469,7 +469,7 @@ template <int T, int KS, bool TILED>
 static void launch_linear(const uint16_t* x, const uint8_t* packed, const uint8_t* scale, uint16_t* y, int64_t m,
                           int64_t n, int64_t k, hipStream_t st) {
   dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)), (unsigned)((m + 15) / 16));
-  hipLaunchKernelGGL((mx_linear_a16_kernel<T, KS, TILED>), grid, dim3(KS * 64), 0, st, x, packed, scale, y, (int)m,
+  MOSAIC_LAUNCH((mx_linear_a16_kernel<T, KS, TILED>), grid, dim3(KS * 64), 0, st, x, packed, scale, y, (int)m,
                      (int)n, (int)k);
 }
 
@@ -569,7 +569,7 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
     // rows of workgroups: at most one per tile, and few enough for the grid to be resident
     const int64_t cols = inter / (8 * kGuT);
     const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(m * top_k + has_shared, kSmallGuResidentWgs / cols));
-    hipLaunchKernelGGL((moe_small_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)cols, (unsigned)rows), dim3(kGuKS * 64), 0,
+    MOSAIC_LAUNCH((moe_small_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)cols, (unsigned)rows), dim3(kGuKS * 64), 0,
                        st, x, logits, route_bias, ids, weights, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale,
                        w.tile_expert, w.tile_rows, w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)m,
                        (int)hidden, (int)inter, (int)n_experts, (int)top_k, has_shared, score_func, renorm,
@@ -593,18 +593,18 @@ extern "C" int mosaic_moe_a16_forward(const uint16_t* x, const float* logits, in
   if (rc != 0) return rc;
   mark(1);
   const unsigned tcap = (unsigned)w.tile_cap;
-  hipLaunchKernelGGL((moe_a16_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)(inter / (8 * kGuT)), tcap),
+  MOSAIC_LAUNCH((moe_a16_gateup_kernel<kGuT, kGuKS>), dim3((unsigned)(inter / (8 * kGuT)), tcap),
                      dim3(kGuKS * 64), 0, st, x, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert,
                      w.tile_rows, w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
                      (int)n_experts, swiglu_limit);
   MOSAIC_LAUNCH_CHECK("moe_a16_gateup");
   mark(2);
-  hipLaunchKernelGGL((moe_a16_down_kernel<kDnT, kDnKS>), dim3((unsigned)(hidden / (16 * kDnT)), tcap),
+  MOSAIC_LAUNCH((moe_a16_down_kernel<kDnT, kDnKS>), dim3((unsigned)(hidden / (16 * kDnT)), tcap),
                      dim3(kDnKS * 64), 0, st, w.z, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert,
                      w.tile_rows, w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
   MOSAIC_LAUNCH_CHECK("moe_a16_down");
   mark(3);
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
+  MOSAIC_LAUNCH(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
                      w.yp, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
   MOSAIC_LAUNCH_CHECK("moe_combine");
   mark(4);

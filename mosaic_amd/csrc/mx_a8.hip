@@ -154,7 +154,7 @@ template <int T, int KS>
 static void launch_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* pt, const uint8_t* st, uint16_t* y,
                              int64_t m, int64_t n, int64_t k, hipStream_t s) {
   dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)), (unsigned)((m + 15) / 16));
-  hipLaunchKernelGGL((mx_linear_a8_kernel<T, KS>), grid, dim3(KS * 64), 0, s, xq, sa, pt, st, y, (int)m, (int)n,
+  MOSAIC_LAUNCH((mx_linear_a8_kernel<T, KS>), grid, dim3(KS * 64), 0, s, xq, sa, pt, st, y, (int)m, (int)n,
                      (int)k);
 }
 
@@ -866,7 +866,7 @@ extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const 
     // GPU idle (128 x 1536 x 7168: 75.8 us staged, 25.8 us on the 16-row kernel;
     // 512 x 7168 x 16384: 236 against 348 us)
     const int64_t tiles8 = ((m + 255) / 256 + 7) / 8 * 8;
-    hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(n / 256 * tiles8)), dim3(kPfWaves * 64), 0, st, xq,
+    MOSAIC_LAUNCH(moe_a8_down_prefill_kernel, dim3((unsigned)(n / 256 * tiles8)), dim3(kPfWaves * 64), 0, st, xq,
                        sa, packed_t, scale_t, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, y, (int)n, (int)k,
                        1, (int)m);
     MOSAIC_RETURN_LAUNCH("mxt16_linear_a8_prefill");
@@ -934,26 +934,26 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
     uint16_t* yb = reinterpret_cast<uint16_t*>(w.yp);  // bf16 partials in the fp32 partial buffer
     const int64_t tcap8 = (tcap + 7) / 8 * 8;
     // the gate/up epilogue writes z already quantized (1x128 pow2 e4m3, as act_quant mode 0)
-    hipLaunchKernelGGL(moe_a8_gateup_prefill_kernel, dim3((unsigned)(inter / 128 * tcap8)), dim3(kPfWaves * 64), 0, st,
+    MOSAIC_LAUNCH(moe_a8_gateup_prefill_kernel, dim3((unsigned)(inter / 128 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.xq, w.xs, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_rows,
                        w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.zq, w.zs, (int)hidden, (int)inter,
                        (int)n_experts, swiglu_limit);
     MOSAIC_LAUNCH_CHECK("moe_a8_gateup_prefill");
     mark(3);
     mark(4);  // the z requant is fused into the gate/up epilogue
-    hipLaunchKernelGGL(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
+    MOSAIC_LAUNCH(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows, w.tile_p0,
                        w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts, 0);
     MOSAIC_LAUNCH_CHECK("moe_a8_down_prefill");
     mark(5);
-    hipLaunchKernelGGL(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 8 + 127) / 128), (unsigned)m), dim3(128),
+    MOSAIC_LAUNCH(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 8 + 127) / 128), (unsigned)m), dim3(128),
                        0, st, yb, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
     MOSAIC_LAUNCH_CHECK("moe_a8_combine_bf16");
     mark(6);
     return kOk;
   }
   constexpr int GT = 2, GKS = 4, DT = 2, DKS = 4;
-  hipLaunchKernelGGL((moe_a8_gateup_kernel<GT, GKS>), dim3((unsigned)(inter / (8 * GT)), (unsigned)tcap), dim3(GKS * 64), 0,
+  MOSAIC_LAUNCH((moe_a8_gateup_kernel<GT, GKS>), dim3((unsigned)(inter / (8 * GT)), (unsigned)tcap), dim3(GKS * 64), 0,
                      st, w.xq, w.xs, gu_packed, gu_scale, sh_gu_packed, sh_gu_scale, w.tile_expert, w.tile_rows,
                      w.tile_p0, w.n_tiles, w.perm_token, w.perm_weight, w.z, (int)hidden, (int)inter,
                      (int)n_experts, swiglu_limit);
@@ -963,12 +963,12 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
   rc = mosaic_act_quant(w.z, MOSAIC_DTYPE_BF16, w.zq, w.zs, A, inter, 128, 0, stream);
   if (rc != 0) return rc;
   mark(4);
-  hipLaunchKernelGGL((moe_a8_down_kernel<DT, DKS>), dim3((unsigned)(hidden / (16 * DT)), (unsigned)tcap), dim3(DKS * 64), 0,
+  MOSAIC_LAUNCH((moe_a8_down_kernel<DT, DKS>), dim3((unsigned)(hidden / (16 * DT)), (unsigned)tcap), dim3(DKS * 64), 0,
                      st, w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows,
                      w.tile_p0, w.n_tiles, w.yp, (int)hidden, (int)inter, (int)n_experts);
   MOSAIC_LAUNCH_CHECK("moe_a8_down");
   mark(5);
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
+  MOSAIC_LAUNCH(moe_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st,
                      w.yp, w.combine_pos, y, (int)m, (int)(top_k + has_shared), (int)hidden);
   MOSAIC_LAUNCH_CHECK("moe_a8_combine");
   mark(6);

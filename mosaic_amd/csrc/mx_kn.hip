@@ -170,7 +170,7 @@ int launch_kn(const uint16_t* x, const int32_t* x_rows, const uint8_t* packed, c
   }
   const dim3 grid((unsigned)((n + kKnWgCols - 1) / kKnWgCols), (unsigned)ks, (unsigned)zdim);
 #define KN_LAUNCH(NSV)                                                                                              \
-  hipLaunchKernelGGL(mx_kn_a16_kernel<NSV>, grid, dim3(256), 0, st, x, x_rows, packed, scale, w_stride, s_stride, \
+  MOSAIC_LAUNCH(mx_kn_a16_kernel<NSV>, grid, dim3(256), 0, st, x, x_rows, packed, scale, w_stride, s_stride, \
                      tl, part, y, (int)m, (int)n, (int)k)
   if (ns == 16)
     KN_LAUNCH(16);
@@ -182,7 +182,7 @@ int launch_kn(const uint16_t* x, const int32_t* x_rows, const uint8_t* packed, c
   MOSAIC_LAUNCH_CHECK("mx_kn_a16");
   if (part) {
     const int64_t mn = m * n;
-    hipLaunchKernelGGL(kn_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, y, mn, (int)ks);
+    MOSAIC_LAUNCH(kn_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, part, y, mn, (int)ks);
     MOSAIC_LAUNCH_CHECK("mx_kn_reduce");
   }
   return kOk;
@@ -318,14 +318,14 @@ extern "C" int mosaic_moe_skinny_forward(const uint16_t* x, const int32_t* ids, 
   rc = launch_kn(x, l.perm_token, gu_packed, gu_scale, hidden * inter, hidden * (2 * inter / 32), tl, l.tile_cap,
                  w.part, (size_t)-1, w.gu, a, 2 * inter, hidden, w.ns_gu, st);
   if (rc != 0) return rc;
-  hipLaunchKernelGGL(skinny_swiglu_kernel, dim3((unsigned)((a * inter + 255) / 256)), dim3(256), 0, st, w.gu, l.z, a,
+  MOSAIC_LAUNCH(skinny_swiglu_kernel, dim3((unsigned)((a * inter + 255) / 256)), dim3(256), 0, st, w.gu, l.z, a,
                      (int)inter);
   MOSAIC_LAUNCH_CHECK("moe_skinny_swiglu");
   uint16_t* yg = reinterpret_cast<uint16_t*>(l.yp);
   rc = launch_kn(l.z, nullptr, d_packed, d_scale, inter * hidden / 2, inter * (hidden / 32), tl, l.tile_cap, w.part,
                  (size_t)-1, yg, a, hidden, inter, w.ns_d, st);
   if (rc != 0) return rc;
-  hipLaunchKernelGGL(skinny_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st, yg,
+  MOSAIC_LAUNCH(skinny_combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)m), dim3(256), 0, st, yg,
                      l.inv_pos, weights, y, (int)m, (int)top_k, (int)hidden);
   MOSAIC_RETURN_LAUNCH("moe_skinny_combine");
 }

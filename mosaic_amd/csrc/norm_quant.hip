@@ -125,7 +125,7 @@ extern "C" int mosaic_rmsnorm_act_quant(const uint16_t* x, const float* w, float
   const int nchunk = (int)((h / 8 + 255) / 256);
 #define NQ_CASE(N)                                                                                               \
   case N:                                                                                                        \
-    hipLaunchKernelGGL(rmsnorm_act_quant_kernel<N>, dim3((unsigned)m), dim3(256), 0, st, x, w, eps, (int)h, y, q, \
+    MOSAIC_LAUNCH(rmsnorm_act_quant_kernel<N>, dim3((unsigned)m), dim3(256), 0, st, x, w, eps, (int)h, y, q, \
                        s, mode);                                                                                 \
     break;
   switch (nchunk) {

@@ -80,10 +80,10 @@ __global__ void __launch_bounds__(256) router_logits_kernel(const TX* __restrict
 template <typename TX, typename TW>
 void launch_router(const void* x, const void* w, float* logits, int64_t m, int64_t e, int64_t h, hipStream_t st) {
   if (m <= 4) {
-    hipLaunchKernelGGL((router_logits_kernel<TX, TW, 4, 1>), dim3((unsigned)e, (unsigned)((m + 3) / 4)), dim3(256), 0,
+    MOSAIC_LAUNCH((router_logits_kernel<TX, TW, 4, 1>), dim3((unsigned)e, (unsigned)((m + 3) / 4)), dim3(256), 0,
                        st, (const TX*)x, (const TW*)w, logits, (int)m, (int)e, (int)h);
   } else {
-    hipLaunchKernelGGL((router_logits_kernel<TX, TW, 8, 2>), dim3((unsigned)((e + 1) / 2), (unsigned)((m + 7) / 8)),
+    MOSAIC_LAUNCH((router_logits_kernel<TX, TW, 8, 2>), dim3((unsigned)((e + 1) / 2), (unsigned)((m + 7) / 8)),
                        dim3(256), 0, st, (const TX*)x, (const TW*)w, logits, (int)m, (int)e, (int)h);
   }
 }

@@ -8,6 +8,9 @@
 namespace mosaic {
 
 static thread_local char g_last_error[512] = "";
+static thread_local uint64_t g_launches = 0;
+
+void note_launch() { ++g_launches; }
 
 void set_last_error(const char* fmt, ...) {
   va_list ap;
@@ -19,5 +22,7 @@ void set_last_error(const char* fmt, ...) {
 }  // namespace mosaic
 
 extern "C" const char* mosaic_last_error(void) { return mosaic::g_last_error; }
+
+extern "C" uint64_t mosaic_launch_count(void) { return mosaic::g_launches; }
 
 extern "C" int mosaic_version(void) { return MOSAIC_AMD_ABI_VERSION; }

@@ -3,39 +3,69 @@
 The reference's GEMV drop-ins accept raw ``packed``/``scale`` tensors and a
 ``prepacked`` argument; a caller that passes only the raw tensors would
 otherwise pay an MXT16 prepack (a full read and write of the weight) on every
-call.  Entries are keyed by the tensors' identity: a weak reference to each
-raw tensor (so a freed tensor whose memory is reused never matches) plus its
-in-place version counter (so an in-place update re-prepacks).  No device data
-is read back.
+call.
+
+An entry is keyed by the caller's source tensors: each one's data pointer,
+shape, strides, dtype and device.  A hit also needs every source's storage
+to be the same live storage object as when the entry was made (torch keeps
+one Python object per live storage, shared by every view of it, dtype views
+included), and its in-place version counter unchanged (views share it, so an
+in-place update through any view re-prepacks).  A fresh ``.view()`` of the
+same weight therefore hits, and a freed tensor whose memory is reused never
+matches.  The entry is dropped as soon as any of its storages is freed, so the
+prepacked copy lives exactly as long as the weight it was made from.  No
+device data is read back.
 """
 from __future__ import annotations
 
 import weakref
-from collections import OrderedDict
+from typing import Callable, Sequence
 
 import torch
 
 from .. import ops
 
-_MAX_ENTRIES = 64
-_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_CACHE: "dict[tuple, tuple]" = {}
+
+
+def _root(t: torch.Tensor):
+    return t.untyped_storage()
+
+
+def _key(srcs: Sequence[torch.Tensor]) -> tuple:
+    return tuple((t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, t.device) for t in srcs)
+
+
+def cached(srcs: Sequence[torch.Tensor], make: Callable[[], object]):
+    """``make()``, reused while every tensor of ``srcs`` is alive and unmodified."""
+    key = _key(srcs)
+    roots = [_root(t) for t in srcs]
+    hit = _CACHE.get(key)
+    if hit is not None:
+        refs, versions, value = hit
+        if all(r() is t for r, t in zip(refs, roots)) and versions == tuple(t._version for t in srcs):
+            return value
+        del _CACHE[key]
+    value = make()
+
+    def _drop(_ref, key=key):
+        # only the entry made with these roots: a newer one under the same key has other refs
+        entry = _CACHE.get(key)
+        if entry is not None and any(r is _ref for r in entry[0]):
+            del _CACHE[key]
+
+    refs = tuple(weakref.ref(t, _drop) for t in roots)
+    _CACHE[key] = (refs, tuple(t._version for t in srcs), value)
+    return value
 
 
 def mxt16(packed: torch.Tensor, scale: torch.Tensor) -> ops.MXT16:
     """ops.mxt16_prepack(packed, scale), reused while both tensors are alive and unmodified."""
-    key = (packed.data_ptr(), scale.data_ptr(), tuple(packed.shape), tuple(scale.shape), packed.device)
-    hit = _CACHE.get(key)
-    if hit is not None:
-        pref, sref, pver, sver, w = hit
-        if pref() is packed and sref() is scale and packed._version == pver and scale._version == sver:
-            _CACHE.move_to_end(key)
-            return w
-    w = ops.mxt16_prepack(packed, scale)
-    _CACHE[key] = (weakref.ref(packed), weakref.ref(scale), packed._version, scale._version, w)
-    _CACHE.move_to_end(key)
-    while len(_CACHE) > _MAX_ENTRIES:
-        _CACHE.popitem(last=False)
-    return w
+    return cached((packed, scale), lambda: ops.mxt16_prepack(packed, scale))
+
+
+def size() -> int:
+    return len(_CACHE)
 
 
 def clear() -> None:

@@ -8,6 +8,7 @@ from __future__ import annotations
 import torch
 
 from .. import ops
+from . import _prepack_cache
 from .mxfp4 import MX_BLOCK
 
 ACT_BLOCK = 128
@@ -59,4 +60,4 @@ def reference_fp4_linear_source_semantics(x_bf16: torch.Tensor, packed: torch.Te
     n, kh = packed.shape
     if kh * 2 != k:
         raise ValueError(f"packed K {kh * 2} != x K {k}")
-    return ops.mxt16_linear_a8(x_bf16, ops.mxt16_prepack(packed, scale_w))
+    return ops.mxt16_linear_a8(x_bf16, _prepack_cache.mxt16(packed, scale_w))

@@ -13,6 +13,14 @@ import torch
 
 from .. import ops
 from . import _a8, _prepack_cache
+from ._launches import LaunchCounter
+
+_LAUNCHES = LaunchCounter()
+
+
+def last_launch_count() -> int:
+    """Kernel launches since ``fused_moe_mxint`` last started (``kernels/mxint.py:33-34,1460``)."""
+    return _LAUNCHES.n
 
 
 @dataclass
@@ -48,13 +56,15 @@ prepack_expert_bank_mxint_packed4 = prepack_expert_bank_mxint
 def mxint_dp4a_gemm(x, packed, scale_w, n_out, prequant=None, xint=None, prepacked=None,
                     weight_repr: str = "hot8") -> torch.Tensor:
     """x [M, K] bf16 -> [M, N] bf16, A8 (``kernels/mxint.py:362-401``)."""
-    return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
+    with _LAUNCHES.track():
+        return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
 
 
 def mxint_imma_gemm(x, packed, scale_w, n_out, prequant=None, xint=None, qpa_k=8, ordered=True, prepacked=None,
                     weight_repr: str = "hot8") -> torch.Tensor:
     """x [M, K] bf16 -> [M, N] bf16, A8 (``kernels/mxint.py:1014-1054``)."""
-    return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
+    with _LAUNCHES.track():
+        return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
 
 
 def fused_moe_mxint(x, expert_ids, expert_weights, packed_gate_up=None, scale_gate_up=None, packed_down=None,
@@ -70,6 +80,14 @@ def fused_moe_mxint(x, expert_ids, expert_weights, packed_gate_up=None, scale_ga
     timed with HIP events and the call waits for them, as the reference does."""
     if weight_repr not in ("hot8", "packed4", "hybrid"):
         raise ValueError(f"weight_repr must be hot8|packed4|hybrid, got {weight_repr}")
+    _LAUNCHES.reset()
+    with _LAUNCHES.track():
+        return _fused_moe_a8(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down,
+                             bank, swiglu_limit, stage_times)
+
+
+def _fused_moe_a8(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down,
+                  bank: MXT16Bank | None, swiglu_limit: float, stage_times: dict | None) -> torch.Tensor:
     if bank is None:
         if packed_gate_up is None or packed_down is None:
             raise TypeError("fused_moe_mxint requires bank= or packed_gate_up/packed_down")

@@ -5,7 +5,15 @@ import torch
 
 from .. import ops
 from . import _a8
-from .mxint import MXT16Bank, fused_moe_mxint, prepack_expert_bank_mxint
+from ._launches import LaunchCounter
+from .mxint import MXT16Bank, _fused_moe_a8, prepack_expert_bank_mxint
+
+_LAUNCHES = LaunchCounter()
+
+
+def last_launch_count() -> int:
+    """Kernel launches since ``fused_moe_qpa`` last started (``kernels/qpa_mma.py:58-59,698``)."""
+    return _LAUNCHES.n
 
 
 def prepack_qpa(packed: torch.Tensor, scale: torch.Tensor, stage: str = "qpa_k32_fragment"):
@@ -25,7 +33,8 @@ def qpa_mma_gemm(x, packed, scale_w, n_out, backend="native", qpa_k=1, prequant=
     e4m3 codes + scales."""
     if x_norm is not None and sA is not None:
         prequant = (x_norm, sA)
-    return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
+    with _LAUNCHES.track():
+        return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
 
 
 def prepack_expert_bank_qpa(packed_g, scale_g, packed_u=None, scale_u=None, packed_d=None, scale_d=None,
@@ -38,5 +47,7 @@ def fused_moe_qpa(x, expert_ids, expert_weights, packed_gate_up=None, scale_gate
                   scale_down=None, bank: MXT16Bank | None = None, crossover: int = 3, qpa_k: int = 8,
                   xsimt_k: int = 4, swiglu_limit: float = 10.0) -> torch.Tensor:
     """A8 routed MoE (``kernels/qpa_mma.py:681-784``); same contract as ``fused_moe_mxint``."""
-    return fused_moe_mxint(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down,
-                           bank=bank, swiglu_limit=swiglu_limit)
+    _LAUNCHES.reset()
+    with _LAUNCHES.track():
+        return _fused_moe_a8(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down,
+                             bank, swiglu_limit, None)

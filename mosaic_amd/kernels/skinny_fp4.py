@@ -12,11 +12,15 @@ from __future__ import annotations
 import torch
 
 from .. import ops
+from ._launches import LaunchCounter
+
+_LAUNCHES = LaunchCounter()
 
 
 def last_launch_count() -> int:
-    """Launches of the last call (the GEMM, plus a split-K sum when K is split)."""
-    return 2
+    """Kernel launches since ``fused_moe_skinny`` last started (``kernels/skinny_fp4.py:17-22``):
+    each ``skinny_mxfp4_gemm`` adds its GEMM (plus a split-K sum when K is split)."""
+    return _LAUNCHES.n
 
 
 def skinny_mxfp4_gemm(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, n_out: int) -> torch.Tensor:
@@ -28,7 +32,8 @@ def skinny_mxfp4_gemm(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor
         raise ValueError(f"n_out={n_out} != packed N={n}")
     if k_p != k:
         raise ValueError(f"packed K={k_p} != x K={k}")
-    return ops.mx_kn_linear_a16(x, packed, scale)
+    with _LAUNCHES.track():
+        return ops.mx_kn_linear_a16(x, packed, scale)
 
 
 def _stack(t):
@@ -42,9 +47,11 @@ def fused_moe_skinny(x, expert_ids, expert_weights, packed_gate_up, scale_gate_u
     (or [k_tok]), expert_weights of the same shape (None = ones); KN banks
     packed_gate_up [E, H, 2I/2] + [E, H, 2I/32] (gate | up along N),
     packed_down [E, I, H/2] + [E, I, H/32] -> [k_tok, H] in x.dtype."""
+    _LAUNCHES.reset()
     ids = expert_ids if expert_ids.dim() == 2 else expert_ids.reshape(-1, 1)
     w = (torch.ones(ids.shape, dtype=torch.float32, device=x.device) if expert_weights is None
          else expert_weights.reshape(ids.shape).to(torch.float32))
-    y = ops.moe_skinny_forward(x.to(torch.bfloat16), ids, w, _stack(packed_gate_up), _stack(scale_gate_up),
-                               _stack(packed_down), _stack(scale_down))
+    with _LAUNCHES.track():
+        y = ops.moe_skinny_forward(x.to(torch.bfloat16), ids, w, _stack(packed_gate_up), _stack(scale_gate_up),
+                                   _stack(packed_down), _stack(scale_down))
     return y.to(x.dtype)

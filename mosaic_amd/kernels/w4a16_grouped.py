@@ -4,8 +4,15 @@ from __future__ import annotations
 import torch
 
 from .. import ops
+from ._launches import LaunchCounter
 
 BLOCK_M = 16
+_LAUNCHES = LaunchCounter()
+
+
+def last_launch_count() -> int:
+    """Kernel launches of this module's operators so far (``kernels/w4a16_grouped.py:15-16``)."""
+    return _LAUNCHES.n
 
 
 def emit_tiles(counts: torch.Tensor, block_m: int = BLOCK_M, max_tiles: int | None = None):
@@ -13,5 +20,6 @@ def emit_tiles(counts: torch.Tensor, block_m: int = BLOCK_M, max_tiles: int | No
     No per-expert cap: the reference stops at MAX_TILES=32 per expert (``:55-60``)."""
     e = counts.numel()
     t_cap = int(max_tiles) if max_tiles is not None else max(e, 1)
-    ei, ms, nt, rows = ops.emit_tiles(counts, block_m, t_cap)
+    with _LAUNCHES.track():
+        ei, ms, nt, rows = ops.emit_tiles(counts, block_m, t_cap)
     return ei, ms, nt, rows

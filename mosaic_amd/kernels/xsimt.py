@@ -5,6 +5,14 @@ import torch
 
 from .. import ops
 from . import _a8
+from ._launches import LaunchCounter
+
+_LAUNCHES = LaunchCounter()
+
+
+def last_launch_count() -> int:
+    """Kernel launches of this module's operators so far (``kernels/xsimt.py:31-32``)."""
+    return _LAUNCHES.n
 
 
 def prepack_xsimt(packed: torch.Tensor, scale: torch.Tensor) -> ops.MXT16:
@@ -22,4 +30,5 @@ def xsimt_gemm(x: torch.Tensor, packed: torch.Tensor, scale_w: torch.Tensor, n_o
     """x [M, K] bf16, packed [N, K/2], scale [N, K/32] -> [M, N] bf16, A8 (``kernels/xsimt.py:292-325``)."""
     if backend not in ("native", "triton"):
         raise ValueError(f"backend {backend}")
-    return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)
+    with _LAUNCHES.track():
+        return _a8.linear(x, packed, scale_w, n_out, prequant, prepacked)

@@ -7,8 +7,8 @@
   (weights fp32 [M, k], ids int64 [M, k]).
 * ``Gate`` -- ``.mosaicvm/source/inference_model.py:550-589``: the upstream gate
   (softmax | sigmoid | sqrtsoftplus, optional bias, renormalized unless
-  softmax, times ``route_scale``; hash layers look their ids up in
-  ``tid2eid``); returns (weights, indices).
+  softmax, times ``route_scale``); returns (weights, indices).  Hash layers
+  (ids looked up from ``tid2eid``) raise: hash routing is not on this path.
 * ``grouped_expert_forward`` -- ``model/layers.py:329-373``: the A16 routed
   expert sum (fp32 SwiGLU with the clamps, route weight before down, bf16 z,
   ascending-expert fp32 combine) over MXFP4 experts.
@@ -80,26 +80,14 @@ class Gate(torch.nn.Module):
             self.bias = torch.nn.Parameter(torch.empty(args.n_routed_experts, dtype=torch.float32, device=device))
 
     def forward(self, x: torch.Tensor, input_ids: torch.Tensor | None = None):
+        if self.hash:
+            # hash routing (ids looked up from tid2eid by token id) is not on the quantized matrix path
+            raise NotImplementedError("hash-routed Gate layers (layer_id < n_hash_layers) are not part of this build")
         logits = ops.router_logits(x.reshape(-1, x.shape[-1]), self.weight.detach())
-        if not self.hash:
-            ids, w = ops.moe_route_topk(logits, self.topk, self.score_func, renorm=self.score_func != "softmax",
-                                        route_scale=float(self.route_scale),
-                                        bias=None if self.bias is None else self.bias.detach())
-            return w, ids.to(torch.int64)
-        # hash layers: fixed ids per token id, weights from the true scores
-        # (each the fp64 function value rounded once to fp32)
-        ids = self.tid2eid.detach()[input_ids].to(torch.int64)
-        lg = logits.double()
-        if self.score_func == "softmax":
-            sc = lg.softmax(dim=-1).float()
-        elif self.score_func == "sigmoid":
-            sc = lg.sigmoid().float()
-        else:
-            sc = torch.nn.functional.softplus(lg).sqrt().float()
-        w = sc.gather(1, ids)
-        if self.score_func != "softmax":
-            w = w / w.sum(dim=-1, keepdim=True)
-        return w * float(self.route_scale), ids
+        ids, w = ops.moe_route_topk(logits, self.topk, self.score_func, renorm=self.score_func != "softmax",
+                                    route_scale=float(self.route_scale),
+                                    bias=None if self.bias is None else self.bias.detach())
+        return w, ids.to(torch.int64)
 
 
 def _as_mxt16_bank(w, what: str) -> ops.MXT16:
@@ -127,8 +115,11 @@ def grouped_expert_forward(x: torch.Tensor, scores: torch.Tensor, idx: torch.Ten
     k = idx.shape[-1]
     if isinstance(gate_up, (tuple, list)) and len(gate_up) == 2 and isinstance(gate_up[0], (tuple, list)):
         (pg, sg), (pu, su) = gate_up
-        gu = _prepack_cache.mxt16(torch.cat([ops._u8(pg, "packed_gate"), ops._u8(pu, "packed_up")], dim=1),
-                                  torch.cat([ops._u8(sg, "scale_gate"), ops._u8(su, "scale_up")], dim=1))
+        # keyed on the caller's four tensors, not on the concatenation (a new tensor every call)
+        gu = _prepack_cache.cached(
+            (pg, sg, pu, su),
+            lambda: ops.mxt16_prepack(torch.cat([ops._u8(pg, "packed_gate"), ops._u8(pu, "packed_up")], dim=1),
+                                      torch.cat([ops._u8(sg, "scale_gate"), ops._u8(su, "scale_up")], dim=1)))
     else:
         gu = _as_mxt16_bank(gate_up, "gate_up")
     dn = _as_mxt16_bank(down, "down")

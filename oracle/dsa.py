@@ -44,7 +44,12 @@ Pinned by ``tests/test_oracle_dsa.py``: the exact dot against an integer
 (int64) restatement; the scores against an independent float64 formula; the
 top-k against a brute-force full sort with ties; closed forms for the
 attention (one valid token and no sink gives that token's row; equal scores
-give the mean; the sink term checked against its definition).
+give the mean; the sink term checked against its definition);
+``head_topk_attention`` against a torch float64 restatement of
+``reference_topk_attention`` (``mosaicvm/kernels/dsa_attention.py:155-167``)
+at the reference test's shape and on a heavily tied case, with the scale
+dropped, softmax over the whole context and ties sent to the higher position
+planted in the restatement and caught.
 """
 from __future__ import annotations
 

@@ -133,6 +133,12 @@ def test_emit_tiles_kat(dev, block_m):
            for t in range((c + block_m - 1) // block_m)]
     assert nt == len(exp)
     assert list(zip(ei[:nt].tolist(), ms[:nt].tolist(), rows[:nt].tolist())) == exp
+    # a cap below the total: n_tiles is still the true total (tile_offsets[-1:] in the
+    # reference), and the entries that fit are the first ones of the full list
+    cap = len(exp) - 2
+    ei, ms, nt, rows = emit_tiles(counts, block_m=block_m, max_tiles=cap)
+    assert int(nt.item()) == len(exp) and ei.numel() == cap
+    assert list(zip(ei.tolist(), ms.tolist(), rows.tolist())) == exp[:cap]
 
 
 @pytest.mark.parametrize("m", [1, 3, 8])

@@ -75,3 +75,32 @@ def test_fused_moe_skinny_vs_oracle(dev, m, k, none_w):
         torch.float8_e8m0fnu), T(dp), T(ds))
     ref = MO.moe_layer_skinny(x, ids, w, gp, gs, dp, ds)
     assert_close(y.float().cpu().numpy(), ref, what=f"fused_moe_skinny m={m} k={k}")
+
+
+def test_last_launch_count_counts_library_launches(dev):
+    """skinny_fp4.last_launch_count (kernels/skinny_fp4.py:17-22): fused_moe_skinny
+    resets it and counts its own launches (layout, gate/up, SwiGLU, down,
+    combine, plus split-K sums); each skinny_mxfp4_gemm adds its GEMM (and its
+    split-K sum).  Every figure equals the library's own launch counter."""
+    from mosaic_amd import _lib
+    from mosaic_amd.kernels import skinny_fp4 as S
+    rng = np.random.default_rng(4)
+    e, h, inter, m, k = 4, 256, 128, 2, 2
+    gp, gs = (np.stack(a) for a in zip(*[_kn(rng, h, 2 * inter) for _ in range(e)]))
+    dp, ds = (np.stack(a) for a in zip(*[_kn(rng, inter, h) for _ in range(e)]))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    x = T(C.round_bf16(rng.standard_normal((m, h)).astype(np.float32))).to(torch.bfloat16)
+    ids = T(np.array([[0, 2], [3, 1]]))
+    lib = _lib.lib()
+    before = lib.mosaic_launch_count()
+    S.fused_moe_skinny(x, ids, None, T(gp), T(gs), T(dp), T(ds))
+    n_moe = S.last_launch_count()
+    assert n_moe == lib.mosaic_launch_count() - before and n_moe >= 5
+    for kk, nn in ((64, 64), (7168, 2048)):
+        p, s = _kn(rng, kk, nn)
+        xl = T(C.round_bf16(rng.standard_normal((1, kk)).astype(np.float32))).to(torch.bfloat16)
+        c0, l0 = S.last_launch_count(), lib.mosaic_launch_count()
+        S.skinny_mxfp4_gemm(xl, T(p), T(s), nn)
+        assert S.last_launch_count() - c0 == lib.mosaic_launch_count() - l0 in (1, 2)
+    S.fused_moe_skinny(x, ids, None, T(gp), T(gs), T(dp), T(ds))
+    assert S.last_launch_count() == n_moe

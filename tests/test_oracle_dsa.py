@@ -195,3 +195,76 @@ def test_decode_indices_static_and_given():
     out2 = D.decode_indices([3, 40], 8, cidx=cidx, nc=3)
     np.testing.assert_array_equal(out2[:, 8:], cidx)
     np.testing.assert_array_equal(out2[:, :8], out[:, :8])
+
+
+# ---- dsa_decode_attention: per-head top-k softmax attention ----------------
+def _t_topk_attention(q, k, v, topk, scale, mistake=None):
+    """``reference_topk_attention`` (mosaicvm/kernels/dsa_attention.py:155-167)
+    restated in torch float64: scores = einsum(q, k) * scale over [ctx, H], the
+    top-k per head (here a stable sort by (-score, position): torch.topk leaves
+    ties open, the build sends them to the lower position), softmax over the
+    picked scores, probabilities times the gathered v rows, summed."""
+    import torch
+    qt, kt, vt = (torch.from_numpy(np.asarray(a, dtype=np.float64)) for a in (q, k, v))
+    scores = torch.einsum("hd,chd->ch", qt, kt)
+    if mistake != "no_scale":
+        scores = scores * scale
+    st = scores.T.contiguous()                                   # [H, ctx]
+    if mistake == "ties_to_higher":
+        rev = torch.sort(-st.flip(-1), dim=-1, stable=True).indices
+        order = (st.shape[1] - 1 - rev)[:, :topk]
+    else:
+        order = torch.sort(-st, dim=-1, stable=True).indices[:, :topk]
+    top = st.gather(1, order)
+    gathered = vt.permute(1, 0, 2).gather(1, order.unsqueeze(-1).expand(-1, -1, vt.shape[-1]))
+    if mistake == "softmax_whole_context":
+        probs = torch.softmax(st, dim=-1).gather(1, order)
+    else:
+        probs = torch.softmax(top, dim=-1)
+    out = (probs.unsqueeze(-1) * gathered).sum(dim=1)
+    return out.numpy(), order.numpy()
+
+
+def _topk_attention_case(tied: bool):
+    """tests/test_dsa_parity.py's shape (64 heads, d 128, ctx 4096, top-256) with
+    bf16 N(0,1) values; the tied case draws q, k from {-1, 0, 1} at d 8 so that
+    many scores are equal across the top-k boundary."""
+    rng = np.random.default_rng(21 if tied else 20)
+    if tied:
+        h, d, ctx, topk = 8, 8, 600, 64
+        q = rng.integers(-1, 2, size=(h, d)).astype(np.float32)
+        k = rng.integers(-1, 2, size=(ctx, h, d)).astype(np.float32)
+    else:
+        h, d, ctx, topk = 64, 128, 4096, 256
+        q = C.round_bf16(rng.standard_normal((h, d)).astype(np.float32))
+        k = C.round_bf16(rng.standard_normal((ctx, h, d)).astype(np.float32))
+    v = C.round_bf16(rng.standard_normal((ctx, h, 128)).astype(np.float32))
+    return q, k, v, topk, 1.0 / np.sqrt(d)
+
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_head_topk_attention_equals_torch_restatement(tied):
+    """The oracle's indices equal the restatement's, and its outputs agree
+    within 1e-6 (the oracle rounds each score once to fp32)."""
+    q, k, v, topk, scale = _topk_attention_case(tied)
+    out, idx = D.head_topk_attention(q, k, v, topk, scale)
+    ref_out, ref_idx = _t_topk_attention(q, k, v, topk, scale)
+    if tied:
+        s = np.einsum("hd,chd->hc", q, k)
+        kth = np.sort(s, axis=1)[:, ::-1][:, topk - 1]
+        assert all((s[i] == kth[i]).sum() > 1 for i in range(len(kth))), "the case must tie at the boundary"
+    np.testing.assert_array_equal(idx, ref_idx)
+    np.testing.assert_allclose(out, ref_out, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("mistake", ["no_scale", "softmax_whole_context", "ties_to_higher"])
+def test_head_topk_attention_planted_mistakes_are_caught(mistake):
+    """Each planted mistake moves the restatement off the oracle: the scale
+    dropped (outputs), softmax over the whole context (outputs), ties sent to
+    the higher position (indices and outputs on the tied case)."""
+    q, k, v, topk, scale = _topk_attention_case(tied=(mistake == "ties_to_higher"))
+    out, idx = D.head_topk_attention(q, k, v, topk, scale)
+    bad_out, bad_idx = _t_topk_attention(q, k, v, topk, scale, mistake=mistake)
+    assert not np.allclose(bad_out, out, rtol=1e-3, atol=1e-3), f"{mistake} not detected in the outputs"
+    if mistake == "ties_to_higher":
+        assert not np.array_equal(bad_idx, idx), "tie order not detected in the indices"
