@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true",
                     help="time the K steps eagerly instead of replaying a HIP graph (for counter-collecting "
                          "profiler passes; the headline line is graph-timed)")
+    ap.add_argument("--launch-table", default="",
+                    help="write the per-launch table behind roofline (the event-timed durations of the M-token "
+                         "gate/up and down dispatches and each launch's algorithmic bytes) to this Markdown file")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the line is printed, copy a buffer of this many MiB device to device three times "
                          "(a plain copy of known size that scales FETCH_SIZE / WRITE_SIZE counter passes)")
@@ -178,6 +181,7 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int, graph: 
     distinct = [len(set(ids.flatten().tolist())) for ids in ids_all]
     layer_bytes = [(u + 1) * EXPERT_BYTES + 2 * m * H * 2 + m * E * 4 for u in distinct]
     gu_bytes = [(u + 1) * GU_BYTES + m * H * 2 + (u + 1) * I * 2 for u in distinct]
+    dn_bytes = [(u + 1) * DN_BYTES + (u + 1) * I * 2 + m * H * 2 for u in distinct]
     gu_s = sum(t["gu_sec"] for t in times)
     return {
         "m": m,
@@ -191,6 +195,8 @@ def run_m(torch, ops, banks, m: int, steps: int, warmup: int, seed: int, graph: 
         "gateup_us": 1e6 * gu_s / steps,
         "gateup_gbs": sum(gu_bytes) / gu_s / 1e9,
         "gateup_bytes_per_launch": sum(gu_bytes) / steps,
+        "per_launch": [{"gu_us": 1e6 * t["gu_sec"], "down_us": 1e6 * t["down_sec"], "gu_bytes": gb, "down_bytes": db,
+                        "distinct": u} for t, gb, db, u in zip(times, gu_bytes, dn_bytes, distinct)],
     }
 
 
@@ -570,7 +576,146 @@ def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7):
             c3[f"m{m}_n{n}_k{k}"] = {"us": round(us, 1), "TFLOPs": round(2 * m * n * k / us / 1e6, 3)}
         del wq, wf
     out["config3_fp8_gemm_torch_fp32"] = c3
+
+    # (5) config 4: the A8 prefill layer's experts on the reference's own CPU kernel (a sample)
+    if lib is not None:
+        out["config4_moe_prefill_reference"] = _cpu_config4(expert, lib, cores)
+    # (6) config 5: indexer + top-2048 and MLA decode, torch-CPU fp32
+    out["config5_dsa_torch_fp32"] = _cpu_config5(torch)
     return out
+
+
+def _cpu_config4(expert, lib, cores: int, m: int = 4096, seed: int = 13) -> dict:
+    """A bounded sample of BASELINE configs[3] on the reference's ``vnni_source_gemm``:
+    config-4 routing (Zipf(1.1) popularity over a seeded permutation, 8 experts
+    pinned to zero, Gumbel-top-8 of 4096 tokens), then the A8 layer
+    (``fused_moe_mxint``: token act_quant, gate/up, SwiGLU limit 10 x route weight,
+    bf16, z act_quant, down, bf16) for four experts across the popularity range:
+    the most loaded one and those at ranks 16, 64 and 128.  Weights are tiled
+    outside the timed region.  Reported as TFLOP/s over the sample and the
+    whole layer's time projected at that rate."""
+    import numpy as np
+
+    from oracle import codecs as C
+    from oracle import moe as MO
+    from oracle import ref_c
+
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(E)
+    logp = np.empty(E)
+    logp[perm] = -1.1 * np.log(np.arange(1, E + 1))
+    logp[perm[-8:]] = -1e4
+    u = rng.uniform(1e-9, 1 - 1e-9, size=(m, E))
+    logits = (logp[None, :] - np.log(-np.log(u))).astype(np.float32)
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :K]
+    sc = MO.score_fn(np.take_along_axis(logits, ids, 1), "sigmoid")
+    w = (sc / sc.sum(1, keepdims=True)).astype(np.float32)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    by_load = np.argsort(-counts, kind="stable")
+    picks = [int(by_load[r]) for r in (0, 16, 64, 128)]
+    x = C.round_bf16(rng.standard_normal((m, H)).astype(np.float32))
+    tiles = {e: (ref_c.prepare_weights(*expert(e)[:2]), ref_c.prepare_weights(*expert(e)[2:])) for e in picks}
+    t, flops, rows_all = 0.0, 0, 0
+    for e in picks:
+        tok, slot = np.nonzero(ids == e)
+        t0 = time.perf_counter()
+        codes, sa = C.act_quant(x[tok], 128, "pow2")
+        g = C.round_bf16(ref_c.gemm(codes, sa, tiles[e][0], lib))
+        z = C.round_bf16((MO.swiglu(g[:, :I], g[:, I:], 10.0) * w[tok, slot][:, None]).astype(np.float32))
+        zc, zs = C.act_quant(z, 128, "pow2")
+        C.round_bf16(ref_c.gemm(zc, zs, tiles[e][1], lib))
+        t += time.perf_counter() - t0
+        flops += 2 * len(tok) * 3 * H * I
+        rows_all += len(tok)
+    rate = flops / t / 1e12
+    layer_flops = 2 * m * (K + 1) * 3 * H * I
+    return {"TFLOPs": round(rate, 4), "projected_layer_ms": round(layer_flops / (rate * 1e12) * 1e3, 1),
+            "cores": cores, "kind": "reference",
+            "sample": f"experts {picks} (loads {[int(counts[e]) for e in picks]}, {rows_all} token rows, "
+                      f"{flops / 1e9:.0f} GFLOP of the layer's {layer_flops / 1e9:.0f}) through vnni_source_gemm, "
+                      f"{t:.2f} s"}
+
+
+def _cpu_config5(torch) -> dict:
+    """BASELINE configs[4] on the CPU in torch fp32, one repetition each: the
+    lightning indexer (e4m3 q and k decoded, per-head dots scaled by q_s and
+    k_s, ReLU, x head weight, summed over 64 heads) + top-2048 at (B, L) =
+    (1, 32768) and (8, 131072), and MLA decode over 2048 picks of an FP8
+    latent cache (128 heads, 512 latent e4m3 with per-64 scales + 64 bf16
+    rope, sink in the denominator) at B = 1 and 8."""
+    g = torch.Generator().manual_seed(14)
+    q8 = lambda *sh: (torch.randn(*sh, generator=g) * 60).clamp(-448, 448).to(torch.float8_e4m3fn)
+    out = {}
+    for b, l in [(1, 32768), (8, 131072)]:
+        k, ks = q8(b, l, 128), torch.rand(b, l, generator=g) * 0.01 + 1e-3
+        q, qs = q8(b, 64, 128), torch.rand(b, 64, generator=g) * 0.01 + 1e-3
+        w = torch.randn(b, 64, generator=g) * 0.01
+        t0 = time.perf_counter()
+        dots = torch.bmm(k.float(), q.float().transpose(1, 2).contiguous())          # [b, l, 64]
+        score = (torch.relu(dots * qs[:, None, :] * ks[:, :, None]) * w[:, None, :]).sum(-1)
+        score.topk(2048, dim=-1)
+        us = (time.perf_counter() - t0) * 1e6
+        byts = b * l * 132 + b * 64 * 136
+        out[f"indexer_b{b}_l{l}"] = {"us": round(us, 1), "GBs": round(byts / us / 1e3, 3)}
+        del k, dots, score
+    for b in (1, 8):
+        n, t_ = 65536, 2048
+        qh = torch.randn(b, 128, 576, generator=g).to(torch.bfloat16)
+        lat, lsc = q8(b, n, 512), torch.rand(b, n, 8, generator=g) * 0.01
+        rope = torch.randn(b, n, 64, generator=g).to(torch.bfloat16)
+        idx = torch.stack([torch.randperm(n, generator=g)[:t_] for _ in range(b)])
+        sink = torch.randn(128, generator=g)
+        t0 = time.perf_counter()
+        gi = idx[:, :, None]
+        latd = (torch.gather(lat.float(), 1, gi.expand(-1, -1, 512)).view(b, t_, 8, 64) *
+                torch.gather(lsc, 1, gi.expand(-1, -1, 8))[..., None]).view(b, t_, 512).to(torch.bfloat16).float()
+        kv = torch.cat([latd, torch.gather(rope, 1, gi.expand(-1, -1, 64)).float()], -1)   # [b, t, 576]
+        s_ = torch.bmm(qh.float(), kv.transpose(1, 2).contiguous()) * 576 ** -0.5      # [b, 128, t]
+        mx = s_.amax(-1, keepdim=True)
+        p_ = torch.exp(s_ - mx)
+        den = p_.sum(-1, keepdim=True) + torch.exp(sink[None, :, None] - mx)
+        torch.bmm(p_.to(torch.bfloat16).float(), latd) / den
+        us = (time.perf_counter() - t0) * 1e6
+        out[f"mla_b{b}"] = {"us": round(us, 1), "TFLOPs": round(2 * b * 128 * t_ * (576 + 512) / us / 1e6, 4)}
+    return out
+
+
+def write_launch_table(path: str, argv: list, r: dict, line: dict) -> None:
+    """The per-launch table behind ``roofline``: every event-timed gate/up (and
+    down) dispatch of the instrumented pass, its algorithmic bytes and rate."""
+    import statistics
+    rows = r["per_launch"]
+    gu = [p["gu_us"] for p in rows]
+    out = [f"# Event-timed launches behind bench.py's roofline: MoE decode, M = {r['m']}", "",
+           "Command (from the repository root on one MI355X):", "", "```",
+           "python3 " + " ".join(argv), "```", "",
+           "The gate/up dispatch of each instrumented step records HIP events itself "
+           "(`hipExtLaunchKernelGGL` start/stop on the kernel's stream), so its duration is the kernel's "
+           "execution.  The down dispatch records only its end, so the down column runs from the gate/up "
+           "kernel's end to the down kernel's end (the dependent-launch gap included).  Algorithmic bytes "
+           "per launch: (distinct experts + shared) x each expert's codes and scales, + x + z (gate/up) or "
+           "z + y (down).", "",
+           "| step | distinct experts | gate/up µs | gate/up bytes | gate/up GB/s | gap + down µs | down bytes | "
+           "down GB/s |", "|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for i, p in enumerate(rows):
+        out.append(f"| {i} | {p['distinct']} | {p['gu_us']:.2f} | {p['gu_bytes']:,} | "
+                   f"{p['gu_bytes'] / p['gu_us'] / 1e3:.0f} | {p['down_us']:.2f} | {p['down_bytes']:,} | "
+                   f"{p['down_bytes'] / p['down_us'] / 1e3:.0f} |")
+    gb = sum(p["gu_bytes"] for p in rows)
+    db = sum(p["down_bytes"] for p in rows)
+    dn = [p["down_us"] for p in rows]
+    out += ["", "| kernel | launches | avg µs | median µs | min µs | max µs | bytes / time | of 8 TB/s |",
+            "|---|---:|---:|---:|---:|---:|---:|---:|",
+            f"| gate/up | {len(gu)} | {statistics.mean(gu):.2f} | {statistics.median(gu):.2f} | {min(gu):.2f} | "
+            f"{max(gu):.2f} | {gb / sum(gu) / 1e3:.1f} GB/s | {gb / sum(gu) / 1e3 / HBM_PEAK_GBS:.4f} |",
+            f"| gap + down | {len(dn)} | {statistics.mean(dn):.2f} | {statistics.median(dn):.2f} | {min(dn):.2f} | "
+            f"{max(dn):.2f} | {db / sum(dn) / 1e3:.1f} GB/s | {db / sum(dn) / 1e3 / HBM_PEAK_GBS:.4f} |", "",
+            f"The line's `roofline` (the gate/up kernel): achieved {line['roofline']['achieved']} GB/s, frac "
+            f"{line['roofline']['frac']}, avg_launch_us {line['roofline']['avg_launch_us']}: the gate/up row "
+            f"above.  The headline layer time of the same run: {line['us_per_layer']} µs "
+            f"({line['config']['timing']}).", ""]
+    with open(path, "w") as f:
+        f.write("\n".join(out))
 
 
 def _gateup_kernel_name(m: int) -> str:
@@ -690,6 +835,8 @@ def main():
         "configs": configs,
     }
     print(json.dumps(line), flush=True)
+    if args.launch_table:
+        write_launch_table(args.launch_table, sys.argv, main_r, line)
     if args.calibration_copy_mib > 0:
         src = torch.ones(args.calibration_copy_mib << 18, dtype=torch.float32, device="cuda:0")
         dst = torch.empty_like(src)

@@ -476,3 +476,24 @@ def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     y = ops.mxt16_linear_a8(T(x).to(torch.bfloat16), ops.mxt16_prepack(T(p), T(s)))
     assert_close(y.float().cpu().numpy(), L.mx_linear_a8(x, p, s), what=f"a8 prefill {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [128, 4096])
+@pytest.mark.parametrize("n,k", [(7168, 16384), (18432, 7168), (24576, 1536), (1536, 7168), (576, 7168)])
+def test_mxt16_linear_a8_config3_shapes(dev, m, n, k):
+    """The timed dense A8 MXFP4 GEMMs (config-3 shapes with MXFP4 weights, as
+    bench.py times them: ceil-recipe weights N(0, 0.02), 1x128 pow2 e4m3
+    activations) at full size: every column of sampled rows against the A8
+    oracle of identical bytes."""
+    ops = _ops()
+    g = torch.Generator(device=dev)
+    g.manual_seed(n + k + m)
+    p, sc = ops.mx_quantize((torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16), "ceil")
+    x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+    xq, sa = ops.act_quant(x, 128, "pow2")
+    y = ops.mxt16_linear_a8(None, ops.mxt16_prepack(p, sc), prequant=(xq, sa))
+    rows = sorted({0, m // 2 - 1, m // 2, m - 1} | set(np.random.default_rng(k).choice(m, 4, replace=False).tolist()))
+    ref = L.mx_linear_a8(None, p.cpu().numpy(), sc.cpu().numpy(),
+                         quant=(xq[rows].view(torch.uint8).cpu().numpy(), sa[rows].cpu().numpy()))
+    assert_close(y[rows].float().cpu().numpy(), ref, what=f"a8 dense ({m}, {n}, {k})")
+    assert torch.isfinite(y.float()).all()

@@ -202,7 +202,13 @@ def _mla(rng, b, h, n, t, sb, masked=0.0):
                                                      (1, 16, 100, 64, 128, True, 0.0),
                                                      (2, 32, 80, 20, 64, True, 0.2),
                                                      (2, 48, 300, 100, 64, True, 0.1),
-                                                     (1, 128, 5000, 300, 64, False, 0.0)])
+                                                     (1, 128, 5000, 300, 64, False, 0.0),
+                                                     # the config-5 timed shape: B = 8, 128 heads, top-2048
+                                                     # (16 splits x 8 rows x 2 groups = 256 workgroups: 4 head tiles)
+                                                     (8, 128, 8192, 2048, 64, True, 0.0),
+                                                     # 48 heads, 16 rows, top-16384 (16 splits x 16 rows x 1 group
+                                                     # of 3 head tiles = 256 workgroups: 3 head tiles)
+                                                     (16, 48, 16400, 16384, 64, True, 0.05)])
 def test_mla_fp8_vs_oracle(dev, b, h, n, t, sb, sink, masked):
     from mosaic_amd import ops
     rng = np.random.default_rng(b * 1000 + t)
@@ -245,11 +251,13 @@ def test_mla_all_masked_row_is_zero(dev):
     _close(out[0], D.mla_sparse_decode(q, lat, ls, rope, np.zeros(16, np.float32), idx, 0.04)[0])
 
 
-@pytest.mark.parametrize("d", [512, 576])
-def test_mla_bf16_kv_vs_oracle(dev, d):
+@pytest.mark.parametrize("d,rows,h,n,t", [(512, 4, 64, 700, 256), (576, 4, 64, 700, 256),
+                                         # 4 rows x 128 heads x top-2048: 4 head tiles per workgroup
+                                         (576, 4, 128, 3000, 2048)])
+def test_mla_bf16_kv_vs_oracle(dev, d, rows, h, n, t):
     from mosaic_amd import ops
-    rng = np.random.default_rng(d)
-    rows, nb, h, n, t = 4, 2, 64, 700, 256
+    rng = np.random.default_rng(d + h + t)
+    nb = 2
     q = C.round_bf16(rng.standard_normal((rows, h, d)).astype(np.float32))
     kv = C.round_bf16(rng.standard_normal((nb, n, d)).astype(np.float32))
     idx = rng.integers(-1, n, size=(rows, t)).astype(np.int32)

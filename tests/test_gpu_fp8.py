@@ -81,3 +81,40 @@ def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     ref = L.fp8_w8a16_linear(x.float().numpy(), bq, bs)
     err = np.abs(y.float().cpu().numpy() - ref) / np.maximum(1.0, np.abs(ref))
     assert err.max() <= 2e-2, err.max()
+
+
+def _device_fp8_case(dev, m, n, k, seed):
+    """The config-3 recipe on the device (as bench.py generates it): W ~ N(0, 0.02)
+    quantized per 128 x 128 with s = amax / 448, x ~ N(0, 1) per 1 x 128 (amax)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    nb = (n + 127) // 128
+    w = torch.zeros(nb * 128, k, device=dev)
+    w[:n] = torch.randn(n, k, generator=g, device=dev) * 0.02
+    wb = w.view(nb, 128, k // 128, 128)
+    bs = (wb.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12)
+    bq = (wb / bs[:, None, :, None]).clamp(-448, 448).reshape(-1, k)[:n].to(torch.float8_e4m3fn)
+    x = torch.randn(m, k, generator=g, device=dev).view(m, k // 128, 128)
+    a_s = (x.abs().amax(dim=2) / 448.0).clamp_min(1e-12)
+    aq = (x / a_s[:, :, None]).clamp(-448, 448).reshape(m, k).to(torch.float8_e4m3fn)
+    return aq, a_s, bq, bs
+
+
+@pytest.mark.parametrize("n,k", [(7168, 16384), (18432, 7168), (24576, 1536), (1536, 7168), (576, 7168)])
+def test_fp8_block_gemm_config3_m4096(dev, n, k):
+    """The timed config-3 GEMMs at M = 4096, full size (the 256 x 256 big-tile
+    kernel for the first three: 448, 1152 and 1536 tiles over 56, 128 and 12
+    K-blocks; tiled<256> and its split-K for N = 1536 and 576): every column of
+    eight sampled rows (the first and last of 256-row tiles among them) against
+    the oracle of identical codes and scales."""
+    from mosaic_amd import ops
+    m = 4096
+    aq, a_s, bq, bs = _device_fp8_case(dev, m, n, k, seed=n + k)
+    c = ops.fp8_block_gemm(aq, a_s, bq, bs, out_dtype=torch.bfloat16)
+    rows = [0, 255, 256, 2047, 2048, 4095] + np.random.default_rng(n).choice(m, 2, replace=False).tolist()
+    ref = L.fp8_block_gemm(aq[rows].view(torch.uint8).cpu().numpy(), a_s[rows].cpu().numpy(),
+                           bq.view(torch.uint8).cpu().numpy(), bs.cpu().numpy(), out_bf16=True)
+    got = c[rows].float().cpu().numpy()
+    err = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
+    assert err.max() <= 2e-2, f"({m}, {n}, {k}): max scaled err {err.max()}"
+    assert torch.isfinite(c.float()).all()

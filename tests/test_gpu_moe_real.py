@@ -171,9 +171,9 @@ def test_moe_paths_reference_router_bit_exact(dev, m, a8):
     assert_close(y.float().cpu().numpy(), ref, what=f"moe m={m} a8={a8} reference router")
 
 
-@pytest.mark.parametrize("m", [4, 16])
+@pytest.mark.parametrize("m", [4, 16, 64])
 def test_moe_a16_baseline_geometry_multi_token(dev, m):
-    """M = 4 / 16 at hidden 7168, inter 2048, top-8, shared expert, on a
+    """M = 4 / 16 / 64 at hidden 7168, inter 2048, top-8, shared expert, on a
     32-expert bank: the layout + grouped gate/up + down + combine kernels at the
     shapes the bench times."""
     ops = _ops()
