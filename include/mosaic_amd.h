@@ -128,6 +128,16 @@ int mosaic_mxt16_linear_a16(const uint16_t* x, const uint8_t* packed_t, const ui
  * (.mosaicvm/source/inference_kernel.py:441-536). */
 int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* packed_t, const uint8_t* scale_t,
                            uint16_t* y, int64_t m, int64_t n, int64_t k, void* stream);
+/* Scratch bytes of mosaic_mxt16_linear_a8_ws: the fp32 partials of the split-K
+ * plan (shapes whose tiles cover at most half of the GPU), else 0. */
+size_t mosaic_mxt16_linear_a8_workspace_bytes(int64_t m, int64_t n, int64_t k);
+/* mosaic_mxt16_linear_a8 with a caller workspace for the split-K plan (without
+ * one, or with too few bytes, the shape runs unsplit).  Same replacement as
+ * above: the upstream fp4_gemm tiles every M and N (block_M 32, block_N 128,
+ * .mosaicvm/source/inference_kernel.py:441-515). */
+int mosaic_mxt16_linear_a8_ws(const uint8_t* xq, const float* sa, const uint8_t* packed_t, const uint8_t* scale_t,
+                              uint16_t* y, int64_t m, int64_t n, int64_t k, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------- FP8 block GEMM ----- */
 /* C [m, n] = sum over 128-K blocks of (A_kb . B_kb^T) * a_s[m, kb] * b_s[n/128, kb]

@@ -741,23 +741,13 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
     const uint8_t* __restrict__ d_s, const uint8_t* __restrict__ sh_p, const uint8_t* __restrict__ sh_s,
     const int32_t* __restrict__ tile_expert, const int32_t* __restrict__ tile_rows,
     const int32_t* __restrict__ tile_p0, const int32_t* __restrict__ n_tiles, uint16_t* __restrict__ yb, int H,
-    int I, int E, int m_dense) {
+    int I, int E) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
   __shared__ __attribute__((aligned(16))) uint8_t chunk[2 * kPfChunk];
   int colt, tile;
   pf_coords(blockIdx.x, H / 256, colt, tile);
-  int e, rows, p0;
-  if (tile_expert) {  // grouped: the MoE tile list
-    if (tile >= n_tiles[0]) return;
-    e = tile_expert[tile];
-    rows = tile_rows[tile];
-    p0 = tile_p0[tile];
-  } else {  // dense A8 GEMM: 256-row tiles of the m_dense rows, one weight matrix (E = 1)
-    p0 = tile * 256;
-    if (p0 >= m_dense) return;
-    rows = min(256, m_dense - p0);
-    e = 0;
-  }
+  if (tile >= n_tiles[0]) return;
+  const int e = tile_expert[tile], rows = tile_rows[tile], p0 = tile_p0[tile];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 15, q = lane >> 4;
   const int h0 = colt * 256;
   const int ns = I / 128, ns4 = (ns + 3) / 4;
@@ -811,6 +801,181 @@ __global__ void __launch_bounds__(kPfWaves * 64, 1) moe_a8_down_prefill_kernel(
       }
 }
 
+// ------------------------------------------------------- dense A8 GEMM -----
+// y [M, N] = A8 linear of (xq e4m3 [M, K] + pow2 scales sa [M, K/128]) with one
+// MXT16 weight, on the staged scaled-MFMA loops of the prefill kernels: tiles of
+// `tr` rows (64: the light-tile loop; 256: the full-tile loop, or the light one
+// when a tile holds at most 64 rows) x 256 columns, and K split into `splits`
+// slices of whole 512-K chunks.  Unsplit, a tile stores bf16 y; split, it stores
+// fp32 partials part[slice][M][N] that mx_gemm_a8_reduce_kernel sums in slice
+// order.  The columns of the last tile past N read the last weight group and
+// are not stored.
+struct DenseA8Plan {
+  int tr, n_row, n_col, splits, row_fastest;
+};
+
+// Workgroup id -> (row tile, column tile, K slice).  The dispatcher deals ids
+// round-robin to the 8 XCDs (id % 8), so each XCD takes one contiguous run of
+// the linear work order: with the row tile fastest, the row tiles of one
+// (column tile, slice) share the XCD's L2 copy of that weight slice; with the
+// column tile fastest, the column tiles share the activation slice.  Every XCD
+// gets work however few row tiles there are.
+__device__ __forceinline__ bool dense_coords(int id, int nwork, int per_xcd, const DenseA8Plan& p, int& rt, int& ct,
+                                             int& ks) {
+  const int lin = (id % 8) * per_xcd + id / 8;
+  if (lin >= nwork) return false;
+  if (p.row_fastest) {
+    rt = lin % p.n_row;
+    ct = (lin / p.n_row) % p.n_col;
+    ks = lin / (p.n_row * p.n_col);
+  } else {
+    ct = lin % p.n_col;
+    rt = (lin / p.n_col) % p.n_row;
+    ks = lin / (p.n_row * p.n_col);
+  }
+  return true;
+}
+
+__global__ void __launch_bounds__(kPfWaves * 64, 1) mx_gemm_a8_kernel(
+    const uint8_t* __restrict__ xq, const float* __restrict__ sa, const uint8_t* __restrict__ pt,
+    const uint8_t* __restrict__ st, uint16_t* __restrict__ y, float* __restrict__ part, int M, int N, int K,
+    DenseA8Plan plan, int per_xcd) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kPfStages][kPfStage];
+  __shared__ __attribute__((aligned(16))) uint8_t chunk[2 * kPfChunk];
+  int rt, ct, ks;
+  if (!dense_coords(blockIdx.x, plan.n_row * plan.n_col * plan.splits, per_xcd, plan, rt, ct, ks)) return;
+  const int p0 = rt * plan.tr, rows = min(plan.tr, M - p0);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 15, q = lane >> 4;
+  const int h0 = ct * 256;
+  const int ns = K / 128, nch = ns / 4;
+  // this slice's steps [s0, s0 + nsl): whole 4-step chunks, so the chunked
+  // scale copies of the loops stay aligned; the sources start at s0
+  const int s0 = 4 * (nch * ks / plan.splits), nsl = 4 * (nch * (ks + 1) / plan.splits) - s0;
+  const int ng = N / 16;
+  const int groups[2] = {min(h0 / 16 + 2 * wv, ng - 1), min(h0 / 16 + 2 * wv + 1, ng - 1)};
+  float* pslice = part ? part + (int64_t)ks * M * N : nullptr;
+  if (rows <= 64) {
+    // light tile: wave wv owns staged groups 2 wv and 2 wv + 1 (columns h0 + 32 wv)
+    const int arow = 8 * wv + (lane >> 3);
+    PfLSrc lsrc;
+    pfl_sources(lsrc, xq + (int64_t)(p0 + (arow < rows ? arow : 0)) * K, pt, st, groups, ns,
+                sa + (int64_t)(p0 + (lane < rows ? lane : 0)) * ns);
+    lsrc.a += 128 * s0;
+    lsrc.as += s0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      lsrc.b[i] += (int64_t)s0 * 1024;
+      lsrc.bs[i] += (int64_t)(s0 / 4) * 256;
+    }
+    f32x4_t lacc[4][2];
+    pfl_kloop(lsrc, nsl, rows, 2 * wv, 2 * wv + 1, lacc, &ring[0][0]);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const int col = h0 + 32 * wv + 16 * gi + c;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mt + 4 * q + r;
+          if (row < rows && col < N) {
+            const int64_t o = (int64_t)(p0 + row) * N + col;
+            if (pslice)
+              pslice[o] = lacc[mt][gi][r];
+            else
+              y[o] = f32_bf16_hw(lacc[mt][gi][r]);
+          }
+        }
+      }
+    return;
+  }
+  const uint8_t* rowp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 32 * wv + 8 * i + (lane >> 3);
+    rowp[i] = xq + (int64_t)(p0 + (row < rows ? row : 0)) * K;
+  }
+  const int srow = 64 * (wv & 3) + lane;
+  const float* as_row = sa + (int64_t)(p0 + (srow < rows ? srow : 0)) * ns;
+  PfSrc src;
+  pf_sources(src, rowp, pt, st, groups, ns, as_row);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) src.a[i] += 128 * s0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    src.b[i] += (int64_t)s0 * 1024;
+    src.bs[i] += (int64_t)(s0 / 4) * 256;
+  }
+  src.as += s0;
+  const int hc = wv & 1;
+  int wg[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) wg[n] = 8 * hc + n;
+  f32x4_t acc[4][8];
+  pf_kloop(src, nsl, rows, wg, acc, ring, chunk);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int col = h0 + 128 * hc + 16 * n + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 64 * (wv >> 1) + 16 * mt + 4 * q + r;
+        if (row < rows && col < N) {
+          const int64_t o = (int64_t)(p0 + row) * N + col;
+          if (pslice)
+            pslice[o] = acc[mt][n][r];
+          else
+            y[o] = f32_bf16_hw(acc[mt][n][r]);
+        }
+      }
+    }
+}
+
+// y = bf16 of the sum of the S fp32 partial slices, in slice order
+__global__ void __launch_bounds__(256) mx_gemm_a8_reduce_kernel(const float* __restrict__ part, int S, int64_t mn,
+                                                                uint16_t* __restrict__ y) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;  // mn % 4 == 0 (N % 16 == 0)
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + i);
+  for (int sl = 1; sl < S; ++sl) v += *reinterpret_cast<const f32x4_t*>(part + (int64_t)sl * mn + i);
+  uint2 o;
+  o.x = (uint32_t)f32_bf16(v[0]) | ((uint32_t)f32_bf16(v[1]) << 16);
+  o.y = (uint32_t)f32_bf16(v[2]) | ((uint32_t)f32_bf16(v[3]) << 16);
+  *reinterpret_cast<uint2*>(y + i) = o;
+}
+
+// The dense plan: the staged kernel holds one workgroup per CU (160 KB of LDS),
+// so a plan aims at one round of at most 256 workgroups.  Up to 256 rows the
+// tiles are 64 rows (the light loop streams the weight at the full per-CU rate
+// and the row tiles of a weight slice share it in L2); above, 256 rows (the
+// full loop does four times the MFMAs per staged weight byte).  K is split
+// while the tiles cover at most half of the CUs, at most 8 ways and into whole
+// 512-K chunks; the weight is then re-read by fewer workgroups than rows would
+// need.  Small-M plans keep the row tiles of one weight slice on one XCD (row
+// tile fastest), large-M plans the column tiles of one activation slice.
+static DenseA8Plan dense_a8_plan(int64_t m, int64_t n, int64_t k) {
+  DenseA8Plan p;
+  p.tr = m <= 256 ? 64 : 256;
+  p.n_row = (int)((m + p.tr - 1) / p.tr);
+  p.n_col = (int)((n + 255) / 256);
+  const int tiles = p.n_row * p.n_col, nch = (int)(k / 512);
+  p.splits = 1;
+  if (tiles * 2 <= 256) p.splits = std::max(1, std::min({8, nch, 256 / tiles}));
+  p.row_fastest = p.tr == 64 ? 1 : 0;
+  return p;
+}
+
+// the staged dense kernel runs when K is whole 512-K chunks and the rows are
+// not decode-sized (up to 32 rows the 16-row kernel streams the weight once per
+// 16 rows, which is at most twice)
+static bool dense_a8_staged(int64_t m, int64_t n, int64_t k) { return m > 32 && k % 512 == 0 && m < (1 << 30); }
+
+static size_t dense_a8_ws_bytes(int64_t m, int64_t n, int64_t k) {
+  if (!dense_a8_staged(m, n, k)) return 0;
+  const DenseA8Plan p = dense_a8_plan(m, n, k);
+  return p.splits > 1 ? (size_t)p.splits * (size_t)m * (size_t)n * 4 : 0;
+}
+
 // y[t][h] = bf16(sum over j of yb[combine_pos[t][j]][h]), bf16 partials; a
 // thread sums 8 consecutive columns (16-byte loads), in ascending j.  W <=
 // kCombineMaxW: every partial load is issued before the in-order sum.
@@ -848,9 +1013,9 @@ __global__ void __launch_bounds__(128) moe_combine_bf16_kernel(const uint16_t* _
 
 using namespace mosaic;
 
-extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* packed_t,
-                                      const uint8_t* scale_t, uint16_t* y, int64_t m, int64_t n, int64_t k,
-                                      void* stream) {
+static int mxt16_linear_a8_impl(const uint8_t* xq, const float* sa, const uint8_t* packed_t, const uint8_t* scale_t,
+                                uint16_t* y, int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   MOSAIC_CHECK_ARG(xq && sa && packed_t && scale_t && y, "mxt16_linear_a8: null pointer");
   MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "mxt16_linear_a8: K=%lld must be a positive multiple of 128",
                    (long long)k);
@@ -859,17 +1024,26 @@ extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const 
                    "mxt16_linear_a8: shape out of range");
   if (m == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
-  if (m > 256 && n % 256 == 0 && k % 512 == 0 && m < (1 << 30)) {
-    // prefill-sized: 256-row tiles through the staged scaled-MFMA kernel of the
-    // MoE down projection (one weight matrix, no tile list).  Up to 256 rows the
-    // 16-row kernel is faster: one 256 x 256 tile per CU leaves most of the
-    // GPU idle (128 x 1536 x 7168: 75.8 us staged, 25.8 us on the 16-row kernel;
-    // 512 x 7168 x 16384: 236 against 348 us)
-    const int64_t tiles8 = ((m + 255) / 256 + 7) / 8 * 8;
-    MOSAIC_LAUNCH(moe_a8_down_prefill_kernel, dim3((unsigned)(n / 256 * tiles8)), dim3(kPfWaves * 64), 0, st, xq,
-                       sa, packed_t, scale_t, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, y, (int)n, (int)k,
-                       1, (int)m);
-    MOSAIC_RETURN_LAUNCH("mxt16_linear_a8_prefill");
+  if (dense_a8_staged(m, n, k) && m * n < (1ll << 40)) {
+    DenseA8Plan plan = dense_a8_plan(m, n, k);
+    float* part = nullptr;
+    if (plan.splits > 1) {
+      if (workspace && workspace_bytes >= dense_a8_ws_bytes(m, n, k))
+        part = (float*)workspace;
+      else
+        plan.splits = 1;  // no workspace: the unsplit plan
+    }
+    const int nwork = plan.n_row * plan.n_col * plan.splits;
+    const int per_xcd = (nwork + 7) / 8;
+    MOSAIC_LAUNCH(mx_gemm_a8_kernel, dim3((unsigned)(8 * per_xcd)), dim3(kPfWaves * 64), 0, st, xq, sa, packed_t,
+                  scale_t, y, part, (int)m, (int)n, (int)k, plan, per_xcd);
+    MOSAIC_LAUNCH_CHECK("mxt16_linear_a8_staged");
+    if (part) {
+      const int64_t mn = m * n;
+      MOSAIC_LAUNCH(mx_gemm_a8_reduce_kernel, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, st, part,
+                    plan.splits, mn, y);
+    }
+    MOSAIC_RETURN_LAUNCH("mxt16_linear_a8_reduce");
   }
   const int64_t mt = (m + 15) / 16;
   if (((n + 63) / 64) * mt * 8 >= 4096)
@@ -879,6 +1053,23 @@ extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const 
   else
     launch_linear_a8<1, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
   MOSAIC_RETURN_LAUNCH("mxt16_linear_a8");
+}
+
+extern "C" int mosaic_mxt16_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* packed_t,
+                                      const uint8_t* scale_t, uint16_t* y, int64_t m, int64_t n, int64_t k,
+                                      void* stream) {
+  return mxt16_linear_a8_impl(xq, sa, packed_t, scale_t, y, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" size_t mosaic_mxt16_linear_a8_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 128 || n % 16) return 0;
+  return dense_a8_ws_bytes(m, n, k);
+}
+
+extern "C" int mosaic_mxt16_linear_a8_ws(const uint8_t* xq, const float* sa, const uint8_t* packed_t,
+                                         const uint8_t* scale_t, uint16_t* y, int64_t m, int64_t n, int64_t k,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  return mxt16_linear_a8_impl(xq, sa, packed_t, scale_t, y, m, n, k, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t mosaic_moe_a8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter, int64_t n_experts,
@@ -943,7 +1134,7 @@ extern "C" int mosaic_moe_a8_forward(const uint16_t* x, const float* logits, int
     mark(4);  // the z requant is fused into the gate/up epilogue
     MOSAIC_LAUNCH(moe_a8_down_prefill_kernel, dim3((unsigned)(hidden / 256 * tcap8)), dim3(kPfWaves * 64), 0, st,
                        w.zq, w.zs, d_packed, d_scale, sh_d_packed, sh_d_scale, w.tile_expert, w.tile_rows, w.tile_p0,
-                       w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts, 0);
+                       w.n_tiles, yb, (int)hidden, (int)inter, (int)n_experts);
     MOSAIC_LAUNCH_CHECK("moe_a8_down_prefill");
     mark(5);
     MOSAIC_LAUNCH(moe_combine_bf16_kernel, dim3((unsigned)((hidden / 8 + 127) / 128), (unsigned)m), dim3(128),

@@ -301,8 +301,11 @@ def mxt16_linear_a8(x: torch.Tensor | None, w: MXT16, prequant: tuple | None = N
         raise ValueError(f"activation shapes {tuple(xq.shape)}/{tuple(sa.shape)} do not match K={w.k}")
     m = xq.shape[0]
     y = torch.empty(m, w.n, dtype=torch.bfloat16, device=xq.device)
-    _lib.call("mosaic_mxt16_linear_a8", _ptr(xq), _ptr(sa), _ptr(w.packed), _ptr(w.scale), _ptr(y), m, w.n, w.k,
-              _stream())
+    # fp32 partials of the split-K plan (shapes whose tiles cover at most half of the GPU)
+    nbytes = _lib.lib().mosaic_mxt16_linear_a8_workspace_bytes(m, w.n, w.k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=xq.device) if nbytes else None
+    _lib.call("mosaic_mxt16_linear_a8_ws", _ptr(xq), _ptr(sa), _ptr(w.packed), _ptr(w.scale), _ptr(y), m, w.n, w.k,
+              _ptr(ws), nbytes, _stream())
     return y
 
 

@@ -463,12 +463,19 @@ def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
 
 
 @pytest.mark.parametrize("m,n,k", [(128, 256, 512), (257, 512, 1024), (1024, 512, 2048), (300, 7168, 512),
-                                   (64, 1536, 1536), (100, 320, 1024), (384, 512, 1536), (400, 256, 512)])
+                                   (64, 1536, 1536), (100, 320, 1024), (384, 512, 1536), (400, 256, 512),
+                                   # staged dense kernel: 64-row tiles (M <= 256), split K over whole 512-K
+                                   # chunks (uneven: 7 chunks in 4 slices), N tails (592 = 2 x 256 + 80,
+                                   # 576 = 2 x 256 + 64), the 33-row threshold, the 16-row kernel at 32 rows
+                                   (33, 256, 1024), (32, 512, 1024), (65, 592, 1536), (200, 576, 2048),
+                                   (128, 8192, 3584), (256, 1040, 4096), (520, 592, 3072), (4096, 576, 1024)])
 def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
     """Dense A8 MXFP4 GEMM at prefill sizes (fp4_gemm, .mosaicvm/source/inference_kernel.py:441-536):
-    256-row tiles through the staged scaled-MFMA kernel when M > 256, N % 256 == 0 and
-    K % 512 == 0 (the 128-, 64- and 100-row cases run the 16-row kernel); the last
-    tile is light (257, 300) or a partial full-path tile (384: 128 rows, 400: 144)."""
+    above 32 rows with K a multiple of 512 the staged scaled-MFMA kernel runs with
+    64-row tiles up to 256 rows and 256-row tiles above (the last tile light or a
+    partial full one), 256-column tiles with the N tail masked, and K split into
+    512-K chunk slices while the tiles cover at most half of the GPU; the other
+    shapes run the 16-row kernel."""
     ops = _ops()
     rng = np.random.default_rng(m + n + k + 7)
     p, s = _quant_weights(rng, n, k)
@@ -476,6 +483,33 @@ def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     y = ops.mxt16_linear_a8(T(x).to(torch.bfloat16), ops.mxt16_prepack(T(p), T(s)))
     assert_close(y.float().cpu().numpy(), L.mx_linear_a8(x, p, s), what=f"a8 prefill {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 1024, 4096), (4096, 576, 2048)])
+def test_mxt16_linear_a8_split_plan_matches_unsplit(dev, m, n, k):
+    """A split-K plan without its workspace runs unsplit (mosaic_mxt16_linear_a8);
+    both agree with the oracle, and the split reduce sums the slices in order
+    (two split calls are bit-identical)."""
+    import ctypes
+    from mosaic_amd import _lib
+    ops = _ops()
+    rng = np.random.default_rng(m + n + k)
+    p, s = _quant_weights(rng, n, k)
+    x = C.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    w = ops.mxt16_prepack(T(p), T(s))
+    assert _lib.lib().mosaic_mxt16_linear_a8_workspace_bytes(m, n, k) > 0, "the shape must take a split plan"
+    xq, sa = ops.act_quant(T(x).to(torch.bfloat16), 128, "pow2")
+    y1 = ops.mxt16_linear_a8(None, w, prequant=(xq, sa))
+    y2 = ops.mxt16_linear_a8(None, w, prequant=(xq, sa))
+    assert torch.equal(y1, y2)
+    y0 = torch.empty_like(y1)
+    _lib.call("mosaic_mxt16_linear_a8", ctypes.c_void_p(xq.data_ptr()), ctypes.c_void_p(sa.data_ptr()),
+              ctypes.c_void_p(w.packed.data_ptr()), ctypes.c_void_p(w.scale.data_ptr()),
+              ctypes.c_void_p(y0.data_ptr()), m, n, k, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    ref = L.mx_linear_a8(x, p, s)
+    assert_close(y1.float().cpu().numpy(), ref, what="split plan")
+    assert_close(y0.float().cpu().numpy(), ref, what="unsplit plan")
 
 
 @pytest.mark.parametrize("m", [128, 4096])
