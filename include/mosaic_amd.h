@@ -335,16 +335,18 @@ int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const uint8_t* k
                             int64_t topk, int32_t offset, void* workspace, size_t workspace_bytes, void* stream);
 
 /* mosaic_dsa_indexer_topk for `rows` query rows that share key caches in
- * groups: query row r scores k [r / rows_per_k] (k [rows / rows_per_k, l, d],
- * k_s [rows / rows_per_k, l]) with its own length lengths[r] -- the causal
- * prefill of Indexer.forward (.mosaicvm/source/inference_model.py:430-437;
- * mosaicvm/model/dsa_layers.py:309-321), where every position of a sequence
- * scores the same compressed cache up to its own bound.  The workspace is
- * mosaic_dsa_indexer_workspace_bytes(rows, l). */
+ * groups: query row r scores the first l tokens of key cache r / rows_per_k
+ * with its own length lengths[r] -- the causal prefill of Indexer.forward
+ * (.mosaicvm/source/inference_model.py:430-437; mosaicvm/model/dsa_layers.py:309-321),
+ * where every position of a sequence scores the same compressed cache up to
+ * its own bound.  The caches are read in place: cache g starts at
+ * k + g * cache_len * d (k_s + g * cache_len), so a [G, max_len, d] cache
+ * sliced to its first l tokens needs no copy (cache_len >= l).  The
+ * workspace is mosaic_dsa_indexer_workspace_bytes(rows, l). */
 int mosaic_dsa_indexer_topk_shared(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
                                    const float* w, const int32_t* lengths, int32_t* idx_out, int64_t rows, int64_t h,
-                                   int64_t d, int64_t l, int64_t rows_per_k, int64_t topk, int32_t offset,
-                                   void* workspace, size_t workspace_bytes, void* stream);
+                                   int64_t d, int64_t l, int64_t cache_len, int64_t rows_per_k, int64_t topk,
+                                   int32_t offset, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The canonical indexer scores themselves, scores [b, l] f32 (the index_score
  * tensor of Indexer.forward, .mosaicvm/source/inference_model.py:424-425). */
@@ -404,6 +406,19 @@ int mosaic_mla_sparse_decode_bf16(const uint16_t* q, const uint16_t* kv, const f
                                   uint16_t* out, int64_t rows, int64_t h, int64_t n, int64_t topk, int64_t d,
                                   int64_t rows_per_kv, float softmax_scale, void* workspace, size_t workspace_bytes,
                                   void* stream);
+
+/* Sparse attention over gathered bf16 KV rows with V = K at head dims 64, 128
+ * and 256: o [rows, h, d] bf16 from q [rows, h, d] bf16 (h a multiple of 16),
+ * kv [rows / rows_per_kv, n, d] bf16 and idx [rows, topk] int32 (-1 or
+ * out-of-range entries excluded); scores q . kv * softmax_scale in fp32,
+ * online softmax, bf16 probabilities in the value product over fp32 sums,
+ * sink (may be NULL) exp(sink[h] - max) in the denominator only; a row with no
+ * valid pick gives 0.  No workspace.
+ * Replaces sparse_attn_fused at d in {64, 128, 256} (mosaicvm/kernels/dsa_sparse.py:92-110,
+ * the Triton kernel :32-89); d = 512 runs mosaic_mla_sparse_decode_bf16. */
+int mosaic_sparse_attn_bf16(const uint16_t* q, const uint16_t* kv, const float* sink, const int32_t* idx,
+                            uint16_t* out, int64_t rows, int64_t h, int64_t n, int64_t topk, int64_t d,
+                            int64_t rows_per_kv, float softmax_scale, void* stream);
 
 /* RMSNorm with the 1x128 activation quantizer fused into its epilogue: the
  * input side of an A8 linear (linear(), .mosaicvm/source/inference_model.py:

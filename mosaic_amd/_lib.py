@@ -62,8 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_dsa_indexer_workspace_bytes": (c_size_t, [I64, I64]),
     "mosaic_dsa_indexer_topk": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, ctypes.c_int32, P, c_size_t,
                                         P]),
-    "mosaic_dsa_indexer_topk_shared": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, ctypes.c_int32,
-                                               P, c_size_t, P]),
+    "mosaic_dsa_indexer_topk_shared": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64,
+                                               ctypes.c_int32, P, c_size_t, P]),
+    "mosaic_sparse_attn_bf16": (c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, F, P]),
     "mosaic_dsa_indexer_scores": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, P]),
     "mosaic_dsa_indexer_bounds": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
     "mosaic_dsa_head_attention_workspace_bytes": (c_size_t, [I64, I64]),

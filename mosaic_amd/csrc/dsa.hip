@@ -156,7 +156,8 @@ template <int HT, int U, int D>
 __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ qs, const uint8_t* __restrict__ k,
     const float* __restrict__ ks, const float* __restrict__ w, const int32_t* __restrict__ lengths,
-    float* __restrict__ lo, float* __restrict__ hi, uint32_t* __restrict__ hist1, int64_t L, int kdiv) {
+    float* __restrict__ lo, float* __restrict__ hi, uint32_t* __restrict__ hist1, int64_t L, int kdiv,
+    int64_t kstride) {
   constexpr int H = HT * 16;
   constexpr int GT = 16 * U;  // tokens per group
   constexpr int kQv = H * kIdxD / 16;  // 16-byte pieces of the q row
@@ -182,8 +183,9 @@ __global__ void __launch_bounds__(256) dsa_index_bound_kernel(
   const int64_t n_groups = (n + GT - 1) / GT;
   const int64_t nw = (int64_t)gridDim.x * 4, wid = (int64_t)blockIdx.x * 4 + wv;
   const int64_t iters = wid < n_groups ? (n_groups - 1 - wid) / nw + 1 : 0;
-  const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;  // kdiv query rows share one key cache
-  const float* ksb = ks + (int64_t)(b / kdiv) * L;
+  // kdiv query rows share one key cache; caches start kstride tokens apart
+  const uint8_t* kb = k + (int64_t)(b / kdiv) * kstride * kIdxD;
+  const float* ksb = ks + (int64_t)(b / kdiv) * kstride;
   float* hib = hi + (int64_t)b * L;
   float* lob = lo ? lo + (int64_t)b * L : hib;  // without lo: a zero-length range, the stores drop
   i32x8_t kr[D][U];
@@ -398,7 +400,7 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
     const float* __restrict__ ks, const float* __restrict__ w, const int32_t* __restrict__ lengths,
     const float* __restrict__ hi, const uint32_t* __restrict__ hist1, const uint32_t* __restrict__ qlimbs,
     uint64_t* __restrict__ keys, uint32_t* __restrict__ wg_counts, float* __restrict__ scores, int64_t L, int topk,
-    int range, int kdiv) {
+    int range, int kdiv, int64_t kstride) {
   constexpr int H = HT * 16;
   constexpr int kCand = PF ? kRsPfRange : kRsMaxRange;
   constexpr int kPfVec = PF ? kRsPfRange * kIdxD / 16 : 1;  // 16-byte pieces of the staged k rows
@@ -422,8 +424,8 @@ __global__ void __launch_bounds__(256) dsa_rescore_kernel(
   if (t_begin >= n) return;
   const int nr = (int)min((int64_t)range, n - t_begin);  // tokens of this workgroup
   const bool select = hi != nullptr && n > topk;
-  const uint8_t* kb = k + (int64_t)(b / kdiv) * L * kIdxD;
-  const float* ksb = ks + (int64_t)(b / kdiv) * L;
+  const uint8_t* kb = k + (int64_t)(b / kdiv) * kstride * kIdxD;
+  const float* ksb = ks + (int64_t)(b / kdiv) * kstride;
   // in flight together: the row's histogram (thread tid holds digit vectors
   // v = tid + 256 i, digits 4 v .. 4 v + 3, coalesced), this range's upper
   // bounds, q, and the range's k rows and scales when they are staged
@@ -1466,23 +1468,23 @@ static void bound_shape(int64_t b, int64_t l, int& gx, int& depth) {
 template <int HT, int D>
 static void launch_bound_d(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t l,
-                           int gx, int kdiv, hipStream_t st) {
+                           int gx, int kdiv, int64_t kstride, hipStream_t st) {
   MOSAIC_LAUNCH((dsa_index_bound_kernel<HT, kBoundU, D>), dim3((unsigned)gx, (unsigned)b), dim3(256), 0, st, q,
-                     qs, k, ks, w, lengths, lo, hi, hist1, l, kdiv);
+                     qs, k, ks, w, lengths, lo, hi, hist1, l, kdiv, kstride);
 }
 
 template <int HT>
 static void launch_bound(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                          const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t l,
-                         int kdiv, hipStream_t st) {
+                         int kdiv, int64_t kstride, hipStream_t st) {
   int gx, depth;
   bound_shape(b, l, gx, depth);
   if (depth == 4)
-    launch_bound_d<HT, 4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, st);
+    launch_bound_d<HT, 4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, kstride, st);
   else if (depth == 2)
-    launch_bound_d<HT, 2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, st);
+    launch_bound_d<HT, 2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, kstride, st);
   else
-    launch_bound_d<HT, 1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, st);
+    launch_bound_d<HT, 1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, gx, kdiv, kstride, st);
 }
 
 static int check_indexer(const void* q, const void* qs, const void* k, const void* ks, const void* w, int64_t b,
@@ -1496,12 +1498,12 @@ static int check_indexer(const void* q, const void* qs, const void* k, const voi
 
 static void dispatch_bound(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, float* lo, float* hi, uint32_t* hist1, int64_t b, int64_t h,
-                           int64_t l, int kdiv, hipStream_t st) {
+                           int64_t l, int kdiv, int64_t kstride, hipStream_t st) {
   switch (h / 16) {
-    case 1: launch_bound<1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
-    case 2: launch_bound<2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
-    case 3: launch_bound<3>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
-    default: launch_bound<4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, st); break;
+    case 1: launch_bound<1>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, kstride, st); break;
+    case 2: launch_bound<2>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, kstride, st); break;
+    case 3: launch_bound<3>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, kstride, st); break;
+    default: launch_bound<4>(q, qs, k, ks, w, lengths, lo, hi, hist1, b, l, kdiv, kstride, st); break;
   }
 }
 
@@ -1519,19 +1521,19 @@ static int rescore_range(int64_t b, int64_t l) {
 static void launch_rescore(const uint8_t* q, const float* qs, const uint8_t* k, const float* ks, const float* w,
                            const int32_t* lengths, const float* hi, const uint32_t* hist1, const uint32_t* qlimbs,
                            uint64_t* keys, uint32_t* wg_counts, float* scores, int64_t b, int64_t h, int64_t l,
-                           int topk, int kdiv, hipStream_t st) {
+                           int topk, int kdiv, int64_t kstride, hipStream_t st) {
   const int range = rescore_range(b, l);
   const dim3 grid((unsigned)((l + range - 1) / range), (unsigned)b);
 #define MOSAIC_RESCORE(HT)                                                                                          \
   if (!qlimbs)                                                                                                      \
     MOSAIC_LAUNCH((dsa_rescore_kernel<HT, false, false>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,   \
-                       hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);                           \
+                       hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv, kstride);                           \
   else if (range <= kRsPfRange)                                                                                     \
     MOSAIC_LAUNCH((dsa_rescore_kernel<HT, true, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths, hi, \
-                       hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);                               \
+                       hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv, kstride);                             \
   else                                                                                                              \
     MOSAIC_LAUNCH((dsa_rescore_kernel<HT, false, true>), grid, dim3(256), 0, st, q, qs, k, ks, w, lengths,    \
-                       hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv);
+                       hi, hist1, qlimbs, keys, wg_counts, scores, l, topk, range, kdiv, kstride);
   switch (h / 16) {
     case 1: MOSAIC_RESCORE(1) break;
     case 2: MOSAIC_RESCORE(2) break;
@@ -1590,8 +1592,8 @@ extern "C" size_t mosaic_dsa_indexer_workspace_bytes(int64_t b, int64_t l) {
 namespace mosaic {
 static int indexer_topk_impl(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s, const float* w,
                              const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h, int64_t d, int64_t l,
-                             int64_t topk, int32_t offset, int64_t kdiv, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+                             int64_t topk, int32_t offset, int64_t kdiv, int64_t kstride, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   int rc = check_indexer(q, q_s, k, k_s, w, b, h, d, l);
   if (rc) return rc;
   MOSAIC_CHECK_ARG(idx_out, "dsa_indexer_topk: null output");
@@ -1600,6 +1602,8 @@ static int indexer_topk_impl(const uint8_t* q, const float* q_s, const uint8_t* 
                    (long long)kRsMaxWgs * kRsMaxRange);
   MOSAIC_CHECK_ARG(kdiv >= 1 && b % kdiv == 0, "dsa_indexer_topk: %lld query rows do not split into groups of %lld",
                    (long long)b, (long long)kdiv);
+  MOSAIC_CHECK_ARG(kstride >= l && kstride < (1ll << 40), "dsa_indexer_topk: cache length %lld < l %lld",
+                   (long long)kstride, (long long)l);
   const size_t need = indexer_ws(b, l, nullptr, nullptr);
   MOSAIC_CHECK_ARG(workspace && workspace_bytes >= need, "dsa_indexer_topk: workspace %zu bytes < %zu",
                    workspace_bytes, need);
@@ -1612,9 +1616,9 @@ static int indexer_topk_impl(const uint8_t* q, const float* q_s, const uint8_t* 
   MOSAIC_LAUNCH(dsa_prep_kernel, dim3((unsigned)((prep_n + 255) / 256)), dim3(256), 0, st, ws.hist1,
                      (int64_t)ws.zero_words, reinterpret_cast<const uint32_t*>(q), ws.qlimbs, qwords, (int)h);
   if (l > 0) {
-    dispatch_bound(q, q_s, k, k_s, w, lengths, nullptr, ws.hi, ws.hist1, b, h, l, (int)kdiv, st);
+    dispatch_bound(q, q_s, k, k_s, w, lengths, nullptr, ws.hi, ws.hist1, b, h, l, (int)kdiv, kstride, st);
     launch_rescore(q, q_s, k, k_s, w, lengths, ws.hi, ws.hist1, ws.qlimbs, ws.keys, ws.wg_counts, nullptr, b, h, l,
-                   (int)topk, (int)kdiv, st);
+                   (int)topk, (int)kdiv, kstride, st);
   }
   MOSAIC_LAUNCH(dsa_finish_kernel, dim3((unsigned)b), dim3(1024), 0, st, ws.keys, ws.wg_counts, lengths, l,
                      rescore_range(b, l), (int)topk, (int)offset, idx_out);
@@ -1626,16 +1630,17 @@ extern "C" int mosaic_dsa_indexer_topk(const uint8_t* q, const float* q_s, const
                                        const float* w, const int32_t* lengths, int32_t* idx_out, int64_t b, int64_t h,
                                        int64_t d, int64_t l, int64_t topk, int32_t offset, void* workspace,
                                        size_t workspace_bytes, void* stream) {
-  return indexer_topk_impl(q, q_s, k, k_s, w, lengths, idx_out, b, h, d, l, topk, offset, 1, workspace,
+  return indexer_topk_impl(q, q_s, k, k_s, w, lengths, idx_out, b, h, d, l, topk, offset, 1, l, workspace,
                            workspace_bytes, stream);
 }
 
 extern "C" int mosaic_dsa_indexer_topk_shared(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
                                               const float* w, const int32_t* lengths, int32_t* idx_out, int64_t rows,
-                                              int64_t h, int64_t d, int64_t l, int64_t rows_per_k, int64_t topk,
-                                              int32_t offset, void* workspace, size_t workspace_bytes, void* stream) {
-  return indexer_topk_impl(q, q_s, k, k_s, w, lengths, idx_out, rows, h, d, l, topk, offset, rows_per_k, workspace,
-                           workspace_bytes, stream);
+                                              int64_t h, int64_t d, int64_t l, int64_t cache_len, int64_t rows_per_k,
+                                              int64_t topk, int32_t offset, void* workspace, size_t workspace_bytes,
+                                              void* stream) {
+  return indexer_topk_impl(q, q_s, k, k_s, w, lengths, idx_out, rows, h, d, l, topk, offset, rows_per_k, cache_len,
+                           workspace, workspace_bytes, stream);
 }
 
 extern "C" int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, const uint8_t* k, const float* k_s,
@@ -1645,7 +1650,7 @@ extern "C" int mosaic_dsa_indexer_scores(const uint8_t* q, const float* q_s, con
   if (rc) return rc;
   MOSAIC_CHECK_ARG(scores, "dsa_indexer_scores: null output");
   if (b == 0 || l == 0) return kOk;
-  launch_rescore(q, q_s, k, k_s, w, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, scores, b, h, l, 0, 1,
+  launch_rescore(q, q_s, k, k_s, w, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, scores, b, h, l, 0, 1, l,
                  (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_scores");
 }
@@ -1657,7 +1662,7 @@ extern "C" int mosaic_dsa_indexer_bounds(const uint8_t* q, const float* q_s, con
   if (rc) return rc;
   MOSAIC_CHECK_ARG(lo && hi, "dsa_indexer_bounds: null output");
   if (b == 0 || l == 0) return kOk;
-  dispatch_bound(q, q_s, k, k_s, w, nullptr, lo, hi, nullptr, b, h, l, 1, (hipStream_t)stream);
+  dispatch_bound(q, q_s, k, k_s, w, nullptr, lo, hi, nullptr, b, h, l, 1, l, (hipStream_t)stream);
   MOSAIC_RETURN_LAUNCH("dsa_indexer_bounds");
 }
 

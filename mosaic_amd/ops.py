@@ -36,6 +36,16 @@ def _cuda(t: torch.Tensor, name: str) -> torch.Tensor:
     return t.contiguous()
 
 
+def _on_device(t: torch.Tensor, name: str) -> torch.Tensor:
+    """The checks of ``_cuda`` without the copy to a contiguous tensor (for
+    operands that are read through their strides)."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (mosaic_amd has no CPU path), got {t.device}")
+    return t
+
+
 def _u8(t: torch.Tensor, name: str) -> torch.Tensor:
     t = _cuda(t, name)
     if t.dtype in (torch.uint8, torch.int8, torch.float8_e8m0fnu, torch.float8_e4m3fn):
@@ -652,9 +662,24 @@ def dsa_indexer_topk_shared(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor,
                             w: torch.Tensor, topk: int, lengths: torch.Tensor, offset: int = 0,
                             workspace: MoEWorkspace | None = None) -> torch.Tensor:
     """Indexer top-k for R query rows q [R, H, D] sharing key caches k [G, L, D]
-    in groups of R / G consecutive rows, each row with its own length."""
-    q, k = _u8(q, "q"), _u8(k, "k")
-    q_s, k_s, w = _f32(q_s, "q_s"), _f32(k_s, "k_s"), _f32(w, "weights")
+    in groups of R / G consecutive rows, each row with its own length.  k and
+    k_s may be the first L tokens of longer caches ([G, max_len, D] sliced
+    along dim 1): they are read in place when both have unit inner strides and
+    the same cache length (k.stride(0) / D == k_s.stride(0))."""
+    q = _u8(q, "q")
+    k = _on_device(k, "k")
+    k = k.view(torch.uint8) if k.dtype in (torch.int8, torch.float8_e4m3fn) else k
+    if k.dtype != torch.uint8:
+        raise ValueError(f"k: expected e4m3 codes (uint8 / float8_e4m3fn), got {k.dtype}")
+    k_s = _on_device(k_s, "k_s")
+    if k_s.dtype != torch.float32:
+        raise ValueError(f"k_s: expected float32, got {k_s.dtype}")
+    q_s, w = _f32(q_s, "q_s"), _f32(w, "weights")
+    strided = (k.dim() == 3 and k_s.dim() == 2 and k.stride(2) == 1 and k.stride(1) == k.shape[2] and
+               k_s.stride(1) == 1 and k.stride(0) % k.shape[2] == 0 and k.stride(0) // k.shape[2] == k_s.stride(0)
+               and k_s.stride(0) >= k_s.shape[1])
+    if not strided:
+        k, k_s = k.contiguous(), k_s.contiguous()
     if q.dim() != 3 or k.dim() != 3 or q.shape[2] != k.shape[2]:
         raise ValueError(f"q must be [R, H, D] and k [G, L, D], got {tuple(q.shape)} and {tuple(k.shape)}")
     r, h, d = q.shape
@@ -669,8 +694,9 @@ def dsa_indexer_topk_shared(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor,
     idx = torch.empty(r, topk, dtype=torch.int32, device=q.device)
     nbytes = _lib.lib().mosaic_dsa_indexer_workspace_bytes(r, l_)
     ws = _workspace(workspace, nbytes, q.device)
+    cache_len = k_s.stride(0) if g > 1 else l_
     _lib.call("mosaic_dsa_indexer_topk_shared", _ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(w), _ptr(lengths),
-              _ptr(idx), r, h, d, l_, r // g, int(topk), int(offset), _ptr(ws), ws.numel(), _stream())
+              _ptr(idx), r, h, d, l_, cache_len, r // g, int(topk), int(offset), _ptr(ws), ws.numel(), _stream())
     return idx
 
 
@@ -771,6 +797,29 @@ def mla_sparse_decode_bf16(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor,
     ws = _workspace(workspace, nbytes, q.device)
     _lib.call("mosaic_mla_sparse_decode_bf16", _ptr(q), _ptr(kv), _ptr(sink), _ptr(idx), _ptr(out), rows, h, n, topk,
               d, rows // nb, float(softmax_scale), _ptr(ws), ws.numel(), _stream())
+    return out
+
+
+def sparse_attn_bf16(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, softmax_scale: float,
+                     sink: torch.Tensor | None = None) -> torch.Tensor:
+    """Sparse attention with V = K at head dims 64, 128 and 256: q [R, H, D] bf16
+    (H a multiple of 16), kv [B, N, D] bf16 with R a multiple of B (query row
+    r reads kv[r // (R // B)]), idx [R, T] int32 (-1 masked) -> o [R, H, D] bf16."""
+    q, kv = _bf16(q, "q"), _bf16(kv, "kv")
+    idx = _cuda(idx, "idx").to(torch.int32).contiguous()
+    if q.dim() != 3 or kv.dim() != 3 or idx.dim() != 2:
+        raise ValueError("q and kv must be 3-D, idx 2-D")
+    rows, h, d = q.shape
+    nb, n, dk = kv.shape
+    if dk != d or idx.shape[0] != rows or nb == 0 or rows % nb:
+        raise ValueError(f"shapes q {tuple(q.shape)}, kv {tuple(kv.shape)}, idx {tuple(idx.shape)} do not agree")
+    if sink is not None:
+        sink = _f32(sink, "sink")
+        if tuple(sink.shape) != (h,):
+            raise ValueError(f"sink must be [H], got {tuple(sink.shape)}")
+    out = torch.empty(rows, h, d, dtype=torch.bfloat16, device=q.device)
+    _lib.call("mosaic_sparse_attn_bf16", _ptr(q), _ptr(kv), _ptr(sink), _ptr(idx), _ptr(out), rows, h, n,
+              idx.shape[1], d, rows // nb, float(softmax_scale), _stream())
     return out
 
 

@@ -285,8 +285,46 @@ def test_upstream_sparse_attn_signature(dev):
     o2 = sparse_attn_fused(T(q[0]).to(torch.bfloat16), T(kv[0]).to(torch.bfloat16), T(sink), T(idx[0]), d ** -0.5)
     _close(o2.float().cpu().numpy(), D.sparse_attn(q[0], kv[:1], sink, idx[0], d ** -0.5, 512, m))
     with pytest.raises(ValueError, match="512"):
-        sparse_attn_fused(T(q[0, :, :, :256]).to(torch.bfloat16).contiguous(),
-                          T(kv[0, :, :256]).to(torch.bfloat16).contiguous(), T(sink), T(idx[0]), 0.1)
+        sparse_attn_fused(T(q[0, :, :, :320]).to(torch.bfloat16).contiguous(),
+                          T(kv[0, :, :320]).to(torch.bfloat16).contiguous(), T(sink), T(idx[0]), 0.1)
+
+
+@pytest.mark.parametrize("s,h,n,t,d,masked", [(3, 16, 300, 128, 64, 0.1), (2, 32, 1000, 512, 128, 0.0),
+                                              (4, 64, 700, 640, 256, 0.3), (1, 16, 64, 5, 128, 0.0),
+                                              (2, 48, 2000, 2048, 256, 0.05), (5, 20, 90, 33, 64, 0.5)])
+def test_sparse_attn_fused_small_head_dims(dev, s, h, n, t, d, masked):
+    """sparse_attn_fused at the reference's other head dims (mosaicvm/kernels/dsa_sparse.py:92-110:
+    d in {64, 128, 256}; V = K): masked picks, a ragged last block, fewer picks
+    than one 32-token block, heads padded to 16 (20 -> 32), every row's sink,
+    against the oracle's sparse_attn (bf16 probabilities in the value product)."""
+    from mosaic_amd.kernels.dsa import sparse_attn_fused
+    rng = np.random.default_rng(s * 100 + d + t)
+    q = C.round_bf16(rng.standard_normal((s, h, d)).astype(np.float32))
+    kv = C.round_bf16(rng.standard_normal((n, d)).astype(np.float32))
+    idx = np.stack([rng.choice(n, t, replace=t > n) for _ in range(s)]).astype(np.int32)
+    idx[rng.random(idx.shape) < masked] = -1
+    sink = rng.standard_normal(h).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    o = sparse_attn_fused(T(q).to(torch.bfloat16), T(kv).to(torch.bfloat16), T(sink), T(idx), d ** -0.5)
+    assert o.shape == (s, h, d) and o.dtype == torch.bfloat16
+    _close(o.float().cpu().numpy(), D.sparse_attn(q, kv[None], sink, idx, d ** -0.5, d, s))
+
+
+def test_sparse_attn_small_all_masked_and_no_sink(dev):
+    """A row with no valid pick gives 0; without a sink the denominator is the
+    picks' sum alone (the oracle with sink None)."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(7)
+    s, h, n, t, d = 3, 16, 200, 96, 128
+    q = C.round_bf16(rng.standard_normal((s, h, d)).astype(np.float32))
+    kv = C.round_bf16(rng.standard_normal((1, n, d)).astype(np.float32))
+    idx = rng.integers(0, n, size=(s, t)).astype(np.int32)
+    idx[1] = -1
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    o = ops.sparse_attn_bf16(T(q).to(torch.bfloat16), T(kv).to(torch.bfloat16), T(idx), 0.09).float().cpu().numpy()
+    assert (o[1] == 0).all()
+    ref = D.sparse_attn(q, kv, None, idx, 0.09, d, s)
+    _close(o[[0, 2]], ref[[0, 2]])
 
 
 def _indexer_drop_in_case(rng, bsz, seqlen, h, n_cache):
@@ -297,8 +335,9 @@ def _indexer_drop_in_case(rng, bsz, seqlen, h, n_cache):
 
 
 def test_indexer_drop_in_decode(dev):
-    """Indexer.forward at decode (start_pos > 0, seqlen 1): min(index_topk, end_pos // 4)
-    picks over the compressed cache, + offset (.mosaicvm/source/inference_model.py:430-439)."""
+    """Indexer scoring at decode (start_pos > 0, seqlen 1): min(index_topk, end_pos // 4)
+    picks over the compressed cache, + offset (.mosaicvm/source/inference_model.py:430-439);
+    the cache is longer than end_pos // 4 and is read in place (a strided slice)."""
     from mosaic_amd.kernels.dsa import Indexer
     rng = np.random.default_rng(31)
     bsz, h, start = 2, 64, 4000
@@ -306,14 +345,14 @@ def test_indexer_drop_in_decode(dev):
     q, qs, k, ks, w = _indexer_drop_in_case(rng, bsz, 1, h, n_c + 50)
     ix = Indexer(index_topk=512)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    got = ix(T(q).view(torch.float8_e4m3fn).reshape(bsz, 1, h, 128), T(qs).reshape(bsz, 1, h),
-             T(w).reshape(bsz, 1, h), T(k).view(torch.float8_e4m3fn), T(ks), start, 128).cpu().numpy()
+    got = ix.score_topk(T(q).view(torch.float8_e4m3fn).reshape(bsz, 1, h, 128), T(qs).reshape(bsz, 1, h),
+                        T(w).reshape(bsz, 1, h), T(k).view(torch.float8_e4m3fn), T(ks), start, 128).cpu().numpy()
     ref = D.indexer_topk(q, qs, k[:, :n_c], ks[:, :n_c], w, 512, None, 128)
     np.testing.assert_array_equal(got.reshape(bsz, 512), ref)
 
 
 def test_indexer_drop_in_prefill_causal(dev):
-    """Indexer.forward at start_pos 0: position i sees the first (i + 1) // 4
+    """Indexer scoring at start_pos 0: position i sees the first (i + 1) // 4
     compressed entries, masked picks are -1, valid ones + offset (the query
     rows of one sequence share its cache)."""
     from mosaic_amd.kernels.dsa import Indexer
@@ -323,8 +362,8 @@ def test_indexer_drop_in_prefill_causal(dev):
     q, qs, k, ks, w = _indexer_drop_in_case(rng, bsz, seqlen, h, n_c)
     ix = Indexer(index_topk=2048)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-    got = ix(T(q).view(torch.float8_e4m3fn).reshape(bsz, seqlen, h, 128), T(qs).reshape(bsz, seqlen, h),
-             T(w).reshape(bsz, seqlen, h), T(k).view(torch.float8_e4m3fn), T(ks), 0, 7).cpu().numpy()
+    got = ix.score_topk(T(q).view(torch.float8_e4m3fn).reshape(bsz, seqlen, h, 128), T(qs).reshape(bsz, seqlen, h),
+                        T(w).reshape(bsz, seqlen, h), T(k).view(torch.float8_e4m3fn), T(ks), 0, 7).cpu().numpy()
     assert got.shape == (bsz, seqlen, n_c)
     kk = np.repeat(k, seqlen, axis=0)
     kss = np.repeat(ks, seqlen, axis=0)
@@ -440,3 +479,79 @@ def test_decode_step_against_oracle(dev, fp8):
     idx = D.decode_indices([p], win, cidx=picks[None], nc=t)
     ref = D.sparse_attn(q, ref_cache[None], sink, idx, scale, dv=512)
     _close(o.float().cpu().numpy(), ref)
+
+
+class _Compressor(torch.nn.Module):
+    """A stand-in for the model's compressor (not on this build's path): every
+    completed group of `ratio` positions writes one bf16 row, a fixed
+    projection of the group's last token (rows depend on x and on the position)."""
+
+    def __init__(self, dim, hd, n_rows, ratio, dev, seed):
+        super().__init__()
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.wc = (torch.randn(dim, hd, generator=g, device=dev) * dim ** -0.5)
+        self.kv_cache = torch.zeros(n_rows, hd, dtype=torch.bfloat16, device=dev)
+        self.ratio = ratio
+        self.calls = []
+
+    def forward(self, x, start_pos):
+        self.calls.append((x.shape[0], start_pos))
+        for p in range(start_pos, start_pos + x.shape[0]):
+            if (p + 1) % self.ratio == 0:
+                self.kv_cache[p // self.ratio] = (x[p - start_pos].float() @ self.wc * 3.0).to(torch.bfloat16)
+
+
+def test_indexer_forward_reference_signature(dev):
+    """Indexer.forward(x, qr, freqs, offset, start_pos) (mosaicvm/model/dsa_layers.py:281-321):
+    a 40-token prefill, then four decode steps.  wq_b runs on the FP8 W8A16
+    linear and weights_proj on the router GEMV; the caller's rope, Hadamard and
+    compressor are applied in the reference's order; the FP8 key cache is
+    quantized incrementally.  Indices are bit-exact against the oracle's FP8
+    indexer fed the same projected q (the rope / Hadamard functions replayed on
+    the GPU's wq_b output), the oracle's act_quant of q and of the compressor's
+    rows, and the oracle's exact-rounded weights_proj."""
+    from mosaic_amd.kernels.dsa import Indexer
+    from mosaic_amd.kernels.fp8 import fp8_linear
+    from oracle import linear as L
+    from oracle import moe as MO
+    import scipy.linalg
+    rng = np.random.default_rng(41)
+    h, hd, dim, qlr, ratio, max_seq = 64, 128, 512, 256, 4, 256
+    wq = (rng.standard_normal((h * hd, qlr)) * 0.05).astype(np.float32)
+    wq_codes, wq_s = L.quantize_fp8_weight_128(wq)
+    wp = C.round_bf16((rng.standard_normal((h, dim)) * 0.05).astype(np.float32))
+    freqs = torch.from_numpy(rng.uniform(0.5, 1.5, size=(max_seq, 64)).astype(np.float32)).to(dev)
+    had = torch.from_numpy((scipy.linalg.hadamard(hd) / np.sqrt(hd)).astype(np.float32)).to(dev)
+    rotary = lambda qp, f: (qp.float() * f[:, None, :]).to(torch.bfloat16)
+    hadamard = lambda q: (q.float() @ had).to(torch.bfloat16)
+    comp = _Compressor(dim, hd, max_seq // ratio, ratio, dev, seed=5)
+    ix = Indexer(n_heads=h, head_dim=hd, index_topk=6, compress_ratio=ratio, max_seq_len=max_seq, rotary=rotary,
+                 hadamard=hadamard, compressor=comp, device=dev)
+    ix.wq_b = torch.from_numpy(wq_codes).to(dev).view(torch.float8_e4m3fn)
+    ix.wq_b_scale = torch.from_numpy(wq_s).to(dev)
+    ix.weights_proj = torch.from_numpy(wp).to(dev).to(torch.bfloat16)
+    pos = 0
+    for s in (40, 1, 1, 1, 1):
+        x = torch.from_numpy(rng.standard_normal((s, dim)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        qr = torch.from_numpy(rng.standard_normal((s, qlr)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        got = ix(x, qr, freqs, 1000, pos).cpu().numpy()
+        end = pos + s
+        n_c = end // ratio
+        assert comp.calls[-1] == (s, pos) and got.shape == (s, min(6, n_c))
+        # the oracle's view of the same call
+        q = fp8_linear(qr, ix.wq_b, ix.wq_b_scale).view(s, h, hd)
+        q = hadamard(torch.cat([q[..., :-64], rotary(q[..., -64:], freqs[pos:end])], -1))
+        qc, qs = C.act_quant(q.float().cpu().numpy().reshape(s * h, hd), hd, "amax")
+        kc, ks = C.act_quant(comp.kv_cache[:n_c].float().cpu().numpy(), hd, "amax")
+        np.testing.assert_array_equal(ix.k_fp8[:n_c].cpu().numpy(), kc)
+        w = (MO.router_logits(x.float().cpu().numpy(), wp) * np.float32(hd ** -0.5 * h ** -0.5)).astype(np.float32)
+        if pos == 0 or s > 1:
+            lengths = ((np.arange(1, s + 1) + pos) // ratio).astype(np.int32)
+        else:
+            lengths = np.full(s, n_c, dtype=np.int32)
+        ref = D.indexer_topk(qc.reshape(s, h, hd), qs.reshape(s, h), np.repeat(kc[None], s, 0),
+                             np.repeat(ks.reshape(1, n_c), s, 0), w, min(6, n_c), lengths, 1000)
+        np.testing.assert_array_equal(got, ref)
+        pos = end
+    assert (got >= 1000).all()
