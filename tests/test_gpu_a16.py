@@ -468,12 +468,15 @@ def test_moe_a8_small_vs_oracle(dev, m, e, h, inter, k, shared, limit):
                                    # chunks (uneven: 7 chunks in 4 slices), N tails (592 = 2 x 256 + 80,
                                    # 576 = 2 x 256 + 64), the 33-row threshold, the 16-row kernel at 32 rows
                                    (33, 256, 1024), (32, 512, 1024), (65, 592, 1536), (200, 576, 2048),
-                                   (128, 8192, 3584), (256, 1040, 4096), (520, 592, 3072), (4096, 576, 1024)])
+                                   (128, 8192, 3584), (256, 1040, 4096), (520, 592, 3072), (4096, 576, 1024),
+                                   # up to 256 rows on one 256-row tile per column, split 3 ways (the 64-row
+                                   # plan would leave most CUs idle), with a 16-column N tail
+                                   (120, 16400, 1536)])
 def test_mxt16_linear_a8_prefill_vs_oracle(dev, m, n, k):
     """Dense A8 MXFP4 GEMM at prefill sizes (fp4_gemm, .mosaicvm/source/inference_kernel.py:441-536):
     above 32 rows with K a multiple of 512 the staged scaled-MFMA kernel runs with
-    64-row tiles up to 256 rows and 256-row tiles above (the last tile light or a
-    partial full one), 256-column tiles with the N tail masked, and K split into
+    64-row tiles up to 256 rows (256-row tiles when 64-row ones would leave most
+    CUs idle) and 256-row tiles above (the last tile light or a partial full one), 256-column tiles with the N tail masked, and K split into
     512-K chunk slices while the tiles cover at most half of the GPU; the other
     shapes run the 16-row kernel."""
     ops = _ops()
