@@ -129,6 +129,20 @@ def test_indexer_topk_bit_exact_fewer_heads(dev, h, b, l, topk):
     np.testing.assert_array_equal(got, D.indexer_topk(q, qs, k, ks, w, topk))
 
 
+def test_indexer_topk_long_ragged_rows_bit_exact(dev):
+    """B = 8 rows of ~98K tokens (every bound-kernel wave walks 16 groups of
+    16 tokens, the deepest ring), a ragged last group, and rows of very
+    different lengths (98341 down to 3000); indices bit-exact against the oracle."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(98)
+    b, l, topk = 8, 98341, 2048
+    q, qs, k, ks, w = _indexer_inputs(rng, b, 64, l)
+    lengths = np.array([l, 98000, 97000, 65537, l, 50001, 98340, 3000], dtype=np.int32)
+    got = ops.dsa_indexer_topk(*_t(dev, q, qs, k, ks, w), topk, lengths=torch.from_numpy(lengths).to(dev),
+                               offset=5).cpu().numpy()
+    np.testing.assert_array_equal(got, D.indexer_topk(q, qs, k, ks, w, topk, lengths, 5))
+
+
 def test_indexer_lengths_offset_and_ties(dev):
     from mosaic_amd import ops
     rng = np.random.default_rng(11)
