@@ -450,14 +450,15 @@ def _cpu_info() -> dict:
             "smt": (siblings // cores) if cores else None, "visible_cpus": os.cpu_count()}
 
 
-def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7):
+def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7, min_seconds: float = 10.0):
     """The reference's CPU path on the host cores, beside the GPU numbers.
 
     ``value``: the reference's own integer-exact A8 CPU kernel (``vnni_source_gemm``,
     ``bench/vnni_source_kernel.c:8-47``, built from the reference's source into
     ``oracle/_ref``) running the A8 MoE layer of ``fused_moe_mxint`` on ``tokens``
     single-token decode steps (8 routed + the shared expert each; weights tiled
-    outside the timed region, as the reference's bench prepares them).  Also
+    outside the timed region, as the reference's bench prepares them), the steps
+    timed again until ``min_seconds`` of CPU work are measured.  Also
     timed: the A16 layer as torch-CPU fp32 dequant-then-matmul (weights
     dequantized outside the timed region), the config-1 linear both ways, and
     the config-3 FP8 shapes as torch-CPU fp32 dequant-then-matmul at every M.
@@ -499,21 +500,27 @@ def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7):
             zc, zs = C.act_quant(z, 128, "pow2")
             return C.round_bf16(ref_c.gemm(zc, zs, tiles[e][1], lib))
 
-        t_a8, nbytes = 0.0, 0
-        for x, ids, w in steps:
-            t0 = time.perf_counter()
-            codes, sa = C.act_quant(x, 128, "pow2")
-            acc = np.zeros((1, H), dtype=np.float32)
-            for s_ in np.argsort(ids[0], kind="stable"):
-                acc = (acc + a8_expert(codes, sa, int(ids[0, s_]), w[0, s_])).astype(np.float32)
-            acc = (acc + a8_expert(codes, sa, E, 1.0)).astype(np.float32)
-            C.round_bf16(acc)
-            t_a8 += time.perf_counter() - t0
-            nbytes += (len(set(ids.flatten().tolist())) + 1) * EXPERT_BYTES + 2 * H * 2
+        # the same layers are timed again until at least min_seconds of CPU work
+        # (their tiled weights, ~0.4 GB a layer, stream from DRAM every pass)
+        t_a8, nbytes, passes, layers = 0.0, 0, 0, 0
+        while passes == 0 or (t_a8 < min_seconds and passes < 400):
+            for x, ids, w in steps:
+                t0 = time.perf_counter()
+                codes, sa = C.act_quant(x, 128, "pow2")
+                acc = np.zeros((1, H), dtype=np.float32)
+                for s_ in np.argsort(ids[0], kind="stable"):
+                    acc = (acc + a8_expert(codes, sa, int(ids[0, s_]), w[0, s_])).astype(np.float32)
+                acc = (acc + a8_expert(codes, sa, E, 1.0)).astype(np.float32)
+                C.round_bf16(acc)
+                t_a8 += time.perf_counter() - t0
+                nbytes += (len(set(ids.flatten().tolist())) + 1) * EXPERT_BYTES + 2 * H * 2
+                layers += 1
+            passes += 1
         out.update({"value": round(nbytes / t_a8 / 1e9, 3), "unit": "GB/s", "kind": "reference",
-                    "us_per_layer": round(t_a8 / tokens * 1e6, 1),
+                    "us_per_layer": round(t_a8 / layers * 1e6, 1),
                     "sample": f"{tokens} single-token A8 decode layers (8 routed + 1 shared expert, hidden {H}, "
-                              f"inter {I}) through vnni_source_gemm ({cores} OpenMP threads), {t_a8:.2f} s"})
+                              f"inter {I}) through vnni_source_gemm ({cores} OpenMP threads), each timed {passes} "
+                              f"times: {layers} layers, {t_a8:.2f} s"})
     # (2) A16 layer, torch-CPU fp32 dequant-then-matmul
     deq = {e: tuple(torch.from_numpy(C.dequant_mxfp4(*expert(e)[2 * j:2 * j + 2])) for j in range(2))
            for e in used + [E]}
