@@ -64,7 +64,9 @@ int mosaic_mx_dequant(const uint8_t* packed, const uint8_t* scale, void* out, in
 /* 1 x block E4M3 activation quantizer: x [m, k] (f32/bf16) -> codes [m, k] + f32 scales [m, k/block].
  * mode 0: power-of-two scale, act_quant_ref (kernels/fp4_source.py:110-129);
  * mode 1: s = max(amax,1e-4)/448, upstream act_quant (.mosaicvm/source/inference_kernel.py:40-125);
- * mode 2: s = amax/448, fp8_act_quant (.mosaicvm/source/hubkernel_act_quant.py:27-35). */
+ * mode 2: s = amax/448, fp8_act_quant (.mosaicvm/source/hubkernel_act_quant.py:27-35);
+ * mode 3: s = amax/448 and 1 for an all-zero block, act_quant_legacy_phase27
+ *         (kernels/fp4_source.py:94-107). */
 int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s, int64_t m, int64_t k, int block, int mode,
                      void* stream);
 
@@ -431,6 +433,26 @@ int mosaic_sparse_attn_bf16(const uint16_t* q, const uint16_t* kv, const float* 
  * h <= 16384. */
 int mosaic_rmsnorm_act_quant(const uint16_t* x, const float* w, float eps, int64_t m, int64_t h, uint16_t* y,
                              uint8_t* q, float* s, int mode, void* stream);
+
+/* Standalone SwiGLU + route weight + 1x128 act_quant epilogue
+ * (mxint_swiglu_quant_down, kernels/mxint.py:1298-1345,1387-1408): gu [a, 2*inter]
+ * bf16 (gate | up), w_a [a] f32 route weights (NULL: 1) -> z = bf16(silu(min(gate, L))
+ * * clamp(up, -L, L) * w) in fp32 (no clamp when limit <= 0), quantized as
+ * mosaic_act_quant mode 0 -> q [a, inter] e4m3 codes, s [a, inter/128] f32.  The
+ * reference returns the codes as three int8 limb planes of 512 * value (its dp4a
+ * operand); the codes themselves are the scaled-MFMA operand here.  inter % 128 == 0,
+ * gu 16-byte and q 8-byte aligned. */
+int mosaic_swiglu_act_quant(const uint16_t* gu, const float* w_a, int64_t a, int64_t inter, float limit, uint8_t* q,
+                            float* s, void* stream);
+
+/* Deterministic routed combine (mxint_routed_reduce, kernels/mxint.py:1346-1365,
+ * 1411-1429): yd [a, h] bf16 expert partials in packed order; for each token t,
+ * out[t] = bf16(fp32 sum over j of yd[slot_rows[t, order[t, j]]]), accumulated in the
+ * order given (order[t] lists the slots by ascending expert id).  slot_rows and order
+ * are int32 [k_tok, top_k]; entries outside [0, a) / [0, top_k) add nothing.
+ * h % 8 == 0; yd and out 16-byte aligned; k_tok <= 65535. */
+int mosaic_routed_reduce(const uint16_t* yd, const int32_t* slot_rows, const int32_t* order, uint16_t* out,
+                         int64_t k_tok, int64_t top_k, int64_t h, int64_t a, void* stream);
 
 /* KV-cache writer of the DSA attention step (the kv rows of ExactAttention.forward
  * and attention_core, mosaicvm/model/dsa_layers.py:550-553 and 579-582, stored

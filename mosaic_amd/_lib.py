@@ -76,6 +76,8 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_dsa_kv_write": (c_int, [P, P, I64, I64, I64, I64, P, P, P, P, P]),
     "mosaic_dsa_decode_indices": (c_int, [P, I64, I64, P, I64, I64, I64, P, P]),
     "mosaic_rmsnorm_act_quant": (c_int, [P, P, F, I64, I64, P, P, P, c_int, P]),
+    "mosaic_swiglu_act_quant": (c_int, [P, P, I64, I64, F, P, P, P]),
+    "mosaic_routed_reduce": (c_int, [P, P, P, P, I64, I64, I64, I64, P]),
 }
 
 _LIB = None

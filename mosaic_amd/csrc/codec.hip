@@ -121,6 +121,7 @@ __global__ void __launch_bounds__(256) mx_dequant_bf16_kernel(const uint8_t* __r
 // mode 0: s = 2^ceil(log2(max(amax,1e-4) * fp32(1/448)))  (power of two)
 // mode 1: s = max(amax,1e-4) * fp32(1/448)
 // mode 2: s = amax / 448
+// mode 3: s = amax / 448, and 1 where that is zero
 template <typename T>
 __global__ void __launch_bounds__(256) act_quant_kernel(const T* __restrict__ x, uint8_t* __restrict__ q,
                                                         float* __restrict__ s_out, int64_t rows, int64_t K,
@@ -142,6 +143,7 @@ __global__ void __launch_bounds__(256) act_quant_kernel(const T* __restrict__ x,
     s = fmaxf(amax, 1e-4f) * 0.002232142925783992f;
   } else {
     s = amax / 448.0f;
+    if (mode == 3 && s == 0.f) s = 1.0f;
   }
   // a power-of-two scale (mode 0) has an exact reciprocal: x * (1 / s) == x / s
   const float inv = mode == 0 ? 1.0f / s : 0.f;
@@ -199,6 +201,7 @@ __global__ void __launch_bounds__(256) act_quant128_kernel(const T* __restrict__
     s = fmaxf(amax, 1e-4f) * 0.002232142925783992f;
   } else {
     s = amax / 448.0f;
+    if (mode == 3 && s == 0.f) s = 1.0f;
   }
   // a power-of-two scale (mode 0) has an exact reciprocal: v * (1 / s) == v / s
   const float inv = mode == 0 ? 1.0f / s : 0.f;
@@ -331,7 +334,7 @@ extern "C" int mosaic_act_quant(const void* x, int x_dtype, uint8_t* q, float* s
   MOSAIC_CHECK_ARG(x && q && s, "act_quant: null pointer");
   MOSAIC_CHECK_ARG(block > 0 && k % block == 0, "act_quant: K=%lld must be a multiple of block %d", (long long)k,
                    block);
-  MOSAIC_CHECK_ARG(mode >= 0 && mode <= 2, "act_quant: mode %d", mode);
+  MOSAIC_CHECK_ARG(mode >= 0 && mode <= 3, "act_quant: mode %d", mode);
   MOSAIC_CHECK_ARG(x_dtype == MOSAIC_DTYPE_F32 || x_dtype == MOSAIC_DTYPE_BF16, "act_quant: dtype %d", x_dtype);
   int64_t waves = m * (k / block);
   if (waves == 0) return kOk;

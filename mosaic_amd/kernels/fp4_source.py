@@ -53,6 +53,16 @@ def act_quant_ref(x: torch.Tensor, block: int = ACT_BLOCK) -> tuple[torch.Tensor
     return ops.act_quant(x, block, "pow2")
 
 
+def act_quant_legacy_phase27(x: torch.Tensor, block: int = ACT_BLOCK) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [M, K] -> (e4m3fn [M, K], fp32 scale [M, K/block]) with s = amax/448, 1 for an
+    all-zero block; kept for comparison with ``act_quant_ref`` (``kernels/fp4_source.py:94-107``)."""
+    if x.dim() != 2:
+        raise ValueError(f"act_quant_legacy_phase27 expects [M, K], got {tuple(x.shape)}")
+    if x.shape[1] % block != 0:
+        raise ValueError(f"K={x.shape[1]} must be a multiple of act block {block}")
+    return ops.act_quant(x, block, "legacy")
+
+
 def reference_fp4_linear_source_semantics(x_bf16: torch.Tensor, packed: torch.Tensor,
                                           scale_w: torch.Tensor) -> torch.Tensor:
     """A8 linear, x [M, K] -> [M, N] bf16 (``kernels/fp4_source.py:132-156``)."""

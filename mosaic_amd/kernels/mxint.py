@@ -105,3 +105,22 @@ def _fused_moe_a8(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, 
         stage_times["decode_int_sec"] = 0.0  # no integer limb split on gfx950
         stage_times["swiglu_sec"] = 0.0      # fused into the gate/up kernels
     return y
+
+
+def mxint_swiglu_quant_down(gu, w_a, inter: int, swiglu_limit: float):
+    """gu [A, 2*inter] bf16 + route weights [A] -> (e4m3fn codes [A, inter], f32 scales
+    [A, inter/128]): clamps, SiLU, route weight, bf16, 1x128 pow2 act_quant in one pass
+    (``kernels/mxint.py:1387-1408``).  The reference returns the codes as three int8 limb
+    planes for its dp4a GEMMs; the codes and scales here are the ``prequant=`` input of
+    this module's GEMMs."""
+    if gu.dim() != 2 or gu.shape[1] != 2 * inter or inter % 128 != 0 or swiglu_limit <= 0:
+        raise ValueError("mxint_swiglu_quant_down requires [A,2*inter], inter%128==0, limit>0")
+    with _LAUNCHES.track():
+        return ops.swiglu_act_quant(gu, w_a, inter, swiglu_limit)
+
+
+def mxint_routed_reduce(yd, slot_rows, order, h: int):
+    """Packed-order down partials bf16 [A, h] -> bf16 [k_tok, h], each token's top_k
+    partials summed in fp32 in ascending expert-id order (``kernels/mxint.py:1411-1429``)."""
+    with _LAUNCHES.track():
+        return ops.routed_reduce(yd, slot_rows, order, h)

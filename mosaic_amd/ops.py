@@ -16,7 +16,7 @@ from . import _lib
 
 DT_F32, DT_BF16 = 0, 1
 SCORE_FUNCS = {"sigmoid": 0, "softmax": 1, "sqrtsoftplus": 2}
-ACT_MODES = {"pow2": 0, "amax": 1, "hf": 2}
+ACT_MODES = {"pow2": 0, "amax": 1, "hf": 2, "legacy": 3}
 RECIPES = {"ceil": 0, "floor": 1}
 
 
@@ -136,6 +136,45 @@ def rmsnorm_act_quant(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6, 
               ACT_MODES[mode], _stream())
     out = (q.view(torch.float8_e4m3fn), s)
     return out + (y,) if return_y else out
+
+
+def swiglu_act_quant(gu: torch.Tensor, w_a: torch.Tensor | None, inter: int,
+                     swiglu_limit: float = 0.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """gu [A, 2*inter] bf16 (gate | up), route weights w_a [A] (None: 1) ->
+    (e4m3fn codes [A, inter], f32 pow2 scales [A, inter/128]) of
+    z = bf16(silu(min(gate, L)) * clamp(up, +-L) * w); no clamp when L <= 0."""
+    gu = _bf16(gu, "gu").contiguous()
+    a = gu.shape[0]
+    if gu.dim() != 2 or gu.shape[1] != 2 * inter or inter % 128:
+        raise ValueError(f"gu must be [A, 2*inter] with inter % 128 == 0, got {tuple(gu.shape)}, inter={inter}")
+    w = None
+    if w_a is not None:
+        w = _cuda(w_a, "w_a").reshape(-1).to(torch.float32).contiguous()
+        if w.numel() != a:
+            raise ValueError(f"w_a must hold {a} weights, got {w.numel()}")
+    q = torch.empty(a, inter, dtype=torch.uint8, device=gu.device)
+    s = torch.empty(a, inter // 128, dtype=torch.float32, device=gu.device)
+    _lib.call("mosaic_swiglu_act_quant", _ptr(gu), _ptr(w), a, inter, float(swiglu_limit), _ptr(q), _ptr(s),
+              _stream())
+    return q.view(torch.float8_e4m3fn), s
+
+
+def routed_reduce(yd: torch.Tensor, slot_rows: torch.Tensor, order: torch.Tensor, h: int) -> torch.Tensor:
+    """yd [A, h] bf16 partials, slot_rows / order [k_tok, top_k] -> bf16 [k_tok, h]:
+    out[t] = fp32 sum of yd[slot_rows[t, order[t, j]]] over j in that order."""
+    yd = _bf16(yd, "yd").contiguous()
+    if yd.dim() != 2 or yd.shape[1] != h:
+        raise ValueError(f"yd must be [A, {h}], got {tuple(yd.shape)}")
+    if slot_rows.dim() != 2 or tuple(order.shape) != tuple(slot_rows.shape):
+        raise ValueError(f"slot_rows and order must be [k_tok, top_k], got {tuple(slot_rows.shape)} "
+                         f"and {tuple(order.shape)}")
+    sr = _cuda(slot_rows, "slot_rows").to(torch.int32).contiguous()
+    od = _cuda(order, "order").to(torch.int32).contiguous()
+    k_tok, top_k = sr.shape
+    out = torch.empty(k_tok, h, dtype=torch.bfloat16, device=yd.device)
+    _lib.call("mosaic_routed_reduce", _ptr(yd), _ptr(sr), _ptr(od), _ptr(out), k_tok, top_k, h, yd.shape[0],
+              _stream())
+    return out
 
 
 def e4m3_decode(codes: torch.Tensor) -> torch.Tensor:

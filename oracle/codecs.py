@@ -245,6 +245,8 @@ def act_quant(x: np.ndarray, block: int = ACT_BLOCK, mode: str = "pow2"):
       (``.mosaicvm/source/inference_kernel.py:75-80``), s = max(amax,1e-4) * fp32(1/448).
     mode "hf": ``_fp8_act_quant_kernel`` (``.mosaicvm/source/hubkernel_act_quant.py:27-35``),
       s = amax / 448 with no floor.
+    mode "legacy": ``act_quant_legacy_phase27`` (``kernels/fp4_source.py:94-107``),
+      s = amax / 448, replaced by 1 where it is zero (``:104``).
     In every mode y = e4m3(clamp(x / s, +-448)) (the HF kernel has no clamp;
     x/s is within 448 by construction there).
     """
@@ -260,6 +262,9 @@ def act_quant(x: np.ndarray, block: int = ACT_BLOCK, mode: str = "pow2"):
         s = (np.maximum(amax, np.float32(1e-4)) * np.float32(1.0 / FP8_MAX)).astype(np.float32)
     elif mode == "hf":
         s = (amax / np.float32(FP8_MAX)).astype(np.float32)
+    elif mode == "legacy":
+        s = (amax / np.float32(FP8_MAX)).astype(np.float32)
+        s = np.where(s == 0, np.float32(1.0), s).astype(np.float32)
     else:
         raise ValueError(mode)
     with np.errstate(divide="ignore", invalid="ignore"):

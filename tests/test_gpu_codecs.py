@@ -77,7 +77,7 @@ def test_mx_quantize_bitexact(dev, recipe):
         np.testing.assert_array_equal(p.cpu().numpy(), p_ref)
 
 
-@pytest.mark.parametrize("mode", ["pow2", "amax", "hf"])
+@pytest.mark.parametrize("mode", ["pow2", "amax", "hf", "legacy"])
 def test_act_quant_bitexact(dev, mode):
     ops = _ops()
     rng = np.random.default_rng(5)

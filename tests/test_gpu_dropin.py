@@ -51,6 +51,27 @@ def test_act_quant_ref_matches_official_math(dev):
     np.testing.assert_array_equal(y.view(torch.uint8).cpu().numpy(), y0)
 
 
+def test_act_quant_legacy_phase27_differs_on_straddling_blocks(dev):
+    """tests/test_fp4_source.py:45-63: the legacy amax/448 scale differs from the pow2 one on
+    straddling blocks; both match the oracle bit for bit, an all-zero block included."""
+    from mosaic_amd.kernels.fp4_source import act_quant_legacy_phase27, act_quant_ref
+    vals = [0.0, 1e-5, -1e-5, 1e-4, 448.0, -448.0, 1.0, 2.0 ** -60]
+    vals += [2.0 ** e * 448.0 for e in (-10, -1, 0, 4)]
+    vals += [2.0 ** e * 448.0 * 1.0000001 for e in (-10, -1, 0, 4)]
+    x = torch.zeros(1, 128 * len(vals), dtype=torch.float32)
+    for i, v in enumerate(vals):
+        x[0, 128 * i + 7] = v
+    xb = x.to(torch.bfloat16)
+    y, s = act_quant_ref(xb.to(dev), 128)
+    yl, sl = act_quant_legacy_phase27(xb.to(dev), 128)
+    assert not torch.equal(sl, s)
+    q_ref, s_ref = C.act_quant(xb.float().numpy(), 128, "legacy")
+    np.testing.assert_array_equal(sl.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(yl.view(torch.uint8).cpu().numpy(), q_ref)
+    with pytest.raises(ValueError):
+        act_quant_legacy_phase27(xb.to(dev)[:, :100], 128)
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 128, 16), (2, 256, 32), (8, 128, 16), (3, 7168, 256)])
 def test_a8_gemvs_vs_source_linear(dev, m, k, n):
     """tests/test_fp4_source.py:76-88 / tests/test_mxint_gemm.py:32-55: every A8 GEMV vs the source oracle."""
@@ -222,3 +243,67 @@ def test_fp8_linear_w8a16_vs_dequant_matmul(dev):
     wd = C.round_bf16(C.e4m3_decode(bq) * np.repeat(np.repeat(bs, 128, 0), 128, 1)[:n, :k])
     _close(y, C.round_bf16((x.float().numpy().astype(np.float64) @ wd.T.astype(np.float64)).astype(np.float32)))
     np.testing.assert_array_equal(fp8.dequant_fp8(T(bq), T(bs)).float().cpu().numpy(), wd)
+
+
+def _swiglu_quant_oracle(gu: np.ndarray, w: np.ndarray | None, inter: int, limit: float):
+    """oracle z = bf16(swiglu * w) and its act_quant_ref, plus a mask of the values
+    whose fp32 z lies within 8 ulp of a bf16 rounding midpoint (there a 1-ulp
+    difference between two exp implementations may pick the other bf16 value)."""
+    z = MO.swiglu(gu[:, :inter], gu[:, inter:], limit)
+    if w is not None:
+        z = (z * w[:, None]).astype(np.float32)
+    low = z.view(np.uint32) & 0xFFFF
+    near = np.abs(low.astype(np.int64) - 0x8000) <= 8
+    q, s = C.act_quant(C.round_bf16(z), 128, "pow2")
+    return q, s, near
+
+
+@pytest.mark.parametrize("a,inter,scale,limit,weighted", [
+    (24, 256, 3.0, 10.0, True),    # tests/test_mxint_epilogue.py:87-104
+    (8, 128, 30.0, 10.0, True),    # clamp engaged, :107-117
+    (37, 2048, 2.0, 10.0, True),   # config geometry (inter 2048)
+    (5, 384, 4.0, 0.0, False),     # no clamp, no route weight (ops entry)
+])
+def test_mxint_swiglu_quant_down_vs_oracle(dev, a, inter, scale, limit, weighted):
+    from mosaic_amd import ops
+    from mosaic_amd.kernels.mxint import mxint_swiglu_quant_down
+    rng = np.random.default_rng(a * 7 + inter)
+    gu = torch.from_numpy((rng.standard_normal((a, 2 * inter)) * scale).astype(np.float32)).to(torch.bfloat16)
+    w = (rng.random(a) * 1.5).astype(np.float32) if weighted else None
+    q_ref, s_ref, near = _swiglu_quant_oracle(gu.float().numpy(), w, inter, limit)
+    if limit > 0:
+        q, s = mxint_swiglu_quant_down(gu.to(dev), torch.from_numpy(w).to(dev), inter, limit)
+    else:
+        q, s = ops.swiglu_act_quant(gu.to(dev), None, inter, 0.0)
+    assert q.dtype == torch.float8_e4m3fn and tuple(s.shape) == (a, inter // 128)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    got = q.view(torch.uint8).cpu().numpy()
+    np.testing.assert_array_equal(got[~near], q_ref[~near])
+    diff = np.abs(C.e4m3_decode(got[near]) - C.e4m3_decode(q_ref[near]))
+    assert (diff <= np.abs(C.e4m3_decode(q_ref[near])) * 2.0 ** -2 + 2.0 ** -9).all()
+    with pytest.raises(ValueError):
+        mxint_swiglu_quant_down(gu.to(dev), None, inter, 0.0)
+
+
+@pytest.mark.parametrize("k_tok,top_k,h,e", [(5, 6, 320, 16), (64, 8, 7168, 256), (1, 8, 7168, 256)])
+def test_mxint_routed_reduce_bitwise(dev, k_tok, top_k, h, e):
+    """tests/test_mxint_epilogue.py:120-148: packed-order partials summed per token in
+    ascending expert id, fp32, one bf16 rounding -- bit-exact against the oracle's
+    combine over the oracle's stable layout."""
+    from mosaic_amd.kernels.mxint import mxint_routed_reduce
+    rng = np.random.default_rng(k_tok + h)
+    ids = np.stack([rng.permutation(e)[:top_k] for _ in range(k_tok)])
+    a = k_tok * top_k
+    yd = torch.from_numpy((rng.standard_normal((a, h)) * 2.0).astype(np.float32)).to(torch.bfloat16)
+    _, perm, _, _ = MO.layout_assignments(ids.reshape(-1), e)
+    row_of_flat = np.empty(a, dtype=np.int64)
+    row_of_flat[perm] = np.arange(a)
+    slot_rows = row_of_flat.reshape(k_tok, top_k)
+    order = np.argsort(ids, axis=1, kind="stable")
+    ydf = yd.float().numpy()
+    partial = {(t, s): ydf[slot_rows[t, s]] for t in range(k_tok) for s in range(top_k)}
+    ref = C.round_bf16(MO._combine(k_tok, h, ids, partial, None))
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    got = mxint_routed_reduce(yd.to(dev), T(slot_rows), T(order), h)
+    assert got.dtype == torch.bfloat16 and tuple(got.shape) == (k_tok, h)
+    np.testing.assert_array_equal(got.float().cpu().numpy(), ref)

@@ -180,6 +180,39 @@ def test_act_quant_pow2_boundaries():
         assert s[0, i] == 2.0 ** math.ceil(math.log2(t))
 
 
+def test_act_quant_legacy_pins():
+    """act_quant_legacy_phase27 (kernels/fp4_source.py:94-107): differs from the pow2 scale on
+    the straddling blocks of tests/test_fp4_source.py:45-63; an all-zero block gets s = 1 and
+    zero codes; amax = 448 gives s = 1 and codes equal to the e4m3 encoding of x; scaling x by
+    2^j scales s by 2^j and keeps the codes; s = fl(amax / 448) lies within half an ulp."""
+    vals = [0.0, 1e-5, -1e-5, 1e-4, 448.0, -448.0, 1.0, 2.0 ** -60]
+    vals += [2.0 ** e * 448.0 for e in (-10, -1, 0, 4)]
+    vals += [2.0 ** e * 448.0 * 1.0000001 for e in (-10, -1, 0, 4)]
+    x = np.zeros((1, 128 * len(vals)), dtype=np.float32)
+    for i, v in enumerate(vals):
+        x[0, 128 * i + 7] = v
+    xb = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    _, sp = C.act_quant(xb, 128, "pow2")
+    ql, sl = C.act_quant(xb, 128, "legacy")
+    assert not np.array_equal(sl, sp)
+    assert sl[0, 0] == 1.0 and (ql[0, :128] == 0).all()
+    rng = np.random.default_rng(11)
+    y = C.round_bf16(rng.uniform(-448, 448, (3, 256)).astype(np.float32))
+    y[:, 0] = 448.0
+    y[:, 128] = -448.0
+    qy, sy = C.act_quant(y, 128, "legacy")
+    assert (sy == 1.0).all()
+    np.testing.assert_array_equal(qy, C.e4m3_encode(y))
+    z = C.round_bf16(rng.standard_normal((4, 512)).astype(np.float32))
+    qz, sz = C.act_quant(z, 128, "legacy")
+    for j in (-20, -3, 5):
+        q2, s2 = C.act_quant(z * np.float32(2.0 ** j), 128, "legacy")
+        np.testing.assert_array_equal(q2, qz)
+        np.testing.assert_array_equal(s2, sz * np.float32(2.0 ** j))
+    amax = np.abs(z.reshape(4, 4, 128)).max(-1).astype(np.float64)
+    assert (np.abs(sz.astype(np.float64) - amax / 448.0) <= np.spacing(sz) / 2).all()
+
+
 def test_act_quant_matches_torch_cast_path():
     """y = e4m3(clamp(x / s)) with torch's cast (kernels/fp4_source.py:126-128)."""
     rng = np.random.default_rng(3)
