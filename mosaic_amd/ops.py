@@ -261,6 +261,8 @@ def moe_skinny_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor
     if tuple(d_packed.shape) != (e, inter, h // 2) or tuple(d_scale.shape) != (e, inter, h // 32):
         raise ValueError(f"down bank {tuple(d_packed.shape)}/{tuple(d_scale.shape)} does not match [{e}, {inter}, {h}]")
     ids = _cuda(ids, "expert_ids")
+    if m == 0:  # an empty batch: nothing to launch
+        return torch.empty(0, h, dtype=torch.bfloat16, device=x.device)
     ids = ids.reshape(m, -1).to(torch.int32).contiguous()
     k = ids.shape[1]
     weights = _cuda(weights, "expert_weights").reshape(m, k).to(torch.float32).contiguous()
@@ -597,6 +599,14 @@ def _moe_forward(a8: bool, x: torch.Tensor, gate_up: MXT16, down: MXT16, *, logi
             raise ValueError(f"logits shape {tuple(logits.shape)} != ({m}, {e})")
         if top_k is None:
             raise ValueError("top_k is required with logits")
+    if m == 0:  # an empty batch: empty outputs, nothing to launch
+        if logits is None and (ids is None or weights is None):
+            raise ValueError("give logits or ids and weights")
+        k = top_k if logits is not None else (ids.shape[1] if ids.dim() == 2 else 0)
+        return (torch.empty(0, h, dtype=torch.bfloat16, device=x.device),
+                torch.empty(0, k, dtype=torch.int32, device=x.device),
+                torch.empty(0, k, dtype=torch.float32, device=x.device))
+    if logits is not None:
         ids = torch.empty(m, top_k, dtype=torch.int32, device=x.device)
         weights = torch.empty(m, top_k, dtype=torch.float32, device=x.device)
     else:

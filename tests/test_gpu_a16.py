@@ -377,6 +377,33 @@ def test_moe_given_ids_repeated_and_dropped_multi_token(dev, a8):
         assert_close(y[t:t + 1].float().cpu().numpy(), ref, what=f"moe repeated ids token {t}")
 
 
+def test_moe_empty_batch_returns_empty(dev):
+    """An empty batch (M = 0) gives empty outputs without a launch, on both contracts,
+    with routing on the device or with given ids, and on the KN (skinny) layout."""
+    ops = _ops()
+    rng = np.random.default_rng(3)
+    e, h, inter = 4, 256, 128
+    gp, gs, dp, ds = _make_bank(rng, e, h, inter)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    gu, dn = ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds))
+    x = torch.empty(0, h, dtype=torch.bfloat16, device=dev)
+    for fwd in (ops.moe_a16_forward, ops.moe_a8_forward):
+        y, ids, w = fwd(x, gu, dn, logits=torch.empty(0, e, device=dev), top_k=2)
+        assert tuple(y.shape) == (0, h) and tuple(ids.shape) == (0, 2) and tuple(w.shape) == (0, 2)
+        y, ids, w = fwd(x, gu, dn, ids=torch.empty(0, 2, dtype=torch.int32, device=dev),
+                        weights=torch.empty(0, 2, device=dev))
+        assert tuple(y.shape) == (0, h) and tuple(ids.shape) == (0, 2)
+        with pytest.raises(ValueError):
+            fwd(x, gu, dn)
+    kn_gu = torch.zeros(e, h, inter, dtype=torch.uint8, device=dev)
+    kn_gs = torch.full((e, h, 2 * inter // 32), 127, dtype=torch.uint8, device=dev)
+    kn_d = torch.zeros(e, inter, h // 2, dtype=torch.uint8, device=dev)
+    kn_ds = torch.full((e, inter, h // 32), 127, dtype=torch.uint8, device=dev)
+    y = ops.moe_skinny_forward(x, torch.empty(0, 2, dtype=torch.int32, device=dev), torch.empty(0, 2, device=dev),
+                               kn_gu, kn_gs, kn_d, kn_ds)
+    assert tuple(y.shape) == (0, h)
+
+
 def test_moe_a8_prefill_tile_boundaries(dev):
     """Prefill kernels (A8) at the tile-shape boundaries, with given ids: experts
     with 1, 64 (last light tile), 65 (first full-tile path), 128 and 129 (the
