@@ -51,3 +51,34 @@ def fused_moe_qpa(x, expert_ids, expert_weights, packed_gate_up=None, scale_gate
     with _LAUNCHES.track():
         return _fused_moe_a8(x, expert_ids, expert_weights, packed_gate_up, scale_gate_up, packed_down, scale_down,
                              bank, swiglu_limit, None)
+
+
+def launch_census(fn) -> dict:
+    """GPU kernel launches of one call of ``fn`` (``kernels/qpa_mma.py:833-856``), counted by
+    the torch profiler: ``total_cuda_launches`` every kernel; ``custom_qpa_launches`` this
+    build's kernels (the library's, which serve every A8 entry) other than routing/layout;
+    ``layout_launches`` kernels whose name mentions emit, bincount, sort, route or layout;
+    ``epilogue_launches`` the rest (torch's own).  ``custom_xsimt_launches`` and
+    ``custom_mxint_launches`` are 0: there are no separate xsimt/mxint kernels.  When the
+    profiler is unavailable: {"launch_census": "custom_only", "custom_launches": n} with n
+    from the library's own launch counter."""
+    from ._launches import LaunchCounter
+    counter = LaunchCounter()
+    try:
+        with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+            fn()
+            torch.cuda.synchronize()
+        names = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA and e.name]
+    except Exception:
+        with counter.track():
+            fn()
+            torch.cuda.synchronize()
+        return {"launch_census": "custom_only", "custom_launches": counter.n}
+    low = [n.lower() for n in names]
+    layout = sum(1 for n in low if any(t in n for t in ("emit", "bincount", "sort", "route", "layout")))
+    custom = sum(1 for n, l in zip(names, low) if "mosaic::" in n and not any(
+        t in l for t in ("emit", "bincount", "sort", "route", "layout")))
+    total = len(names)
+    return {"total_cuda_launches": total, "custom_qpa_launches": custom, "custom_xsimt_launches": 0,
+            "custom_mxint_launches": 0, "layout_launches": layout,
+            "epilogue_launches": max(0, total - custom - layout)}

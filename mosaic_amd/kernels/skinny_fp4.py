@@ -36,6 +36,16 @@ def skinny_mxfp4_gemm(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor
         return ops.mx_kn_linear_a16(x, packed, scale)
 
 
+def pack_gate_up_mxfp4(w_gate: torch.Tensor, w_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """KN gate [K, I] and up [K, I] -> one KN gate|up weight: the two concatenated along N,
+    then ``pack_mxfp4`` -> packed [K, I] (2I nibbles) + e8m0 [K, 2I/32] (``kernels/skinny_fp4.py:231-234``);
+    I % 32 == 0 keeps every 32-column scale block inside gate or up."""
+    from .mxfp4 import pack_mxfp4
+    if w_gate.dim() != 2 or tuple(w_gate.shape) != tuple(w_up.shape):
+        raise ValueError(f"gate {tuple(w_gate.shape)} and up {tuple(w_up.shape)} must be equal [K, I]")
+    return pack_mxfp4(torch.cat([w_gate, w_up], dim=1))
+
+
 def _stack(t):
     if torch.is_tensor(t):
         return t if t.dim() == 3 else t.unsqueeze(0)

@@ -152,7 +152,8 @@ def emit_tiles(counts: np.ndarray, block_m: int):
 # ------------------------------------------------------------ MoE (A16) -----
 def _silu32(g):
     g = np.asarray(g, dtype=np.float32)
-    return (g / (np.float32(1.0) + np.exp(-g).astype(np.float32))).astype(np.float32)
+    with np.errstate(over="ignore"):  # exp(-g) = inf for g < -88.7: g / inf = -0, as in fp32 torch
+        return (g / (np.float32(1.0) + np.exp(-g).astype(np.float32))).astype(np.float32)
 
 
 def swiglu(gate: np.ndarray, up: np.ndarray, limit: float) -> np.ndarray:

@@ -307,3 +307,69 @@ def test_mxint_routed_reduce_bitwise(dev, k_tok, top_k, h, e):
     got = mxint_routed_reduce(yd.to(dev), T(slot_rows), T(order), h)
     assert got.dtype == torch.bfloat16 and tuple(got.shape) == (k_tok, h)
     np.testing.assert_array_equal(got.float().cpu().numpy(), ref)
+
+
+def test_pack_gate_up_mxfp4_matches_packing_the_concatenation(dev):
+    """kernels/skinny_fp4.py:231-234: gate|up concatenated along N, then the floor packer;
+    the result feeds fused_moe_skinny's KN bank."""
+    from mosaic_amd.kernels.skinny_fp4 import pack_gate_up_mxfp4
+    rng = np.random.default_rng(41)
+    k, inter = 256, 96
+    g = (rng.standard_normal((k, inter)) * 0.05).astype(np.float32)
+    u = (rng.standard_normal((k, inter)) * 0.05).astype(np.float32)
+    gb, ub = (torch.from_numpy(a).to(torch.bfloat16) for a in (g, u))
+    p, s = pack_gate_up_mxfp4(gb.to(dev), ub.to(dev))
+    p_ref, s_ref = C.quantize_mxfp4_floor(torch.cat([gb, ub], 1).float().numpy())
+    assert tuple(p.shape) == (k, inter) and tuple(s.shape) == (k, 2 * inter // 32)
+    np.testing.assert_array_equal(p.cpu().numpy(), p_ref)
+    np.testing.assert_array_equal(s.view(torch.uint8).cpu().numpy(), s_ref)
+    with pytest.raises(ValueError):
+        pack_gate_up_mxfp4(gb.to(dev), ub.to(dev)[:, :64])
+
+
+def test_xsimt_prepack_expert_bank_and_exact_decode(dev):
+    """kernels/xsimt.py:380-394 (a stacked bank, cached) and :96-113 (e4m3 -> exact f16)."""
+    from mosaic_amd import ops
+    from mosaic_amd.kernels import _prepack_cache
+    from mosaic_amd.kernels.xsimt import decode_activation_exact, prepack_expert_bank
+    rng = np.random.default_rng(43)
+    e, n, k = 3, 64, 256
+    P = torch.from_numpy(rng.integers(0, 256, (e, n, k // 2), dtype=np.uint8)).to(dev)
+    S = torch.from_numpy(rng.integers(100, 140, (e, n, k // 32), dtype=np.uint8)).to(dev)
+    bank = prepack_expert_bank(P, S)
+    assert prepack_expert_bank(P, S) is bank
+    ref = ops.mxt16_prepack(P, S)
+    assert torch.equal(bank.packed, ref.packed) and torch.equal(bank.scale, ref.scale)
+    p2, s2 = ops.mxt16_unpack(bank)
+    assert torch.equal(p2, P) and torch.equal(s2, S)
+    del bank, ref
+    _prepack_cache.clear()
+    codes = np.arange(256, dtype=np.uint8)
+    codes = codes[(codes & 0x7F) != 0x7F].reshape(2, 127)  # NaN codes excluded
+    x8 = torch.from_numpy(codes).to(dev).view(torch.float8_e4m3fn)
+    out = decode_activation_exact((x8, None))
+    assert out.dtype == torch.float16
+    np.testing.assert_array_equal(out.float().cpu().numpy(), C.e4m3_decode(codes))
+
+
+def test_qpa_launch_census_counts_library_launches(dev):
+    """kernels/qpa_mma.py:833-856: the census of one fused_moe_qpa call has the reference's
+    keys and counts at least the MoE's gate/up and down launches as the library's."""
+    from mosaic_amd.kernels import qpa_mma
+    rng = np.random.default_rng(47)
+    e, h, inter, m, k = 8, 256, 128, 3, 2
+    gp, gs, dp, ds = _bank(rng, e, h, inter)
+    x = torch.from_numpy(rng.standard_normal((m, h)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    ids = torch.from_numpy(np.stack([rng.choice(e, k, replace=False) for _ in range(m)])).to(dev)
+    w = torch.from_numpy(rng.random((m, k)).astype(np.float32)).to(dev)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    fn = lambda: qpa_mma.fused_moe_qpa(x, ids, w, T(gp), T(gs), T(dp), T(ds))
+    fn()
+    c = qpa_mma.launch_census(fn)
+    if "launch_census" in c:
+        assert c["custom_launches"] >= 2
+    else:
+        assert set(c) == {"total_cuda_launches", "custom_qpa_launches", "custom_xsimt_launches",
+                          "custom_mxint_launches", "layout_launches", "epilogue_launches"}
+        assert c["custom_qpa_launches"] >= 2
+        assert c["total_cuda_launches"] == c["custom_qpa_launches"] + c["layout_launches"] + c["epilogue_launches"]
