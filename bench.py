@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: MXFP4 routed-expert MoE decode layer on one MI355X.
 
-Workload (BASELINE configs[1]): DeepSeek-V3/V4 geometry, hidden 7168, 256
+Workload (BASELINE.json configs[1]): DeepSeek-V3/V4 geometry, hidden 7168, 256
 routed experts + 1 shared expert, each gate+up [2*2048, 7168] and down
 [7168, 2048] in MXFP4 (weights N(0, 0.02) quantized with the ceil e8m0 recipe
 and RNE E2M1, then MXT16-prepacked), tokens bf16 N(0, 1), router logits
@@ -59,7 +59,7 @@ def parse():
     ap.add_argument("--m", type=int, default=1, help="tokens per decode step")
     ap.add_argument("--sweep", default="4,16,64", help="extra M values reported under m_sweep ('' to skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 1, 3, 4, 5")
+    ap.add_argument("--no-configs", action="store_true", help="skip BASELINE.json configs 1, 3, 4, 5")
     ap.add_argument("--configs", default="",
                     help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config3_mxfp4_gemm, "
                          "config4_moe_prefill, config5_dsa to run (default: all); config3_vendor_fp8 (the "
@@ -221,7 +221,7 @@ def _graph_time(torch, fn, calls: int, reps: int = 5) -> float:
 
 
 def config1_linear(torch, ops):
-    """BASELINE configs[0]: one MXFP4 linear [2048, 7168] at M=1 (A16, MXT16 weights);
+    """BASELINE.json configs[0]: one MXFP4 linear [2048, 7168] at M=1 (A16, MXT16 weights);
     ~70 weight copies (> the 256 MB MALL) rotate through the graph."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
@@ -241,7 +241,7 @@ def config1_linear(torch, ops):
 
 
 def config3_fp8(torch, ops):
-    """BASELINE configs[2]: FP8 block-scaled GEMMs, 5 shapes x M in {1, 16, 128, 4096}.
+    """BASELINE.json configs[2]: FP8 block-scaled GEMMs, 5 shapes x M in {1, 16, 128, 4096}.
     Copies of the weight (over 512 MB in all, twice the 256 MB MALL) rotate through
     the graph, so every call reads its weight from HBM."""
     dev = torch.device("cuda:0")
@@ -333,7 +333,7 @@ def config3_mxfp4(torch, ops):
 
 
 def config4_prefill(torch, ops, bank, m: int = 4096, seed: int = 13):
-    """BASELINE configs[3]: MoE prefill at M=4096 with Zipf(1.1) expert popularity over a
+    """BASELINE.json configs[3]: MoE prefill at M=4096 with Zipf(1.1) expert popularity over a
     seeded permutation (8 experts pinned to zero), Gumbel-top-8, A8 contract."""
     import math
     dev = torch.device("cuda:0")
@@ -374,7 +374,7 @@ def config4_prefill(torch, ops, bank, m: int = 4096, seed: int = 13):
 
 
 def config5_dsa(torch, ops):
-    """BASELINE configs[4]: FP8 lightning indexer + top-2048 and MLA decode over the picks."""
+    """BASELINE.json configs[4]: FP8 lightning indexer + top-2048 and MLA decode over the picks."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(14)
@@ -593,7 +593,7 @@ def cpu_baseline(torch, ops, bank, tokens: int = 6, seed: int = 7, min_seconds: 
 
 
 def _cpu_config4(expert, lib, cores: int, m: int = 4096, seed: int = 13) -> dict:
-    """A bounded sample of BASELINE configs[3] on the reference's ``vnni_source_gemm``:
+    """A bounded sample of BASELINE.json configs[3] on the reference's ``vnni_source_gemm``:
     config-4 routing (Zipf(1.1) popularity over a seeded permutation, 8 experts
     pinned to zero, Gumbel-top-8 of 4096 tokens), then the A8 layer
     (``fused_moe_mxint``: token act_quant, gate/up, SwiGLU limit 10 x route weight,
@@ -644,7 +644,7 @@ def _cpu_config4(expert, lib, cores: int, m: int = 4096, seed: int = 13) -> dict
 
 
 def _cpu_config5(torch) -> dict:
-    """BASELINE configs[4] on the CPU in torch fp32, one repetition each: the
+    """BASELINE.json configs[4] on the CPU in torch fp32, one repetition each: the
     lightning indexer (e4m3 q and k decoded, per-head dots scaled by q_s and
     k_s, ReLU, x head weight, summed over 64 heads) + top-2048 at (B, L) =
     (1, 32768) and (8, 131072), and MLA decode over 2048 picks of an FP8
@@ -755,7 +755,7 @@ def _config_fns(torch, ops, banks):
             ("config5_dsa", lambda: config5_dsa(torch, ops))]
 
 
-# run only when named in --configs (calibration lines, not BASELINE configs)
+# run only when named in --configs (calibration lines, not BASELINE.json configs)
 def _optional_config_fns(torch, ops):
     return [("config3_vendor_fp8", lambda: config3_vendor_fp8(torch, ops))]
 
@@ -819,7 +819,7 @@ def main():
         "vs_baseline": None,
         "dtype": "mxfp4 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded N(0,1) tokens/logits, N(0,0.02) weights quantized to MXFP4)",
-        "config": {"workload": "MXFP4 MoE decode layer (BASELINE configs[1])", "tokens": args.m, "hidden": H,
+        "config": {"workload": "MXFP4 MoE decode layer (BASELINE.json configs[1])", "tokens": args.m, "hidden": H,
                    "inter": I, "experts": E, "top_k": K, "shared_experts": 1, "score": "sigmoid",
                    "contract": "A16 dequant-then-matmul", "weight_layout": "MXT16 prepacked", "banks": N_BANKS,
                    "bank_reuse_distance_bytes": round((N_BANKS - 1) * main_r["layer_bytes_avg"]),

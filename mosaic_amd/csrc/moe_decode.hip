@@ -667,7 +667,7 @@ static int dec_dn_ks(int64_t nsi) {
 }
 // the batch-1 down kernel: 8 parts of 2 steps at inter 2048 as well (3584 waves
 // instead of 1792 keep more bytes in flight; measured 13.5-13.7 against
-// 13.8-14.2 us at the BASELINE shape)
+// 13.8-14.2 us at the benchmark decode shape)
 static int dec1_dn_ks(int64_t nsi) { return nsi == 16 ? 8 : dec_dn_ks(nsi); }
 
 bool moe_decode1_supported(int64_t m, int64_t hidden, int64_t inter, int64_t top_k, int has_shared) {

@@ -12,7 +12,7 @@
   d in {64, 128, 256, 512}, the reference's set).
 * ``indexer_topk`` / ``indexer_scores`` -- the FP8 indexer of ``Indexer.forward``
   (``.mosaicvm/source/inference_model.py:408-439``) from quantized q/k.
-* ``mla_decode_fp8`` -- MLA decode over an FP8 latent cache (BASELINE format).
+* ``mla_decode_fp8`` -- MLA decode over an FP8 latent cache (the benchmark spec's format).
 * ``dsa_decode_attention(q, k_index, v_full, topk, scale)`` --
   ``mosaicvm/kernels/dsa_attention.py:113-154``: per-head top-k positions and
   softmax attention over them for one token (q [H, d], k_index [ctx, H, d],

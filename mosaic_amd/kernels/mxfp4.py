@@ -3,7 +3,7 @@
 ``pack_mxfp4`` quantizes along the LAST dim in blocks of 32 with the reference
 packer's FLOOR e8m0 recipe (``kernels/mxfp4.py:32-43,91-127``; the quack
 ``to_mxfp4`` it prefers is not importable, so the reference takes this path);
-``quantize_mxfp4`` offers the BASELINE ceil recipe.  Low nibble = even index."""
+``quantize_mxfp4`` offers the benchmark spec's ceil recipe.  Low nibble = even index."""
 from __future__ import annotations
 
 import torch
@@ -30,7 +30,7 @@ def pack_mxfp4(w_bf16: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 def quantize_mxfp4(w: torch.Tensor, recipe: str = "ceil") -> tuple[torch.Tensor, torch.Tensor]:
-    """BASELINE recipe (scale 2^ceil(log2(amax/6)), upstream fp4_quant_kernel) or 'floor'."""
+    """The benchmark spec's recipe (scale 2^ceil(log2(amax/6)), upstream fp4_quant_kernel) or 'floor'."""
     p, s = ops.mx_quantize(w, recipe)
     return p, s.view(torch.float8_e8m0fnu)
 

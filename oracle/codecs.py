@@ -8,7 +8,7 @@ Covers the element formats of the path:
 * E8M0 scale decode by exponent-field insertion (A2): ``e8m0_to_fp32``
   ``kernels/fp4_source.py:67-75``; byte 0x00 -> 0.0, 0xFF -> +inf
   (torch's ``float8_e8m0fnu`` would give 2^-127 / NaN).
-* MXFP4 quantizers (A3): the BASELINE "ceil" recipe of the upstream
+* MXFP4 quantizers (A3): the benchmark spec's "ceil" recipe of the upstream
   ``fp4_quant_kernel`` (``.mosaicvm/source/inference_kernel.py:128-183``,
   ``fast_round_scale`` ``:23-37``) and the reference packer's FLOOR fallback
   (``kernels/mxfp4.py:32-82``, ``kernels/fp4_source.py:35-64``); both round E2M1
@@ -144,7 +144,7 @@ def pow2_ceil_scale(amax: np.ndarray, max_inv: float) -> np.ndarray:
 
 
 def quantize_mxfp4_ceil(w: np.ndarray):
-    """BASELINE recipe == upstream ``fp4_quant_kernel``
+    """The benchmark spec's recipe == upstream ``fp4_quant_kernel``
     (``.mosaicvm/source/inference_kernel.py:128-183``): per 32 contiguous
     elements of the last dim, amax = max|w| clamped to >= 6*2^-126, scale =
     2^ceil(log2(amax*(1/6))), codes = RNE-E2M1(clamp(w/scale, +-6)).

@@ -6,7 +6,7 @@
   score[t] = sum_h w_h * ReLU(q_h . k_t), then top-k with the causal / length
   mask and ``+ offset`` on the kept indices (``inference_model.py:432-438``).
   Here q and k are FP8 e4m3 codes with one fp32 scale per (row, head) and per
-  token (the BASELINE format; the reference feeds bf16 after an fp4
+  token (the benchmark spec's format; the reference feeds bf16 after an fp4
   simulation), and the arithmetic is pinned to one canonical sequence so the
   indices can be compared bit for bit:
 
@@ -107,7 +107,7 @@ def indexer_topk(q, q_s, k, k_s, w, topk: int, lengths=None, offset: int = 0) ->
 
 
 def quantize_rows_e4m3(x: np.ndarray):
-    """Per-row (last axis) e4m3 quantization with s = amax/448 (the BASELINE
+    """Per-row (last axis) e4m3 quantization with s = amax/448 (the benchmark spec's
     'per-token fp32 scale'); returns (codes, scales)."""
     x = np.asarray(x, dtype=np.float32)
     amax = np.abs(x).max(axis=-1).astype(np.float32)

@@ -1,6 +1,6 @@
 """Linear-layer oracles (numpy) -- TEST INFRASTRUCTURE ONLY, see ``oracle/__init__``.
 
-* ``mx_linear_a16`` (A7): BASELINE's "dequant-then-matmul": bf16 x against the
+* ``mx_linear_a16`` (A7): the benchmark spec's "dequant-then-matmul": bf16 x against the
   exactly dequantized MXFP4 W, accumulated wide, rounded once to bf16.
   Restates ``x @ dequant_mxfp4(...)`` (``tests/test_skinny_fp4.py:23``,
   ``kernels/mxfp4.py:130-160``) and the per-expert matmuls of

@@ -1,7 +1,7 @@
 """GPU parity of the A16 MXFP4 linear, routing, expert sort and A16 MoE layer.
 
 Float bar: |got - ref| <= 2e-2 * max(1, |ref|) elementwise against the CPU
-oracle's dequant-then-matmul of identical packed bytes (BASELINE tolerance).
+oracle's dequant-then-matmul of identical packed bytes (the benchmark spec's 2e-2 tolerance).
 Index bar: routing ids, permutation, tile list bit-exact.
 """
 from __future__ import annotations
@@ -431,7 +431,7 @@ def test_moe_a8_prefill_tile_boundaries(dev):
 
 
 def test_moe_a16_decode1_baseline_geometry(dev):
-    """BASELINE configs[1] geometry (hidden 7168, inter 2048, top-8, shared) on a
+    """BASELINE.json configs[1] geometry (hidden 7168, inter 2048, top-8, shared) on a
     32-expert bank quantized on the device; oracle over the experts actually used."""
     ops = _ops()
     e, h, inter, k = 32, 7168, 2048, 8

@@ -168,7 +168,7 @@ def test_indexer_all_tied_takes_lowest_indices(dev):
 
 
 def test_indexer_full_size_properties(dev):
-    """BASELINE config 5 at full size (B=8, L=131072, top-2048): indices are
+    """BASELINE.json configs[4] at full size (B=8, L=131072, top-2048): indices are
     distinct, ordered by the (bit-exact) canonical scores, and no unselected
     token beats a selected one."""
     from mosaic_amd import ops

@@ -1,5 +1,5 @@
 """GPU parity of the reference Router's own scoring path and of the MoE layer
-at the BASELINE geometry (hidden 7168, inter 2048, top-8).
+at the benchmark geometry (hidden 7168, inter 2048, top-8).
 
 * The reference Router (``model/layers.py:127-150``): sqrtsoftplus scores, an
   ``e_score_correction_bias`` added for selection only, renormalization with
@@ -9,11 +9,11 @@ at the BASELINE geometry (hidden 7168, inter 2048, top-8).
   decode kernel (routing fused into gate/up) and both layout kernels.
 * M = 4 and 16 at hidden 7168 / inter 2048 on a 32-expert bank (one GPU's
   expert-parallel share), A16 contract.
-* BASELINE configs[3] at full size: 4096 tokens, 256 experts, Zipf(1.1)
+* BASELINE.json configs[3] at full size: 4096 tokens, 256 experts, Zipf(1.1)
   popularity with 8 experts pinned to zero, A8 contract; sampled tokens,
   including one routed to the most loaded expert, against the oracle.
 
-Float bar: |got - ref| <= 2e-2 * max(1, |ref|) elementwise (BASELINE).
+Float bar: |got - ref| <= 2e-2 * max(1, |ref|) elementwise (the benchmark spec).
 """
 from __future__ import annotations
 
@@ -195,7 +195,7 @@ def test_moe_a16_baseline_geometry_multi_token(dev, m):
 
 
 def test_moe_a8_prefill_config4_full_size(dev):
-    """BASELINE configs[3] at full size: 4096 tokens, 256 experts + shared,
+    """BASELINE.json configs[3] at full size: 4096 tokens, 256 experts + shared,
     hidden 7168, inter 2048, top-8 by Gumbel-top-k over Zipf(1.1) popularity
     on a seeded expert permutation with 8 experts pinned to zero.  Routing,
     layout and the empty experts are checked in full; four sampled tokens (one
