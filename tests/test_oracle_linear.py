@@ -30,6 +30,24 @@ def test_a16_brute_force_tiny():
             assert got[i, j] == np.float32(acc)
 
 
+def test_kn_a16_pins():
+    """mx_linear_kn_a16 (KN layout of kernels/skinny_fp4.py:50-144: packed [K, N/2], one e8m0 per 32
+    consecutive N): a one-hot x selects a dequantized ROW of the KN weight; brute force (a
+    double-precision sum per output) on a small case; and a planted reversal of N fails."""
+    rng = np.random.default_rng(5)
+    k, n = 96, 64
+    packed, scale = _rand_mx(rng, k, n, std=1.0)         # KN: rows are K, blocks of 32 along N
+    wkn = C.dequant_mxfp4(packed, scale)                   # [K, N]
+    x = np.eye(k, dtype=np.float32)[[0, 7, 95]]
+    np.testing.assert_array_equal(L.mx_linear_kn_a16(x, packed, scale, out_bf16=False), wkn[[0, 7, 95]])
+    xr = C.round_bf16(rng.standard_normal((3, k)).astype(np.float32))
+    got = L.mx_linear_kn_a16(xr, packed, scale, out_bf16=False)
+    want = np.array([[sum(float(xr[i, kk]) * float(wkn[kk, j]) for kk in range(k)) for j in range(n)]
+                     for i in range(3)], dtype=np.float32)
+    np.testing.assert_array_equal(got, want)
+    assert not np.array_equal(got, (xr.astype(np.float64) @ wkn[:, ::-1].astype(np.float64)).astype(np.float32))
+
+
 def test_a16_onehot_selects_column():
     rng = np.random.default_rng(1)
     packed, scale = _rand_mx(rng, 16, 128, std=1.0)
