@@ -80,3 +80,53 @@ def test_fp8_block_gemm_random_shapes(dev, seed):
     T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
     c = ops.fp8_block_gemm(T(aq), T(a_s), T(bq), T(bs))
     _close(c.float().cpu().numpy(), L.fp8_block_gemm(aq, a_s, bq, bs), f"fp8 {m}x{n}x{k}")
+
+
+def _bank(rng, e, h, inter):
+    q = lambda r, c: C.quantize_mxfp4_ceil(_bf16(rng.standard_normal((r, c)) * 0.05).float().numpy())
+    gu = [q(2 * inter, h) for _ in range(e)]
+    d = [q(h, inter) for _ in range(e)]
+    return (np.stack([a[0] for a in gu]), np.stack([a[1] for a in gu]), np.stack([a[0] for a in d]),
+            np.stack([a[1] for a in d]))
+
+
+def _moe_case(rng, a8):
+    e = int(rng.choice([4, 8, 16, 32, 64]))
+    k = int(rng.integers(1, min(8, e) + 1))
+    h = int(rng.choice([512, 1024] if a8 else [256, 384, 512]))
+    inter = int(rng.choice([512, 1024] if a8 else [128, 256, 512]))
+    m = int(rng.choice([1, 2, 3, 4, 7, 16, 33, 130, 200] if a8 else [1, 2, 3, 4, 7, 16, 33]))
+    func = str(rng.choice(["sigmoid", "softmax", "sqrtsoftplus"]))
+    return m, e, h, inter, k, bool(rng.integers(0, 2)), float(rng.choice([0.0, 10.0])), func
+
+
+@pytest.mark.parametrize("a8", [False, True])
+@pytest.mark.parametrize("seed", range(10))
+def test_moe_random_configs(dev, seed, a8):
+    """Routing on the device (sigmoid / softmax / sqrtsoftplus scores, top-k with ties to the
+    lower index, renormalized) then the layer: ids bit-exact, y within the float bar, for
+    random expert counts, top-k, widths, batch sizes (decode, layout and, for A8, prefill
+    paths), shared expert on or off and SwiGLU limit 0 or 10."""
+    from oracle import moe as MO
+    from mosaic_amd import ops
+    rng = np.random.default_rng(9300 + 17 * seed + a8)
+    m, e, h, inter, k, shared, limit, func = _moe_case(rng, a8)
+    gp, gs, dp, ds = _bank(rng, e, h, inter)
+    sh = _bank(rng, 1, h, inter) if shared else None
+    x = _bf16(rng.standard_normal((m, h)))
+    logits = rng.standard_normal((m, e)).astype(np.float32)
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    gu_b, d_b = ops.mxt16_prepack(T(gp), T(gs)), ops.mxt16_prepack(T(dp), T(ds))
+    shb = None if sh is None else (ops.mxt16_prepack(T(sh[0][0]), T(sh[1][0])),
+                                   ops.mxt16_prepack(T(sh[2][0]), T(sh[3][0])))
+    fwd = ops.moe_a8_forward if a8 else ops.moe_a16_forward
+    y, ids, w = fwd(x.to(dev), gu_b, d_b, logits=T(logits), top_k=k, shared=shb, swiglu_limit=limit,
+                    score_func=func)
+    ids_ref, w_ref = MO.route_topk(logits, k, func)
+    what = f"{'a8' if a8 else 'a16'} m={m} e={e} h={h} i={inter} k={k} shared={shared} limit={limit} {func}"
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref, err_msg=what)
+    np.testing.assert_array_equal(w.cpu().numpy(), w_ref, err_msg=what)
+    layer = MO.moe_layer_a8 if a8 else MO.moe_layer_a16
+    ref = layer(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds, swiglu_limit=limit,
+                shared=None if sh is None else tuple(t[0] for t in sh))
+    _close(y.float().cpu().numpy(), ref, what)
