@@ -130,3 +130,33 @@ def test_moe_random_configs(dev, seed, a8):
     ref = layer(x.float().numpy(), ids_ref, w_ref, gp, gs, dp, ds, swiglu_limit=limit,
                 shared=None if sh is None else tuple(t[0] for t in sh))
     _close(y.float().cpu().numpy(), ref, what)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_indexer_topk_random_configs(dev, seed):
+    """Lightning indexer + exact top-k over random batch, head count, length, top-k, per-row
+    lengths (0 to L), offsets and planted ties: indices bit-exact against the oracle."""
+    from oracle import dsa as D
+    from mosaic_amd import ops
+    rng = np.random.default_rng(9400 + seed)
+    b = int(rng.integers(1, 5))
+    h = int(rng.choice([16, 32, 48, 64]))
+    l = int(rng.integers(1, 20001))
+    topk = int(rng.choice([1, 5, 64, 256, 512, 1024, 2048]))
+    q, qs = D.quantize_rows_e4m3(rng.standard_normal((b, h, 128)))
+    k, ks = D.quantize_rows_e4m3(rng.standard_normal((b, l, 128)))
+    w = (rng.standard_normal((b, h)) * (128 ** -0.5) * (h ** -0.5)).astype(np.float32)
+    if seed % 3 == 0 and l > 8:  # exact ties: one key row copied over a run of positions
+        a = int(rng.integers(0, l // 2))
+        k[:, a:a + l // 3] = k[:, a:a + 1]
+        ks[:, a:a + l // 3] = ks[:, a:a + 1]
+    lengths = None
+    if seed % 2 == 1:
+        lengths = rng.integers(0, l + 1, size=b).astype(np.int32)
+        lengths[0] = l if b > 1 else lengths[0]
+    offset = int(rng.integers(0, 51))
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    got = ops.dsa_indexer_topk(T(q), T(qs), T(k), T(ks), T(w), topk,
+                               lengths=None if lengths is None else T(lengths), offset=offset).cpu().numpy()
+    want = D.indexer_topk(q, qs, k, ks, w, topk, lengths, offset)
+    np.testing.assert_array_equal(got, want, err_msg=f"b={b} h={h} l={l} topk={topk} lengths={lengths}")
