@@ -160,3 +160,54 @@ def test_indexer_topk_random_configs(dev, seed):
                                lengths=None if lengths is None else T(lengths), offset=offset).cpu().numpy()
     want = D.indexer_topk(q, qs, k, ks, w, topk, lengths, offset)
     np.testing.assert_array_equal(got, want, err_msg=f"b={b} h={h} l={l} topk={topk} lengths={lengths}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_mla_decode_random_configs(dev, seed):
+    """MLA decode over the FP8 latent cache at random batch, head count, cache length, pick
+    count, scale block, sink and masked picks, against the oracle."""
+    from oracle import dsa as D
+    from mosaic_amd import ops
+    rng = np.random.default_rng(9500 + seed)
+    b = int(rng.integers(1, 9))
+    h = int(rng.choice([16, 32, 48, 64, 128, 192, 256]))
+    n = int(rng.integers(16, 6001))
+    t = int(rng.integers(1, min(n, 3000) + 1))
+    sb = int(rng.choice([64, 128, 512]))
+    masked = float(rng.choice([0.0, 0.1, 0.5]))
+    q = C.round_bf16(rng.standard_normal((b, h, 576)).astype(np.float32))
+    lat, ls = D.quantize_rows_e4m3(rng.standard_normal((b, n, 512 // sb, sb)) * 2.0)
+    lat = lat.reshape(b, n, 512)
+    rope = C.round_bf16(rng.standard_normal((b, n, 64)).astype(np.float32))
+    idx = np.stack([rng.choice(n, t, replace=False) for _ in range(b)]).astype(np.int32)
+    idx[rng.random(idx.shape) < masked] = -1
+    snk = rng.standard_normal(h).astype(np.float32) if seed % 2 else None
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    out = ops.mla_sparse_decode(T(q).to(torch.bfloat16), T(lat), T(ls), T(rope).to(torch.bfloat16), T(idx),
+                                576 ** -0.5, None if snk is None else T(snk))
+    _close(out.float().cpu().numpy(), D.mla_sparse_decode(q, lat, ls, rope, snk, idx, 576 ** -0.5, sb),
+           f"mla b={b} h={h} n={n} t={t} sb={sb} masked={masked}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_sparse_attn_fused_random_configs(dev, seed):
+    """sparse_attn_fused (V = K) at head dims 64, 128, 256 and 512 with random rows, head
+    counts (padded to 16), cache lengths, pick counts and masked picks (all masked included)."""
+    from oracle import dsa as D
+    from mosaic_amd.kernels.dsa import sparse_attn_fused
+    rng = np.random.default_rng(9600 + seed)
+    d = int(rng.choice([64, 128, 256, 512]))
+    s = int(rng.integers(1, 7))
+    h = int(rng.integers(1, 81))
+    n = int(rng.integers(1, 3001))
+    t = int(rng.integers(1, 1201))
+    masked = float(rng.choice([0.0, 0.3, 1.0]))
+    q = C.round_bf16(rng.standard_normal((s, h, d)).astype(np.float32))
+    kv = C.round_bf16(rng.standard_normal((n, d)).astype(np.float32))
+    idx = rng.integers(0, n, size=(s, t)).astype(np.int32)
+    idx[rng.random(idx.shape) < masked] = -1
+    sink = rng.standard_normal(h).astype(np.float32)
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    o = sparse_attn_fused(T(q).to(torch.bfloat16), T(kv).to(torch.bfloat16), T(sink), T(idx), d ** -0.5)
+    _close(o.float().cpu().numpy(), D.sparse_attn(q, kv[None], sink, idx, d ** -0.5, d, s),
+           f"sparse_attn d={d} s={s} h={h} n={n} t={t} masked={masked}")
