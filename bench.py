@@ -62,8 +62,9 @@ def parse():
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE.json configs 1, 3, 4, 5")
     ap.add_argument("--configs", default="",
                     help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config3_mxfp4_gemm, "
-                         "config4_moe_prefill, config5_dsa to run (default: all); config3_vendor_fp8 (the "
-                         "vendor library's FP8 GEMM at the config-3 shapes, a calibration) runs only when named")
+                         "config4_moe_prefill, config5_dsa to run (default: all); config3_vendor_fp8 and "
+                         "config3_vendor_mx (the vendor library's per-tensor FP8 and MX block-scaled GEMMs at "
+                         "the config-3 shapes, calibrations) run only when named")
     ap.add_argument("--no-headline", action="store_true",
                     help="skip the decode layer (one bank is still built for config 4); for profiling the configs")
     ap.add_argument("--no-graph", action="store_true",
@@ -296,6 +297,43 @@ def config3_vendor_fp8(torch, ops):
         out[f"m4096_n{n}_k{k}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
                                    "mfma_frac": round(fl / us / 1e6 / 5000.0, 4)}
         del bs, b0
+    return out
+
+
+def config3_vendor_mx(torch, ops):
+    """Calibration, not a path of this build: hipBLASLt's MX block-scaled GEMM (torch._scaled_mm
+    with one e8m0 scale per 32 K on both operands, bf16 out) at the config-3 M = 4096 shapes,
+    fp8 x fp8 (the scaled MFMA at the fp8 rate, as this build's fp8 x fp4 A8 GEMM runs) and
+    fp4 x fp4 (twice that rate), weights rotating past the MALL as in config 3."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    out = {}
+    for n, k in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (18432, 7168)]:
+        # unit scales; the library takes them in 128-row blocks (rows padded to a multiple of 128)
+        sa = torch.full((4096, k // 32), 127, dtype=torch.uint8, device=dev).view(torch.float8_e8m0fnu)
+        sb = torch.full(((n + 127) // 128 * 128, k // 32), 127, dtype=torch.uint8,
+                        device=dev).view(torch.float8_e8m0fnu)
+        fl = 2 * 4096 * n * k
+        for fmt in ("fp8", "fp4"):
+            if fmt == "fp8":
+                a = (torch.randn(4096, k, generator=g, device=dev) * 8.0).clamp(-448, 448).to(torch.float8_e4m3fn)
+                b0 = (torch.randn(n, k, generator=g, device=dev) * 8.0).clamp(-448, 448).to(torch.float8_e4m3fn)
+                peak = 5000.0
+            else:
+                a = torch.randint(0, 256, (4096, k // 2), generator=g, device=dev,
+                                  dtype=torch.uint8).view(torch.float4_e2m1fn_x2)
+                b0 = torch.randint(0, 256, (n, k // 2), generator=g, device=dev,
+                                   dtype=torch.uint8).view(torch.float4_e2m1fn_x2)
+                peak = 10000.0
+            nrot = (512 << 20) // (b0.numel() * b0.element_size()) + 1
+            bs = [b0] + [b0.clone() for _ in range(nrot - 1)]
+            it = iter(range(10 ** 9))
+            us = _graph_time(torch, lambda: torch._scaled_mm(a, bs[next(it) % nrot].t(), scale_a=sa, scale_b=sb,
+                                                             out_dtype=torch.bfloat16), nrot, reps=1)
+            out[f"{fmt}_m4096_n{n}_k{k}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                                             "mfma_frac": round(fl / us / 1e6 / peak, 4)}
+            del bs, b0, a
     return out
 
 
@@ -757,7 +795,8 @@ def _config_fns(torch, ops, banks):
 
 # run only when named in --configs (calibration lines, not BASELINE.json configs)
 def _optional_config_fns(torch, ops):
-    return [("config3_vendor_fp8", lambda: config3_vendor_fp8(torch, ops))]
+    return [("config3_vendor_fp8", lambda: config3_vendor_fp8(torch, ops)),
+            ("config3_vendor_mx", lambda: config3_vendor_mx(torch, ops))]
 
 
 def _selected_configs(args, torch, ops, banks):
