@@ -167,6 +167,24 @@ int mosaic_fp8_block_gemm_ws(const uint8_t* a, const float* a_s, const uint8_t* 
                              int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* T16 prepack of an e4m3 weight [n, k] (n % 16 == 0, k % 128 == 0) into the
+ * decode kernel's lane order, n * k bytes: block (g, kb) of 2048 bytes at
+ * (g * k/128 + kb) * 2048 holds byte W[16g + c][128kb + 64h + 16q + j] at
+ * 1024h + 16(4c + q) + j (c < 16, q < 4, h < 2, j < 16).  A bit-exact
+ * permutation; mosaic_fp8_t16_unpack is its inverse.  No counterpart in the
+ * reference, whose fp8_gemm (.mosaicvm/source/inference_kernel.py:203-273)
+ * reads the checkpoint layout; it serves the same call sites at decode sizes,
+ * where each 1 KB load of the prepacked weight is contiguous. */
+int mosaic_fp8_t16_prepack(const uint8_t* w, uint8_t* out, int64_t n, int64_t k, void* stream);
+int mosaic_fp8_t16_unpack(const uint8_t* t16, uint8_t* w, int64_t n, int64_t k, void* stream);
+
+/* mosaic_fp8_block_gemm with B given as its T16 prepack (bt, n * k bytes) and
+ * m <= 16; b_s as for mosaic_fp8_block_gemm.  The same MFMA operands as the
+ * checkpoint-layout decode kernel, so the same C bit for bit.  Same call sites
+ * as mosaic_fp8_block_gemm (fp8_gemm, w8a8_block_fp8_matmul) at M <= 16. */
+int mosaic_fp8_block_gemm_t16(const uint8_t* a, const float* a_s, const uint8_t* bt, const float* b_s, void* c,
+                              int out_dtype, int64_t m, int64_t n, int64_t k, void* stream);
+
 /* W8A16 linear with the in-GEMM weight decode of fp8_linear's fused kernel
  * (bench/fp8_core.py:160-231): y [m, n] bf16 = sum over 128-K blocks of
  * (x_kb . decode(W_kb)^T) * s[n/128, kb], x bf16 [m, k], W e4m3 [n, k]

@@ -106,11 +106,21 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemm_skinny_kernel(
 // with buffer loads: B rows past N and A rows past M read zeros, entries past
 // the wave's range reload its last block and are scaled by 0, so the loop has
 // no branches.  The K parts meet in LDS in wave order.
+// B layouts (L): 0, checkpoint [N, K] rows, each load reads 64 bytes of 16
+// rows (lane (c, q): row c, bytes 16q.. and 64 + 16q..).  1, the same rows,
+// each load reading whole 128-byte lines: the first covers rows 0..7 of the
+// tile (lane c < 8: row c, bytes 16q..; lane c >= 8: row c - 8, bytes
+// 64 + 16q..), the second rows 8..15 the same way, and two DPP moves per
+// dword (row rotate by 8, half the lanes written) give lane (c, q) row c's
+// bytes [16q, 16q + 16) and [64 + 16q, 64 + 16q + 16), the A operand's map.
+// 2, the T16 prepack (fp8_t16_pack_kernel): each 16-row x 128-K block is 2 KB
+// in lane order, so each load reads 1 KB contiguous.  All three hand the MFMA
+// the same operands, so their results are identical.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t fp8_rsrc(const void* base, int64_t records) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)records, 0x00020000);
 }
 
-template <int T, int KS, int D>
+template <int T, int KS, int D, int L>
 __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __restrict__ A, const float* __restrict__ As,
                                                            const uint8_t* __restrict__ B,
                                                            const float* __restrict__ Bs, void* __restrict__ C, int M,
@@ -135,9 +145,19 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
     const int kb = kb0 + (i < nb ? i : nb - 1);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const uint32_t off = (uint32_t)((16 * t + c) * K + kb * 128 + 16 * q);
-      rbv[s][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
-      rbv[s][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(off + 64), 0, 0);
+      if (L == 2) {
+        const uint32_t off = (uint32_t)(16 * t * K + kb * 2048 + 16 * (4 * c + q));
+        rbv[s][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
+        rbv[s][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(off + 1024), 0, 0);
+      } else if (L == 1) {
+        const uint32_t off = (uint32_t)((16 * t + (c & 7)) * K + kb * 128 + 16 * (q + 4 * (c >> 3)));
+        rbv[s][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
+        rbv[s][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(off + 8 * K), 0, 0);
+      } else {
+        const uint32_t off = (uint32_t)((16 * t + c) * K + kb * 128 + 16 * q);
+        rbv[s][t][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
+        rbv[s][t][1] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(off + 64), 0, 0);
+      }
       rsb[s][t] = bs_row[t][kb];
     }
     rav[s][0] = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_row + kb * 128), 0, 0);
@@ -152,8 +172,13 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
                        (int)rav[s][1][0], (int)rav[s][1][1], (int)rav[s][1][2], (int)rav[s][1][3]};
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const i32x8_t bo = {(int)rbv[s][t][0][0], (int)rbv[s][t][0][1], (int)rbv[s][t][0][2], (int)rbv[s][t][0][3],
-                          (int)rbv[s][t][1][0], (int)rbv[s][t][1][1], (int)rbv[s][t][1][2], (int)rbv[s][t][1][3]};
+      i32x8_t bo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int x0 = (int)rbv[s][t][0][j], x1 = (int)rbv[s][t][1][j];
+        bo[j] = L == 1 ? __builtin_amdgcn_update_dpp(x0, x1, 0x128, 0xF, 0xC, false) : x0;
+        bo[4 + j] = L == 1 ? __builtin_amdgcn_update_dpp(x1, x0, 0x128, 0xF, 0x3, false) : x1;
+      }
       const f32x4_t d = mfma_fp8_block(bo, a);
       const float sc = i < nb ? rsa[s] * rsb[s][t] : 0.f;
 #pragma unroll
@@ -196,22 +221,63 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
   }
 }
 
-template <int T, int KS>
+// Ring depth D: a divisor of the wave's block count where one exists, so no
+// ring entry reloads a block past the wave's range (each such reload is a
+// wasted 2 KB read per tile; with 1.5 blocks a wave and D = 4 the launch ran
+// 1.7x slower).
+template <int T, int KS, int L>
 static void launch_fp8_gemv(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c, int64_t m,
                             int64_t n, int64_t k, int out_f32, hipStream_t st) {
   const int nb = (int)(k / 128 / KS);
   const dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)));
 #define FP8_GEMV(DV) \
-  MOSAIC_LAUNCH((fp8_gemv_kernel<T, KS, DV>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, out_f32)
+  MOSAIC_LAUNCH((fp8_gemv_kernel<T, KS, DV, L>), grid, dim3(KS * 64), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, \
+                out_f32)
   if (nb % 8 == 0)
     FP8_GEMV(8);
   else if (nb % 7 == 0)
     FP8_GEMV(7);
   else if (nb % 6 == 0)
     FP8_GEMV(6);
+  else if (nb % 5 == 0)
+    FP8_GEMV(5);
+  else if (nb % 4 == 0)
+    FP8_GEMV(4);
+  else if (nb % 3 == 0)
+    FP8_GEMV(3);
   else
     FP8_GEMV(4);
 #undef FP8_GEMV
+}
+
+// Ring-kernel plans: few rows, one 16-column tile per workgroup (more
+// workgroups), K split wider where there are few column tiles; more rows, two
+// tiles share each A fragment, except where that leaves under 192 workgroups
+// (measured with the weights cold in HBM, M = 1 and 16, N = 4096..24576).
+// Short K (at most 16 blocks): the widest split of 8, 4 or 2 waves that
+// divides the blocks and leaves each wave at least 3 (K = 1536: 4 waves of 3
+// blocks, 3.3-4.0 against 4.5-6.0 us at N = 576..4096 with the T16 layout),
+// except for two-tile workgroups over the checkpoint layout, whose whole-line
+// loads ran faster with 2 waves (M = 16, N = 7168, K = 2048: 5.7 against 6.4 us).
+template <int L>
+static void dispatch_fp8_gemv(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c,
+                              int64_t m, int64_t n, int64_t k, int out_f32, hipStream_t st) {
+  const int64_t t16 = (n + 15) / 16, nkb = k / 128;
+  int T = 1, KS;
+  if (m <= 4)
+    KS = t16 <= 256 ? 8 : t16 <= 1152 ? 4 : 2;
+  else if ((n + 31) / 32 < 192)
+    KS = 8;
+  else
+    T = 2, KS = 2;
+  if (nkb <= 16 && (L == 2 || T == 1)) {
+    KS = 8;
+    while (KS > 2 && (nkb % KS || nkb / KS < 3)) KS /= 2;
+  }
+#define FP8_PLAN(TT, KK) \
+  if (T == TT && KS == KK) return launch_fp8_gemv<TT, KK, L>(a, as, b, bs, c, m, n, k, out_f32, st);
+  FP8_PLAN(1, 8) FP8_PLAN(1, 4) FP8_PLAN(1, 2) FP8_PLAN(2, 8) FP8_PLAN(2, 4) FP8_PLAN(2, 2)
+#undef FP8_PLAN
 }
 
 template <int T, int KS>
@@ -687,6 +753,24 @@ __global__ void __launch_bounds__(256) fp8_block_dequant_kernel(const uint8_t* _
   o[3] = f32_bf16(hi[1] * sc);
 }
 
+// T16 prepack of e4m3 weights for the ring kernel: [N, K] (N % 16 == 0,
+// K % 128 == 0) -> blocks of 2048 bytes, block (g, kb) at (g * K/128 + kb) *
+// 2048 holding rows 16g..16g+15, K bytes 128kb..128kb+127, in lane order:
+// byte 1024h + 16(4c + q) + j = W[16g + c][128kb + 64h + 16q + j].  One
+// thread moves one 16-byte chunk; PACK false is the exact inverse.
+template <bool PACK>
+__global__ void __launch_bounds__(256) fp8_t16_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                      int64_t chunks, int64_t k) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= chunks) return;
+  const int64_t nkb = k / 128, blk = o >> 7;
+  const int w = (int)(o & 127), h = w >> 6, c = (w >> 2) & 15, q = w & 3;
+  const int64_t row = (blk / nkb) * 16 + c, col = (blk % nkb) * 128 + 64 * h + 16 * q;
+  const int64_t raw = row * k + col, t16 = o * 16;
+  const int64_t from = PACK ? raw : t16, to = PACK ? t16 : raw;
+  *reinterpret_cast<u32x4_t*>(dst + to) = *reinterpret_cast<const u32x4_t*>(src + from);
+}
+
 extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16_t* out, int64_t n, int64_t k,
                                         int block_n, int block_k, void* stream) {
   MOSAIC_CHECK_ARG(w && s && out, "fp8_block_dequant: null pointer");
@@ -763,26 +847,13 @@ static int fp8_block_gemm_impl(const uint8_t* a, const float* a_s, const uint8_t
                          (int)n, (int)k, f32);
       break;
     }
-    case 4: {
-      // few rows: one 16-column tile per workgroup (more workgroups), K split
-      // wider where there are few column tiles; more rows: two tiles share each
-      // A fragment, except where that leaves under 192 workgroups (measured
-      // with the weights cold in HBM, M = 1 and 16, N = 4096..24576)
-      const int64_t t16 = (n + 15) / 16;
-      if (m <= 4) {
-        if (t16 <= 256)
-          launch_fp8_gemv<1, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
-        else if (t16 <= 1152)
-          launch_fp8_gemv<1, 4>(a, a_s, b, b_s, c, m, n, k, f32, st);
-        else
-          launch_fp8_gemv<1, 2>(a, a_s, b, b_s, c, m, n, k, f32, st);
-      } else if ((n + 31) / 32 < 192) {
-        launch_fp8_gemv<1, 8>(a, a_s, b, b_s, c, m, n, k, f32, st);
-      } else {
-        launch_fp8_gemv<2, 2>(a, a_s, b, b_s, c, m, n, k, f32, st);
-      }
+    case 4:
+      // whole-line loads pay where a workgroup has more than 4 rows of work
+      if (m <= 4)
+        dispatch_fp8_gemv<0>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      else
+        dispatch_fp8_gemv<1>(a, a_s, b, b_s, c, m, n, k, f32, st);
       break;
-    }
     case 2: launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     case 1: launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     default:
@@ -812,4 +883,41 @@ extern "C" int mosaic_fp8_block_gemm_ws(const uint8_t* a, const float* a_s, cons
                                         void* c, int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
                                         size_t workspace_bytes, void* stream) {
   return fp8_block_gemm_impl(a, a_s, b, b_s, c, out_dtype, m, n, k, workspace, workspace_bytes, stream);
+}
+
+static int fp8_t16_convert(bool pack, const uint8_t* src, uint8_t* dst, int64_t n, int64_t k, void* stream) {
+  MOSAIC_CHECK_ARG(src && dst, "fp8_t16: null pointer");
+  MOSAIC_CHECK_ARG(n >= 0 && n % 16 == 0 && k > 0 && k % 128 == 0,
+                   "fp8_t16: N=%lld must be a multiple of 16 and K=%lld a positive multiple of 128", (long long)n,
+                   (long long)k);
+  if (n == 0) return kOk;
+  const int64_t chunks = n * k / 16;
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  if (pack)
+    MOSAIC_LAUNCH(fp8_t16_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, src, dst, chunks, k);
+  else
+    MOSAIC_LAUNCH(fp8_t16_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, src, dst, chunks, k);
+  MOSAIC_RETURN_LAUNCH("fp8_t16");
+}
+
+extern "C" int mosaic_fp8_t16_prepack(const uint8_t* w, uint8_t* out, int64_t n, int64_t k, void* stream) {
+  return fp8_t16_convert(true, w, out, n, k, stream);
+}
+
+extern "C" int mosaic_fp8_t16_unpack(const uint8_t* t16, uint8_t* w, int64_t n, int64_t k, void* stream) {
+  return fp8_t16_convert(false, t16, w, n, k, stream);
+}
+
+extern "C" int mosaic_fp8_block_gemm_t16(const uint8_t* a, const float* a_s, const uint8_t* bt, const float* b_s,
+                                         void* c, int out_dtype, int64_t m, int64_t n, int64_t k, void* stream) {
+  MOSAIC_CHECK_ARG(a && a_s && bt && b_s && c, "fp8_block_gemm_t16: null pointer");
+  MOSAIC_CHECK_ARG(m >= 0 && m <= 16, "fp8_block_gemm_t16: M=%lld; the T16 layout serves M <= 16", (long long)m);
+  MOSAIC_CHECK_ARG(n >= 0 && n % 16 == 0 && k > 0 && k % 128 == 0 && (int64_t)n * k < (1ll << 31),
+                   "fp8_block_gemm_t16: N=%lld (multiple of 16), K=%lld (multiple of 128), N*K < 2^31", (long long)n,
+                   (long long)k);
+  MOSAIC_CHECK_ARG(out_dtype == MOSAIC_DTYPE_F32 || out_dtype == MOSAIC_DTYPE_BF16,
+                   "fp8_block_gemm_t16: out dtype %d", out_dtype);
+  if (m == 0 || n == 0) return kOk;
+  dispatch_fp8_gemv<2>(a, a_s, bt, b_s, c, m, n, k, out_dtype == MOSAIC_DTYPE_F32, (hipStream_t)stream);
+  MOSAIC_RETURN_LAUNCH("fp8_block_gemm_t16");
 }

@@ -1,9 +1,9 @@
-"""Prepacked-weight cache of the drop-ins that receive raw NK MXFP4 tensors.
+"""Prepacked-weight cache of the drop-ins that receive raw NK MXFP4 tensors
+(MXT16) or FP8 e4m3 weights at decode sizes (T16).
 
 The reference's GEMV drop-ins accept raw ``packed``/``scale`` tensors and a
 ``prepacked`` argument; a caller that passes only the raw tensors would
-otherwise pay an MXT16 prepack (a full read and write of the weight) on every
-call.
+otherwise pay a prepack (a full read and write of the weight) on every call.
 
 An entry is keyed by the caller's source tensors: each one's data pointer,
 shape, strides, dtype and device.  A hit also needs every source's storage
@@ -62,6 +62,11 @@ def cached(srcs: Sequence[torch.Tensor], make: Callable[[], object]):
 def mxt16(packed: torch.Tensor, scale: torch.Tensor) -> ops.MXT16:
     """ops.mxt16_prepack(packed, scale), reused while both tensors are alive and unmodified."""
     return cached((packed, scale), lambda: ops.mxt16_prepack(packed, scale))
+
+
+def fp8_t16(b: torch.Tensor) -> ops.FP8T16:
+    """ops.fp8_t16_prepack(b), reused while ``b`` is alive and unmodified."""
+    return cached((b,), lambda: ops.fp8_t16_prepack(b))
 
 
 def size() -> int:

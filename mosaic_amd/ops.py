@@ -361,15 +361,54 @@ def mxt16_linear_a8(x: torch.Tensor | None, w: MXT16, prequant: tuple | None = N
 
 
 # ------------------------------------------------------- FP8 block GEMM -----
-def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
-                   out_dtype=torch.bfloat16) -> torch.Tensor:
-    """C [M, N] = block-scaled e4m3 GEMM (A [M, K] + a_s [M, K/128], B [N, K] + b_s [ceil(N/128), K/128])."""
-    a = _u8(a, "a")
+FP8_T16_MAX_M = 16  # rows up to which fp8_block_gemm takes a T16-prepacked weight
+
+
+@dataclass
+class FP8T16:
+    """An e4m3 weight [N, K] (N % 16 == 0, K % 128 == 0) prepacked for the decode
+    kernel: ``codes`` holds the same N * K bytes, each 16-row x 128-K block as
+    2 KB in MFMA lane order (``mosaic_fp8_t16_prepack``)."""
+    codes: torch.Tensor
+    n: int
+    k: int
+
+
+def fp8_t16_prepack(b: torch.Tensor) -> FP8T16:
+    """e4m3 codes [N, K] -> FP8T16 (bit-exact permutation)."""
     b = _u8(b, "b")
-    if a.dim() != 2 or b.dim() != 2:
+    if b.dim() != 2:
+        raise ValueError(f"b must be [N, K], got {tuple(b.shape)}")
+    n, k = b.shape
+    if n % 16 or k % 128 or k == 0:
+        raise ValueError(f"FP8T16 needs N % 16 == 0 and K a positive multiple of 128, got N={n} K={k}")
+    out = torch.empty_like(b)
+    _lib.call("mosaic_fp8_t16_prepack", _ptr(b), _ptr(out), n, k, _stream())
+    return FP8T16(out, n, k)
+
+
+def fp8_t16_unpack(w: FP8T16) -> torch.Tensor:
+    """Inverse of ``fp8_t16_prepack``: uint8 codes [N, K]."""
+    out = torch.empty_like(w.codes)
+    _lib.call("mosaic_fp8_t16_unpack", _ptr(w.codes), _ptr(out), w.n, w.k, _stream())
+    return out
+
+
+def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor | FP8T16, b_s: torch.Tensor,
+                   out_dtype=torch.bfloat16) -> torch.Tensor:
+    """C [M, N] = block-scaled e4m3 GEMM (A [M, K] + a_s [M, K/128], B [N, K] + b_s [ceil(N/128), K/128]).
+
+    ``b`` may be an ``FP8T16`` prepack for M <= 16 (the same C bit for bit)."""
+    a = _u8(a, "a")
+    t16 = isinstance(b, FP8T16)
+    if not t16:
+        b = _u8(b, "b")
+    if a.dim() != 2 or (not t16 and b.dim() != 2):
         raise ValueError("a and b must be 2-D")
     m, k = a.shape
-    n, kb = b.shape
+    n, kb = (b.n, b.k) if t16 else b.shape
+    if t16 and m > FP8_T16_MAX_M:
+        raise ValueError(f"a T16-prepacked weight serves M <= {FP8_T16_MAX_M}, got M={m}; pass the [N, K] codes")
     if kb != k:
         raise ValueError(f"K mismatch: a {k}, b {kb}")
     if k % 128:
@@ -383,11 +422,16 @@ def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: tor
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"out_dtype {out_dtype}")
     c = torch.empty(m, n, dtype=out_dtype, device=a.device)
+    dt = DT_F32 if out_dtype == torch.float32 else DT_BF16
+    if t16:
+        _lib.call("mosaic_fp8_block_gemm_t16", _ptr(a), _ptr(a_s), _ptr(b.codes), _ptr(b_s), _ptr(c), dt, m, n, k,
+                  _stream())
+        return c
     # partials of the split-K plan (shapes whose tiles cover under half the GPU)
     nbytes = _lib.lib().mosaic_fp8_block_gemm_workspace_bytes(m, n, k)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
-    _lib.call("mosaic_fp8_block_gemm_ws", _ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(c),
-              DT_F32 if out_dtype == torch.float32 else DT_BF16, m, n, k, _ptr(ws), nbytes, _stream())
+    _lib.call("mosaic_fp8_block_gemm_ws", _ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(c), dt, m, n, k, _ptr(ws),
+              nbytes, _stream())
     return c
 
 

@@ -118,3 +118,95 @@ def test_fp8_block_gemm_config3_m4096(dev, n, k):
     err = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
     assert err.max() <= 2e-2, f"({m}, {n}, {k}): max scaled err {err.max()}"
     assert torch.isfinite(c.float()).all()
+
+
+def _t16_layout(w: np.ndarray) -> np.ndarray:
+    """The T16 byte order by axis permutation: W [G*16 (c), nkb*128 (h, q, j)] viewed
+    as [G, c, nkb, h, q, j] and laid out as [G, nkb, h, c, q, j]."""
+    n, k = w.shape
+    return w.reshape(n // 16, 16, k // 128, 2, 4, 16).transpose(0, 2, 3, 1, 4, 5).reshape(n, k)
+
+
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (576, 7168), (4096, 1536)])
+def test_fp8_t16_prepack_layout_and_inverse(dev, n, k):
+    from mosaic_amd import ops
+    w = np.random.default_rng(n + k).integers(0, 256, (n, k), dtype=np.uint8)
+    t = ops.fp8_t16_prepack(torch.from_numpy(w).to(dev))
+    assert (t.n, t.k) == (n, k)
+    assert np.array_equal(t.codes.cpu().numpy(), _t16_layout(w))
+    assert np.array_equal(ops.fp8_t16_unpack(t).cpu().numpy(), w)
+
+
+def test_fp8_t16_rejects_bad_shapes(dev):
+    from mosaic_amd import ops
+    for n, k in [(20, 128), (16, 200)]:
+        with pytest.raises(ValueError):
+            ops.fp8_t16_prepack(torch.zeros(n, k, dtype=torch.uint8, device=dev))
+    t = ops.fp8_t16_prepack(torch.zeros(32, 256, dtype=torch.uint8, device=dev))
+    a = torch.zeros(17, 256, dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        ops.fp8_block_gemm(a, torch.ones(17, 2, device=dev), t, torch.ones(1, 2, device=dev))
+
+
+# every ring plan: K parts of 8 / 4 / 2 (one tile) and 2 / 4 (two tiles), ring
+# depths 3..8, short K (4 waves of 3 blocks), ragged K parts; N from one tile to
+# 24576 columns with N % 128 != 0 among them
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 576, 7168), (4, 1536, 1536), (1, 4096, 1536),
+                                   (2, 24576, 1536), (3, 7168, 2048), (1, 7168, 16384), (4, 18432, 1024),
+                                   (5, 2048, 1536), (16, 576, 7168), (16, 7168, 2048), (16, 24576, 1536),
+                                   (7, 6160, 1152), (16, 8192, 7168), (9, 4112, 640), (1, 1552, 2304)])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_fp8_block_gemm_t16_vs_oracle(dev, m, n, k, out):
+    """The GEMM over the T16 prepack: against the oracle (the float bar, and the
+    fp32 reassociation bound for an f32 output), and bit for bit against the
+    checkpoint-layout call wherever that one runs the same ring kernel."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(m * 11 + n + 3 * k)
+    aq, a_s, bq, bs = _case(rng, m, n, k)
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    od = torch.bfloat16 if out == "bf16" else torch.float32
+    c = ops.fp8_block_gemm(T(aq), T(a_s), ops.fp8_t16_prepack(T(bq)), T(bs), out_dtype=od)
+    ref = L.fp8_block_gemm(aq, a_s, bq, bs, out_bf16=(out == "bf16"))
+    got = c.float().cpu().numpy()
+    err = np.abs(got - ref) / np.maximum(1.0, np.abs(ref))
+    assert err.max() <= 2e-2, f"max scaled err {err.max()}"
+    if out == "f32":
+        abs_sum = L.fp8_block_gemm(aq & 0x7F, a_s, bq & 0x7F, np.abs(bs), out_bf16=False)
+        bound = 2.0 * (k // 128 + 128) * 2.0 ** -24 * abs_sum + 1e-30
+        assert (np.abs(got - ref) - bound).max() <= 0
+    nkb = k // 128
+    # the checkpoint-layout call runs the same ring plan (K parts included): ring
+    # shapes, except short K with two-tile workgroups, split 2 ways there
+    two_tile = m > 4 and (n + 31) // 32 >= 192
+    if nkb >= 8 and (n >= 4096 or nkb >= 32) and not (nkb <= 16 and two_tile):
+        c_raw = ops.fp8_block_gemm(T(aq), T(a_s), T(bq), T(bs), out_dtype=od)
+        assert torch.equal(c, c_raw)
+
+
+def test_fp8_gemm_dropin_caches_t16(dev):
+    """fp8_gemm / w8a8_block_fp8_matmul at M <= 16 read the cached T16 prepack:
+    one cache entry per weight, the checkpoint-layout result bit for bit, and a
+    new prepack after an in-place update of the weight."""
+    from mosaic_amd import ops
+    from mosaic_amd.kernels import _prepack_cache, fp8
+    m, n, k = 2, 4096, 2048
+    aq, a_s, bq, bs = _case(np.random.default_rng(5), m, n, k)
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    a, sa, b, sb = T(aq).view(torch.float8_e4m3fn), T(a_s), T(bq).view(torch.float8_e4m3fn), T(bs)
+    _prepack_cache.clear()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        c1 = fp8.fp8_gemm(a, sa, b, sb)
+        assert _prepack_cache.size() == 1
+        c2 = fp8.w8a8_block_fp8_matmul(a, b, sa, sb, [128, 128], torch.bfloat16)
+        assert _prepack_cache.size() == 1
+        raw = ops.fp8_block_gemm(a, sa, b, sb)
+        assert torch.equal(c1, raw) and torch.equal(c2, raw)
+        b.view(torch.uint8)[:16] = 0  # rows 0..15 now contribute nothing
+        c3 = fp8.fp8_gemm(a, sa, b, sb)
+        assert torch.equal(c3, ops.fp8_block_gemm(a, sa, b, sb))
+        assert (c3[:, :16] == 0).all() and torch.equal(c3[:, 16:], raw[:, 16:])
+    finally:
+        torch.set_default_dtype(prev)
+        _prepack_cache.clear()

@@ -1,7 +1,7 @@
 """Seeded random shapes through every dispatch of the linears, against the CPU oracle:
 the A8 MXFP4 linear (16-row kernel, staged 64- and 256-row plans, split K, N tails),
 the A16 MXFP4 linear (NK and KN layouts) and the FP8 block GEMM (skinny, decode ring,
-tiled, split K, big tiles).  Float bar |got - ref| <= 2e-2 * max(1, |ref|).  Sizes keep
+tiled, split K, big tiles; at M <= 16 also over the T16 prepack).  Float bar |got - ref| <= 2e-2 * max(1, |ref|).  Sizes keep
 each oracle call under ~1e8 multiply-adds."""
 from __future__ import annotations
 
@@ -80,6 +80,11 @@ def test_fp8_block_gemm_random_shapes(dev, seed):
     T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
     c = ops.fp8_block_gemm(T(aq), T(a_s), T(bq), T(bs))
     _close(c.float().cpu().numpy(), L.fp8_block_gemm(aq, a_s, bq, bs), f"fp8 {m}x{n}x{k}")
+    n16 = n - n % 16  # the T16 prepack of the weight's first whole 16-row groups
+    if m <= ops.FP8_T16_MAX_M and n16:
+        b16, s16 = bq[:n16], bs[:(n16 + 127) // 128]
+        ct = ops.fp8_block_gemm(T(aq), T(a_s), ops.fp8_t16_prepack(T(b16)), T(s16))
+        _close(ct.float().cpu().numpy(), L.fp8_block_gemm(aq, a_s, b16, s16), f"fp8 t16 {m}x{n16}x{k}")
 
 
 def _bank(rng, e, h, inter):
