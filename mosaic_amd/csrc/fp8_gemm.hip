@@ -415,7 +415,8 @@ __global__ void __launch_bounds__(BM * 2, 1) fp8_gemm_tiled_kernel(
   for (int nt = 0; nt < 4; ++nt) dp[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float sp = 0.f;
   const int kb0 = (int)blockIdx.y * kps, cnt = min(nkb, kb0 + kps) - kb0;
-  issue(0, kb0);
+  // a slice past K (never launched) copies nothing and writes zero partials
+  if (cnt > 0) issue(0, kb0);
   if (cnt > 1) issue(1, kb0 + 1);
   for (int i = 0; i < cnt; ++i) {
     // block kb0 + i landed for every wave (its copies, then the barrier); the next may still fly
@@ -513,6 +514,9 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
                              float* part = nullptr) {
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + kTileN - 1) / kTileN);
   const int nkb = (int)(k / 128), kps = (nkb + S - 1) / S;
+  // slices of kps blocks: only the non-empty ones are launched (K = 33 blocks
+  // in 8 slices of 5 would leave slice 7 starting past K)
+  S = (nkb + kps - 1) / kps;
   MOSAIC_LAUNCH((fp8_gemm_tiled_kernel<BM>), dim3((unsigned)tiles, (unsigned)S), dim3(BM * 2), 0, st, a, as, b,
                      bs, c, (int)m, (int)n, (int)k, out_f32, kps, S > 1 ? part : nullptr);
   if (S > 1) {

@@ -34,6 +34,9 @@ def _case(rng, m, n, k):
                                    (4096, 4608, 1152), (2560, 7000, 1408), (4000, 4352, 640),
                                    # split K (tiles under half the GPU): tiled<128> x 8 / x 4, tiled<256> x 3
                                    (128, 576, 7168), (128, 7168, 4096), (4096, 576, 7168),
+                                   # split K whose slices of ceil(K-blocks / S) would leave the last ones
+                                   # empty (33 blocks in 8 slices of 5, 25 in 6 of 5): 7 and 5 slices run
+                                   (128, 512, 4224), (256, 512, 4224), (128, 768, 3200), (256, 640, 3200),
                                    # decode ring kernel (M <= 16, N >= 4096): full rows, ragged N, uneven K parts;
                                    # tiles x K parts 2x2, 1x4, 1x8 (M > 4), 1x8 (M <= 4), 1x2
                                    (16, 7168, 4096), (3, 4100, 1024), (7, 5000, 2176), (2, 4096, 1152)])
