@@ -242,9 +242,10 @@ def config1_linear(torch, ops):
 
 
 def config3_fp8(torch, ops):
-    """FP8 block-scaled GEMMs, 5 shapes x M in {1, 16, 128, 4096}.
-    Copies of the weight (over 512 MB in all, twice the 256 MB MALL) rotate through
-    the graph, so every call reads its weight from HBM.  At M <= 16 the drop-ins
+    """BASELINE.json configs[2]: FP8 block-scaled GEMMs, 5 shapes x M in {1, 16, 128, 4096}
+    (and M = 64, not in the config: the mid-size kernel's range).  Copies of the
+    weight (over 512 MB in all, twice the 256 MB MALL) rotate through the graph,
+    so every call reads its weight from HBM.  At M <= 64 the drop-ins
     (fp8_gemm, w8a8_block_fp8_matmul) read the weight's cached T16 prepack, so
     ``us`` times that (each copy prepacked once, outside the timed graph) and
     ``us_checkpoint_layout`` the same call over the [N, K] codes."""
@@ -264,7 +265,7 @@ def config3_fp8(torch, ops):
         nrot = (512 << 20) // (n * k) + 1
         bqs = [bq0] + [bq0.clone() for _ in range(nrot - 1)]
         tqs = [ops.fp8_t16_prepack(b) for b in bqs]
-        for m in (1, 16, 128, 4096):
+        for m in (1, 16, 64, 128, 4096):
             x = torch.randn(m, k, generator=g, device=dev)
             aq, a_s = ops.act_quant(x, 128, "amax")
 

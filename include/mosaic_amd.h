@@ -179,11 +179,16 @@ int mosaic_fp8_t16_prepack(const uint8_t* w, uint8_t* out, int64_t n, int64_t k,
 int mosaic_fp8_t16_unpack(const uint8_t* t16, uint8_t* w, int64_t n, int64_t k, void* stream);
 
 /* mosaic_fp8_block_gemm with B given as its T16 prepack (bt, n * k bytes) and
- * m <= 16; b_s as for mosaic_fp8_block_gemm.  The same MFMA operands as the
- * checkpoint-layout decode kernel, so the same C bit for bit.  Same call sites
- * as mosaic_fp8_block_gemm (fp8_gemm, w8a8_block_fp8_matmul) at M <= 16. */
+ * m <= 64; b_s as for mosaic_fp8_block_gemm.  m <= 16: the decode kernel, the
+ * same MFMA operands as over the checkpoint layout, so the same C bit for bit.
+ * 16 < m <= 64: the weight streamed once against 2 or 4 groups of 16 rows
+ * of A, K split over the caller's workspace of workspace_bytes when it holds
+ * mosaic_fp8_block_gemm_t16_workspace_bytes(m, n, k) (NULL: unsplit).  Same
+ * call sites as mosaic_fp8_block_gemm (fp8_gemm, w8a8_block_fp8_matmul). */
+size_t mosaic_fp8_block_gemm_t16_workspace_bytes(int64_t m, int64_t n, int64_t k);
 int mosaic_fp8_block_gemm_t16(const uint8_t* a, const float* a_s, const uint8_t* bt, const float* b_s, void* c,
-                              int out_dtype, int64_t m, int64_t n, int64_t k, void* stream);
+                              int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* W8A16 linear with the in-GEMM weight decode of fp8_linear's fused kernel
  * (bench/fp8_core.py:160-231): y [m, n] bf16 = sum over 128-K blocks of

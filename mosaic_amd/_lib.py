@@ -39,7 +39,8 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_fp8_block_gemm_ws": (c_int, [P, P, P, P, P, I, I64, I64, I64, P, c_size_t, P]),
     "mosaic_fp8_t16_prepack": (c_int, [P, P, I64, I64, P]),
     "mosaic_fp8_t16_unpack": (c_int, [P, P, I64, I64, P]),
-    "mosaic_fp8_block_gemm_t16": (c_int, [P, P, P, P, P, I, I64, I64, I64, P]),
+    "mosaic_fp8_block_gemm_t16_workspace_bytes": (c_size_t, [I64, I64, I64]),
+    "mosaic_fp8_block_gemm_t16": (c_int, [P, P, P, P, P, I, I64, I64, I64, P, c_size_t, P]),
     "mosaic_mxt16_linear_a8": (c_int, [P, P, P, P, P, I64, I64, I64, P]),
     "mosaic_mxt16_linear_a8_workspace_bytes": (c_size_t, [I64, I64, I64]),
     "mosaic_mxt16_linear_a8_ws": (c_int, [P, P, P, P, P, I64, I64, I64, P, c_size_t, P]),

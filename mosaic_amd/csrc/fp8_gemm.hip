@@ -526,6 +526,197 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
   }
 }
 
+// Mid-size kernel (16 < M <= 64): the decode ring's weight stream with G
+// groups of 16 rows of A.  A workgroup owns 64 columns of C and one K slice
+// (blockIdx.y): four compute waves, a 16-column tile each, and a copier wave.
+// Every compute wave streams its tile's weight blocks through a register ring
+// LB blocks ahead with buffer loads (L = 2: the T16 prepack, 1 KB contiguous
+// per load; L = 0: the checkpoint rows), and waits for them only where the
+// compiler's own count places the wait.  The copier wave alone copies the A
+// blocks (G x 16 rows x 128 bytes, XOR-swizzled 16-byte chunks as the tiled
+// kernel stages them) and their a_s values into an LDS ring LA blocks ahead
+// with global -> LDS copies, so its copy wait is exact and no compute wave
+// waits behind a copy: each A block is read once per workgroup and used by
+// the four compute waves.  One barrier per block hands a stage over.  Per
+// block a compute wave runs G unit-scale MFMAs (roles transposed: lane (c, q)
+// holds C[16 g + c][n .. n + 3]) and rescales them by a_s x b_s into separate
+// fp32 accumulators.  The loop runs whole chunks of LB blocks; blocks past the
+// slice reload its last block and are scaled by 0.  With `part` the slice
+// writes its fp32 partials to part[slice][M][N].
+constexpr int kMidLA = 3, kMidDA = kMidLA + 1, kMidLB = 8;
+
+template <int G>
+struct Fp8Mid {
+  static constexpr int RUNS = 2 * G;                        // 1 KB A runs per block (copier wave)
+  static constexpr int SLOTS = G * 16 < 64 ? 64 : G * 16;   // a_s slots of a stage
+  static constexpr int SCOPIES = SLOTS / 64;                // 64-slot a_s copies per block
+  static constexpr int SA = G * 2048;                       // a_s offset in a stage
+  static constexpr int STAGE = SA + SLOTS * 4;
+  static constexpr int OPA = RUNS + SCOPIES;                // copies per block
+  static_assert((kMidLA - 1) * OPA <= 63, "the copy wait count fits vmcnt");
+};
+
+template <int G, int L>
+__global__ void __launch_bounds__(320) fp8_gemm_mid_kernel(const uint8_t* __restrict__ A, const float* __restrict__ As,
+                                                           const uint8_t* __restrict__ B,
+                                                           const float* __restrict__ Bs, void* __restrict__ C, int M,
+                                                           int N, int K, int out_f32, float* __restrict__ part) {
+  using TT = Fp8Mid<G>;
+  constexpr int LA = kMidLA, DA = kMidDA, LB = kMidLB;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[DA][TT::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int nkb = K / 128, ntile = N / 16;
+  const int S = gridDim.y;
+  const int kb0 = nkb * (int)blockIdx.y / S, nb = nkb * ((int)blockIdx.y + 1) / S - kb0;
+  const int nchunks = (nb + LB - 1) / LB;
+  if (wv == 4) {
+    // copier wave: run r is rows 8 r .. 8 r + 7 of the A block; the a_s copy j
+    // takes slots 64 j .. 64 j + 63
+    if (nb <= 0) return;
+    const uint8_t* gsrc[TT::RUNS];
+#pragma unroll
+    for (int r = 0; r < TT::RUNS; ++r) {
+      const int row = 8 * r + (lane >> 3);
+      const int logical = (lane & 7) ^ ((row >> 1) & 7);
+      gsrc[r] = A + (int64_t)min(row, M - 1) * K + logical * 16;
+    }
+    const float* ssrc[TT::SCOPIES];
+#pragma unroll
+    for (int j = 0; j < TT::SCOPIES; ++j) ssrc[j] = As + (int64_t)min(64 * j + lane, M - 1) * nkb;
+    auto issue = [&](int st, int kb) {
+      const uint32_t base = fp8_lds_addr(lds[st]);
+#pragma unroll
+      for (int r = 0; r < TT::RUNS; ++r) fp8_copy16(gsrc[r] + (int64_t)kb * 128, base + (uint32_t)(r * 1024));
+#pragma unroll
+      for (int j = 0; j < TT::SCOPIES; ++j) fp8_copy4(ssrc[j] + kb, base + (uint32_t)(TT::SA + 256 * j));
+    };
+#pragma unroll
+    for (int j = 0; j < LA; ++j) issue(j, kb0 + (j < nb ? j : nb - 1));
+    for (int ch = 0; ch < nchunks; ++ch) {
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int i = ch * LB + u;
+        // block i has landed: after its copies only those of the LA - 1 next blocks were issued
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((LA - 1) * TT::OPA) : "memory");
+        issue((u + LA) % DA, kb0 + (i + LA < nb ? i + LA : nb - 1));
+      }
+    }
+    // the copies issued past the slice land before the LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  const int tile = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + wv), tile_c = min(tile, ntile - 1);
+  // this wave's weight tile and its 128-row scale row
+  const __amdgpu_buffer_rsrc_t rb = fp8_rsrc(B + (int64_t)tile_c * 16 * K, (int64_t)16 * K);
+  const float* bs_row = Bs + (int64_t)(tile_c * 16 / 128) * nkb;
+  u32x4_t rbv[LB][2];
+  float rsb[LB];
+  auto load_b = [&](int s, int i) {
+    const int kb = kb0 + (i < nb ? i : nb - 1);
+    const uint32_t off = L == 2 ? (uint32_t)(kb * 2048 + 16 * (4 * c + q)) : (uint32_t)(c * K + kb * 128 + 16 * q);
+    rbv[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)off, 0, 0);
+    rbv[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(off + (L == 2 ? 1024 : 64)), 0, 0);
+    rsb[s] = bs_row[kb];
+  };
+  f32x4_t acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (nb > 0) {
+    // in slot order (the compiler's wait for slot u counts the loads issued after it)
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      load_b(j, j);
+      asm volatile("" ::: "memory");
+    }
+    for (int ch = 0; ch < nchunks; ++ch) {
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int i = ch * LB + u;
+        // this wave's reads of the stage the copier refills next are done
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const uint8_t* stg = lds[u % DA];
+        const float* sas = reinterpret_cast<const float*>(stg + TT::SA);
+        const i32x8_t bo = {(int)rbv[u][0][0], (int)rbv[u][0][1], (int)rbv[u][0][2], (int)rbv[u][0][3],
+                            (int)rbv[u][1][0], (int)rbv[u][1][1], (int)rbv[u][1][2], (int)rbv[u][1][3]};
+        const float sb = i < nb ? rsb[u] : 0.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const f32x4_t d = mfma_fp8_block(bo, lds_fp8_operand(stg, 16 * g + c, q));
+          const float sc = sas[16 * g + c] * sb;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[g][r] = __builtin_fmaf(d[r], sc, acc[g][r]);
+        }
+        load_b(u, i + LB);
+      }
+    }
+  }
+  if (tile >= ntile) return;
+  const int n = tile * 16 + 4 * q;
+  // 4-column vector stores where the output base allows them (N % 16 == 0)
+  const bool vec = (reinterpret_cast<uintptr_t>(part ? (const void*)part : C) & 15) == 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int m = 16 * g + c;
+    if (m >= M) continue;
+    const f32x4_t v = acc[g];
+    if (part || out_f32) {
+      float* o = part ? part + ((int64_t)blockIdx.y * M + m) * N + n : reinterpret_cast<float*>(C) + (int64_t)m * N + n;
+      if (vec) {
+        *reinterpret_cast<f32x4_t*>(o) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = v[r];
+      }
+    } else {
+      uint16_t* o = reinterpret_cast<uint16_t*>(C) + (int64_t)m * N + n;
+      if (vec) {
+        const uint32_t lo = (uint32_t)f32_bf16(v[0]) | ((uint32_t)f32_bf16(v[1]) << 16);
+        const uint32_t hi = (uint32_t)f32_bf16(v[2]) | ((uint32_t)f32_bf16(v[3]) << 16);
+        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = f32_bf16(v[r]);
+      }
+    }
+  }
+}
+
+// Mid-kernel plan: G groups of 16 rows (2 or 4); K split while the
+// workgroups number under 512, each slice keeping at least 8 blocks (the
+// slices' fp32 partials are summed by fp8_splitk_reduce_kernel).
+struct Fp8MidPlan {
+  int G, S;
+};
+static Fp8MidPlan fp8_mid_plan(int64_t m, int64_t n, int64_t k) {
+  const int G = m <= 32 ? 2 : 4;
+  const int64_t wgs = (n / 16 + 3) / 4, nkb = k / 128;
+  const int64_t s = std::min<int64_t>(8, std::min<int64_t>(512 / std::max<int64_t>(wgs, 1), nkb / 8));
+  return {G, (int)std::max<int64_t>(1, s)};
+}
+
+template <int L>
+static void launch_fp8_mid(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c, int64_t m,
+                           int64_t n, int64_t k, int out_f32, hipStream_t st, Fp8MidPlan plan, float* part) {
+  const int S = part ? plan.S : 1;
+  const dim3 grid((unsigned)((n / 16 + 3) / 4), (unsigned)S);
+  float* pp = S > 1 ? part : nullptr;
+#define FP8_MID(GV) \
+  MOSAIC_LAUNCH((fp8_gemm_mid_kernel<GV, L>), grid, dim3(320), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, \
+                out_f32, pp)
+  if (plan.G == 2)
+    FP8_MID(2);
+  else
+    FP8_MID(4);
+#undef FP8_MID
+  if (S > 1) {
+    const int64_t mn = m * n;
+    MOSAIC_LAUNCH(fp8_splitk_reduce_kernel, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, part, S, mn, c,
+                  out_f32);
+  }
+}
+
 // Large tiled kernel (enough 256 x 256 tiles to fill the chip): a workgroup
 // of 8 waves owns a 256 x 256 block of C; wave w owns rows 128 (w >> 2) and
 // columns 64 (w & 3) of it.  Twice the columns of the 256 x 128 kernel for
@@ -789,7 +980,7 @@ extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16
 
 // Kernel choice of the block GEMM.  kind 0: skinny, 1: tiled<128>, 2: tiled<256>,
 // 3: big tiles, 4: decode ring (M <= 16 with N >= 4096, or narrower N when K has
-// at least 32 blocks).  The tiled kernels split K into S slices (S > 1 needs the
+// at least 32 blocks), 5: mid kernel (17..64 rows, N % 16 == 0; its own K split).  The tiled kernels split K into S slices (S > 1 needs the
 // S * M * N * 4-byte partials workspace) when their tiles cover fewer than
 // half of the 256 CUs: S = min(8, 256 / tiles, K-blocks / 4).
 struct Fp8Plan {
@@ -807,7 +998,9 @@ static Fp8Plan fp8_plan(int64_t m, int64_t n, int64_t k) {
     if (big_tiles >= 256 && m * k < (1ll << 32) && n * k < (1ll << 32)) return {3, 1};
     return {2, split(((m + 255) / 256) * ((n + 127) / 128))};
   }
-  if (m >= 96) {
+  // 65..95 rows: the tiled kernel for weights of 8 MB and more (18432 x 7168:
+  // 180 -> 55 us), the skinny kernel below (576 x 7168: 11.7 against 16.9 us)
+  if (m >= 96 || (m > 64 && n * k >= (8ll << 20))) {
     const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
     const int s = split(tiles);
     if (tiles * s >= 32) return {1, s};
@@ -817,6 +1010,11 @@ static Fp8Plan fp8_plan(int64_t m, int64_t n, int64_t k) {
   // N = 576..2048, K = 7168: 9.2-9.6 -> 7.2-8.1 us and 11.8-12.3 -> 10.6-10.7 us
   // against the skinny kernel; at K = 1536 the skinny kernel stays faster)
   if (m <= 16 && nkb >= 8 && (n >= 4096 || nkb >= 32) && (int64_t)n * k < (1ll << 31)) return {4, 1};
+  // 17..64 rows over the checkpoint layout: the mid kernel, its weight read once,
+  // for weights of 8 MB and more (18432 x 7168, M = 64: 147 -> 61 us); below, the
+  // skinny kernel's latency is lower (576 x 7168, M = 64: 12.1 against 13.6 us)
+  if (m > 16 && m <= 64 && n % 16 == 0 && n * k >= (8ll << 20) && n * k < (1ll << 31))
+    return {5, fp8_mid_plan(m, n, k).S};
   return {0, 1};
 }
 
@@ -857,6 +1055,8 @@ static int fp8_block_gemm_impl(const uint8_t* a, const float* a_s, const uint8_t
         dispatch_fp8_gemv<0>(a, a_s, b, b_s, c, m, n, k, f32, st);
       else
         dispatch_fp8_gemv<1>(a, a_s, b, b_s, c, m, n, k, f32, st);
+      break;
+    case 5: launch_fp8_mid<0>(a, a_s, b, b_s, c, m, n, k, f32, st, fp8_mid_plan(m, n, k), plan.S > 1 ? part : nullptr);
       break;
     case 2: launch_fp8_tiled<256>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
     case 1: launch_fp8_tiled<128>(a, a_s, b, b_s, c, m, n, k, f32, st, plan.S, part); break;
@@ -912,16 +1112,31 @@ extern "C" int mosaic_fp8_t16_unpack(const uint8_t* t16, uint8_t* w, int64_t n, 
   return fp8_t16_convert(false, t16, w, n, k, stream);
 }
 
+extern "C" size_t mosaic_fp8_block_gemm_t16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 16 || m > 64 || n <= 0 || k <= 0 || k % 128 || n % 16) return 0;
+  const Fp8MidPlan plan = fp8_mid_plan(m, n, k);
+  return plan.S > 1 ? (size_t)plan.S * (size_t)m * (size_t)n * 4 : 0;
+}
+
 extern "C" int mosaic_fp8_block_gemm_t16(const uint8_t* a, const float* a_s, const uint8_t* bt, const float* b_s,
-                                         void* c, int out_dtype, int64_t m, int64_t n, int64_t k, void* stream) {
+                                         void* c, int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
   MOSAIC_CHECK_ARG(a && a_s && bt && b_s && c, "fp8_block_gemm_t16: null pointer");
-  MOSAIC_CHECK_ARG(m >= 0 && m <= 16, "fp8_block_gemm_t16: M=%lld; the T16 layout serves M <= 16", (long long)m);
+  MOSAIC_CHECK_ARG(m >= 0 && m <= 64, "fp8_block_gemm_t16: M=%lld; the T16 layout serves M <= 64", (long long)m);
   MOSAIC_CHECK_ARG(n >= 0 && n % 16 == 0 && k > 0 && k % 128 == 0 && (int64_t)n * k < (1ll << 31),
                    "fp8_block_gemm_t16: N=%lld (multiple of 16), K=%lld (multiple of 128), N*K < 2^31", (long long)n,
                    (long long)k);
   MOSAIC_CHECK_ARG(out_dtype == MOSAIC_DTYPE_F32 || out_dtype == MOSAIC_DTYPE_BF16,
                    "fp8_block_gemm_t16: out dtype %d", out_dtype);
   if (m == 0 || n == 0) return kOk;
-  dispatch_fp8_gemv<2>(a, a_s, bt, b_s, c, m, n, k, out_dtype == MOSAIC_DTYPE_F32, (hipStream_t)stream);
+  const int f32 = out_dtype == MOSAIC_DTYPE_F32;
+  hipStream_t st = (hipStream_t)stream;
+  if (m <= 16) {
+    dispatch_fp8_gemv<2>(a, a_s, bt, b_s, c, m, n, k, f32, st);
+  } else {
+    const Fp8MidPlan plan = fp8_mid_plan(m, n, k);
+    const bool split = plan.S > 1 && workspace && workspace_bytes >= (size_t)plan.S * m * n * 4;
+    launch_fp8_mid<2>(a, a_s, bt, b_s, c, m, n, k, f32, st, plan, split ? (float*)workspace : nullptr);
+  }
   MOSAIC_RETURN_LAUNCH("fp8_block_gemm_t16");
 }

@@ -39,8 +39,8 @@ def act_quant(x: torch.Tensor, block_size: int = 128, scale_fmt: str | None = No
 
 
 def _decode_weight(b: torch.Tensor, m: int):
-    """The cached T16 prepack of ``b`` for decode-sized calls (M <= 16, N % 16 == 0),
-    whose kernel then reads each 1 KB of weight contiguously; ``b`` itself otherwise.
+    """The cached T16 prepack of ``b`` for calls of up to 64 rows (N % 16 == 0), whose
+    kernels then read each 1 KB of weight contiguously; ``b`` itself otherwise.
     The prepack is one more copy of the weight, held while ``b`` lives unmodified."""
     if (m <= ops.FP8_T16_MAX_M and b.dim() == 2 and b.size(0) % 16 == 0 and b.size(1) % 128 == 0
             and b.size(1) > 0 and b.is_contiguous() and b.size(0) * b.size(1) < 2 ** 31):
@@ -51,7 +51,7 @@ def _decode_weight(b: torch.Tensor, m: int):
 def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
              scale_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """C[M, N] = A[M, K] @ B[N, K]^T with per-128 block scales (``inference_kernel.py:257-273``).
-    At M <= 16 the weight's T16 prepack is cached and read instead (the same C bit for bit)."""
+    At M <= 64 the weight's T16 prepack is cached and read instead (at M <= 16 the same C bit for bit)."""
     k = a.size(-1)
     m = a.numel() // k
     n = b.size(0)
@@ -81,7 +81,7 @@ def fp4_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
 def w8a8_block_fp8_matmul(A: torch.Tensor, B: torch.Tensor, As: torch.Tensor, Bs: torch.Tensor,
                           block_size: list[int], output_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """``hubkernel_matmul.py:333-360``: C = A @ B.T with [M, K/128] and [N/128, K/128] scales
-    (the weight's cached T16 prepack at M <= 16, as in ``fp8_gemm``)."""
+    (the weight's cached T16 prepack at M <= 64, as in ``fp8_gemm``)."""
     if list(block_size) != [128, 128]:
         raise ValueError(f"block_size {block_size}: only [128, 128] is supported")
     k = A.size(-1)

@@ -361,7 +361,7 @@ def mxt16_linear_a8(x: torch.Tensor | None, w: MXT16, prequant: tuple | None = N
 
 
 # ------------------------------------------------------- FP8 block GEMM -----
-FP8_T16_MAX_M = 16  # rows up to which fp8_block_gemm takes a T16-prepacked weight
+FP8_T16_MAX_M = 64  # rows up to which fp8_block_gemm takes a T16-prepacked weight
 
 
 @dataclass
@@ -398,7 +398,7 @@ def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor | FP8T16,
                    out_dtype=torch.bfloat16) -> torch.Tensor:
     """C [M, N] = block-scaled e4m3 GEMM (A [M, K] + a_s [M, K/128], B [N, K] + b_s [ceil(N/128), K/128]).
 
-    ``b`` may be an ``FP8T16`` prepack for M <= 16 (the same C bit for bit)."""
+    ``b`` may be an ``FP8T16`` prepack for M <= 64 (at M <= 16 the same C bit for bit)."""
     a = _u8(a, "a")
     t16 = isinstance(b, FP8T16)
     if not t16:
@@ -424,8 +424,10 @@ def fp8_block_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor | FP8T16,
     c = torch.empty(m, n, dtype=out_dtype, device=a.device)
     dt = DT_F32 if out_dtype == torch.float32 else DT_BF16
     if t16:
+        nbytes = _lib.lib().mosaic_fp8_block_gemm_t16_workspace_bytes(m, n, k)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=a.device) if nbytes else None
         _lib.call("mosaic_fp8_block_gemm_t16", _ptr(a), _ptr(a_s), _ptr(b.codes), _ptr(b_s), _ptr(c), dt, m, n, k,
-                  _stream())
+                  _ptr(ws), nbytes, _stream())
         return c
     # partials of the split-K plan (shapes whose tiles cover under half the GPU)
     nbytes = _lib.lib().mosaic_fp8_block_gemm_workspace_bytes(m, n, k)

@@ -39,7 +39,12 @@ def _case(rng, m, n, k):
                                    (128, 512, 4224), (256, 512, 4224), (128, 768, 3200), (256, 640, 3200),
                                    # decode ring kernel (M <= 16, N >= 4096): full rows, ragged N, uneven K parts;
                                    # tiles x K parts 2x2, 1x4, 1x8 (M > 4), 1x8 (M <= 4), 1x2
-                                   (16, 7168, 4096), (3, 4100, 1024), (7, 5000, 2176), (2, 4096, 1152)])
+                                   (16, 7168, 4096), (3, 4100, 1024), (7, 5000, 2176), (2, 4096, 1152),
+                                   # mid kernel (17..64 rows, N % 16 == 0, weights of 8 MB and more): 2 and
+                                   # 4 row groups, ragged rows, partial workgroups, K splits of 8 / 7 / none;
+                                   # and the tiled kernel at 65..95 rows
+                                   (17, 1280, 7168), (33, 1024, 8192), (50, 2064, 4096), (64, 4096, 2048),
+                                   (61, 2048, 8192), (24, 18432, 512), (80, 2048, 4096)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
     from mosaic_amd import ops
@@ -146,9 +151,9 @@ def test_fp8_t16_rejects_bad_shapes(dev):
         with pytest.raises(ValueError):
             ops.fp8_t16_prepack(torch.zeros(n, k, dtype=torch.uint8, device=dev))
     t = ops.fp8_t16_prepack(torch.zeros(32, 256, dtype=torch.uint8, device=dev))
-    a = torch.zeros(17, 256, dtype=torch.uint8, device=dev)
+    a = torch.zeros(65, 256, dtype=torch.uint8, device=dev)
     with pytest.raises(ValueError):
-        ops.fp8_block_gemm(a, torch.ones(17, 2, device=dev), t, torch.ones(1, 2, device=dev))
+        ops.fp8_block_gemm(a, torch.ones(65, 2, device=dev), t, torch.ones(1, 2, device=dev))
 
 
 # every ring plan: K parts of 8 / 4 / 2 (one tile) and 2 / 4 (two tiles), ring
@@ -157,7 +162,10 @@ def test_fp8_t16_rejects_bad_shapes(dev):
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 576, 7168), (4, 1536, 1536), (1, 4096, 1536),
                                    (2, 24576, 1536), (3, 7168, 2048), (1, 7168, 16384), (4, 18432, 1024),
                                    (5, 2048, 1536), (16, 576, 7168), (16, 7168, 2048), (16, 24576, 1536),
-                                   (7, 6160, 1152), (16, 8192, 7168), (9, 4112, 640), (1, 1552, 2304)])
+                                   (7, 6160, 1152), (16, 8192, 7168), (9, 4112, 640), (1, 1552, 2304),
+                                   # the mid kernel over the prepack (17..64 rows)
+                                   (17, 576, 7168), (32, 1536, 1536), (33, 48, 8192), (50, 2064, 1024),
+                                   (64, 4096, 2048), (40, 16, 128), (24, 18432, 256)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_t16_vs_oracle(dev, m, n, k, out):
     """The GEMM over the T16 prepack: against the oracle (the float bar, and the
@@ -179,15 +187,17 @@ def test_fp8_block_gemm_t16_vs_oracle(dev, m, n, k, out):
         assert (np.abs(got - ref) - bound).max() <= 0
     nkb = k // 128
     # the checkpoint-layout call runs the same ring plan (K parts included): ring
-    # shapes, except short K with two-tile workgroups, split 2 ways there
+    # shapes, except short K with two-tile workgroups, split 2 ways there; and
+    # the same mid-kernel plan at 17..64 rows for weights of 8 MB and more
     two_tile = m > 4 and (n + 31) // 32 >= 192
-    if nkb >= 8 and (n >= 4096 or nkb >= 32) and not (nkb <= 16 and two_tile):
+    ring = m <= 16 and nkb >= 8 and (n >= 4096 or nkb >= 32) and not (nkb <= 16 and two_tile)
+    if ring or (m > 16 and n * k >= 8 << 20):
         c_raw = ops.fp8_block_gemm(T(aq), T(a_s), T(bq), T(bs), out_dtype=od)
         assert torch.equal(c, c_raw)
 
 
 def test_fp8_gemm_dropin_caches_t16(dev):
-    """fp8_gemm / w8a8_block_fp8_matmul at M <= 16 read the cached T16 prepack:
+    """fp8_gemm / w8a8_block_fp8_matmul at M <= 64 read the cached T16 prepack:
     one cache entry per weight, the checkpoint-layout result bit for bit, and a
     new prepack after an in-place update of the weight."""
     from mosaic_amd import ops

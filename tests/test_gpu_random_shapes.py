@@ -1,7 +1,7 @@
 """Seeded random shapes through every dispatch of the linears, against the CPU oracle:
 the A8 MXFP4 linear (16-row kernel, staged 64- and 256-row plans, split K, N tails),
 the A16 MXFP4 linear (NK and KN layouts) and the FP8 block GEMM (skinny, decode ring,
-tiled, split K, big tiles; at M <= 16 also over the T16 prepack).  Float bar |got - ref| <= 2e-2 * max(1, |ref|).  Sizes keep
+tiled, split K, big tiles, mid; at M <= 64 also over the T16 prepack).  Float bar |got - ref| <= 2e-2 * max(1, |ref|).  Sizes keep
 each oracle call under ~1e8 multiply-adds."""
 from __future__ import annotations
 
