@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
                                                            const float* __restrict__ Bs, void* __restrict__ C, int M,
                                                            int N, int K, int out_f32) {
   __shared__ f32x4_t red[KS][T][64];
-  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * 16 * T;
   const int nkb = K / 128;
@@ -168,6 +168,9 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](int s, int i) {
+    // a_s read here, not hoisted to the chunk's start (where it would wait for every load in flight)
+    float sa = rsa[s];
+    asm volatile("" : "+v"(sa));
     const i32x8_t a = {(int)rav[s][0][0], (int)rav[s][0][1], (int)rav[s][0][2], (int)rav[s][0][3],
                        (int)rav[s][1][0], (int)rav[s][1][1], (int)rav[s][1][2], (int)rav[s][1][3]};
 #pragma unroll
@@ -180,7 +183,7 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
         bo[4 + j] = L == 1 ? __builtin_amdgcn_update_dpp(x1, x0, 0x128, 0xF, 0x3, false) : x1;
       }
       const f32x4_t d = mfma_fp8_block(bo, a);
-      const float sc = i < nb ? rsa[s] * rsb[s][t] : 0.f;
+      const float sc = i < nb ? sa * rsb[s][t] : 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(d[r], sc, acc[t][r]);
     }
@@ -188,12 +191,16 @@ __global__ void __launch_bounds__(KS * 64) fp8_gemv_kernel(const uint8_t* __rest
   const int nchunks = (nb + D - 1) / D;
   if (nb > 0) {
 #pragma unroll
-    for (int s = 0; s < D; ++s) load(s, s);
+    for (int s = 0; s < D; ++s) {
+      load(s, s);
+      asm volatile("" ::: "memory");  // in slot order: the compiler's waits count the later loads
+    }
     for (int ch = 0; ch + 1 < nchunks; ++ch) {
 #pragma unroll
       for (int s = 0; s < D; ++s) {
         compute(s, ch * D + s);
         load(s, ch * D + s + D);
+        asm volatile("" ::: "memory");
       }
     }
 #pragma unroll
