@@ -166,7 +166,10 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_gateup_kernel(
     }
   };
 #pragma unroll
-  for (int s = 0; s < D; ++s) load_step(s, rw_w[s], rw_s[s]);
+  for (int s = 0; s < D; ++s) {
+    load_step(s, rw_w[s], rw_s[s]);
+    asm volatile("" ::: "memory");  // in step order: the compiler's waits count the later loads
+  }
   // 4. x part -> wave-private LDS (the wave reads only what it wrote)
   uint8_t* xs = dec_smem + (size_t)w * nsp * 256;
 #pragma unroll
@@ -186,10 +189,17 @@ __global__ void __launch_bounds__(KS * 64) moe_dec1_gateup_kernel(
       dec_x(xs, real ? n : 0, q, xv);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint32_t sb = real ? (rw_s[s][t] >> (8 * (S & 3))) & 0xFFu : 0u;  // padded step: scale 0 -> W = 0
+        // the scale dword is read here, not hoisted to the chunk's start, where
+        // its wait would drain every load in flight
+        uint32_t sw = rw_s[s][t];
+        asm volatile("" : "+v"(sw));
+        const uint32_t sb = real ? (sw >> (8 * (S & 3))) & 0xFFu : 0u;  // padded step: scale 0 -> W = 0
         dec_mfma(rw_w[s][t], sb, xv, acc[t]);
       }
-      if constexpr (decltype(more)::value) load_step(n + D, rw_w[s], rw_s[s]);
+      if constexpr (decltype(more)::value) {
+        load_step(n + D, rw_w[s], rw_s[s]);
+        asm volatile("" ::: "memory");
+      }
     }
   };
   for (int ch = 0; ch < nchunks - 1; ++ch) chunk(ch, std::true_type{});
