@@ -41,7 +41,7 @@ __global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __r
                                                              const float* __restrict__ Ws, uint16_t* __restrict__ Y,
                                                              int M, int N, int K) {
   __shared__ f32x4_t red[KS][T][64];
-  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16;
   const int nkb = K / 128;
@@ -73,8 +73,14 @@ __global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __r
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](int s, int i) {
+    // this step's operands pass through empty volatile asm statements, which
+    // keep its MFMAs behind the previous step's loads: hoisted, their waits
+    // drained the ring
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(rxv[s][j]));
 #pragma unroll
     for (int t = 0; t < T; ++t) {
+      asm volatile("" : "+v"(rwv[s][t][0]), "+v"(rwv[s][t][1]));
       f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -82,7 +88,11 @@ __global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __r
         const bf16x8_t wb = e4m3x8_bf16(wv[2 * (j & 1)], wv[2 * (j & 1) + 1]);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, __builtin_bit_cast(bf16x8_t, rxv[s][j]), d, 0, 0, 0);
       }
-      const float sc = i < nb ? rs[s][t] : 0.f;
+      // the scale read here, not hoisted to the chunk's start (where its wait
+      // would drain every load in flight)
+      float sv = rs[s][t];
+      asm volatile("" : "+v"(sv));
+      const float sc = i < nb ? sv : 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(d[r], sc, acc[t][r]);
     }
@@ -90,12 +100,16 @@ __global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __r
   const int nchunks = (nb + D - 1) / D;
   if (nb > 0) {
 #pragma unroll
-    for (int s = 0; s < D; ++s) load(s, s);
+    for (int s = 0; s < D; ++s) {
+      load(s, s);
+      asm volatile("" ::: "memory");  // in slot order: the compiler's waits count the later loads
+    }
     for (int ch = 0; ch + 1 < nchunks; ++ch) {
 #pragma unroll
       for (int s = 0; s < D; ++s) {
         compute(s, ch * D + s);
         load(s, ch * D + s + D);
+        asm volatile("" ::: "memory");
       }
     }
 #pragma unroll
