@@ -150,6 +150,115 @@ __global__ void __launch_bounds__(KS * 64) mx_linear_a8_kernel(const uint8_t* __
   }
 }
 
+// Decode-shaped A8 linear (M <= 16): a workgroup owns 16 T columns and its KS
+// waves take K slices of whole 4-step groups; each wave streams its steps
+// through a register ring of D entries (the T tiles' 1 KB MXT16 code blocks
+// and scale dwords, the A operand and its 1x128 scale), issued D steps ahead.
+// Steps past the wave's slice reload its last step with a zero A operand, so
+// the loop has no branches.  A step's operands pass through empty volatile
+// asm statements and the loads are pinned in slot order, so the compiler's
+// waits keep the ring full.  The K slices meet in LDS in wave order.
+template <int T, int KS, int D>
+__global__ void __launch_bounds__(KS * 64) mx_gemv_a8_kernel(const uint8_t* __restrict__ xq,
+                                                              const float* __restrict__ sa,
+                                                              const uint8_t* __restrict__ packed_t,
+                                                              const uint8_t* __restrict__ scale_t,
+                                                              uint16_t* __restrict__ y, int M, int N, int K) {
+  __shared__ f32x4_t red[KS][T][64];
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16 * T;
+  const int ns = K / 128;
+  const uint8_t* wt[T];
+  const uint8_t* st[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) a8_ptrs(packed_t, scale_t, min(n0 / 16 + t, N / 16 - 1), ns, lane, wt[t], st[t]);
+  int s0, s1;
+  a8_k_slice(ns, ks, KS, s0, s1);
+  const int nb = s1 - s0;
+  const bool xvalid = c < M;
+  const uint8_t* xrow = xq + (int64_t)(xvalid ? c : 0) * K;
+  const float* sarow = sa + (int64_t)(xvalid ? c : 0) * ns;
+  u32x4_t rw[D][T], rx[D][2];
+  uint32_t rs[D][T];
+  float ra[D];
+  auto load = [&](int s, int i) {
+    const int S = s0 + (i < nb ? i : nb - 1);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      rw[s][t] = load_nt_u32x4(wt[t] + (int64_t)S * 1024);
+      rs[s][t] = *reinterpret_cast<const uint32_t*>(st[t] + (int64_t)(S >> 2) * 256);
+    }
+    rx[s][0] = *reinterpret_cast<const u32x4_t*>(xrow + 128 * S + 16 * q);
+    rx[s][1] = *reinterpret_cast<const u32x4_t*>(xrow + 128 * S + 64 + 16 * q);
+    ra[s] = sarow[S];
+  };
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int s, int i) {
+    const int S = s0 + i;
+    asm volatile("" : "+v"(rx[s][0]), "+v"(rx[s][1]), "+v"(ra[s]));
+    const bool real = i < nb && xvalid;
+    const u32x4_t lo = real ? rx[s][0] : u32x4_t{0u, 0u, 0u, 0u};
+    const u32x4_t hi = real ? rx[s][1] : u32x4_t{0u, 0u, 0u, 0u};
+    const i32x8_t av = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    const int sav = real ? pow2_e8m0(ra[s]) : 127;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      asm volatile("" : "+v"(rw[s][t]), "+v"(rs[s][t]));
+      const uint32_t sw = (rs[s][t] >> (8 * (S & 3))) & 0xFFu;
+      acc[t] = mfma_a8<0>(av, sav, rw[s][t], sw, acc[t]);
+    }
+  };
+  const int nchunks = (nb + D - 1) / D;
+  if (nb > 0) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      load(s, s);
+      asm volatile("" ::: "memory");  // in slot order: the compiler's waits count the later loads
+    }
+    for (int ch = 0; ch + 1 < nchunks; ++ch) {
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        compute(s, ch * D + s);
+        load(s, ch * D + s + D);
+        asm volatile("" ::: "memory");
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s) compute(s, (nchunks - 1) * D + s);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) red[ks][t][lane] = acc[t];
+  __syncthreads();
+  if (ks < T) {
+    const int t = ks;
+    f32x4_t v = red[0][t][lane];
+    for (int k2 = 1; k2 < KS; ++k2) v += red[k2][t][lane];
+    const int n = n0 + 16 * t + c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int mi = 4 * q + r;
+      if (mi < M && n < N) y[(int64_t)mi * N + n] = f32_bf16(v[r]);
+    }
+  }
+}
+
+// ring plans: few column tiles -> K split 8 ways, more -> 4 or 2 (as the FP8 decode ring)
+template <int T, int KS>
+static void launch_gemv_a8(const uint8_t* xq, const float* sa, const uint8_t* pt, const uint8_t* st, uint16_t* y,
+                           int64_t m, int64_t n, int64_t k, hipStream_t s) {
+  const dim3 grid((unsigned)((n + 16 * T - 1) / (16 * T)));
+  // 8-deep ring where the wave has at least 8 steps (7 or 6 deep, dividing the
+  // steps, measured 5-30% slower)
+  const int nb = (int)(k / 128 / KS);
+  if (nb >= 8)
+    MOSAIC_LAUNCH((mx_gemv_a8_kernel<T, KS, 8>), grid, dim3(KS * 64), 0, s, xq, sa, pt, st, y, (int)m, (int)n, (int)k);
+  else
+    MOSAIC_LAUNCH((mx_gemv_a8_kernel<T, KS, 4>), grid, dim3(KS * 64), 0, s, xq, sa, pt, st, y, (int)m, (int)n, (int)k);
+}
+
 template <int T, int KS>
 static void launch_linear_a8(const uint8_t* xq, const float* sa, const uint8_t* pt, const uint8_t* st, uint16_t* y,
                              int64_t m, int64_t n, int64_t k, hipStream_t s) {
@@ -1061,6 +1170,18 @@ static int mxt16_linear_a8_impl(const uint8_t* xq, const float* sa, const uint8_
     MOSAIC_RETURN_LAUNCH("mxt16_linear_a8_reduce");
   }
   const int64_t mt = (m + 15) / 16;
+  // one row: the ring kernel (18432 x 7168: 18.6 -> 17.0 us, 24576 x 1536: 7.9 ->
+  // 6.4 us); from two rows the 16-row kernel's shared A operand wins on some shapes
+  if (m == 1) {
+    const int64_t t16 = n / 16;
+    if (t16 <= 256)
+      launch_gemv_a8<1, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
+    else if (t16 <= 1152)
+      launch_gemv_a8<1, 4>(xq, sa, packed_t, scale_t, y, m, n, k, st);
+    else
+      launch_gemv_a8<1, 2>(xq, sa, packed_t, scale_t, y, m, n, k, st);
+    MOSAIC_RETURN_LAUNCH("mxt16_linear_a8");
+  }
   if (((n + 63) / 64) * mt * 8 >= 4096)
     launch_linear_a8<4, 8>(xq, sa, packed_t, scale_t, y, m, n, k, st);
   else if (((n + 31) / 32) * mt * 8 >= 4096)

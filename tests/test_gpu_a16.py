@@ -106,7 +106,10 @@ def test_mxt16_linear_a16_vs_oracle(dev, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (1, 2048, 7168), (3, 48, 640), (16, 64, 1024), (20, 7168, 2048),
-                                   (70, 96, 512)])
+                                   (70, 96, 512),
+                                   # one row: the ring kernel's plans (K split 8 / 4 / 2 ways, rings of 4 and 8,
+                                   # waves with no steps, a K tail of one step past whole 4-step groups)
+                                   (1, 7168, 2048), (1, 4608, 7168), (1, 20480, 640), (1, 1536, 1152)])
 def test_mxt16_linear_a8_vs_oracle(dev, m, n, k):
     """A8 "source semantics" linear (kernels/fp4_source.py:132-156) on the scaled MFMA."""
     ops = _ops()
