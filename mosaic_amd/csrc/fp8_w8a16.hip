@@ -131,6 +131,135 @@ __global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __r
   }
 }
 
+// 17..80 rows: the weight streamed once against G groups of 16 rows of x
+// (rows past m read row m - 1, their results are not stored).  A workgroup
+// owns 64 columns: four compute waves, a 16-column tile each, streaming their
+// weight blocks through an 8-deep register ring with exact waits (step
+// operands pinned behind the previous step's loads), and one copier wave that
+// alone copies the x blocks (G x 16 rows x 256 bytes; the 16-byte chunks of
+// row r XOR-swizzled by r % 16) into a four-stage LDS ring three blocks ahead
+// with global -> LDS copies, so its copy wait is exact.  One barrier per block
+// hands a stage over.  As in the decode kernel, lane (c, q) of MFMA step j
+// takes K indices 16q + 8(j & 1) + 64(j >> 1) + 0..7 of both operands.
+constexpr int kW8LA = 3, kW8DA = kW8LA + 1, kW8LB = 8;
+
+__device__ __forceinline__ uint32_t w8_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// one 16-byte global -> LDS copy per lane; the LDS address of lane i is base + 16 i
+__device__ __forceinline__ void w8_copy16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(g) : "memory", "m0");
+}
+
+template <int G>
+__global__ void __launch_bounds__(320) w8a16_mid_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+                                                        const float* __restrict__ Ws, uint16_t* __restrict__ Y, int M,
+                                                        int N, int K) {
+  constexpr int LA = kW8LA, DA = kW8DA, LB = kW8LB;
+  constexpr int RUNS = 4 * G;             // 1 KB x runs per block: 4 rows of 256 bytes each
+  constexpr int STAGE = G * 4096;
+  static_assert((LA - 1) * RUNS <= 63, "the copy wait count fits vmcnt");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[DA][STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int nkb = K / 128, ntile = (N + 15) / 16;
+  const int nchunks = (nkb + LB - 1) / LB;
+  if (wv == 4) {
+    // copier wave: run r is rows 4 r .. 4 r + 3; lane l copies physical chunk
+    // l % 16 of row 4 r + l / 16, which holds logical chunk (l % 16) ^ (row % 16)
+    const uint8_t* gsrc[RUNS];
+#pragma unroll
+    for (int r = 0; r < RUNS; ++r) {
+      const int row = 4 * r + (lane >> 4);
+      const int logical = (lane & 15) ^ (row & 15);
+      gsrc[r] = reinterpret_cast<const uint8_t*>(X + (int64_t)min(row, M - 1) * K) + logical * 16;
+    }
+    auto issue = [&](int st, int kb) {
+      const uint32_t base = w8_lds_addr(lds[st]);
+#pragma unroll
+      for (int r = 0; r < RUNS; ++r) w8_copy16(gsrc[r] + (int64_t)kb * 256, base + (uint32_t)(r * 1024));
+    };
+#pragma unroll
+    for (int j = 0; j < LA; ++j) issue(j, j < nkb ? j : nkb - 1);
+    for (int ch = 0; ch < nchunks; ++ch) {
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int i = ch * LB + u;
+        // block i has landed: after its copies only those of the LA - 1 next blocks were issued
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((LA - 1) * RUNS) : "memory");
+        issue((u + LA) % DA, i + LA < nkb ? i + LA : nkb - 1);
+      }
+    }
+    // the copies issued past K land before the LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  const int tile = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + wv), tile_c = min(tile, ntile - 1);
+  const int n0 = tile_c * 16;
+  const __amdgpu_buffer_rsrc_t rw = w8_rsrc(W + (int64_t)n0 * K, (int64_t)min(N - n0, 16) * K);
+  const float* s_row = Ws + (int64_t)(n0 / 128) * nkb;
+  u32x4_t rwv[LB][2];
+  float rs[LB];
+  auto load = [&](int s, int i) {
+    const int kb = i < nkb ? i : nkb - 1;
+    const uint32_t off = (uint32_t)(c * K + kb * 128 + 16 * q);
+    rwv[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, 0);
+    rwv[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(off + 64), 0, 0);
+    rs[s] = s_row[kb];
+  };
+  f32x4_t acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < LB; ++s) {
+    load(s, s);
+    asm volatile("" ::: "memory");  // in slot order: the compiler's waits count the later loads
+  }
+  for (int ch = 0; ch < nchunks; ++ch) {
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      const int i = ch * LB + u;
+      // this wave's reads of the stage the copier refills next are done
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const uint8_t* stg = lds[u % DA];
+      asm volatile("" : "+v"(rwv[u][0]), "+v"(rwv[u][1]));
+      bf16x8_t wb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wb[j] = e4m3x8_bf16(rwv[u][j >> 1][2 * (j & 1)], rwv[u][j >> 1][2 * (j & 1) + 1]);
+      const float sc = i < nkb ? rs[u] : 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int row = 16 * g + c;
+        const uint8_t* xr = stg + row * 256;
+        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int chunk = 2 * q + (j & 1) + 8 * (j >> 1);
+          const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xr + ((chunk ^ (row & 15)) << 4));
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[j], __builtin_bit_cast(bf16x8_t, xv), d, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[g][r] = __builtin_fmaf(d[r], sc, acc[g][r]);
+      }
+      load(u, i + LB);
+      asm volatile("" ::: "memory");
+    }
+  }
+  if (tile >= ntile) return;
+  // lane (c, q) of group g: y[16 g + c][n .. n + 3], n = 16 tile + 4 q
+  const int n = tile * 16 + 4 * q;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int m = 16 * g + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) Y[(int64_t)m * N + n + r] = f32_bf16(acc[g][r]);
+  }
+}
+
 template <int KS>
 void launch_w8a16(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m, int64_t n, int64_t k,
                   hipStream_t st) {
@@ -155,6 +284,19 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
   MOSAIC_CHECK_ARG(n * k < (1ll << 31) && m * k * 2 < (1ll << 31), "fp8_w8a16_linear: operands beyond 2 GiB");
   if (m == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
+  // 17..80 rows and N >= 4096 (at least 64 workgroups of 64 columns): the mid
+  // kernel, the weight read once (18432 x 7168 at M = 64: 172.5 -> 89.3 us);
+  // narrower N keeps the m-tile grid (1536 x 7168 at M = 64: 24.0 against 42.0 us)
+  if (m > 16 && n >= 4096) {
+    const dim3 grid((unsigned)(((n + 15) / 16 + 3) / 4));
+    if (m <= 32)
+      MOSAIC_LAUNCH(w8a16_mid_kernel<2>, grid, dim3(320), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+    else if (m <= 64)
+      MOSAIC_LAUNCH(w8a16_mid_kernel<4>, grid, dim3(320), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+    else
+      MOSAIC_LAUNCH(w8a16_mid_kernel<5>, grid, dim3(320), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+    MOSAIC_RETURN_LAUNCH("fp8_w8a16_linear");
+  }
   const int64_t tiles = (n + 15) / 16 * ((m + 15) / 16);
   if (tiles <= 256 && (k / 128) >= 16)
     launch_w8a16<8>(x, w, s, y, m, n, k, st);

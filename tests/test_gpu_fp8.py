@@ -69,7 +69,11 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
 
 @pytest.mark.parametrize("m,n,k,e8m0", [(1, 1536, 7168, False), (1, 18432, 7168, True), (16, 576, 7168, False),
                                         (37, 200, 1024, True), (80, 4096, 512, False), (3, 24576, 1536, True),
-                                        (5, 16, 128, False)])
+                                        (5, 16, 128, False),
+                                        # 17..80 rows, N >= 4096 (the mid kernel): 2, 4 and 5 row groups, N not a
+                                        # multiple of 16 / 128, one K block, K past one ring chunk; and below
+                                        (17, 4096, 2048, False), (64, 4112, 1024, True), (50, 4100, 384, False),
+                                        (72, 4096, 128, True), (33, 4608, 9216, False), (40, 1536, 1024, False)])
 def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
     identical codes and scales: bar 2e-2 * max(1, |ref|)."""
