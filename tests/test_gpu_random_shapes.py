@@ -1,8 +1,9 @@
 """Seeded random shapes through every dispatch of the linears, against the CPU oracle:
 the A8 MXFP4 linear (16-row kernel, staged 64- and 256-row plans, split K, N tails),
 the A16 MXFP4 linear (NK and KN layouts) and the FP8 block GEMM (skinny, decode ring,
-tiled, split K, big tiles, mid; at M <= 64 also over the T16 prepack).  Float bar |got - ref| <= 2e-2 * max(1, |ref|).  Sizes keep
-each oracle call under ~1e8 multiply-adds."""
+tiled, split K, big tiles, mid; at M <= 64 also over the T16 prepack), the one-row A8 ring
+and fp8_w8a16_linear.  Float bar |got - ref| <= 2e-2 * max(1, |ref|).  Sizes keep each
+oracle call under ~1e8 multiply-adds (a few 1e8-1e9 for the wide FP8 and W8A16 cases)."""
 from __future__ import annotations
 
 import numpy as np
@@ -85,6 +86,61 @@ def test_fp8_block_gemm_random_shapes(dev, seed):
         b16, s16 = bq[:n16], bs[:(n16 + 127) // 128]
         ct = ops.fp8_block_gemm(T(aq), T(a_s), ops.fp8_t16_prepack(T(b16)), T(s16))
         _close(ct.float().cpu().numpy(), L.fp8_block_gemm(aq, a_s, b16, s16), f"fp8 t16 {m}x{n16}x{k}")
+
+
+@pytest.mark.parametrize("seed", range(9))
+def test_a8_linear_one_row_random_shapes(dev, seed):
+    """One row through the A8 decode ring: N drawn so that every third case falls in each
+    of its plans (up to 256, up to 1152 and more 16-row tiles), K any multiple of 128."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(9250 + seed)
+    lo, hi = [(1, 256), (257, 1152), (1153, 1600)][seed % 3]
+    n = 16 * int(rng.integers(lo, hi + 1))
+    k = 128 * int(rng.integers(1, min(64, int(4e7 // (n * 128))) + 1))
+    p, s = C.quantize_mxfp4_ceil(_bf16(rng.standard_normal((n, k)) * 0.05).float().numpy())
+    x = _bf16(rng.standard_normal((1, k)))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    y = ops.mxt16_linear_a8(x.to(dev), ops.mxt16_prepack(T(p), T(s)))
+    _close(y.float().cpu().numpy(), L.mx_linear_a8(x.float().numpy(), p, s), f"a8 1x{n}x{k}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_fp8_w8a16_random_shapes(dev, seed):
+    """fp8_w8a16_linear at 1..80 rows: the decode ring (<= 16 rows), the mid kernel
+    (17..80 rows, N >= 4096) and the row-tile grid (narrower N), any N, K a multiple of 128."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(9260 + seed)
+    m = int(rng.integers(1, 17)) if seed % 3 == 0 else int(rng.integers(17, ops.W8A16_MAX_M + 1))
+    n = int(rng.integers(4096, 9001)) if seed % 3 != 2 else int(rng.integers(1, 4096))
+    k = 128 * int(rng.integers(1, min(24, int(4e8 // (m * n * 128))) + 1))
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    bq, bs = L.quantize_fp8_weight_128(w)
+    x = _bf16(rng.standard_normal((m, k)))
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    y = ops.fp8_w8a16_linear(x.to(dev), T(bq), T(bs))
+    _close(y.float().cpu().numpy(), L.fp8_w8a16_linear(x.float().numpy(), bq, bs), f"w8a16 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fp8_mid_random_shapes(dev, seed):
+    """17..64 rows with a weight of 8 MB and more (the mid kernel over the checkpoint rows,
+    split K when its workgroups are few), and the same weight over the T16 prepack."""
+    from mosaic_amd import ops
+    rng = np.random.default_rng(9270 + seed)
+    m = int(rng.integers(17, ops.FP8_T16_MAX_M + 1))
+    n = 16 * int(rng.integers(64, 513))
+    kmin = -(-(8 << 20) // (n * 128))
+    k = 128 * int(rng.integers(kmin, max(kmin, (24 << 20) // (n * 128)) + 1))
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    bq, bs = L.quantize_fp8_weight_128(w)
+    aq, a_s = C.act_quant(x, 128, "amax")
+    T = lambda v: torch.from_numpy(np.ascontiguousarray(v)).to(dev)
+    ref = L.fp8_block_gemm(aq, a_s, bq, bs)
+    c = ops.fp8_block_gemm(T(aq), T(a_s), T(bq), T(bs))
+    _close(c.float().cpu().numpy(), ref, f"fp8 mid {m}x{n}x{k}")
+    ct = ops.fp8_block_gemm(T(aq), T(a_s), ops.fp8_t16_prepack(T(bq)), T(bs))
+    _close(ct.float().cpu().numpy(), ref, f"fp8 mid t16 {m}x{n}x{k}")
 
 
 def _bank(rng, e, h, inter):
