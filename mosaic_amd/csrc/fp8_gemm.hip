@@ -534,8 +534,8 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
 }
 
 // Mid-size kernel (16 < M <= 64): the decode ring's weight stream with G
-// groups of 16 rows of A.  A workgroup owns 64 columns of C and one K slice
-// (blockIdx.y): four compute waves, a 16-column tile each, and a copier wave.
+// groups of 16 rows of A.  A workgroup owns 16 W columns of C and one K slice
+// (blockIdx.y): W compute waves, a 16-column tile each, and a copier wave.
 // Every compute wave streams its tile's weight blocks through a register ring
 // LB blocks ahead with buffer loads (L = 2: the T16 prepack, 1 KB contiguous
 // per load; L = 0: the checkpoint rows), and waits for them only where the
@@ -544,7 +544,7 @@ static void launch_fp8_tiled(const uint8_t* a, const float* as, const uint8_t* b
 // kernel stages them) and their a_s values into an LDS ring LA blocks ahead
 // with global -> LDS copies, so its copy wait is exact and no compute wave
 // waits behind a copy: each A block is read once per workgroup and used by
-// the four compute waves.  One barrier per block hands a stage over.  Per
+// its W compute waves.  One barrier per block hands a stage over.  Per
 // block a compute wave runs G unit-scale MFMAs (roles transposed: lane (c, q)
 // holds C[16 g + c][n .. n + 3]) and rescales them by a_s x b_s into separate
 // fp32 accumulators.  The loop runs whole chunks of LB blocks; blocks past the
@@ -563,8 +563,8 @@ struct Fp8Mid {
   static_assert((kMidLA - 1) * OPA <= 63, "the copy wait count fits vmcnt");
 };
 
-template <int G, int L>
-__global__ void __launch_bounds__(320) fp8_gemm_mid_kernel(const uint8_t* __restrict__ A, const float* __restrict__ As,
+template <int G, int L, int W>
+__global__ void __launch_bounds__((W + 1) * 64) fp8_gemm_mid_kernel(const uint8_t* __restrict__ A, const float* __restrict__ As,
                                                            const uint8_t* __restrict__ B,
                                                            const float* __restrict__ Bs, void* __restrict__ C, int M,
                                                            int N, int K, int out_f32, float* __restrict__ part) {
@@ -578,7 +578,7 @@ __global__ void __launch_bounds__(320) fp8_gemm_mid_kernel(const uint8_t* __rest
   const int S = gridDim.y;
   const int kb0 = nkb * (int)blockIdx.y / S, nb = nkb * ((int)blockIdx.y + 1) / S - kb0;
   const int nchunks = (nb + LB - 1) / LB;
-  if (wv == 4) {
+  if (wv == W) {
     // copier wave: run r is rows 8 r .. 8 r + 7 of the A block; the a_s copy j
     // takes slots 64 j .. 64 j + 63
     if (nb <= 0) return;
@@ -614,7 +614,7 @@ __global__ void __launch_bounds__(320) fp8_gemm_mid_kernel(const uint8_t* __rest
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
   }
-  const int tile = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + wv), tile_c = min(tile, ntile - 1);
+  const int tile = __builtin_amdgcn_readfirstlane((int)blockIdx.x * W + wv), tile_c = min(tile, ntile - 1);
   // this wave's weight tile and its 128-row scale row
   const __amdgpu_buffer_rsrc_t rb = fp8_rsrc(B + (int64_t)tile_c * 16 * K, (int64_t)16 * K);
   const float* bs_row = Bs + (int64_t)(tile_c * 16 / 128) * nkb;
@@ -690,32 +690,60 @@ __global__ void __launch_bounds__(320) fp8_gemm_mid_kernel(const uint8_t* __rest
   }
 }
 
-// Mid-kernel plan: G groups of 16 rows (2 or 4); K split while the
-// workgroups number under 512, each slice keeping at least 8 blocks (the
-// slices' fp32 partials are summed by fp8_splitk_reduce_kernel).
+// Mid-kernel plan: G groups of 16 rows (2 or 4), W compute waves (16-column
+// tiles) per workgroup and S K slices of at least 8 blocks each (the slices'
+// fp32 partials are summed by fp8_splitk_reduce_kernel).  Every workgroup
+// copies the whole A block stream of its slice, so wider workgroups copy A
+// fewer times; the (W, S) with 4 <= W <= 8 whose grid comes closest to one
+// workgroup per CU without passing 256 is taken, the fewest slices and then
+// the fewest waves on ties.  Measured with the weights cold at M = 32 / 64
+// against the earlier 4 waves and up to 512 workgroups: 18432 x 7168 (5, 1)
+// 38.5 -> 32.4 / 50.0 -> 42.0 us, 7168 x 16384 (7, 4) 34-35 -> 30.7 / 41-43 ->
+// 36.6 us, 24576 x 1536 (6, 1) 13.9 -> 12.3 / 16.9 -> 15.3 us; narrow N
+// keeps 4 waves.
 struct Fp8MidPlan {
-  int G, S;
+  int G, S, W;  // row groups, K slices, compute waves per workgroup
 };
 static Fp8MidPlan fp8_mid_plan(int64_t m, int64_t n, int64_t k) {
   const int G = m <= 32 ? 2 : 4;
-  const int64_t wgs = (n / 16 + 3) / 4, nkb = k / 128;
-  const int64_t s = std::min<int64_t>(8, std::min<int64_t>(512 / std::max<int64_t>(wgs, 1), nkb / 8));
-  return {G, (int)std::max<int64_t>(1, s)};
+  const int64_t tiles = n / 16, nkb = k / 128;
+  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(8, nkb / 8));
+  Fp8MidPlan plan{G, 1, 8};  // more than 2048 tiles: the widest workgroups, unsplit
+  int64_t best = 0;
+  for (int64_t sl = 1; sl <= smax; ++sl)
+    for (int w = 4; w <= 8; ++w) {
+      const int64_t wgs = (tiles + w - 1) / w * sl;
+      if (wgs <= 256 && wgs > best) {
+        best = wgs;
+        plan = {G, (int)sl, w};
+      }
+    }
+  return plan;
 }
 
 template <int L>
 static void launch_fp8_mid(const uint8_t* a, const float* as, const uint8_t* b, const float* bs, void* c, int64_t m,
                            int64_t n, int64_t k, int out_f32, hipStream_t st, Fp8MidPlan plan, float* part) {
   const int S = part ? plan.S : 1;
-  const dim3 grid((unsigned)((n / 16 + 3) / 4), (unsigned)S);
+  const dim3 grid((unsigned)((n / 16 + plan.W - 1) / plan.W), (unsigned)S);
   float* pp = S > 1 ? part : nullptr;
-#define FP8_MID(GV) \
-  MOSAIC_LAUNCH((fp8_gemm_mid_kernel<GV, L>), grid, dim3(320), 0, st, a, as, b, bs, c, (int)m, (int)n, (int)k, \
-                out_f32, pp)
-  if (plan.G == 2)
-    FP8_MID(2);
-  else
-    FP8_MID(4);
+#define FP8_MID(GV, WV)                                                                                           \
+  MOSAIC_LAUNCH((fp8_gemm_mid_kernel<GV, L, WV>), grid, dim3((WV + 1) * 64), 0, st, a, as, b, bs, c, (int)m, (int)n, \
+                (int)k, out_f32, pp)
+#define FP8_MID_W(GV)  \
+  switch (plan.W) {    \
+    case 5: FP8_MID(GV, 5); break; \
+    case 6: FP8_MID(GV, 6); break; \
+    case 7: FP8_MID(GV, 7); break; \
+    case 8: FP8_MID(GV, 8); break; \
+    default: FP8_MID(GV, 4); break; \
+  }
+  if (plan.G == 2) {
+    FP8_MID_W(2)
+  } else {
+    FP8_MID_W(4)
+  }
+#undef FP8_MID_W
 #undef FP8_MID
   if (S > 1) {
     const int64_t mn = m * n;

@@ -133,7 +133,7 @@ __global__ void __launch_bounds__(KS * 64) w8a16_gemv_kernel(const uint16_t* __r
 
 // 17..80 rows: the weight streamed once against G groups of 16 rows of x
 // (rows past m read row m - 1, their results are not stored).  A workgroup
-// owns 64 columns: four compute waves, a 16-column tile each, streaming their
+// owns 16 NW columns: NW compute waves, a 16-column tile each, streaming their
 // weight blocks through an 8-deep register ring with exact waits (step
 // operands pinned behind the previous step's loads), and one copier wave that
 // alone copies the x blocks (G x 16 rows x 256 bytes; the 16-byte chunks of
@@ -152,8 +152,8 @@ __device__ __forceinline__ void w8_copy16(const void* g, uint32_t lds) {
                "v"(g) : "memory", "m0");
 }
 
-template <int G>
-__global__ void __launch_bounds__(320) w8a16_mid_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+template <int G, int NW>
+__global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                                         const float* __restrict__ Ws, uint16_t* __restrict__ Y, int M,
                                                         int N, int K) {
   constexpr int LA = kW8LA, DA = kW8DA, LB = kW8LB;
@@ -166,7 +166,7 @@ __global__ void __launch_bounds__(320) w8a16_mid_kernel(const uint16_t* __restri
   const int c = lane & 15, q = lane >> 4;
   const int nkb = K / 128, ntile = (N + 15) / 16;
   const int nchunks = (nkb + LB - 1) / LB;
-  if (wv == 4) {
+  if (wv == NW) {
     // copier wave: run r is rows 4 r .. 4 r + 3; lane l copies physical chunk
     // l % 16 of row 4 r + l / 16, which holds logical chunk (l % 16) ^ (row % 16)
     const uint8_t* gsrc[RUNS];
@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(320) w8a16_mid_kernel(const uint16_t* __restri
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
   }
-  const int tile = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + wv), tile_c = min(tile, ntile - 1);
+  const int tile = __builtin_amdgcn_readfirstlane((int)blockIdx.x * NW + wv), tile_c = min(tile, ntile - 1);
   const int n0 = tile_c * 16;
   const __amdgpu_buffer_rsrc_t rw = w8_rsrc(W + (int64_t)n0 * K, (int64_t)min(N - n0, 16) * K);
   const float* s_row = Ws + (int64_t)(n0 / 128) * nkb;
@@ -284,17 +284,43 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
   MOSAIC_CHECK_ARG(n * k < (1ll << 31) && m * k * 2 < (1ll << 31), "fp8_w8a16_linear: operands beyond 2 GiB");
   if (m == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
-  // 17..80 rows and N >= 4096 (at least 64 workgroups of 64 columns): the mid
-  // kernel, the weight read once (18432 x 7168 at M = 64: 172.5 -> 89.3 us);
-  // narrower N keeps the m-tile grid (1536 x 7168 at M = 64: 24.0 against 42.0 us)
+  // 17..80 rows and N >= 4096 (at least 256 16-column tiles): the mid kernel,
+  // the weight read once (18432 x 7168 at M = 64: 172.5 -> 89.3 us with four
+  // compute waves a workgroup); narrower N keeps the m-tile grid (1536 x 7168
+  // at M = 64: 24.0 against 42.0 us)
   if (m > 16 && n >= 4096) {
-    const dim3 grid((unsigned)(((n + 15) / 16 + 3) / 4));
-    if (m <= 32)
-      MOSAIC_LAUNCH(w8a16_mid_kernel<2>, grid, dim3(320), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
-    else if (m <= 64)
-      MOSAIC_LAUNCH(w8a16_mid_kernel<4>, grid, dim3(320), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
-    else
-      MOSAIC_LAUNCH(w8a16_mid_kernel<5>, grid, dim3(320), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
+    // NW compute waves a workgroup (4..8; 7 for 5 row groups, whose 8-wave
+    // build spills): the widest grid that stays within one workgroup per CU,
+    // the fewest waves on ties (each workgroup copies all of x, so wider
+    // workgroups copy it fewer times)
+    const int64_t tiles = (n + 15) / 16;
+    const int nw_max = m > 64 ? 7 : 8;
+    int nw = nw_max;
+    int64_t best = 0;
+    for (int v = 4; v <= nw_max; ++v) {
+      const int64_t wgs = (tiles + v - 1) / v;
+      if (wgs <= 256 && wgs > best) best = wgs, nw = v;
+    }
+#define W8_MID(GV, NWV)                                                                                     \
+  MOSAIC_LAUNCH((w8a16_mid_kernel<GV, NWV>), dim3((unsigned)((tiles + NWV - 1) / NWV)), dim3((NWV + 1) * 64), 0, \
+                st, x, w, s, y, (int)m, (int)n, (int)k)
+#define W8_MID_G(GV)                  \
+  switch (nw) {                       \
+    case 5: W8_MID(GV, 5); break;     \
+    case 6: W8_MID(GV, 6); break;     \
+    case 7: W8_MID(GV, 7); break;     \
+    case 8: if constexpr (GV < 5) W8_MID(GV, 8); else W8_MID(GV, 7); break; \
+    default: W8_MID(GV, 4); break;    \
+  }
+    if (m <= 32) {
+      W8_MID_G(2)
+    } else if (m <= 64) {
+      W8_MID_G(4)
+    } else {
+      W8_MID_G(5)
+    }
+#undef W8_MID_G
+#undef W8_MID
     MOSAIC_RETURN_LAUNCH("fp8_w8a16_linear");
   }
   const int64_t tiles = (n + 15) / 16 * ((m + 15) / 16);
