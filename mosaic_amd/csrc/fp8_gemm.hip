@@ -705,7 +705,7 @@ struct Fp8MidPlan {
   int G, S, W;  // row groups, K slices, compute waves per workgroup
 };
 static Fp8MidPlan fp8_mid_plan(int64_t m, int64_t n, int64_t k) {
-  const int G = m <= 32 ? 2 : 4;
+  const int G = m <= 16 ? 1 : m <= 32 ? 2 : 4;
   const int64_t tiles = n / 16, nkb = k / 128;
   const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(8, nkb / 8));
   Fp8MidPlan plan{G, 1, 8};  // more than 2048 tiles: the widest workgroups, unsplit
@@ -719,6 +719,19 @@ static Fp8MidPlan fp8_mid_plan(int64_t m, int64_t n, int64_t k) {
       }
     }
   return plan;
+}
+
+// 12..16 rows: the mid kernel with one row group replaces the decode ring where
+// its plan needs no K split (a very wide N) and K has at least 48 blocks; the
+// ring's two-tile workgroups read A once per 32 columns, the mid kernel once
+// per 16 W.  Interleaved A/B, weights cold, M = 12 / 16, T16 and checkpoint
+// rows: 18432 x 7168 30.0 / 32.1 -> 26.4 / 26.6 us and 34.8 / 37.4 -> 29.3 /
+// 29.6 us; 32768 x 7168 46.2 / 48.5 -> 45.7 / 45.7 us and 50.2 / 55.4 -> 48.5 /
+// 48.8 us.  Not taken: 8 rows (32768 x 7168 over the checkpoint rows 46.4 ->
+// 48.4 us), K = 4096 (16384 x 4096: 15.3-18.6 -> 16.7-20.2 us), and the
+// narrower or shorter config shapes, which stay faster on the ring.
+static bool fp8_mid_small(int64_t m, int64_t n, int64_t k) {
+  return m >= 12 && m <= 16 && n % 16 == 0 && k / 128 >= 48 && fp8_mid_plan(m, n, k).S == 1;
 }
 
 template <int L>
@@ -738,7 +751,9 @@ static void launch_fp8_mid(const uint8_t* a, const float* as, const uint8_t* b, 
     case 8: FP8_MID(GV, 8); break; \
     default: FP8_MID(GV, 4); break; \
   }
-  if (plan.G == 2) {
+  if (plan.G == 1) {
+    FP8_MID_W(1)
+  } else if (plan.G == 2) {
     FP8_MID_W(2)
   } else {
     FP8_MID_W(4)
@@ -1015,7 +1030,8 @@ extern "C" int mosaic_fp8_block_dequant(const uint8_t* w, const float* s, uint16
 
 // Kernel choice of the block GEMM.  kind 0: skinny, 1: tiled<128>, 2: tiled<256>,
 // 3: big tiles, 4: decode ring (M <= 16 with N >= 4096, or narrower N when K has
-// at least 32 blocks), 5: mid kernel (17..64 rows, N % 16 == 0; its own K split).  The tiled kernels split K into S slices (S > 1 needs the
+// at least 32 blocks), 5: mid kernel (17..64 rows, N % 16 == 0, its own K split;
+// and 12..16 rows where fp8_mid_small holds).  The tiled kernels split K into S slices (S > 1 needs the
 // S * M * N * 4-byte partials workspace) when their tiles cover fewer than
 // half of the 256 CUs: S = min(8, 256 / tiles, K-blocks / 4).
 struct Fp8Plan {
@@ -1044,6 +1060,7 @@ static Fp8Plan fp8_plan(int64_t m, int64_t n, int64_t k) {
   // enough for its 8-wave split to leave each wave >= 4 blocks (M = 1 / 16,
   // N = 576..2048, K = 7168: 9.2-9.6 -> 7.2-8.1 us and 11.8-12.3 -> 10.6-10.7 us
   // against the skinny kernel; at K = 1536 the skinny kernel stays faster)
+  if (fp8_mid_small(m, n, k) && n * k < (1ll << 31)) return {5, 1};
   if (m <= 16 && nkb >= 8 && (n >= 4096 || nkb >= 32) && (int64_t)n * k < (1ll << 31)) return {4, 1};
   // 17..64 rows over the checkpoint layout: the mid kernel, its weight read once,
   // for weights of 8 MB and more (18432 x 7168, M = 64: 147 -> 61 us); below, the
@@ -1148,7 +1165,7 @@ extern "C" int mosaic_fp8_t16_unpack(const uint8_t* t16, uint8_t* w, int64_t n, 
 }
 
 extern "C" size_t mosaic_fp8_block_gemm_t16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-  if (m <= 16 || m > 64 || n <= 0 || k <= 0 || k % 128 || n % 16) return 0;
+  if (m <= 0 || m > 64 || n <= 0 || k <= 0 || k % 128 || n % 16 || (m <= 16 && !fp8_mid_small(m, n, k))) return 0;
   const Fp8MidPlan plan = fp8_mid_plan(m, n, k);
   return plan.S > 1 ? (size_t)plan.S * (size_t)m * (size_t)n * 4 : 0;
 }
@@ -1166,7 +1183,7 @@ extern "C" int mosaic_fp8_block_gemm_t16(const uint8_t* a, const float* a_s, con
   if (m == 0 || n == 0) return kOk;
   const int f32 = out_dtype == MOSAIC_DTYPE_F32;
   hipStream_t st = (hipStream_t)stream;
-  if (m <= 16) {
+  if (m <= 16 && !fp8_mid_small(m, n, k)) {
     dispatch_fp8_gemv<2>(a, a_s, bt, b_s, c, m, n, k, f32, st);
   } else {
     const Fp8MidPlan plan = fp8_mid_plan(m, n, k);

@@ -169,7 +169,10 @@ def test_fp8_t16_rejects_bad_shapes(dev):
                                    (7, 6160, 1152), (16, 8192, 7168), (9, 4112, 640), (1, 1552, 2304),
                                    # the mid kernel over the prepack (17..64 rows)
                                    (17, 576, 7168), (32, 1536, 1536), (33, 48, 8192), (50, 2064, 1024),
-                                   (64, 4096, 2048), (40, 16, 128), (24, 18432, 256)])
+                                   (64, 4096, 2048), (40, 16, 128), (24, 18432, 256),
+                                   # 12..16 rows on very wide shapes with K >= 48 blocks: the
+                                   # mid kernel with one row group instead of the ring
+                                   (12, 16384, 6144), (16, 18432, 6144)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_t16_vs_oracle(dev, m, n, k, out):
     """The GEMM over the T16 prepack: against the oracle (the float bar, and the
@@ -192,7 +195,8 @@ def test_fp8_block_gemm_t16_vs_oracle(dev, m, n, k, out):
     nkb = k // 128
     # the checkpoint-layout call runs the same ring plan (K parts included): ring
     # shapes, except short K with two-tile workgroups, split 2 ways there; and
-    # the same mid-kernel plan at 17..64 rows for weights of 8 MB and more
+    # the same mid-kernel plan at 17..64 rows for weights of 8 MB and more (and
+    # at 12..16 rows where both layouts take the mid kernel)
     two_tile = m > 4 and (n + 31) // 32 >= 192
     ring = m <= 16 and nkb >= 8 and (n >= 4096 or nkb >= 32) and not (nkb <= 16 and two_tile)
     if ring or (m > 16 and n * k >= 8 << 20):
