@@ -288,19 +288,29 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
   // the weight read once (18432 x 7168 at M = 64: 172.5 -> 89.3 us with four
   // compute waves a workgroup); narrower N keeps the m-tile grid (1536 x 7168
   // at M = 64: 24.0 against 42.0 us)
-  if (m > 16 && n >= 4096) {
-    // NW compute waves a workgroup (4..8; 7 for 5 row groups, whose 8-wave
-    // build spills): the widest grid that stays within one workgroup per CU,
-    // the fewest waves on ties (each workgroup copies all of x, so wider
-    // workgroups copy it fewer times)
-    const int64_t tiles = (n + 15) / 16;
-    const int nw_max = m > 64 ? 7 : 8;
-    int nw = nw_max;
-    int64_t best = 0;
-    for (int v = 4; v <= nw_max; ++v) {
-      const int64_t wgs = (tiles + v - 1) / v;
-      if (wgs <= 256 && wgs > best) best = wgs, nw = v;
-    }
+  // NW compute waves a workgroup (4..8; 7 for 5 row groups, whose 8-wave
+  // build spills): the widest grid that stays within one workgroup per CU,
+  // the fewest waves on ties (each workgroup copies all of x, so wider
+  // workgroups copy it fewer times)
+  const int64_t tiles = (n + 15) / 16;
+  const int nw_max = m > 64 ? 7 : 8;
+  int nw = nw_max;
+  int64_t best = 0;
+  for (int v = 4; v <= nw_max; ++v) {
+    const int64_t wgs = (tiles + v - 1) / v;
+    if (wgs <= 256 && wgs > best) best = wgs, nw = v;
+  }
+  // 4..16 rows with K >= 48 blocks and N wide enough for >= 224 such
+  // workgroups: the mid kernel with one row group instead of the decode ring,
+  // whose time grows with the rows (x is re-read once per 16-column tile)
+  // while the mid kernel's stays flat.  Weights cold, M = 4 / 8 / 16, ring
+  // against mid: 18432 x 7168 38.3 / 44.9 / 57.6 -> 30.1 / 30.4 / 31.9 us,
+  // 32768 x 7168 57.1 / 65.5 / 81.1 -> 48.4 / 49.1 / 49.6 us, 16384 x 7168
+  // 33.7 / 38.6 / 47.2 -> 29.8 / 29.5 / 30.2 us.  Not taken: 192 workgroups
+  // (12288 x 7168: 26.1 / 30.0 against 28.6 / 28.5 us at M = 4 / 8) and 1..3
+  // rows (16384 x 6144 at M = 1: 23.6 against 25.4 us).
+  const bool small_mid = m >= 4 && m <= 16 && k / 128 >= 48 && best >= 224;
+  if ((m > 16 && n >= 4096) || small_mid) {
 #define W8_MID(GV, NWV)                                                                                     \
   MOSAIC_LAUNCH((w8a16_mid_kernel<GV, NWV>), dim3((unsigned)((tiles + NWV - 1) / NWV)), dim3((NWV + 1) * 64), 0, \
                 st, x, w, s, y, (int)m, (int)n, (int)k)
@@ -312,7 +322,9 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
     case 8: if constexpr (GV < 5) W8_MID(GV, 8); else W8_MID(GV, 7); break; \
     default: W8_MID(GV, 4); break;    \
   }
-    if (m <= 32) {
+    if (m <= 16) {
+      W8_MID_G(1)
+    } else if (m <= 32) {
       W8_MID_G(2)
     } else if (m <= 64) {
       W8_MID_G(4)
@@ -323,10 +335,10 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
 #undef W8_MID
     MOSAIC_RETURN_LAUNCH("fp8_w8a16_linear");
   }
-  const int64_t tiles = (n + 15) / 16 * ((m + 15) / 16);
-  if (tiles <= 256 && (k / 128) >= 16)
+  const int64_t mtiles = tiles * ((m + 15) / 16);
+  if (mtiles <= 256 && (k / 128) >= 16)
     launch_w8a16<8>(x, w, s, y, m, n, k, st);
-  else if (tiles <= 1152 && (k / 128) >= 8)
+  else if (mtiles <= 1152 && (k / 128) >= 8)
     launch_w8a16<4>(x, w, s, y, m, n, k, st);
   else
     launch_w8a16<2>(x, w, s, y, m, n, k, st);

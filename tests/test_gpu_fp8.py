@@ -73,7 +73,9 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
                                         # 17..80 rows, N >= 4096 (the mid kernel): 2, 4 and 5 row groups, N not a
                                         # multiple of 16 / 128, one K block, K past one ring chunk; and below
                                         (17, 4096, 2048, False), (64, 4112, 1024, True), (50, 4100, 384, False),
-                                        (72, 4096, 128, True), (33, 4608, 9216, False), (40, 1536, 1024, False)])
+                                        (72, 4096, 128, True), (33, 4608, 9216, False), (40, 1536, 1024, False),
+                                        # 4..16 rows, K >= 48 blocks, wide N: the mid kernel with one row group
+                                        (4, 16384, 6144, False), (12, 16384, 6144, True), (16, 18432, 6144, False)])
 def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
     identical codes and scales: bar 2e-2 * max(1, |ref|)."""
