@@ -198,6 +198,14 @@ int mosaic_fp8_block_gemm_t16(const uint8_t* a, const float* a_s, const uint8_t*
  * dequantize + library GEMM path above 80 rows). */
 int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m, int64_t n,
                             int64_t k, void* stream);
+/* Bytes of the fp32 partials workspace that mosaic_fp8_w8a16_linear_ws uses to
+ * split K for this shape (0: the shape does not split). */
+size_t mosaic_fp8_w8a16_workspace_bytes(int64_t m, int64_t n, int64_t k);
+/* mosaic_fp8_w8a16_linear with a caller workspace (>= the bytes above to split
+ * K where the workgroups of one K pass would cover few CUs; with less, or
+ * NULL, the whole K runs in one pass).  Same arguments and result otherwise. */
+int mosaic_fp8_w8a16_linear_ws(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m,
+                               int64_t n, int64_t k, void* workspace, size_t workspace_bytes, void* stream);
 
 /* e4m3 [n, k] with one f32 scale per block_n x block_k block -> bf16 [n, k].
  * Replaces dequant_fp8 (runtime/fp8.py:52-64), dsa.dequant_weight

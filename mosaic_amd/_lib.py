@@ -46,6 +46,8 @@ SIGNATURES: dict[str, tuple] = {
     "mosaic_mxt16_linear_a8_ws": (c_int, [P, P, P, P, P, I64, I64, I64, P, c_size_t, P]),
     "mosaic_fp8_block_dequant": (c_int, [P, P, P, I64, I64, I, I, P]),
     "mosaic_fp8_w8a16_linear": (c_int, [P, P, P, P, I64, I64, I64, P]),
+    "mosaic_fp8_w8a16_workspace_bytes": (c_size_t, [I64, I64, I64]),
+    "mosaic_fp8_w8a16_linear_ws": (c_int, [P, P, P, P, I64, I64, I64, P, c_size_t, P]),
     "mosaic_moe_route_topk": (c_int, [P, I64, I64, I64, I, I, F, P, P, P, P]),
     "mosaic_router_logits": (c_int, [P, I, P, I, P, I64, I64, I64, P]),
     "mosaic_moe_layout_workspace_bytes": (c_size_t, [I64, I64, I64, I]),

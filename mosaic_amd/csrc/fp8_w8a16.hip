@@ -16,6 +16,8 @@
 // its blocks through a register ring of D entries issued D blocks ahead with
 // buffer loads (rows past n / m read zeros; entries past the wave's range are
 // scaled by 0), as the FP8 x FP8 decode kernel does.
+#include <algorithm>
+
 #include "common.h"
 #include "../../include/mosaic_amd.h"
 
@@ -155,7 +157,7 @@ __device__ __forceinline__ void w8_copy16(const void* g, uint32_t lds) {
 template <int G, int NW>
 __global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
                                                         const float* __restrict__ Ws, uint16_t* __restrict__ Y, int M,
-                                                        int N, int K) {
+                                                        int N, int K, float* __restrict__ part) {
   constexpr int LA = kW8LA, DA = kW8DA, LB = kW8LB;
   constexpr int RUNS = 4 * G;             // 1 KB x runs per block: 4 rows of 256 bytes each
   constexpr int STAGE = G * 4096;
@@ -164,8 +166,10 @@ __global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, q = lane >> 4;
-  const int nkb = K / 128, ntile = (N + 15) / 16;
-  const int nchunks = (nkb + LB - 1) / LB;
+  // K slice blockIdx.y of gridDim.y (at least 8 blocks each when split)
+  const int nkb = K / 128, ntile = (N + 15) / 16, S = gridDim.y;
+  const int kb0 = nkb * (int)blockIdx.y / S, nb = nkb * ((int)blockIdx.y + 1) / S - kb0;
+  const int nchunks = (nb + LB - 1) / LB;
   if (wv == NW) {
     // copier wave: run r is rows 4 r .. 4 r + 3; lane l copies physical chunk
     // l % 16 of row 4 r + l / 16, which holds logical chunk (l % 16) ^ (row % 16)
@@ -182,14 +186,14 @@ __global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t
       for (int r = 0; r < RUNS; ++r) w8_copy16(gsrc[r] + (int64_t)kb * 256, base + (uint32_t)(r * 1024));
     };
 #pragma unroll
-    for (int j = 0; j < LA; ++j) issue(j, j < nkb ? j : nkb - 1);
+    for (int j = 0; j < LA; ++j) issue(j, kb0 + (j < nb ? j : nb - 1));
     for (int ch = 0; ch < nchunks; ++ch) {
 #pragma unroll
       for (int u = 0; u < LB; ++u) {
         const int i = ch * LB + u;
         // block i has landed: after its copies only those of the LA - 1 next blocks were issued
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((LA - 1) * RUNS) : "memory");
-        issue((u + LA) % DA, i + LA < nkb ? i + LA : nkb - 1);
+        issue((u + LA) % DA, kb0 + (i + LA < nb ? i + LA : nb - 1));
       }
     }
     // the copies issued past K land before the LDS is released
@@ -203,7 +207,7 @@ __global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t
   u32x4_t rwv[LB][2];
   float rs[LB];
   auto load = [&](int s, int i) {
-    const int kb = i < nkb ? i : nkb - 1;
+    const int kb = kb0 + (i < nb ? i : nb - 1);
     const uint32_t off = (uint32_t)(c * K + kb * 128 + 16 * q);
     rwv[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, 0);
     rwv[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(off + 64), 0, 0);
@@ -228,7 +232,7 @@ __global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t
       bf16x8_t wb[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) wb[j] = e4m3x8_bf16(rwv[u][j >> 1][2 * (j & 1)], rwv[u][j >> 1][2 * (j & 1) + 1]);
-      const float sc = i < nkb ? rs[u] : 0.f;
+      const float sc = i < nb ? rs[u] : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int row = 16 * g + c;
@@ -256,7 +260,12 @@ __global__ void __launch_bounds__((NW + 1) * 64) w8a16_mid_kernel(const uint16_t
     if (m >= M) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      if (n + r < N) Y[(int64_t)m * N + n + r] = f32_bf16(acc[g][r]);
+      if (n + r < N) {
+        if (part)
+          part[((int64_t)blockIdx.y * M + m) * N + n + r] = acc[g][r];
+        else
+          Y[(int64_t)m * N + n + r] = f32_bf16(acc[g][r]);
+      }
   }
 }
 
@@ -271,13 +280,74 @@ void launch_w8a16(const uint16_t* x, const uint8_t* w, const float* s, uint16_t*
     MOSAIC_LAUNCH((w8a16_gemv_kernel<1, KS, 2>), grid, dim3(KS * 64), 0, st, x, w, s, y, (int)m, (int)n, (int)k);
 }
 
+
+// y = sum over the S slices of part, in slice order, as bf16; 4 elements a thread
+__global__ void __launch_bounds__(256) w8a16_splitk_reduce_kernel(const float* __restrict__ part, int S, int64_t mn,
+                                                                  uint16_t* __restrict__ Y) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = i0 + j;
+    if (i >= mn) break;
+    float v = part[i];
+    for (int sl = 1; sl < S; ++sl) v += part[(int64_t)sl * mn + i];
+    Y[i] = f32_bf16(v);
+  }
+}
+
+// Mid-kernel plan.  Every workgroup copies all of x for its K slice, so wider
+// workgroups copy it fewer times: NW compute waves (4..8; 7 for 5 row groups,
+// whose 8-wave build spills) and S K slices of at least 12 blocks (S > 1 only
+// with a partials workspace) are chosen for the widest grid that stays
+// within one workgroup per CU, the fewest slices and then the fewest waves on
+// ties.  Split against one pass, weights cold, M = 17 / 32 / 64 / 80:
+// 7168 x 16384 67.2 / 67.5 / 86.1 / 106.1 -> 38.4 / 39.8 / 46.6 / 51.6 us,
+// 4096 x 7168 31.0 / 31.4 / 39.0 / 50.5 -> 16.8 / 17.7 / 21.5 / 25.3 us;
+// slices of 8 blocks (7168 x 2048) gained nothing (11.9-18.4 against
+// 11.4-18.4 us).  4..16 rows take the mid kernel (one row group, unsplit) only where K
+// has >= 48 blocks and N gives >= 224 workgroups; there the decode ring's time
+// grows with the rows (x re-read once per 16-column tile) while the mid
+// kernel's stays flat.  Weights cold, M = 4 / 8 / 16, ring against mid:
+// 18432 x 7168 38.3 / 44.9 / 57.6 -> 30.1 / 30.4 / 31.9 us, 32768 x 7168
+// 57.1 / 65.5 / 81.1 -> 48.4 / 49.1 / 49.6 us, 16384 x 7168 33.7 / 38.6 /
+// 47.2 -> 29.8 / 29.5 / 30.2 us; not taken: 192 workgroups (12288 x 7168:
+// 26.1 / 30.0 against 28.6 / 28.5 us at M = 4 / 8) and 1..3 rows (16384 x
+// 6144 at M = 1: 23.6 against 25.4 us).
+struct W8MidPlan {
+  bool mid;
+  int nw, S;
+};
+static W8MidPlan w8_mid_plan(int64_t m, int64_t n, int64_t k, bool allow_split) {
+  const int64_t tiles = (n + 15) / 16, nkb = k / 128;
+  const int nw_max = m > 64 ? 7 : 8;
+  auto pick = [&](int64_t smax, int64_t& best) {
+    W8MidPlan p{true, nw_max, 1};
+    best = 0;
+    for (int64_t sl = 1; sl <= smax; ++sl)
+      for (int v = 4; v <= nw_max; ++v) {
+        const int64_t wgs = (tiles + v - 1) / v * sl;
+        if (wgs <= 256 && wgs > best) {
+          best = wgs;
+          p = {true, v, (int)sl};
+        }
+      }
+    return p;
+  };
+  int64_t best = 0;
+  if (m > 16 && n >= 4096)
+    return pick(allow_split ? std::max<int64_t>(1, std::min<int64_t>(8, nkb / 12)) : 1, best);
+  const W8MidPlan p = pick(1, best);
+  if (m >= 4 && m <= 16 && nkb >= 48 && best >= 224) return p;
+  return {false, 0, 1};
+}
+
 }  // namespace
 }  // namespace mosaic
 
 using namespace mosaic;
 
-extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m,
-                                       int64_t n, int64_t k, void* stream) {
+static int w8a16_linear_impl(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m, int64_t n,
+                             int64_t k, void* workspace, size_t workspace_bytes, void* stream) {
   MOSAIC_CHECK_ARG(x && w && s && y, "fp8_w8a16_linear: null pointer");
   MOSAIC_CHECK_ARG(k > 0 && k % 128 == 0, "fp8_w8a16_linear: K=%lld must be a positive multiple of 128", (long long)k);
   MOSAIC_CHECK_ARG(n > 0 && m >= 0 && m <= 80, "fp8_w8a16_linear: m=%lld (0..80) n=%lld", (long long)m, (long long)n);
@@ -286,34 +356,23 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
   hipStream_t st = (hipStream_t)stream;
   // 17..80 rows and N >= 4096 (at least 256 16-column tiles): the mid kernel,
   // the weight read once (18432 x 7168 at M = 64: 172.5 -> 89.3 us with four
-  // compute waves a workgroup); narrower N keeps the m-tile grid (1536 x 7168
-  // at M = 64: 24.0 against 42.0 us)
-  // NW compute waves a workgroup (4..8; 7 for 5 row groups, whose 8-wave
-  // build spills): the widest grid that stays within one workgroup per CU,
-  // the fewest waves on ties (each workgroup copies all of x, so wider
-  // workgroups copy it fewer times)
-  const int64_t tiles = (n + 15) / 16;
-  const int nw_max = m > 64 ? 7 : 8;
-  int nw = nw_max;
-  int64_t best = 0;
-  for (int v = 4; v <= nw_max; ++v) {
-    const int64_t wgs = (tiles + v - 1) / v;
-    if (wgs <= 256 && wgs > best) best = wgs, nw = v;
+  // compute waves a workgroup and no K split); narrower N keeps the m-tile
+  // grid (1536 x 7168 at M = 64: 24.0 against 42.0 us)
+  W8MidPlan plan = w8_mid_plan(m, n, k, true);
+  float* part = nullptr;
+  if (plan.mid && plan.S > 1) {
+    if (workspace && workspace_bytes >= (size_t)plan.S * m * n * 4)
+      part = reinterpret_cast<float*>(workspace);
+    else
+      plan = w8_mid_plan(m, n, k, false);  // no partials workspace: the whole K in one slice
   }
-  // 4..16 rows with K >= 48 blocks and N wide enough for >= 224 such
-  // workgroups: the mid kernel with one row group instead of the decode ring,
-  // whose time grows with the rows (x is re-read once per 16-column tile)
-  // while the mid kernel's stays flat.  Weights cold, M = 4 / 8 / 16, ring
-  // against mid: 18432 x 7168 38.3 / 44.9 / 57.6 -> 30.1 / 30.4 / 31.9 us,
-  // 32768 x 7168 57.1 / 65.5 / 81.1 -> 48.4 / 49.1 / 49.6 us, 16384 x 7168
-  // 33.7 / 38.6 / 47.2 -> 29.8 / 29.5 / 30.2 us.  Not taken: 192 workgroups
-  // (12288 x 7168: 26.1 / 30.0 against 28.6 / 28.5 us at M = 4 / 8) and 1..3
-  // rows (16384 x 6144 at M = 1: 23.6 against 25.4 us).
-  const bool small_mid = m >= 4 && m <= 16 && k / 128 >= 48 && best >= 224;
-  if ((m > 16 && n >= 4096) || small_mid) {
-#define W8_MID(GV, NWV)                                                                                     \
-  MOSAIC_LAUNCH((w8a16_mid_kernel<GV, NWV>), dim3((unsigned)((tiles + NWV - 1) / NWV)), dim3((NWV + 1) * 64), 0, \
-                st, x, w, s, y, (int)m, (int)n, (int)k)
+  const int64_t tiles = (n + 15) / 16;
+  if (plan.mid) {
+    const int nw = plan.nw;
+    const dim3 pgrid(1, (unsigned)plan.S);
+#define W8_MID(GV, NWV)                                                                                             \
+  MOSAIC_LAUNCH((w8a16_mid_kernel<GV, NWV>), dim3((unsigned)((tiles + NWV - 1) / NWV), pgrid.y), dim3((NWV + 1) * 64), \
+                0, st, x, w, s, y, (int)m, (int)n, (int)k, part)
 #define W8_MID_G(GV)                  \
   switch (nw) {                       \
     case 5: W8_MID(GV, 5); break;     \
@@ -333,6 +392,11 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
     }
 #undef W8_MID_G
 #undef W8_MID
+    if (part) {
+      const int64_t mn = m * n;
+      MOSAIC_LAUNCH(w8a16_splitk_reduce_kernel, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, part,
+                    plan.S, mn, y);
+    }
     MOSAIC_RETURN_LAUNCH("fp8_w8a16_linear");
   }
   const int64_t mtiles = tiles * ((m + 15) / 16);
@@ -343,4 +407,21 @@ extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, cons
   else
     launch_w8a16<2>(x, w, s, y, m, n, k, st);
   MOSAIC_RETURN_LAUNCH("fp8_w8a16_linear");
+}
+
+extern "C" int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m,
+                                       int64_t n, int64_t k, void* stream) {
+  return w8a16_linear_impl(x, w, s, y, m, n, k, nullptr, 0, stream);
+}
+
+extern "C" size_t mosaic_fp8_w8a16_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || m > 80 || n <= 0 || k <= 0 || k % 128) return 0;
+  const W8MidPlan plan = w8_mid_plan(m, n, k, true);
+  return plan.mid && plan.S > 1 ? (size_t)plan.S * (size_t)m * (size_t)n * 4 : 0;
+}
+
+extern "C" int mosaic_fp8_w8a16_linear_ws(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m,
+                                          int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                                          void* stream) {
+  return w8a16_linear_impl(x, w, s, y, m, n, k, workspace, workspace_bytes, stream);
 }

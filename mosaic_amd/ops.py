@@ -457,7 +457,11 @@ def fp8_w8a16_linear(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor) -> torch
     if tuple(s.shape) != ((n + 127) // 128, k // 128):
         raise ValueError(f"scale shape {tuple(s.shape)} != ({(n + 127) // 128}, {k // 128})")
     y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
-    _lib.call("mosaic_fp8_w8a16_linear", _ptr(x), _ptr(w), _ptr(s), _ptr(y), m, n, k, _stream())
+    # partials of the split-K plan (shapes whose workgroups cover few CUs in one K pass)
+    nbytes = _lib.lib().mosaic_fp8_w8a16_workspace_bytes(m, n, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
+    _lib.call("mosaic_fp8_w8a16_linear_ws", _ptr(x), _ptr(w), _ptr(s), _ptr(y), m, n, k, _ptr(ws), nbytes,
+              _stream())
     return y
 
 

@@ -75,7 +75,10 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
                                         (17, 4096, 2048, False), (64, 4112, 1024, True), (50, 4100, 384, False),
                                         (72, 4096, 128, True), (33, 4608, 9216, False), (40, 1536, 1024, False),
                                         # 4..16 rows, K >= 48 blocks, wide N: the mid kernel with one row group
-                                        (4, 16384, 6144, False), (12, 16384, 6144, True), (16, 18432, 6144, False)])
+                                        (4, 16384, 6144, False), (12, 16384, 6144, True), (16, 18432, 6144, False),
+                                        # 17..80 rows over few tiles: the mid kernel with K split (2 and 4 slices,
+                                        # N % 16 != 0 with 5 row groups)
+                                        (32, 7168, 8192, False), (64, 4096, 7168, True), (80, 4100, 3072, False)])
 def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
     identical codes and scales: bar 2e-2 * max(1, |ref|)."""
@@ -95,6 +98,30 @@ def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     ref = L.fp8_w8a16_linear(x.float().numpy(), bq, bs)
     err = np.abs(y.float().cpu().numpy() - ref) / np.maximum(1.0, np.abs(ref))
     assert err.max() <= 2e-2, err.max()
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 7168, 8192), (80, 4100, 3072)])
+def test_fp8_w8a16_split_matches_unsplit_entry(dev, m, n, k):
+    """The workspace entry splits K for these shapes (fp32 partials summed in slice
+    order); the plain entry runs the whole K in one pass: both within the float bar
+    of the oracle, and within fp32 reassociation of each other."""
+    from mosaic_amd import _lib, ops
+    assert _lib.lib().mosaic_fp8_w8a16_workspace_bytes(m, n, k) > 0
+    rng = np.random.default_rng(m + 7 * n + k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    bq, bs = L.quantize_fp8_weight_128(w)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    wd, sd = torch.from_numpy(bq).to(dev), torch.from_numpy(bs).to(dev)
+    y_split = ops.fp8_w8a16_linear(x, wd, sd)
+    y_one = torch.empty_like(y_split)
+    _lib.call("mosaic_fp8_w8a16_linear", x.data_ptr(), wd.data_ptr(), sd.data_ptr(), y_one.data_ptr(), m, n, k,
+              torch.cuda.current_stream().cuda_stream)
+    ref = L.fp8_w8a16_linear(x.float().cpu().numpy(), bq, bs)
+    for y in (y_split, y_one):
+        err = np.abs(y.float().cpu().numpy() - ref) / np.maximum(1.0, np.abs(ref))
+        assert err.max() <= 2e-2, err.max()
+    diff = (y_split.float() - y_one.float()).abs() / y_one.float().abs().clamp_min(1.0)
+    assert diff.max().item() <= 2 ** -7  # one bf16 rounding apart at most
 
 
 def _device_fp8_case(dev, m, n, k, seed):
