@@ -311,8 +311,10 @@ __global__ void __launch_bounds__(256) w8a16_splitk_reduce_kernel(const float* _
 // 18432 x 7168 38.3 / 44.9 / 57.6 -> 30.1 / 30.4 / 31.9 us, 32768 x 7168
 // 57.1 / 65.5 / 81.1 -> 48.4 / 49.1 / 49.6 us, 16384 x 7168 33.7 / 38.6 /
 // 47.2 -> 29.8 / 29.5 / 30.2 us; not taken: 192 workgroups (12288 x 7168:
-// 26.1 / 30.0 against 28.6 / 28.5 us at M = 4 / 8) and 1..3 rows (16384 x
-// 6144 at M = 1: 23.6 against 25.4 us).
+// 26.1 / 30.0 against 28.6 / 28.5 us at M = 4 / 8).  1..3 rows take it only
+// with 5 or more compute waves a workgroup (M = 1: 18432 x 7168 33.1 -> 30.2,
+// 32768 x 7168 51.3 -> 48.6 us); with 4 the ring stays faster (16384 x 6144
+// at M = 1: 23.6 against 25.4 us).
 struct W8MidPlan {
   bool mid;
   int nw, S;
@@ -337,7 +339,7 @@ static W8MidPlan w8_mid_plan(int64_t m, int64_t n, int64_t k, bool allow_split) 
   if (m > 16 && n >= 4096)
     return pick(allow_split ? std::max<int64_t>(1, std::min<int64_t>(8, nkb / 12)) : 1, best);
   const W8MidPlan p = pick(1, best);
-  if (m >= 4 && m <= 16 && nkb >= 48 && best >= 224) return p;
+  if (m <= 16 && nkb >= 48 && best >= 224 && (m >= 4 || p.nw >= 5)) return p;
   return {false, 0, 1};
 }
 
