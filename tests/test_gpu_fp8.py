@@ -79,7 +79,10 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
                                         (1, 18432, 6144, True),
                                         # 17..80 rows over few tiles: the mid kernel with K split (2 and 4 slices,
                                         # N % 16 != 0 with 5 row groups)
-                                        (32, 7168, 8192, False), (64, 4096, 7168, True), (80, 4100, 3072, False)])
+                                        (32, 7168, 8192, False), (64, 4096, 7168, True), (80, 4100, 3072, False),
+                                        # 6 and 7 compute waves (K split 4 ways), and 5 row groups past 256
+                                        # workgroups (7 waves)
+                                        (64, 24576, 1536, False), (48, 7168, 6144, True), (72, 32768, 512, False)])
 def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
     identical codes and scales: bar 2e-2 * max(1, |ref|)."""
@@ -202,7 +205,9 @@ def test_fp8_t16_rejects_bad_shapes(dev):
                                    (64, 4096, 2048), (40, 16, 128), (24, 18432, 256),
                                    # 12..16 rows on very wide shapes with K >= 48 blocks: the
                                    # mid kernel with one row group instead of the ring
-                                   (12, 16384, 6144), (16, 18432, 6144)])
+                                   (12, 16384, 6144), (16, 18432, 6144),
+                                   # 6, 7 (K split 4 ways) and 8 compute waves a workgroup
+                                   (20, 24576, 1536), (40, 7168, 4096), (24, 32768, 1024)])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_fp8_block_gemm_t16_vs_oracle(dev, m, n, k, out):
     """The GEMM over the T16 prepack: against the oracle (the float bar, and the
