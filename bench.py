@@ -64,7 +64,8 @@ def parse():
                     help="comma-separated subset of config1_linear_m1, config3_fp8_gemm, config3_mxfp4_gemm, "
                          "config4_moe_prefill, config5_dsa to run (default: all); config3_vendor_fp8 and "
                          "config3_vendor_mx (the vendor library's per-tensor FP8 and MX block-scaled GEMMs at "
-                         "the config-3 shapes, calibrations) run only when named")
+                         "the config-3 shapes, calibrations) and config3_w8a16 (fp8_linear's W8A16 path at the "
+                         "config-3 weight shapes) run only when named")
     ap.add_argument("--no-headline", action="store_true",
                     help="skip the decode layer (one bank is still built for config 4); for profiling the configs")
     ap.add_argument("--no-graph", action="store_true",
@@ -308,6 +309,31 @@ def config3_vendor_fp8(torch, ops):
         out[f"m4096_n{n}_k{k}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
                                    "mfma_frac": round(fl / us / 1e6 / 5000.0, 4)}
         del bs, b0
+    return out
+
+
+def config3_w8a16(torch, ops):
+    """fp8_linear's W8A16 path (bench/fp8_core.py:160-231; not a BASELINE.json row): bf16
+    activations against e4m3 weights with 128 x 128 fp32 block scales, the weight decoded
+    inside the GEMM (ops.fp8_w8a16_linear, with its split-K workspace), at M = 1, 16, 64 and
+    80 on the config-3 weight shapes, the weights rotating past the MALL as in config 3."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    out = {}
+    for n, k in [(1536, 7168), (24576, 1536), (576, 7168), (7168, 16384), (18432, 7168)]:
+        nrot = (512 << 20) // (n * k) + 1
+        w0 = (torch.randn(n, k, generator=g, device=dev) * 0.02).clamp(-0.4, 0.4).to(torch.float8_e4m3fn)
+        ws = [w0.view(torch.uint8)] + [w0.view(torch.uint8).clone() for _ in range(nrot - 1)]
+        s = torch.rand((n + 127) // 128, k // 128, generator=g, device=dev) * 1e-3 + 1e-4
+        for m in (1, 16, 64, 80):
+            x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+            it = iter(range(10 ** 9))
+            us = _graph_time(torch, lambda: ops.fp8_w8a16_linear(x, ws[next(it) % nrot], s), nrot, reps=3)
+            byt = n * k + 4 * ((n + 127) // 128) * (k // 128) + 2 * m * k + 2 * m * n
+            out[f"m{m}_n{n}_k{k}"] = {"us": round(us, 2), "GBs": round(byt / us / 1e3, 1),
+                                      "hbm_frac": round(byt / us / 1e3 / 8000.0, 4)}
+        del ws, w0
     return out
 
 
@@ -804,10 +830,11 @@ def _config_fns(torch, ops, banks):
             ("config5_dsa", lambda: config5_dsa(torch, ops))]
 
 
-# run only when named in --configs (calibration lines, not BASELINE.json configs)
+# run only when named in --configs (calibration lines and the W8A16 drop-in, not BASELINE.json configs)
 def _optional_config_fns(torch, ops):
     return [("config3_vendor_fp8", lambda: config3_vendor_fp8(torch, ops)),
-            ("config3_vendor_mx", lambda: config3_vendor_mx(torch, ops))]
+            ("config3_vendor_mx", lambda: config3_vendor_mx(torch, ops)),
+            ("config3_w8a16", lambda: config3_w8a16(torch, ops))]
 
 
 def _selected_configs(args, torch, ops, banks):

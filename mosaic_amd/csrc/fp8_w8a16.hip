@@ -340,6 +340,15 @@ static W8MidPlan w8_mid_plan(int64_t m, int64_t n, int64_t k, bool allow_split) 
     return pick(allow_split ? std::max<int64_t>(1, std::min<int64_t>(8, nkb / 12)) : 1, best);
   const W8MidPlan p = pick(1, best);
   if (m <= 16 && nkb >= 48 && best >= 224 && (m >= 4 || p.nw >= 5)) return p;
+  // 12..16 rows over a narrower N with a weight of >= 40 MB: the K split fills
+  // the grid (ring against split mid at M = 12 / 16: 7168 x 16384 40.8 / 46.2
+  // -> 35.9 / 36.3 us, 7168 x 8192 22.0 / 24.3 -> 19.6 / 19.8 us, 8192 x 7168
+  // 22.2 / 24.6 -> 19.3 / 19.2 us); below 40 MB the split's fixed cost loses
+  // (4096 x 7168: 12.2 / 13.6 against 14.4 / 14.6 us), and so do 8 rows or fewer
+  if (allow_split && m >= 12 && m <= 16 && nkb >= 48 && n * k >= (40ll << 20)) {
+    const W8MidPlan q = pick(std::max<int64_t>(1, std::min<int64_t>(8, nkb / 12)), best);
+    if (best >= 224) return q;
+  }
   return {false, 0, 1};
 }
 

@@ -82,7 +82,9 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
                                         (32, 7168, 8192, False), (64, 4096, 7168, True), (80, 4100, 3072, False),
                                         # 6 and 7 compute waves (K split 4 ways), and 5 row groups past 256
                                         # workgroups (7 waves)
-                                        (64, 24576, 1536, False), (48, 7168, 6144, True), (72, 32768, 512, False)])
+                                        (64, 24576, 1536, False), (48, 7168, 6144, True), (72, 32768, 512, False),
+                                        # 12..16 rows, a weight of >= 40 MB over few tiles: one row group, K split
+                                        (16, 7168, 8192, False)])
 def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
     identical codes and scales: bar 2e-2 * max(1, |ref|)."""
@@ -104,7 +106,7 @@ def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     assert err.max() <= 2e-2, err.max()
 
 
-@pytest.mark.parametrize("m,n,k", [(32, 7168, 8192), (80, 4100, 3072)])
+@pytest.mark.parametrize("m,n,k", [(32, 7168, 8192), (80, 4100, 3072), (12, 7168, 8192)])
 def test_fp8_w8a16_split_matches_unsplit_entry(dev, m, n, k):
     """The workspace entry splits K for these shapes (fp32 partials summed in slice
     order); the plain entry runs the whole K in one pass: both within the float bar
