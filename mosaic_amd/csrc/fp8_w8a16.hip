@@ -336,8 +336,14 @@ static W8MidPlan w8_mid_plan(int64_t m, int64_t n, int64_t k, bool allow_split) 
     return p;
   };
   int64_t best = 0;
-  if (m > 16 && n >= 4096)
-    return pick(allow_split ? std::max<int64_t>(1, std::min<int64_t>(8, nkb / 12)) : 1, best);
+  const int64_t smax = allow_split ? std::max<int64_t>(1, std::min<int64_t>(8, nkb / 12)) : 1;
+  if (m > 16 && n >= 4096) return pick(smax, best);
+  // 33..80 rows over 1536..4095 columns with K >= 32 blocks: only with a K
+  // split (the m-tile ring re-reads the weight once per 16 rows; unsplit, the
+  // mid kernel's few workgroups lose).  Ring against split mid at M = 64 / 80:
+  // 1536 x 7168 23.8 / 23.8 -> 19.5 / 22.3 us, 2048 x 7168 24.1 / 34.4 -> 19.9 /
+  // 22.4 us; 576 columns, K = 2048 and 32 rows or fewer stay on the ring.
+  if (smax > 1 && m > 32 && n >= 1536 && nkb >= 32) return pick(smax, best);
   const W8MidPlan p = pick(1, best);
   if (m <= 16 && nkb >= 48 && best >= 224 && (m >= 4 || p.nw >= 5)) return p;
   // 12..16 rows over a narrower N with a weight of >= 40 MB: the K split fills

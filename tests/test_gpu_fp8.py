@@ -84,7 +84,9 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
                                         # workgroups (7 waves)
                                         (64, 24576, 1536, False), (48, 7168, 6144, True), (72, 32768, 512, False),
                                         # 12..16 rows, a weight of >= 40 MB over few tiles: one row group, K split
-                                        (16, 7168, 8192, False)])
+                                        (16, 7168, 8192, False),
+                                        # 33..80 rows over 1536..4095 columns: the mid kernel with a K split
+                                        (64, 2048, 4096, True), (80, 1536, 7168, False)])
 def test_fp8_w8a16_linear_vs_oracle(dev, m, n, k, e8m0):
     """fp8_linear's fused decode (bench/fp8_core.py:160-194) against the oracle of
     identical codes and scales: bar 2e-2 * max(1, |ref|)."""
