@@ -202,8 +202,10 @@ int mosaic_fp8_w8a16_linear(const uint16_t* x, const uint8_t* w, const float* s,
  * split K for this shape (0: the shape does not split). */
 size_t mosaic_fp8_w8a16_workspace_bytes(int64_t m, int64_t n, int64_t k);
 /* mosaic_fp8_w8a16_linear with a caller workspace (>= the bytes above to split
- * K where the workgroups of one K pass would cover few CUs; with less, or
- * NULL, the whole K runs in one pass).  Same arguments and result otherwise. */
+ * K where the workgroups of one K pass would cover few CUs: 17..80 rows over
+ * N >= 4096, 33..80 rows over 1536 <= N < 4096 with K >= 4096, 12..16 rows
+ * over weights of >= 40 MB with K >= 6144; with less, or NULL, the whole K
+ * runs in one pass).  Same arguments and result otherwise. */
 int mosaic_fp8_w8a16_linear_ws(const uint16_t* x, const uint8_t* w, const float* s, uint16_t* y, int64_t m,
                                int64_t n, int64_t k, void* workspace, size_t workspace_bytes, void* stream);
 
