@@ -346,6 +346,11 @@ static W8MidPlan w8_mid_plan(int64_t m, int64_t n, int64_t k, bool allow_split) 
   if (smax > 1 && m > 32 && n >= 1536 && nkb >= 32) return pick(smax, best);
   const W8MidPlan p = pick(1, best);
   if (m <= 16 && nkb >= 48 && best >= 224 && (m >= 4 || p.nw >= 5)) return p;
+  // shorter K (12..47 blocks) from 12 rows: ring against mid at M = 12 / 16,
+  // 24576 x 1536 14.3 / 16.1 -> 13.6 / 13.8 us, 18432 x 2048 14.9 / 16.6 ->
+  // 11.9 / 12.1 us, 16384 x 4096 22.8 / 24.6 -> 18.6 / 18.8 us (at 4..8 rows
+  // the ring won on some of them: 24576 x 1536 at M = 8 12.7 against 13.4 us)
+  if (m >= 12 && m <= 16 && nkb >= 12 && best >= 224) return p;
   // 12..16 rows over a narrower N with a weight of >= 40 MB: the K split fills
   // the grid (ring against split mid at M = 12 / 16: 7168 x 16384 40.8 / 46.2
   // -> 35.9 / 36.3 us, 7168 x 8192 22.0 / 24.3 -> 19.6 / 19.8 us, 8192 x 7168

@@ -76,7 +76,7 @@ def test_fp8_block_gemm_vs_oracle(dev, m, n, k, out):
                                         (72, 4096, 128, True), (33, 4608, 9216, False), (40, 1536, 1024, False),
                                         # 4..16 rows, K >= 48 blocks, wide N: the mid kernel with one row group
                                         (4, 16384, 6144, False), (12, 16384, 6144, True), (16, 18432, 6144, False),
-                                        (1, 18432, 6144, True),
+                                        (1, 18432, 6144, True), (12, 24576, 1536, False), (16, 18432, 2048, True),
                                         # 17..80 rows over few tiles: the mid kernel with K split (2 and 4 slices,
                                         # N % 16 != 0 with 5 row groups)
                                         (32, 7168, 8192, False), (64, 4096, 7168, True), (80, 4100, 3072, False),
